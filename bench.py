@@ -1,0 +1,206 @@
+"""Batch-1 decode benchmark of the per-token path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--workload qwen2.5-0.5b]
+
+A step is one decode token at batch 1: one HIP graph launch covering every
+layer, the LM head and the greedy argmax, with the token fed back on the
+device.  The default workload is the Qwen2.5-0.5B-shaped decoder (24 layers,
+hidden 896, q4 g32 linears, fp16 tied head): a 128-token random prompt, then
+K = 256 greedy decode steps timed (positions 127..382), after W untimed
+warm-up steps over the same positions.  Weights are synthetic N(0, 0.02).
+
+Prints one JSON line.  Besides tok/s it reports the fraction of the HBM
+roofline (algorithmic bytes per token over 8 TB/s), the LM head kernel's
+roofline (the dominant kernel: 57% of the bytes) and a CPU baseline: the
+oracle's single-threaded restatement of the reference CPU path timed on a
+bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+HBM_PEAK = 8.0e12  # bytes/s, MI355X HBM3E
+
+
+def _package():
+    import importlib.util
+    if "three_llm_amd" in sys.modules:
+        return sys.modules["three_llm_amd"]
+    pkg_dir = ROOT / "three-llm_amd"
+    spec = importlib.util.spec_from_file_location("three_llm_amd", pkg_dir / "__init__.py",
+                                                  submodule_search_locations=[str(pkg_dir)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["three_llm_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def bytes_per_token(hw, position: int, kv_first: int = 0) -> float:
+    """Algorithmic HBM bytes to compute the token at `position` (reads the
+    cache rows [kv_first, position]): weights once, one embedding row, norms,
+    biases, the KV read and the KV write.  Activations are excluded."""
+    r = hw.recipe
+    H, I, V, L = r.hidden_size, r.inner_size, r.vocab_size, r.layer_count
+    nqkv = r.q_size + 2 * r.kv_size
+    bpw = {"q4": 0.5 + 2.0 / 32, "f16": 2.0, "f32": 4.0}
+    lin = L * bpw[hw.storage.linear] * (nqkv * H + H * r.q_size + 2 * I * H + H * I)
+    head = V * H * (2.0 if r.tied_embeddings else bpw[hw.storage.head])
+    emb = H * (4 if hw.storage.embed == "f32" else 2)
+    norms = (2 * L + 1) * H * 4 + (L * nqkv * 4 if r.qkv_bias else 0)
+    esz = 4 if hw.storage.kv == "f32" else 2
+    kv_row = L * 2 * r.kv_head_count * r.head_dim * esz
+    return lin + head + emb + norms + (position + 1 - kv_first) * kv_row + kv_row
+
+
+def lm_head_bytes(hw) -> float:
+    r = hw.recipe
+    return r.vocab_size * r.hidden_size * 2.0 + r.hidden_size * 4 + r.vocab_size * 4
+
+
+def read_traffic(kernel: str):
+    """HBM bytes per launch measured with rocprofv3 PMC counters, from the
+    committed profile summary (None if that summary does not exist yet)."""
+    p = ROOT / "profiles" / f"{kernel}_traffic.txt"
+    if not p.exists():
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(hw, prompt, budget_s: float):
+    """The oracle (C restatement of the reference CPU path: fp32 storage,
+    double accumulation, one thread) over positions 0, 1, ... of the same
+    prompt until the time budget is spent."""
+    sys.path.insert(0, str(ROOT))
+    sys.path.insert(0, str(ROOT / "tests"))
+    from bridge import oracle_model  # the checker, used here only as the baseline
+
+    om = oracle_model(hw, max(len(prompt), 64), kv_f16=False, threads=1)
+    t0 = time.perf_counter()
+    n = 0
+    while n < len(prompt) and (time.perf_counter() - t0) < budget_s:
+        om.forward(int(prompt[n]), n)
+        n += 1
+    dt = time.perf_counter() - t0
+    om.close()
+    return n / dt, n, dt
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--workload", default="qwen2.5-0.5b")
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work (0 disables)")
+    ap.add_argument("--kernel-iters", type=int, default=50)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU; the multi-GPU (tensor-parallel) decode path is a design "
+              "only (see DESIGN.md), so --gpus must be 1", file=sys.stderr)
+        sys.exit(2)
+
+    pkg = _package()
+    W, R, tlm = pkg.weights, pkg.runner, pkg.tlm
+    wl = W.WORKLOADS[args.workload]
+    t0 = time.perf_counter()
+    hw = W.synthetic(wl)
+    hw.keep = True
+    ctx = tlm.Context(0)
+    dev_name, cus = ctx.info()
+    max_tokens = max(wl.max_tokens, wl.kv_prefill + wl.prompt_len + args.steps + 1)
+    runner = R.DecoderHIPRunner(hw, {"maxTokens": max_tokens}, ctx=ctx)
+    log(f"[bench] {wl.name} on {dev_name}: weights ready in {time.perf_counter() - t0:.1f}s")
+    log(f"[bench] layout: {runner.model.describe()}")
+    prompt = [int(t) for t in W.prompt_tokens(wl)]
+    start = wl.kv_prefill
+    if wl.kv_prefill:
+        runner.model.kv_fill_normal(0xC0FFEE, wl.kv_prefill)
+    # prompt prefill (reference semantics: the decode graph replayed per token)
+    prefill_n = len(prompt) - 1
+    ctx.sync()
+    tp = time.perf_counter()
+    if prefill_n > 0:
+        runner.prefillTokens([0] * start + prompt, start, start + prefill_n)
+    ctx.sync()
+    prefill_s = time.perf_counter() - tp
+    last, pos0 = prompt[-1], start + prefill_n
+    steps, warmup = args.steps, args.warmup
+    if pos0 + max(steps, warmup) > max_tokens:
+        raise SystemExit("bench.py: steps exceed the context")
+    # warm-up over the same positions, then the timed region
+    if warmup:
+        runner.decodeGreedy(last, pos0, warmup)
+    ctx.sync()
+    t1 = time.perf_counter()
+    tokens = runner.decodeGreedy(last, pos0, steps)  # launches K graphs, one sync at the end
+    ctx.sync()
+    wall = time.perf_counter() - t1
+    ev_ms = runner.model.time_decode(last, pos0, 0, steps)
+    toks = steps / wall
+    ms_step = wall * 1e3 / steps
+    mean_bytes = sum(bytes_per_token(hw, pos0 + i, 0) for i in range(steps)) / steps
+    hbm_frac = mean_bytes * toks / HBM_PEAK
+    # dominant kernel: the LM head (HIP events on the model stream)
+    lm_ms = runner.model.time_kernel(0, args.kernel_iters)
+    lm_bytes = lm_head_bytes(hw)
+    lm_bw = lm_bytes / (lm_ms * 1e-3)
+    stage_ms = {name: runner.model.time_kernel(k, args.kernel_iters)
+                for name, k in (("qkv", 4), ("attention", 1), ("o", 5), ("gate_up", 2), ("down", 3))}
+    log(f"[bench] decode {toks:.1f} tok/s ({ms_step * 1e3:.1f} us/token wall, {ev_ms * 1e3 / steps:.1f} us/token "
+        f"events), {mean_bytes / 1e6:.2f} MB/token -> {hbm_frac * 100:.1f}% of HBM roofline")
+    log(f"[bench] LM head {lm_ms * 1e3:.1f} us/launch = {lm_bw / 1e9:.0f} GB/s; per-launch stage times (us): "
+        + ", ".join(f"{k} {v * 1e3:.1f}" for k, v in stage_ms.items()))
+    log(f"[bench] prefill {prefill_n} tokens in {prefill_s * 1e3:.1f} ms; first tokens {list(tokens[:8])}")
+    cpu = None
+    if args.cpu_budget > 0:
+        ncpu = os.cpu_count()
+        rate, n, dt = cpu_baseline(hw, prompt if len(prompt) > 1 else list(W.prompt_tokens(
+            W.Workload("s", wl.config, wl.storage, 64, 0, 64))), args.cpu_budget)
+        cpu = {"value": round(rate, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+               "sample": f"oracle forward of the first {n} prompt positions of the same workload "
+                         f"({dt:.1f} s, fp32 weights, double accumulation, 1 of {ncpu} host threads)"}
+        log(f"[bench] cpu baseline {rate:.3f} tok/s over {n} tokens")
+    result = {
+        "metric": "decode tok/s @bs=1 and % of HBM roofline; prefill tok/s (Qwen2.5-0.5B shape)",
+        "value": round(toks, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "hbm_roofline_frac": round(hbm_frac, 4),
+        "bytes_per_token": round(mean_bytes),
+        "prefill_tok_s": round(prefill_n / prefill_s, 1) if prefill_n > 0 and prefill_s > 0 else None,
+        "config": {"workload": wl.name, "prompt": wl.prompt_len, "decode": steps, "batch": 1,
+                   "linears": wl.storage.linear + (" g32 fp16 scales" if wl.storage.linear == "q4" else ""),
+                   "head": "fp16 tied" if hw.recipe.tied_embeddings else wl.storage.head, "kv": wl.storage.kv,
+                   "kv_prefill": wl.kv_prefill, "device": dev_name},
+        "roofline": {"bound": "hbm", "kernel": "lm_head_kernel", "achieved": round(lm_bw / 1e9, 1),
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(lm_bw / HBM_PEAK, 4),
+                     "traffic": read_traffic("lm_head"), "avg_launch_us": round(lm_ms * 1e3, 2)},
+        "cpu_baseline": cpu,
+    }
+    runner.close()
+    ctx.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

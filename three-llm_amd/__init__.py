@@ -2,9 +2,10 @@
 
 The compute lives in libtlm.so (hand-written HIP kernels for gfx950 behind the
 C ABI declared in include/tlm.h).  This package is the host side: the ctypes
-binding, the runner that mirrors the reference's DecoderTSLRunner controls, and
-the restated generate loop.
+binding (tlm), the runner that mirrors the reference's DecoderTSLRunner
+controls (runner), the restated generate loop and host sampling (generate),
+the recipe/RoPE tables (recipe) and canonical weights (weights).
 """
-from . import recipe  # noqa: F401
+from . import generate, recipe, runner, tlm, weights  # noqa: F401
 
-__all__ = ["recipe"]
+__all__ = ["generate", "recipe", "runner", "tlm", "weights"]

@@ -1,0 +1,1189 @@
+// C ABI (include/tlm.h) over the gfx950 kernels of tlm_kernels.hip.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "../../include/tlm.h"
+#include "tlm_kernels.h"
+
+using namespace tlm;
+
+// ----------------------------------------------------------------- errors --
+
+static thread_local std::string g_error;
+
+static int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                                   \
+  do {                                                                                                  \
+    hipError_t e_ = (expr);                                                                             \
+    if (e_ != hipSuccess)                                                                               \
+      return fail(e_ == hipErrorOutOfMemory ? TLM_ERR_OOM : TLM_ERR_HIP, "HIP: %s failed: %s", #expr,   \
+                  hipGetErrorString(e_));                                                               \
+  } while (0)
+
+#define CHECK_LAUNCH(component)                                                                         \
+  do {                                                                                                  \
+    hipError_t e_ = hipGetLastError();                                                                  \
+    if (e_ != hipSuccess) return fail(TLM_ERR_HIP, "%s: launch failed: %s", component, hipGetErrorString(e_)); \
+  } while (0)
+
+// ---------------------------------------------------------------- objects --
+
+struct tlm_ctx {
+  int device = 0;
+  int cus = 256;
+  char name[256] = {0};
+  hipStream_t stream = nullptr;
+  // scratch for op-level argmax
+  float* arg_val = nullptr;
+  int* arg_idx = nullptr;
+  int* ticket = nullptr;
+};
+
+struct GemvPlan {
+  int waves = 4, cps = 1, splits = 1, gx = 1;
+};
+
+struct tlm_linear {
+  tlm_ctx* ctx = nullptr;
+  int fmt = TLM_FMT_F16;
+  int N = 0, K = 0, T = 0, C = 0;
+  uint4* w = nullptr;
+  uint16_t* s = nullptr;
+  GemvPlan plan;
+  float* part = nullptr;  // op-level partials [splits][N]
+};
+
+struct tlm_attn {
+  tlm_ctx* ctx = nullptr;
+  tlm_attn_desc d{};
+  int G = 1, gmax = 1, nsplit = 1, chmin = 32;
+  float scale = 1.f;
+  void* kc = nullptr;
+  void* vc = nullptr;
+  float* rope_cos = nullptr;
+  float* rope_sin = nullptr;
+  float* pacc = nullptr;
+  float* pml = nullptr;
+  int* ticket = nullptr;
+  int* ctrl = nullptr;
+};
+
+struct Layer {
+  float* attn_norm = nullptr;
+  float* ffn_norm = nullptr;
+  float* bqkv = nullptr;
+  tlm_linear* qkv = nullptr;
+  tlm_linear* o = nullptr;
+  tlm_linear* gu = nullptr;
+  tlm_linear* down = nullptr;
+  void* kc = nullptr;
+  void* vc = nullptr;
+};
+
+struct tlm_model {
+  tlm_ctx* ctx = nullptr;
+  tlm_model_desc d{};
+  int Nqkv = 0, QS = 0;
+  std::vector<Layer> layers;
+  void* emb = nullptr;
+  tlm_linear* head = nullptr;
+  float* final_norm = nullptr;
+  // activations and partials
+  int* ctrl = nullptr;
+  int* tokens_out = nullptr;
+  int* prompt = nullptr;
+  float *xa = nullptr, *xb = nullptr, *xf = nullptr, *attn_out = nullptr;
+  float *pq = nullptr, *po = nullptr, *pgu = nullptr, *pd = nullptr;
+  float* logits = nullptr;
+  float* arg_val = nullptr;
+  int* arg_idx = nullptr;
+  int* ticket = nullptr;
+  // attention (shared by the layers; they run one after another)
+  tlm_attn attn;
+  GemvPlan lm_plan;
+  hipGraphExec_t g_logits = nullptr, g_prefill = nullptr;
+  hipGraph_t graph_logits = nullptr, graph_prefill = nullptr;
+  bool finalized = false;
+};
+
+// ------------------------------------------------------------ layout/plan --
+
+// Chunks per row: 16-byte units of 32 q4 weights or 8 fp16 weights.
+static int chunk_k(int fmt) { return fmt == TLM_FMT_Q4 ? 32 : 8; }
+
+// Split-K plan for one GEMV: enough waves to keep every CU busy on a latency-
+// bound batch-1 product, at least one 16-byte chunk per wave, and few partial
+// vectors for the consumer to fold in.
+static GemvPlan plan_gemv(int T, int C, int cus, int CK, bool single_split) {
+  GemvPlan p;
+  if (single_split) {
+    p.waves = C >= 64 ? 8 : 4;
+    p.cps = C;
+    p.splits = 1;
+    p.gx = T;
+    return p;
+  }
+  const long units = (long)T * C;
+  const long target = 8L * cus;
+  const int cpw = (int)std::max(1L, (units + target - 1) / target);
+  p.waves = C >= 64 ? 8 : 4;
+  int cps = std::max(1, std::min(C, p.waves * cpw));
+  int S = (C + cps - 1) / cps;
+  S = std::min(S, 32);
+  cps = (C + S - 1) / S;
+  const int max_cps = 8192 / CK;  // x slice <= 32 KB of LDS
+  if (cps > max_cps) {
+    cps = max_cps;
+    S = (C + cps - 1) / cps;
+  }
+  p.cps = cps;
+  p.splits = S;
+  p.gx = T;
+  if (p.waves > cps) p.waves = cps >= 8 ? 8 : cps >= 4 ? 4 : cps >= 2 ? 2 : 1;
+  return p;
+}
+
+// Host repack of canonical rows [r0, r0 + rows) into the device tile layout.
+// Tiles shared with rows outside the range are read back first.
+static int linear_write_rows(tlm_linear* L, int r0, int rows, const void* data, const uint16_t* scales) {
+  if (rows <= 0) return TLM_OK;
+  const int t0 = r0 / kTile, t1 = (r0 + rows - 1) / kTile + 1;
+  const size_t tiles = (size_t)(t1 - t0);
+  const size_t chunk_elems = (size_t)L->C * kTile;  // chunks per tile
+  const bool aligned = (r0 % kTile == 0) && ((r0 + rows) % kTile == 0 || r0 + rows == L->N);
+  hipStream_t st = L->ctx->stream;
+  HIP_TRY(hipStreamSynchronize(st));
+  if (data) {
+    std::vector<uint4> host(tiles * chunk_elems);
+    uint4* dst = L->w + (size_t)t0 * chunk_elems;
+    if (!aligned) HIP_TRY(hipMemcpy(host.data(), dst, host.size() * sizeof(uint4), hipMemcpyDeviceToHost));
+    const int CK = chunk_k(L->fmt);
+    const int Kc = L->fmt == TLM_FMT_Q4 ? L->K / 2 : L->K;  // canonical row length in units
+    for (int r = r0; r < r0 + rows; r++) {
+      const int t = r / kTile - t0, lane = r % kTile;
+      for (int c = 0; c < L->C; c++) {
+        uint4 v = {0, 0, 0, 0};
+        if (L->fmt == TLM_FMT_Q4) {
+          const uint8_t* src = (const uint8_t*)data + (size_t)(r - r0) * Kc + (size_t)c * 16;
+          memcpy(&v, src, 16);
+        } else {
+          uint16_t tmp[8] = {0};
+          const uint16_t* src = (const uint16_t*)data + (size_t)(r - r0) * Kc;
+          for (int j = 0; j < 8; j++) {
+            const int k = c * CK + j;
+            if (k < L->K) tmp[j] = src[k];
+          }
+          memcpy(&v, tmp, 16);
+        }
+        host[((size_t)t * L->C + c) * kTile + lane] = v;
+      }
+    }
+    HIP_TRY(hipMemcpy(dst, host.data(), host.size() * sizeof(uint4), hipMemcpyHostToDevice));
+  }
+  if (scales && L->fmt == TLM_FMT_Q4) {
+    std::vector<uint16_t> host(tiles * chunk_elems);
+    uint16_t* dst = L->s + (size_t)t0 * chunk_elems;
+    if (!aligned) HIP_TRY(hipMemcpy(host.data(), dst, host.size() * sizeof(uint16_t), hipMemcpyDeviceToHost));
+    const int G = L->K / 32;
+    for (int r = r0; r < r0 + rows; r++) {
+      const int t = r / kTile - t0, lane = r % kTile;
+      for (int c = 0; c < L->C; c++)
+        host[((size_t)t * L->C + c) * kTile + lane] = c < G ? scales[(size_t)(r - r0) * G + c] : 0;
+    }
+    HIP_TRY(hipMemcpy(dst, host.data(), host.size() * sizeof(uint16_t), hipMemcpyHostToDevice));
+  }
+  return TLM_OK;
+}
+
+static int linear_alloc(tlm_ctx* ctx, int fmt, int N, int K, bool single_split, tlm_linear** out) {
+  if (fmt != TLM_FMT_F16 && fmt != TLM_FMT_Q4) return fail(TLM_ERR_INVALID, "TLMLinear: unsupported format %d", fmt);
+  if (N <= 0 || K <= 0) return fail(TLM_ERR_INVALID, "TLMLinear: invalid shape %dx%d", N, K);
+  if (fmt == TLM_FMT_Q4 && K % 32 != 0) return fail(TLM_ERR_INVALID, "TLMLinear: q4 needs K %% 32 == 0 (K=%d)", K);
+  tlm_linear* L = new tlm_linear();
+  L->ctx = ctx;
+  L->fmt = fmt;
+  L->N = N;
+  L->K = K;
+  L->T = (N + kTile - 1) / kTile;
+  L->C = (K + chunk_k(fmt) - 1) / chunk_k(fmt);
+  L->plan = plan_gemv(L->T, L->C, ctx->cus, chunk_k(fmt), single_split);
+  const size_t chunks = (size_t)L->T * L->C * kTile;
+  hipError_t e = hipMalloc(&L->w, chunks * 16);
+  if (e == hipSuccess && fmt == TLM_FMT_Q4) e = hipMalloc(&L->s, chunks * 2);
+  if (e == hipSuccess) e = hipMemset(L->w, 0, chunks * 16);
+  if (e == hipSuccess && L->s) e = hipMemset(L->s, 0, chunks * 2);
+  if (e != hipSuccess) {
+    hipFree(L->w);
+    hipFree(L->s);
+    delete L;
+    return fail(TLM_ERR_OOM, "TLMLinear: device allocation of %zu bytes failed", chunks * 18);
+  }
+  *out = L;
+  return TLM_OK;
+}
+
+static void fill_gemv_args(GemvArgs& a, const tlm_linear* L, float* out) {
+  memset(&a, 0, sizeof a);
+  a.w = L->w;
+  a.s = L->s;
+  a.N = L->N;
+  a.T = L->T;
+  a.C = L->C;
+  a.K = L->K;
+  a.cps = L->plan.cps;
+  a.out = out;
+}
+
+static int wfmt(int fmt) { return fmt == TLM_FMT_Q4 ? WF_Q4 : WF_F16; }
+
+// ------------------------------------------------------------------ context --
+
+extern "C" {
+
+int tlm_abi_version(void) { return TLM_ABI_VERSION; }
+
+const char* tlm_last_error(void) { return g_error.c_str(); }
+
+int tlm_open(int device, tlm_ctx** out) {
+  if (!out) return fail(TLM_ERR_INVALID, "TLMContext: null output");
+  int count = 0;
+  HIP_TRY(hipGetDeviceCount(&count));
+  if (device < 0 || device >= count) return fail(TLM_ERR_INVALID, "TLMContext: no device %d (%d present)", device, count);
+  HIP_TRY(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, device));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(TLM_ERR_STATE, "TLMContext: device %d is %s; this library is built for gfx950", device,
+                prop.gcnArchName);
+  tlm_ctx* c = new tlm_ctx();
+  c->device = device;
+  c->cus = prop.multiProcessorCount;
+  snprintf(c->name, sizeof c->name, "%s (%s)", prop.name, prop.gcnArchName);
+  hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipMalloc(&c->arg_val, 4096 * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&c->arg_idx, 4096 * sizeof(int));
+  if (e == hipSuccess) e = hipMalloc(&c->ticket, 64 * sizeof(int));
+  if (e == hipSuccess) e = hipMemset(c->ticket, 0, 64 * sizeof(int));
+  if (e != hipSuccess) {
+    tlm_close(c);
+    return fail(TLM_ERR_HIP, "TLMContext: setup failed: %s", hipGetErrorString(e));
+  }
+  *out = c;
+  return TLM_OK;
+}
+
+void tlm_close(tlm_ctx* ctx) {
+  if (!ctx) return;
+  if (ctx->stream) hipStreamSynchronize(ctx->stream);
+  hipFree(ctx->arg_val);
+  hipFree(ctx->arg_idx);
+  hipFree(ctx->ticket);
+  if (ctx->stream) hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+int tlm_sync(tlm_ctx* ctx) {
+  if (!ctx) return fail(TLM_ERR_INVALID, "TLMContext: null context");
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return TLM_OK;
+}
+
+int tlm_device_info(tlm_ctx* ctx, char* name, size_t name_len, int* cu_count) {
+  if (!ctx) return fail(TLM_ERR_INVALID, "TLMContext: null context");
+  if (name && name_len) snprintf(name, name_len, "%s", ctx->name);
+  if (cu_count) *cu_count = ctx->cus;
+  return TLM_OK;
+}
+
+int tlm_alloc(tlm_ctx* ctx, size_t bytes, void** dptr) {
+  if (!ctx || !dptr) return fail(TLM_ERR_INVALID, "TLMBuffer: null argument");
+  HIP_TRY(hipMalloc(dptr, std::max<size_t>(bytes, 4)));
+  return TLM_OK;
+}
+
+int tlm_free(tlm_ctx* ctx, void* dptr) {
+  if (!ctx) return fail(TLM_ERR_INVALID, "TLMBuffer: null context");
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  HIP_TRY(hipFree(dptr));
+  return TLM_OK;
+}
+
+int tlm_upload(tlm_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(TLM_ERR_INVALID, "TLMBuffer: null argument");
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+  return TLM_OK;
+}
+
+int tlm_download(tlm_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(TLM_ERR_INVALID, "TLMBuffer: null argument");
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+  return TLM_OK;
+}
+
+// ------------------------------------------------------------------ linear --
+
+int tlm_linear_create(tlm_ctx* ctx, int fmt, int n_out, int k_in, const void* weights, const uint16_t* scales,
+                      tlm_linear** out) {
+  if (!ctx || !out || !weights || (fmt == TLM_FMT_Q4 && !scales))
+    return fail(TLM_ERR_INVALID, "TLMLinear: null argument");
+  tlm_linear* L = nullptr;
+  int rc = linear_alloc(ctx, fmt, n_out, k_in, false, &L);
+  if (rc) return rc;
+  rc = linear_write_rows(L, 0, n_out, weights, scales);
+  if (rc == TLM_OK && hipMalloc(&L->part, sizeof(float) * (size_t)L->plan.splits * L->N) != hipSuccess)
+    rc = fail(TLM_ERR_OOM, "TLMLinear: partials allocation failed");
+  if (rc) {
+    tlm_linear_destroy(L);
+    return rc;
+  }
+  *out = L;
+  return TLM_OK;
+}
+
+void tlm_linear_destroy(tlm_linear* L) {
+  if (!L) return;
+  hipStreamSynchronize(L->ctx->stream);
+  hipFree(L->w);
+  hipFree(L->s);
+  hipFree(L->part);
+  delete L;
+}
+
+int tlm_linear_dequant(tlm_linear* L, float* host_out) {
+  if (!L || !host_out) return fail(TLM_ERR_INVALID, "TLMLinear: null argument");
+  float* d = nullptr;
+  const size_t bytes = sizeof(float) * (size_t)L->N * L->K;
+  HIP_TRY(hipMalloc(&d, bytes));
+  launch_dequant(wfmt(L->fmt), L->w, L->s, L->N, L->T, L->C, L->K, d, L->ctx->stream);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) e = hipStreamSynchronize(L->ctx->stream);
+  if (e == hipSuccess) e = hipMemcpy(host_out, d, bytes, hipMemcpyDeviceToHost);
+  hipFree(d);
+  if (e != hipSuccess) return fail(TLM_ERR_HIP, "TLMLinear: dequant failed: %s", hipGetErrorString(e));
+  return TLM_OK;
+}
+
+int tlm_op_linear(tlm_linear* L, const float* x, const float* bias, float* y) {
+  if (!L || !x || !y) return fail(TLM_ERR_INVALID, "TLMLinear: null argument");
+  GemvArgs a;
+  const bool direct = L->plan.splits == 1;
+  fill_gemv_args(a, L, direct ? y : L->part);
+  a.in = x;
+  a.bias = direct ? bias : nullptr;
+  if (!launch_gemv(wfmt(L->fmt), PRO_COPY, L->plan.waves, dim3(L->plan.gx, L->plan.splits), a, L->ctx->stream))
+    return fail(TLM_ERR_STATE, "TLMLinear: no kernel variant for this shape");
+  CHECK_LAUNCH("TLMLinear");
+  if (!direct) {
+    launch_reduce(L->part, L->plan.splits, L->N, bias, L->N, y, L->ctx->stream);
+    CHECK_LAUNCH("TLMLinear");
+  }
+  return TLM_OK;
+}
+
+// -------------------------------------------------------------- element ops --
+
+int tlm_op_rmsnorm(tlm_ctx* ctx, const float* x, const float* w, int n, double eps, int offset, float* y) {
+  if (!ctx || !x || !y || n <= 0) return fail(TLM_ERR_INVALID, "TLMRMSNorm: invalid argument");
+  launch_rmsnorm(x, w, n, (float)eps, offset, y, ctx->stream);
+  CHECK_LAUNCH("TLMRMSNorm");
+  return TLM_OK;
+}
+
+int tlm_op_silu_mul(tlm_ctx* ctx, const float* gate, const float* up, int n, float* out) {
+  if (!ctx || !gate || !up || !out || n <= 0) return fail(TLM_ERR_INVALID, "TLMSiLUMul: invalid argument");
+  launch_silu_mul(gate, up, n, out, ctx->stream);
+  CHECK_LAUNCH("TLMSiLUMul");
+  return TLM_OK;
+}
+
+int tlm_op_gated_mlp(tlm_linear* gu, tlm_linear* down, const float* x, float* y) {
+  if (!gu || !down || !x || !y) return fail(TLM_ERR_INVALID, "TLMGatedMLP: null argument");
+  if (gu->N != 2 * down->K || gu->K != down->N)
+    return fail(TLM_ERR_INVALID, "TLMGatedMLP: gate/up %dx%d does not match down %dx%d", gu->N, gu->K, down->N,
+                down->K);
+  hipStream_t st = gu->ctx->stream;
+  GemvArgs a;
+  fill_gemv_args(a, gu, gu->part);
+  a.in = x;
+  if (!launch_gemv(wfmt(gu->fmt), PRO_COPY, gu->plan.waves, dim3(gu->plan.gx, gu->plan.splits), a, st))
+    return fail(TLM_ERR_STATE, "TLMGatedMLP: no kernel variant for this shape");
+  CHECK_LAUNCH("TLMGatedMLP");
+  GemvArgs b;
+  const bool direct = down->plan.splits == 1;
+  fill_gemv_args(b, down, direct ? y : down->part);
+  b.pin = gu->part;
+  b.n_pin = gu->plan.splits;
+  b.pin_stride = gu->N;
+  b.up_off = down->K;
+  if (!launch_gemv(wfmt(down->fmt), PRO_SWIGLU, down->plan.waves, dim3(down->plan.gx, down->plan.splits), b, st))
+    return fail(TLM_ERR_STATE, "TLMGatedMLP: no kernel variant for this shape");
+  CHECK_LAUNCH("TLMGatedMLP");
+  if (!direct) {
+    launch_reduce(down->part, down->plan.splits, down->N, nullptr, down->N, y, st);
+    CHECK_LAUNCH("TLMGatedMLP");
+  }
+  return TLM_OK;
+}
+
+// ---------------------------------------------------------------- attention --
+
+// cos/sin of pos * inv_freq[j] in double, times the attention factor, rounded
+// to fp32 (the CPU reference evaluates the angle in double, math.ts:144-146).
+static void rope_tables(int max_tokens, int rd, const float* inv_freq, double af, std::vector<float>& cs,
+                        std::vector<float>& sn) {
+  const int half = rd / 2;
+  cs.assign((size_t)max_tokens * half, 0.f);
+  sn.assign((size_t)max_tokens * half, 0.f);
+  for (int p = 0; p < max_tokens; p++)
+    for (int j = 0; j < half; j++) {
+      const double angle = (double)p * (double)inv_freq[j];
+      cs[(size_t)p * half + j] = (float)(cos(angle) * af);
+      sn[(size_t)p * half + j] = (float)(sin(angle) * af);
+    }
+}
+
+static int attn_init(tlm_ctx* ctx, const tlm_attn_desc* d, tlm_attn* A, bool own_cache) {
+  if (d->heads <= 0 || d->kv_heads <= 0 || d->heads % d->kv_heads != 0)
+    return fail(TLM_ERR_INVALID, "TLMAttention: heads %d must be a multiple of kv heads %d", d->heads, d->kv_heads);
+  if (d->head_dim <= 0 || d->head_dim % 2 != 0 || d->head_dim > 256)
+    return fail(TLM_ERR_INVALID, "TLMAttention: head_dim %d must be even and <= 256", d->head_dim);
+  if (d->rotary_dim < 0 || d->rotary_dim > d->head_dim || d->rotary_dim % 2 != 0)
+    return fail(TLM_ERR_INVALID, "TLMAttention: invalid rotary dimension %d", d->rotary_dim);
+  if (d->rotary_dim > 0 && !d->inv_freq) return fail(TLM_ERR_INVALID, "TLMAttention: missing inv_freq");
+  if (d->max_tokens <= 0) return fail(TLM_ERR_INVALID, "TLMAttention: max_tokens must be positive");
+  A->ctx = ctx;
+  A->d = *d;
+  A->G = d->heads / d->kv_heads;
+  if (A->G > 16) return fail(TLM_ERR_INVALID, "TLMAttention: more than 16 query heads per kv head");
+  A->gmax = A->G <= 1 ? 1 : A->G <= 2 ? 2 : A->G <= 4 ? 4 : A->G <= 8 ? 8 : 16;
+  A->scale = (float)(d->attn_scale > 0 ? d->attn_scale : 1.0 / sqrt((double)d->head_dim));
+  if (attn_smem_bytes(A->G, d->head_dim) > 65536)
+    return fail(TLM_ERR_INVALID, "TLMAttention: %d heads per kv head x head_dim %d exceed the LDS budget", A->G,
+                d->head_dim);
+  A->chmin = 32;
+  const int by_tile = (d->max_tokens + 255) / 256;
+  const int by_cus = std::max(1, 2 * ctx->cus / d->kv_heads);
+  const int by_min = (d->max_tokens + A->chmin - 1) / A->chmin;
+  A->nsplit = std::max(by_tile, std::min(by_min, by_cus));
+  const int D = d->head_dim;
+  const size_t esz = d->kv_fmt == TLM_FMT_F32 ? 4 : 2;
+  std::vector<float> cs, sn;
+  const int half = std::max(1, d->rotary_dim / 2);
+  if (d->rotary_dim > 0) rope_tables(d->max_tokens, d->rotary_dim, d->inv_freq, d->attention_factor, cs, sn);
+  else cs.assign(half, 0.f), sn.assign(half, 0.f);
+  HIP_TRY(hipMalloc(&A->rope_cos, cs.size() * sizeof(float)));
+  HIP_TRY(hipMalloc(&A->rope_sin, sn.size() * sizeof(float)));
+  HIP_TRY(hipMemcpy(A->rope_cos, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy(A->rope_sin, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice));
+  HIP_TRY(hipMalloc(&A->pacc, sizeof(float) * (size_t)d->heads * A->nsplit * D));
+  HIP_TRY(hipMalloc(&A->pml, sizeof(float) * (size_t)d->heads * A->nsplit * 2));
+  HIP_TRY(hipMalloc(&A->ticket, sizeof(int) * d->kv_heads));
+  HIP_TRY(hipMemset(A->ticket, 0, sizeof(int) * d->kv_heads));
+  if (own_cache) {
+    const size_t cache = (size_t)d->kv_heads * d->max_tokens * D * esz;
+    HIP_TRY(hipMalloc(&A->kc, cache));
+    HIP_TRY(hipMalloc(&A->vc, cache));
+    HIP_TRY(hipMemset(A->kc, 0, cache));
+    HIP_TRY(hipMemset(A->vc, 0, cache));
+    HIP_TRY(hipMalloc(&A->ctrl, sizeof(int) * 8));
+    HIP_TRY(hipMemset(A->ctrl, 0, sizeof(int) * 8));
+  }
+  return TLM_OK;
+}
+
+static void attn_free(tlm_attn* A, bool own_cache) {
+  hipFree(A->rope_cos);
+  hipFree(A->rope_sin);
+  hipFree(A->pacc);
+  hipFree(A->pml);
+  hipFree(A->ticket);
+  if (own_cache) {
+    hipFree(A->kc);
+    hipFree(A->vc);
+    hipFree(A->ctrl);
+  }
+}
+
+static AttnArgs attn_args(const tlm_attn* A, const float* src, int n_src, int stride, const float* bias,
+                          const int* ctrl, void* kc, void* vc, float* out) {
+  AttnArgs a;
+  memset(&a, 0, sizeof a);
+  a.src = src;
+  a.n_src = n_src;
+  a.src_stride = stride;
+  a.bias = bias;
+  a.ctrl = ctrl;
+  a.kc = kc;
+  a.vc = vc;
+  a.rope_cos = A->rope_cos;
+  a.rope_sin = A->rope_sin;
+  a.out = out;
+  a.pacc = A->pacc;
+  a.pml = A->pml;
+  a.ticket = A->ticket;
+  a.Hq = A->d.heads;
+  a.Hkv = A->d.kv_heads;
+  a.D = A->d.head_dim;
+  a.G = A->G;
+  a.rd = A->d.rotary_dim;
+  a.max_tokens = A->d.max_tokens;
+  a.window = A->d.sliding_window;
+  a.nsplit = A->nsplit;
+  a.chmin = A->chmin;
+  a.scale = A->scale;
+  return a;
+}
+
+int tlm_attn_create(tlm_ctx* ctx, const tlm_attn_desc* desc, tlm_attn** out) {
+  if (!ctx || !desc || !out) return fail(TLM_ERR_INVALID, "TLMAttention: null argument");
+  tlm_attn* A = new tlm_attn();
+  int rc = attn_init(ctx, desc, A, true);
+  if (rc) {
+    attn_free(A, true);
+    delete A;
+    return rc;
+  }
+  *out = A;
+  return TLM_OK;
+}
+
+void tlm_attn_destroy(tlm_attn* A) {
+  if (!A) return;
+  hipStreamSynchronize(A->ctx->stream);
+  attn_free(A, true);
+  delete A;
+}
+
+int tlm_op_attention(tlm_attn* A, const float* qkv, int position, float* out) {
+  if (!A || !qkv || !out) return fail(TLM_ERR_INVALID, "TLMAttention: null argument");
+  if (position < 0 || position >= A->d.max_tokens)
+    return fail(TLM_ERR_RANGE, "TLMAttention: position %d outside [0, %d)", position, A->d.max_tokens);
+  hipStream_t st = A->ctx->stream;
+  launch_set_ctrl(A->ctrl, 0, position, 0, 0, 0, st);
+  const int total = (A->d.heads + 2 * A->d.kv_heads) * A->d.head_dim;
+  AttnArgs a = attn_args(A, qkv, 1, total, nullptr, A->ctrl, A->kc, A->vc, out);
+  if (!launch_attention(A->d.kv_fmt == TLM_FMT_F32, A->gmax, a, st))
+    return fail(TLM_ERR_STATE, "TLMAttention: no kernel variant for this shape");
+  CHECK_LAUNCH("TLMAttention");
+  return TLM_OK;
+}
+
+int tlm_attn_reset(tlm_attn* A) {
+  if (!A) return fail(TLM_ERR_INVALID, "TLMAttention: null argument");
+  const size_t esz = A->d.kv_fmt == TLM_FMT_F32 ? 4 : 2;
+  const size_t cache = (size_t)A->d.kv_heads * A->d.max_tokens * A->d.head_dim * esz;
+  HIP_TRY(hipMemsetAsync(A->kc, 0, cache, A->ctx->stream));
+  HIP_TRY(hipMemsetAsync(A->vc, 0, cache, A->ctx->stream));
+  return TLM_OK;
+}
+
+static float elem_to_f32(const void* p, size_t i, bool f32) {
+  if (f32) return ((const float*)p)[i];
+  const uint16_t h = ((const uint16_t*)p)[i];
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t e = (h >> 10) & 0x1f, m = h & 0x3ffu, bits;
+  if (e == 0) {
+    if (m == 0)
+      bits = sign;
+    else {
+      int sh = 0;
+      while (!(m & 0x400u)) {
+        m <<= 1;
+        sh++;
+      }
+      bits = sign | ((uint32_t)(113 - sh) << 23) | ((m & 0x3ffu) << 13);
+    }
+  } else if (e == 31)
+    bits = sign | 0x7f800000u | (m << 13);
+  else
+    bits = sign | ((e + 112u) << 23) | (m << 13);
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+int tlm_attn_read_cache(tlm_attn* A, int count, float* k_out, float* v_out) {
+  if (!A || !k_out || !v_out || count < 0 || count > A->d.max_tokens)
+    return fail(TLM_ERR_INVALID, "TLMAttention: invalid read");
+  const bool f32 = A->d.kv_fmt == TLM_FMT_F32;
+  const size_t esz = f32 ? 4 : 2;
+  const int Hkv = A->d.kv_heads, D = A->d.head_dim, M = A->d.max_tokens;
+  std::vector<uint8_t> kbuf((size_t)Hkv * M * D * esz), vbuf(kbuf.size());
+  HIP_TRY(hipStreamSynchronize(A->ctx->stream));
+  HIP_TRY(hipMemcpy(kbuf.data(), A->kc, kbuf.size(), hipMemcpyDeviceToHost));
+  HIP_TRY(hipMemcpy(vbuf.data(), A->vc, vbuf.size(), hipMemcpyDeviceToHost));
+  for (int t = 0; t < count; t++)
+    for (int h = 0; h < Hkv; h++)
+      for (int d = 0; d < D; d++) {
+        const size_t src = ((size_t)h * M + t) * D + d, dst = ((size_t)t * Hkv + h) * D + d;
+        k_out[dst] = elem_to_f32(kbuf.data(), src, f32);
+        v_out[dst] = elem_to_f32(vbuf.data(), src, f32);
+      }
+  return TLM_OK;
+}
+
+// ------------------------------------------------------------------- logits --
+
+int tlm_op_logits(tlm_linear* head, const float* x, float* logits, int32_t* token) {
+  if (!head || !x || !token) return fail(TLM_ERR_INVALID, "TLMLogits: null argument");
+  tlm_ctx* ctx = head->ctx;
+  GemvPlan p = plan_gemv(head->T, head->C, ctx->cus, chunk_k(head->fmt), true);
+  p.gx = std::min(head->T, 4096);
+  GemvArgs a;
+  fill_gemv_args(a, head, nullptr);
+  a.cps = p.cps;
+  a.in = x;
+  a.logits = logits;
+  a.arg_val = ctx->arg_val;
+  a.arg_idx = ctx->arg_idx;
+  a.ticket = ctx->ticket;
+  // a scratch ctrl block: the sampled token lands in ctrl[C_TOKEN]
+  a.ctrl = token;
+  a.advance = 0;
+  a.tokens_out = nullptr;
+  if (gemv_smem_bytes(wfmt(head->fmt), p.cps, p.waves) > 65536)
+    return fail(TLM_ERR_INVALID, "TLMLogits: hidden size %d too large for one block", head->K);
+  if (!launch_lm_head(wfmt(head->fmt), p.waves, dim3(p.gx), a, ctx->stream))
+    return fail(TLM_ERR_STATE, "TLMLogits: no kernel variant for this shape");
+  CHECK_LAUNCH("TLMLogits");
+  return TLM_OK;
+}
+
+int tlm_op_argmax(tlm_ctx* ctx, const float* logits, int n, int32_t* token) {
+  if (!ctx || !logits || !token || n <= 0) return fail(TLM_ERR_INVALID, "TLMLogits: invalid argmax argument");
+  const int blocks = std::max(1, std::min(1024, (n + 1023) / 1024));
+  launch_argmax(logits, n, ctx->arg_val, ctx->arg_idx, ctx->ticket + 1, token, blocks, ctx->stream);
+  CHECK_LAUNCH("TLMLogits");
+  return TLM_OK;
+}
+
+// -------------------------------------------------------------------- model --
+
+static int model_alloc(void** p, size_t bytes) {
+  if (hipMalloc(p, std::max<size_t>(bytes, 4)) != hipSuccess)
+    return fail(TLM_ERR_OOM, "TLMModel: device allocation of %zu bytes failed", bytes);
+  if (hipMemset(*p, 0, std::max<size_t>(bytes, 4)) != hipSuccess)
+    return fail(TLM_ERR_HIP, "TLMModel: memset failed");
+  return TLM_OK;
+}
+
+void tlm_model_destroy(tlm_model* m);
+
+int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
+  if (!ctx || !d || !out) return fail(TLM_ERR_INVALID, "TLMModel: null argument");
+  if (d->hidden_size <= 0 || d->intermediate_size <= 0 || d->num_layers <= 0 || d->vocab_size <= 0 ||
+      d->max_tokens <= 0)
+    return fail(TLM_ERR_INVALID, "TLMModel: invalid dimensions");
+  if (d->linear_fmt != TLM_FMT_Q4 && d->linear_fmt != TLM_FMT_F16)
+    return fail(TLM_ERR_INVALID, "TLMModel: linear_fmt must be q4 or fp16");
+  if (d->embed_fmt != TLM_FMT_F16 && d->embed_fmt != TLM_FMT_F32)
+    return fail(TLM_ERR_INVALID, "TLMModel: embed_fmt must be fp16 or fp32");
+  if (d->tied && d->embed_fmt != TLM_FMT_F16)
+    return fail(TLM_ERR_INVALID, "TLMModel: a tied head needs an fp16 embedding table");
+  if (!d->tied && d->head_fmt != TLM_FMT_F16 && d->head_fmt != TLM_FMT_Q4)
+    return fail(TLM_ERR_INVALID, "TLMModel: head_fmt must be fp16 or q4");
+  tlm_model* m = new tlm_model();
+  m->ctx = ctx;
+  m->d = *d;
+  const int H = d->hidden_size, I = d->intermediate_size, D = d->head_dim;
+  m->QS = d->num_heads * D;
+  m->Nqkv = m->QS + 2 * d->num_kv_heads * D;
+  tlm_attn_desc ad{};
+  ad.heads = d->num_heads;
+  ad.kv_heads = d->num_kv_heads;
+  ad.head_dim = D;
+  ad.max_tokens = d->max_tokens;
+  ad.rotary_dim = d->rotary_dim;
+  ad.sliding_window = d->sliding_window;
+  ad.kv_fmt = d->kv_fmt == TLM_FMT_F32 ? TLM_FMT_F32 : TLM_FMT_F16;
+  ad.inv_freq = d->inv_freq;
+  ad.attention_factor = d->attention_factor;
+  ad.attn_scale = 0;
+  int rc = attn_init(ctx, &ad, &m->attn, false);
+#define M_TRY(x)               \
+  do {                         \
+    if (rc == TLM_OK) rc = (x); \
+  } while (0)
+  const int lf = d->linear_fmt;
+  m->layers.resize(d->num_layers);
+  const size_t esz = ad.kv_fmt == TLM_FMT_F32 ? 4 : 2;
+  const size_t cache = (size_t)d->num_kv_heads * d->max_tokens * D * esz;
+  for (auto& L : m->layers) {
+    M_TRY(linear_alloc(ctx, lf, m->Nqkv, H, false, &L.qkv));
+    M_TRY(linear_alloc(ctx, lf, H, m->QS, false, &L.o));
+    M_TRY(linear_alloc(ctx, lf, 2 * I, H, false, &L.gu));
+    M_TRY(linear_alloc(ctx, lf, H, I, false, &L.down));
+    M_TRY(model_alloc((void**)&L.attn_norm, sizeof(float) * H));
+    M_TRY(model_alloc((void**)&L.ffn_norm, sizeof(float) * H));
+    if (d->qkv_bias) M_TRY(model_alloc((void**)&L.bqkv, sizeof(float) * m->Nqkv));
+    M_TRY(model_alloc(&L.kc, cache));
+    M_TRY(model_alloc(&L.vc, cache));
+  }
+  M_TRY(model_alloc(&m->emb, (size_t)d->vocab_size * H * (d->embed_fmt == TLM_FMT_F32 ? 4 : 2)));
+  M_TRY(linear_alloc(ctx, d->tied ? TLM_FMT_F16 : d->head_fmt, d->vocab_size, H, true, &m->head));
+  M_TRY(model_alloc((void**)&m->final_norm, sizeof(float) * H));
+  M_TRY(model_alloc((void**)&m->ctrl, sizeof(int) * 8));
+  M_TRY(model_alloc((void**)&m->tokens_out, sizeof(int) * d->max_tokens));
+  M_TRY(model_alloc((void**)&m->prompt, sizeof(int) * d->max_tokens));
+  M_TRY(model_alloc((void**)&m->xa, sizeof(float) * H));
+  M_TRY(model_alloc((void**)&m->xb, sizeof(float) * H));
+  M_TRY(model_alloc((void**)&m->xf, sizeof(float) * H));
+  M_TRY(model_alloc((void**)&m->attn_out, sizeof(float) * m->QS));
+  if (rc == TLM_OK) {
+    const Layer& L0 = m->layers[0];
+    M_TRY(model_alloc((void**)&m->pq, sizeof(float) * L0.qkv->plan.splits * m->Nqkv));
+    M_TRY(model_alloc((void**)&m->po, sizeof(float) * L0.o->plan.splits * H));
+    M_TRY(model_alloc((void**)&m->pgu, sizeof(float) * L0.gu->plan.splits * 2 * I));
+    M_TRY(model_alloc((void**)&m->pd, sizeof(float) * L0.down->plan.splits * H));
+    m->lm_plan = plan_gemv(m->head->T, m->head->C, ctx->cus, chunk_k(m->head->fmt), true);
+    m->lm_plan.gx = std::min(m->head->T, 4096);
+    if (gemv_smem_bytes(wfmt(m->head->fmt), m->lm_plan.cps, m->lm_plan.waves) > 65536)
+      rc = fail(TLM_ERR_INVALID, "TLMModel: hidden size %d too large for one LM head block", H);
+  }
+  M_TRY(model_alloc((void**)&m->logits, sizeof(float) * d->vocab_size));
+  M_TRY(model_alloc((void**)&m->arg_val, sizeof(float) * 4096));
+  M_TRY(model_alloc((void**)&m->arg_idx, sizeof(int) * 4096));
+  M_TRY(model_alloc((void**)&m->ticket, sizeof(int) * 4));
+#undef M_TRY
+  if (rc) {
+    std::string msg = g_error;
+    tlm_model_destroy(m);
+    g_error = msg;
+    return rc;
+  }
+  *out = m;
+  return TLM_OK;
+}
+
+void tlm_model_destroy(tlm_model* m) {
+  if (!m) return;
+  hipStreamSynchronize(m->ctx->stream);
+  if (m->g_logits) hipGraphExecDestroy(m->g_logits);
+  if (m->g_prefill) hipGraphExecDestroy(m->g_prefill);
+  if (m->graph_logits) hipGraphDestroy(m->graph_logits);
+  if (m->graph_prefill) hipGraphDestroy(m->graph_prefill);
+  for (auto& L : m->layers) {
+    tlm_linear_destroy(L.qkv);
+    tlm_linear_destroy(L.o);
+    tlm_linear_destroy(L.gu);
+    tlm_linear_destroy(L.down);
+    hipFree(L.attn_norm);
+    hipFree(L.ffn_norm);
+    hipFree(L.bqkv);
+    hipFree(L.kc);
+    hipFree(L.vc);
+  }
+  tlm_linear_destroy(m->head);
+  attn_free(&m->attn, false);
+  void* bufs[] = {m->emb, m->final_norm, m->ctrl, m->tokens_out, m->prompt, m->xa, m->xb, m->xf, m->attn_out,
+                  m->pq, m->po, m->pgu, m->pd, m->logits, m->arg_val, m->arg_idx, m->ticket};
+  for (void* p : bufs) hipFree(p);
+  delete m;
+}
+
+static int upload_f32(float* dst, const void* host, size_t bytes, size_t expect, const char* what) {
+  if (bytes != expect) return fail(TLM_ERR_INVALID, "TLMModel: %s expects %zu bytes, got %zu", what, expect, bytes);
+  HIP_TRY(hipMemcpy(dst, host, bytes, hipMemcpyHostToDevice));
+  return TLM_OK;
+}
+
+static int upload_linear(tlm_linear* L, int r0, int rows, int cols, bool scales, const void* host, size_t bytes,
+                         const char* what) {
+  if (L->fmt == TLM_FMT_Q4) {
+    const size_t expect = scales ? (size_t)rows * (cols / 32) * 2 : (size_t)rows * cols / 2;
+    if (bytes != expect) return fail(TLM_ERR_INVALID, "TLMModel: %s expects %zu bytes, got %zu", what, expect, bytes);
+    return scales ? linear_write_rows(L, r0, rows, nullptr, (const uint16_t*)host)
+                  : linear_write_rows(L, r0, rows, host, nullptr);
+  }
+  if (scales) return fail(TLM_ERR_INVALID, "TLMModel: %s: fp16 linears have no scales", what);
+  const size_t expect = (size_t)rows * cols * 2;
+  if (bytes != expect) return fail(TLM_ERR_INVALID, "TLMModel: %s expects %zu bytes, got %zu", what, expect, bytes);
+  return linear_write_rows(L, r0, rows, host, nullptr);
+}
+
+int tlm_model_upload(tlm_model* m, int tensor, int layer, const void* host, size_t bytes) {
+  if (!m || !host) return fail(TLM_ERR_INVALID, "TLMModel: null argument");
+  const tlm_model_desc& d = m->d;
+  const int H = d.hidden_size, I = d.intermediate_size, V = d.vocab_size;
+  const bool per_layer = tensor >= TLM_T_ATTN_NORM;
+  if (per_layer && (layer < 0 || layer >= d.num_layers))
+    return fail(TLM_ERR_INVALID, "TLMModel: layer %d outside [0, %d)", layer, d.num_layers);
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  Layer* L = per_layer ? &m->layers[layer] : nullptr;
+  switch (tensor) {
+    case TLM_T_EMBED: {
+      const size_t esz = d.embed_fmt == TLM_FMT_F32 ? 4 : 2;
+      if (bytes != (size_t)V * H * esz)
+        return fail(TLM_ERR_INVALID, "TLMModel: embedding expects %zu bytes, got %zu", (size_t)V * H * esz, bytes);
+      HIP_TRY(hipMemcpy(m->emb, host, bytes, hipMemcpyHostToDevice));
+      if (d.tied) return linear_write_rows(m->head, 0, V, host, nullptr);
+      return TLM_OK;
+    }
+    case TLM_T_LM_HEAD:
+    case TLM_T_LM_HEAD_SCALES:
+      if (d.tied) return fail(TLM_ERR_STATE, "TLMModel: the LM head is tied to the embedding");
+      return upload_linear(m->head, 0, V, H, tensor == TLM_T_LM_HEAD_SCALES, host, bytes, "lm_head");
+    case TLM_T_FINAL_NORM: return upload_f32(m->final_norm, host, bytes, sizeof(float) * H, "final norm");
+    case TLM_T_ATTN_NORM: return upload_f32(L->attn_norm, host, bytes, sizeof(float) * H, "attn norm");
+    case TLM_T_FFN_NORM: return upload_f32(L->ffn_norm, host, bytes, sizeof(float) * H, "ffn norm");
+    case TLM_T_WQKV:
+    case TLM_T_WQKV_SCALES:
+      return upload_linear(L->qkv, 0, m->Nqkv, H, tensor == TLM_T_WQKV_SCALES, host, bytes, "wqkv");
+    case TLM_T_BQKV:
+      if (!d.qkv_bias) return fail(TLM_ERR_STATE, "TLMModel: model was created without a QKV bias");
+      return upload_f32(L->bqkv, host, bytes, sizeof(float) * m->Nqkv, "bqkv");
+    case TLM_T_WO:
+    case TLM_T_WO_SCALES: return upload_linear(L->o, 0, H, m->QS, tensor == TLM_T_WO_SCALES, host, bytes, "wo");
+    case TLM_T_WGATE:
+    case TLM_T_WGATE_SCALES:
+      return upload_linear(L->gu, 0, I, H, tensor == TLM_T_WGATE_SCALES, host, bytes, "wgate");
+    case TLM_T_WUP:
+    case TLM_T_WUP_SCALES: return upload_linear(L->gu, I, I, H, tensor == TLM_T_WUP_SCALES, host, bytes, "wup");
+    case TLM_T_WDOWN:
+    case TLM_T_WDOWN_SCALES:
+      return upload_linear(L->down, 0, H, I, tensor == TLM_T_WDOWN_SCALES, host, bytes, "wdown");
+  }
+  return fail(TLM_ERR_INVALID, "TLMModel: unknown tensor id %d", tensor);
+}
+
+// ----------------------------------------------------- the per-token schedule
+
+// Kernels of one layer.  which: -1 all; otherwise a single stage (timing).
+static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which) {
+  bool ok = true;
+  const tlm_model_desc& d = m->d;
+  const int H = d.hidden_size, I = d.intermediate_size;
+  Layer& L = m->layers[l];
+  const Layer& P = m->layers[l > 0 ? l - 1 : 0];
+  // 1. x = (layer 0: embedding row; else x_mid + down partials); RMSNorm; QKV GEMV
+  if (which < 0 || which == 4) {
+    GemvArgs a;
+    fill_gemv_args(a, L.qkv, m->pq);
+    if (l == 0) {
+      a.base = nullptr;
+      a.emb = m->emb;
+      a.emb_f32 = d.embed_fmt == TLM_FMT_F32;
+      a.n_pin = 0;
+    } else {
+      a.base = m->xb;
+      a.pin = m->pd;
+      a.n_pin = P.down->plan.splits;
+      a.pin_stride = H;
+    }
+    a.ctrl = m->ctrl;
+    a.norm_w = L.attn_norm;
+    a.eps = (float)d.rms_eps;
+    a.xout = m->xa;
+    ok &= launch_gemv(wfmt(L.qkv->fmt), PRO_RMS, L.qkv->plan.waves, dim3(L.qkv->plan.gx, L.qkv->plan.splits), a, st);
+  }
+  // 2. RoPE + KV append + split-K attention
+  if (which < 0 || which == 1) {
+    AttnArgs a = attn_args(&m->attn, m->pq, L.qkv->plan.splits, m->Nqkv, L.bqkv, m->ctrl, L.kc, L.vc, m->attn_out);
+    ok &= launch_attention(d.kv_fmt == TLM_FMT_F32, m->attn.gmax, a, st);
+  }
+  // 3. O projection
+  if (which < 0 || which == 5) {
+    GemvArgs a;
+    fill_gemv_args(a, L.o, m->po);
+    a.in = m->attn_out;
+    ok &= launch_gemv(wfmt(L.o->fmt), PRO_COPY, L.o->plan.waves, dim3(L.o->plan.gx, L.o->plan.splits), a, st);
+  }
+  // 4. x_mid = x + O partials; RMSNorm; gate|up GEMV
+  if (which < 0 || which == 2) {
+    GemvArgs a;
+    fill_gemv_args(a, L.gu, m->pgu);
+    a.base = m->xa;
+    a.pin = m->po;
+    a.n_pin = L.o->plan.splits;
+    a.pin_stride = H;
+    a.norm_w = L.ffn_norm;
+    a.eps = (float)d.rms_eps;
+    a.xout = m->xb;
+    a.ctrl = m->ctrl;
+    ok &= launch_gemv(wfmt(L.gu->fmt), PRO_RMS, L.gu->plan.waves, dim3(L.gu->plan.gx, L.gu->plan.splits), a, st);
+  }
+  // 5. silu(gate) * up folded into the down GEMV
+  if (which < 0 || which == 3) {
+    GemvArgs a;
+    fill_gemv_args(a, L.down, m->pd);
+    a.pin = m->pgu;
+    a.n_pin = L.gu->plan.splits;
+    a.pin_stride = 2 * I;
+    a.up_off = I;
+    ok &= launch_gemv(wfmt(L.down->fmt), PRO_SWIGLU, L.down->plan.waves,
+                      dim3(L.down->plan.gx, L.down->plan.splits), a, st);
+  }
+  return ok;
+}
+
+static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, bool final_norm) {
+  const tlm_model_desc& d = m->d;
+  const Layer& last = m->layers.back();
+  if (final_norm)
+    launch_final_norm(m->xb, m->pd, last.down->plan.splits, d.hidden_size, m->final_norm, d.hidden_size,
+                      (float)d.rms_eps, m->xf, st);
+  GemvArgs a;
+  fill_gemv_args(a, m->head, nullptr);
+  a.cps = m->lm_plan.cps;
+  a.in = m->xf;
+  a.logits = m->logits;
+  a.arg_val = m->arg_val;
+  a.arg_idx = m->arg_idx;
+  a.ticket = m->ticket;
+  a.ctrl = m->ctrl;
+  a.tokens_out = advance ? m->tokens_out : nullptr;
+  a.advance = advance ? 1 : 0;
+  a.max_steps = d.max_tokens;
+  return launch_lm_head(wfmt(m->head->fmt), m->lm_plan.waves, dim3(m->lm_plan.gx), a, st);
+}
+
+static int capture(tlm_model* m, bool logits, hipGraph_t* g, hipGraphExec_t* ge) {
+  hipStream_t st = m->ctx->stream;
+  HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  bool ok = true;
+  for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1);
+  if (logits)
+    ok &= enqueue_head(m, st, true, true);
+  else
+    launch_prefill_advance(m->ctrl, m->prompt, st);
+  hipError_t le = hipGetLastError();
+  HIP_TRY(hipStreamEndCapture(st, g));
+  if (le != hipSuccess) return fail(TLM_ERR_HIP, "TLMModel: launch during capture failed: %s", hipGetErrorString(le));
+  if (!ok) return fail(TLM_ERR_STATE, "TLMModel: no kernel variant for a stage of this model");
+  HIP_TRY(hipGraphInstantiate(ge, *g, nullptr, nullptr, 0));
+  return TLM_OK;
+}
+
+int tlm_model_finalize(tlm_model* m) {
+  if (!m) return fail(TLM_ERR_INVALID, "TLMModel: null model");
+  if (m->finalized) return TLM_OK;
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  int rc = capture(m, true, &m->graph_logits, &m->g_logits);
+  if (rc == TLM_OK) rc = capture(m, false, &m->graph_prefill, &m->g_prefill);
+  if (rc) return rc;
+  m->finalized = true;
+  return TLM_OK;
+}
+
+static int check_token(tlm_model* m, int32_t token, int32_t position) {
+  if (token < 0 || token >= m->d.vocab_size)
+    return fail(TLM_ERR_RANGE, "TLMModel: token %d outside [0, %d)", token, m->d.vocab_size);
+  if (position < 0 || position >= m->d.max_tokens)
+    return fail(TLM_ERR_RANGE, "TLMModel: position %d outside [0, %d)", position, m->d.max_tokens);
+  return TLM_OK;
+}
+
+int tlm_compute_token(tlm_model* m, int32_t token, int32_t position, int flags) {
+  if (!m) return fail(TLM_ERR_INVALID, "TLMModel: null model");
+  int rc = check_token(m, token, position);
+  if (rc) return rc;
+  rc = tlm_model_finalize(m);
+  if (rc) return rc;
+  hipStream_t st = m->ctx->stream;
+  launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, st);
+  CHECK_LAUNCH("TLMModel");
+  HIP_TRY(hipGraphLaunch((flags & TLM_LOGITS) ? m->g_logits : m->g_prefill, st));
+  return TLM_OK;
+}
+
+int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end) {
+  if (!m || (!tokens && end > start)) return fail(TLM_ERR_INVALID, "TLMModel: null argument");
+  if (start < 0 || end > m->d.max_tokens || start > end)
+    return fail(TLM_ERR_RANGE, "TLMModel: prefill range [%d, %d) outside [0, %d)", start, end, m->d.max_tokens);
+  if (start == end) return TLM_OK;
+  for (int i = start; i < end; i++)
+    if (tokens[i] < 0 || tokens[i] >= m->d.vocab_size)
+      return fail(TLM_ERR_RANGE, "TLMModel: token %d outside [0, %d)", tokens[i], m->d.vocab_size);
+  int rc = tlm_model_finalize(m);
+  if (rc) return rc;
+  hipStream_t st = m->ctx->stream;
+  HIP_TRY(hipStreamSynchronize(st));
+  HIP_TRY(hipMemcpy(m->prompt, tokens + start, sizeof(int32_t) * (end - start), hipMemcpyHostToDevice));
+  launch_set_ctrl(m->ctrl, tokens[start], start, 0, start, end - start, st);
+  CHECK_LAUNCH("TLMModel");
+  for (int i = start; i < end; i++) HIP_TRY(hipGraphLaunch(m->g_prefill, st));
+  return TLM_OK;
+}
+
+int tlm_read_logits(tlm_model* m, float* out, size_t n) {
+  if (!m || !out || n > (size_t)m->d.vocab_size) return fail(TLM_ERR_INVALID, "TLMModel: invalid logits read");
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  HIP_TRY(hipMemcpy(out, m->logits, sizeof(float) * n, hipMemcpyDeviceToHost));
+  return TLM_OK;
+}
+
+int tlm_read_hidden(tlm_model* m, float* out, size_t n) {
+  if (!m || !out || n > (size_t)m->d.hidden_size) return fail(TLM_ERR_INVALID, "TLMModel: invalid hidden read");
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  HIP_TRY(hipMemcpy(out, m->xf, sizeof(float) * n, hipMemcpyDeviceToHost));
+  return TLM_OK;
+}
+
+int tlm_read_token(tlm_model* m, int32_t* token) {
+  if (!m || !token) return fail(TLM_ERR_INVALID, "TLMModel: null argument");
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  HIP_TRY(hipMemcpy(token, m->ctrl + C_TOKEN, sizeof(int32_t), hipMemcpyDeviceToHost));
+  return TLM_OK;
+}
+
+int tlm_decode_greedy(tlm_model* m, int32_t token, int32_t position, int n, int32_t* out) {
+  if (!m || (!out && n > 0) || n < 0) return fail(TLM_ERR_INVALID, "TLMModel: invalid decode argument");
+  int rc = check_token(m, token, position);
+  if (rc) return rc;
+  if ((long)position + n > m->d.max_tokens)
+    return fail(TLM_ERR_RANGE, "TLMModel: decode of %d tokens from %d passes max_tokens %d", n, position,
+                m->d.max_tokens);
+  rc = tlm_model_finalize(m);
+  if (rc) return rc;
+  hipStream_t st = m->ctx->stream;
+  launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, st);
+  CHECK_LAUNCH("TLMModel");
+  for (int i = 0; i < n; i++) HIP_TRY(hipGraphLaunch(m->g_logits, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  if (n > 0) HIP_TRY(hipMemcpy(out, m->tokens_out, sizeof(int32_t) * n, hipMemcpyDeviceToHost));
+  return TLM_OK;
+}
+
+int tlm_reset_cache(tlm_model* m) {
+  if (!m) return fail(TLM_ERR_INVALID, "TLMModel: null model");
+  const size_t esz = m->d.kv_fmt == TLM_FMT_F32 ? 4 : 2;
+  const size_t cache = (size_t)m->d.num_kv_heads * m->d.max_tokens * m->d.head_dim * esz;
+  for (auto& L : m->layers) {
+    HIP_TRY(hipMemsetAsync(L.kc, 0, cache, m->ctx->stream));
+    HIP_TRY(hipMemsetAsync(L.vc, 0, cache, m->ctx->stream));
+  }
+  return TLM_OK;
+}
+
+static int kv_copy(tlm_model* m, int layer, int pos0, int count, void* k, void* v, bool write) {
+  if (!m || !k || !v) return fail(TLM_ERR_INVALID, "TLMModel: null argument");
+  if (layer < 0 || layer >= m->d.num_layers || pos0 < 0 || count < 0 || pos0 + count > m->d.max_tokens)
+    return fail(TLM_ERR_RANGE, "TLMModel: KV range outside the cache");
+  const size_t esz = m->d.kv_fmt == TLM_FMT_F32 ? 4 : 2;
+  const int Hkv = m->d.num_kv_heads, D = m->d.head_dim, M = m->d.max_tokens;
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  for (int h = 0; h < Hkv; h++) {
+    // canonical rows are [t][h][d]; device rows are [h][t][d]
+    HIP_TRY(hipMemcpy2D(
+        write ? (char*)m->layers[layer].kc + ((size_t)h * M + pos0) * D * esz : (char*)k + (size_t)h * D * esz,
+        write ? D * esz : (size_t)Hkv * D * esz,
+        write ? (const char*)k + (size_t)h * D * esz : (const char*)m->layers[layer].kc + ((size_t)h * M + pos0) * D * esz,
+        write ? (size_t)Hkv * D * esz : D * esz, D * esz, count, write ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy2D(
+        write ? (char*)m->layers[layer].vc + ((size_t)h * M + pos0) * D * esz : (char*)v + (size_t)h * D * esz,
+        write ? D * esz : (size_t)Hkv * D * esz,
+        write ? (const char*)v + (size_t)h * D * esz : (const char*)m->layers[layer].vc + ((size_t)h * M + pos0) * D * esz,
+        write ? (size_t)Hkv * D * esz : D * esz, D * esz, count, write ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost));
+  }
+  return TLM_OK;
+}
+
+int tlm_kv_write(tlm_model* m, int layer, int pos0, int count, const void* k, const void* v) {
+  return kv_copy(m, layer, pos0, count, const_cast<void*>(k), const_cast<void*>(v), true);
+}
+
+int tlm_kv_read(tlm_model* m, int layer, int pos0, int count, void* k, void* v) {
+  return kv_copy(m, layer, pos0, count, k, v, false);
+}
+
+int tlm_kv_fill_normal(tlm_model* m, uint64_t seed, int count) {
+  if (!m || count < 0 || count > m->d.max_tokens) return fail(TLM_ERR_RANGE, "TLMModel: invalid fill count");
+  for (int l = 0; l < m->d.num_layers; l++) {
+    launch_kv_fill(m->layers[l].kc, m->layers[l].vc, m->d.kv_fmt == TLM_FMT_F32, 0, m->d.num_kv_heads,
+                   m->d.max_tokens, m->d.head_dim, count, seed + (uint64_t)l * 0x100000000ull, m->ctx->stream);
+    CHECK_LAUNCH("TLMModel");
+  }
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  return TLM_OK;
+}
+
+// ------------------------------------------------------------------- timing --
+
+int tlm_time_decode(tlm_model* m, int32_t token, int32_t position, int warmup, int n, double* ms) {
+  if (!m || !ms || n <= 0 || warmup < 0) return fail(TLM_ERR_INVALID, "TLMModel: invalid timing argument");
+  int rc = check_token(m, token, position);
+  if (rc) return rc;
+  if ((long)position + warmup + n > m->d.max_tokens)
+    return fail(TLM_ERR_RANGE, "TLMModel: timed decode passes max_tokens");
+  rc = tlm_model_finalize(m);
+  if (rc) return rc;
+  hipStream_t st = m->ctx->stream;
+  launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, st);
+  for (int i = 0; i < warmup; i++) HIP_TRY(hipGraphLaunch(m->g_logits, st));
+  hipEvent_t e0, e1;
+  HIP_TRY(hipEventCreate(&e0));
+  HIP_TRY(hipEventCreate(&e1));
+  HIP_TRY(hipStreamSynchronize(st));
+  HIP_TRY(hipEventRecord(e0, st));
+  for (int i = 0; i < n; i++) HIP_TRY(hipGraphLaunch(m->g_logits, st));
+  HIP_TRY(hipEventRecord(e1, st));
+  HIP_TRY(hipEventSynchronize(e1));
+  float f = 0.f;
+  HIP_TRY(hipEventElapsedTime(&f, e0, e1));
+  hipEventDestroy(e0);
+  hipEventDestroy(e1);
+  *ms = f;
+  return TLM_OK;
+}
+
+int tlm_time_kernel(tlm_model* m, int which, int iters, double* avg_ms) {
+  if (!m || !avg_ms || iters <= 0 || which < 0 || which > 5)
+    return fail(TLM_ERR_INVALID, "TLMModel: invalid kernel timing argument");
+  int rc = tlm_model_finalize(m);
+  if (rc) return rc;
+  hipStream_t st = m->ctx->stream;
+  hipEvent_t e0, e1;
+  HIP_TRY(hipEventCreate(&e0));
+  HIP_TRY(hipEventCreate(&e1));
+  auto one = [&]() { return which == 0 ? enqueue_head(m, st, false, false) : enqueue_layer(m, 0, st, which); };
+  if (!one()) return fail(TLM_ERR_STATE, "TLMModel: no kernel variant for stage %d", which);  // warm
+  CHECK_LAUNCH("TLMModel");
+  HIP_TRY(hipStreamSynchronize(st));
+  HIP_TRY(hipEventRecord(e0, st));
+  for (int i = 0; i < iters; i++) one();
+  HIP_TRY(hipEventRecord(e1, st));
+  HIP_TRY(hipEventSynchronize(e1));
+  CHECK_LAUNCH("TLMModel");
+  float f = 0.f;
+  HIP_TRY(hipEventElapsedTime(&f, e0, e1));
+  hipEventDestroy(e0);
+  hipEventDestroy(e1);
+  *avg_ms = f / iters;
+  return TLM_OK;
+}
+
+int tlm_model_describe(tlm_model* m, char* out, size_t len) {
+  if (!m || !out) return fail(TLM_ERR_INVALID, "TLMModel: null argument");
+  const Layer& L = m->layers[0];
+  auto p = [](const tlm_linear* x) {
+    char b[128];
+    snprintf(b, sizeof b, "%dx%d T=%d C=%d waves=%d cps=%d splits=%d", x->N, x->K, x->T, x->C, x->plan.waves,
+             x->plan.cps, x->plan.splits);
+    return std::string(b);
+  };
+  std::string s = "qkv[" + p(L.qkv) + "] o[" + p(L.o) + "] gate_up[" + p(L.gu) + "] down[" + p(L.down) + "] head[" +
+                  p(m->head) + " grid=" + std::to_string(m->lm_plan.gx) + " waves=" +
+                  std::to_string(m->lm_plan.waves) + "] attn[nsplit=" + std::to_string(m->attn.nsplit) +
+                  " G=" + std::to_string(m->attn.G) + "]";
+  snprintf(out, len, "%s", s.c_str());
+  return TLM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,91 @@
+// Kernel argument blocks and launchers shared by tlm_kernels.hip and tlm_api.hip.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tlm {
+
+constexpr int kTile = 64;      // output rows per tile: one row per lane of a wave64
+constexpr int kMaxChunks = 8;  // 16-byte chunks a wave keeps in flight per batch
+
+enum WeightFmt { WF_F16 = 1, WF_Q4 = 2 };
+
+// GEMV prologues: how the input slice x[k0, k1) is formed in LDS.
+enum Prologue {
+  PRO_COPY = 0,    // x = in
+  PRO_RMS = 1,     // x = rmsnorm(base + sum_j pin[j]) * w   (base: fp32 vector or embedding row)
+  PRO_SWIGLU = 2,  // x = silu(sum_j pin[j][k]) * (sum_j pin[j][up_off + k])
+};
+
+// ctrl block (device int32[8]): per-token state read by every kernel so that one
+// captured graph serves every position.
+enum Ctrl { C_TOKEN = 0, C_POS = 1, C_STEP = 2, C_BASE = 3, C_LEN = 4 };
+
+struct GemvArgs {
+  const uint4* w;      // [T][C][64] 16-byte chunks (q4: 32 k, fp16: 8 k)
+  const uint16_t* s;   // q4 scales [T][C][64] (fp16 bits)
+  int N, T, C, K, cps; // rows, tiles, chunks/row, logical K, chunks per split
+  float* out;          // [S][N] partial sums (S = gridDim.y)
+  const float* bias;   // added by split 0 (may be null)
+  // PRO_COPY
+  const float* in;
+  // PRO_RMS
+  const float* base;   // fp32 [K] residual, or null to gather the embedding row
+  const void* emb;     // embedding table [V][K] when base == null
+  int emb_f32;
+  const int* ctrl;
+  const float* pin;    // partials to add (RMS) / gate|up partials (SWIGLU)
+  int n_pin, pin_stride;
+  const float* norm_w;
+  float eps;
+  float* xout;         // block (0,0) stores base + sum pin here (residual stream)
+  int up_off;          // SWIGLU: offset of the up rows in pin
+  // LM head epilogue
+  float* logits;       // full logits (may be null)
+  float* arg_val;      // per-block argmax partials
+  int* arg_idx;
+  int* ticket;         // arrival counter (zero between launches)
+  int* tokens_out;     // greedy stream (indexed by ctrl[C_STEP]), may be null
+  int advance;         // 1: last block advances ctrl (token <- argmax, pos++, step++)
+  int max_steps;
+};
+
+struct AttnArgs {
+  const float* src;     // q|k|v partial sums [n_src][src_stride]
+  int n_src, src_stride;
+  const float* bias;    // [(Hq + 2Hkv) D] or null
+  const int* ctrl;      // position at ctrl[C_POS]
+  void* kc;             // [Hkv][max_tokens][D] (this layer)
+  void* vc;
+  const float* rope_cos;  // [max_tokens][rd/2], attention factor folded in
+  const float* rope_sin;
+  float* out;           // [Hq D]
+  float* pacc;          // [Hq][nsplit][D]
+  float* pml;           // [Hq][nsplit][2] (m, l)
+  int* ticket;          // [Hkv]
+  int Hq, Hkv, D, G, rd, max_tokens, window, nsplit, chmin;
+  float scale;
+};
+
+// launchers (stream-ordered, graph-capturable: no memset, no host sync)
+// launchers return false when no compiled variant matches (nothing is launched)
+bool launch_gemv(int fmt, int pro, int waves, dim3 grid, const GemvArgs& a, hipStream_t st);
+bool launch_lm_head(int fmt, int waves, dim3 grid, const GemvArgs& a, hipStream_t st);
+bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, hipStream_t st);
+size_t gemv_smem_bytes(int fmt, int cps, int waves);
+void launch_final_norm(const float* base, const float* pin, int n_pin, int pin_stride, const float* w, int n,
+                       float eps, float* y, hipStream_t st);
+void launch_rmsnorm(const float* x, const float* w, int n, float eps, int offset, float* y, hipStream_t st);
+void launch_silu_mul(const float* g, const float* u, int n, float* out, hipStream_t st);
+void launch_reduce(const float* part, int n_part, int stride, const float* bias, int n, float* y, hipStream_t st);
+void launch_argmax(const float* logits, int n, float* pval, int* pidx, int* ticket, int* token, int blocks,
+                   hipStream_t st);
+void launch_set_ctrl(int* ctrl, int token, int pos, int step, int base, int len, hipStream_t st);
+void launch_prefill_advance(int* ctrl, const int* prompt, hipStream_t st);
+void launch_dequant(int fmt, const uint4* w, const uint16_t* s, int N, int T, int C, int K, float* out,
+                    hipStream_t st);
+void launch_kv_fill(void* kc, void* vc, bool f32, size_t heads_stride, int Hkv, int max_tokens, int D, int count,
+                    uint64_t seed, hipStream_t st);
+size_t attn_smem_bytes(int G, int D);
+
+}  // namespace tlm
