@@ -33,8 +33,11 @@ def test_hf_fixture_fp16_storage_on_gpu(ctx, hf_fixture, case_index):
     """reference.browser.test.ts:7-40 on the device: fp16 weights (embedding
     fp32, like the fixture's fp16-storage contract), fp32 KV cache."""
     case = hf_fixture["cases"][case_index]
-    hw = W.from_hf(case["config"], fixture_tensors(hf_fixture),
-                   W.Storage(linear="f16", head="f16", embed="f32", kv="f32"))
+    # the fixture rounds every parameter except the embedding to fp16 once
+    # (scripts/reference/generate.py:77-84), norm weights included
+    tensors = {k: (v if k == "model.embed_tokens.weight" else v.astype(np.float16).astype(np.float32))
+               for k, v in fixture_tensors(hf_fixture).items()}
+    hw = W.from_hf(case["config"], tensors, W.Storage(linear="f16", head="f16", embed="f32", kv="f32"))
     runner = R.DecoderHIPRunner(hw, {"maxTokens": 64}, ctx=ctx)
     om = oracle_model(hw, 64, kv_f16=False)
     ids = hf_fixture["input_ids"]

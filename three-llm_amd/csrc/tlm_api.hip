@@ -2,6 +2,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -51,7 +52,6 @@ struct tlm_ctx {
   // scratch for op-level argmax
   float* arg_val = nullptr;
   int* arg_idx = nullptr;
-  int* ticket = nullptr;
 };
 
 struct GemvPlan {
@@ -71,7 +71,7 @@ struct tlm_linear {
 struct tlm_attn {
   tlm_ctx* ctx = nullptr;
   tlm_attn_desc d{};
-  int G = 1, gmax = 1, nsplit = 1, chmin = 32;
+  int G = 1, gmax = 1, nsplit = 1, chmin = 32, lpp = 1;
   float scale = 1.f;
   void* kc = nullptr;
   void* vc = nullptr;
@@ -79,7 +79,6 @@ struct tlm_attn {
   float* rope_sin = nullptr;
   float* pacc = nullptr;
   float* pml = nullptr;
-  int* ticket = nullptr;
   int* ctrl = nullptr;
 };
 
@@ -112,13 +111,13 @@ struct tlm_model {
   float* logits = nullptr;
   float* arg_val = nullptr;
   int* arg_idx = nullptr;
-  int* ticket = nullptr;
   // attention (shared by the layers; they run one after another)
   tlm_attn attn;
   GemvPlan lm_plan;
   hipGraphExec_t g_logits = nullptr, g_prefill = nullptr;
   hipGraph_t graph_logits = nullptr, graph_prefill = nullptr;
   bool finalized = false;
+  bool use_graphs = true;  // TLM_GRAPHS=0 enqueues the same kernels directly (profilers, debugging)
 };
 
 // ------------------------------------------------------------ layout/plan --
@@ -144,7 +143,7 @@ static GemvPlan plan_gemv(int T, int C, int cus, int CK, bool single_split) {
   p.waves = C >= 64 ? 8 : 4;
   int cps = std::max(1, std::min(C, p.waves * cpw));
   int S = (C + cps - 1) / cps;
-  S = std::min(S, 32);
+  S = std::min(S, kMaxPart);  // consumers fold at most kMaxPart partials in one round trip
   cps = (C + S - 1) / S;
   const int max_cps = 8192 / CK;  // x slice <= 32 KB of LDS
   if (cps > max_cps) {
@@ -277,8 +276,6 @@ int tlm_open(int device, tlm_ctx** out) {
   hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipMalloc(&c->arg_val, 4096 * sizeof(float));
   if (e == hipSuccess) e = hipMalloc(&c->arg_idx, 4096 * sizeof(int));
-  if (e == hipSuccess) e = hipMalloc(&c->ticket, 64 * sizeof(int));
-  if (e == hipSuccess) e = hipMemset(c->ticket, 0, 64 * sizeof(int));
   if (e != hipSuccess) {
     tlm_close(c);
     return fail(TLM_ERR_HIP, "TLMContext: setup failed: %s", hipGetErrorString(e));
@@ -292,7 +289,6 @@ void tlm_close(tlm_ctx* ctx) {
   if (ctx->stream) hipStreamSynchronize(ctx->stream);
   hipFree(ctx->arg_val);
   hipFree(ctx->arg_idx);
-  hipFree(ctx->ticket);
   if (ctx->stream) hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -462,8 +458,8 @@ static void rope_tables(int max_tokens, int rd, const float* inv_freq, double af
 static int attn_init(tlm_ctx* ctx, const tlm_attn_desc* d, tlm_attn* A, bool own_cache) {
   if (d->heads <= 0 || d->kv_heads <= 0 || d->heads % d->kv_heads != 0)
     return fail(TLM_ERR_INVALID, "TLMAttention: heads %d must be a multiple of kv heads %d", d->heads, d->kv_heads);
-  if (d->head_dim <= 0 || d->head_dim % 2 != 0 || d->head_dim > 256)
-    return fail(TLM_ERR_INVALID, "TLMAttention: head_dim %d must be even and <= 256", d->head_dim);
+  if (d->head_dim <= 0 || d->head_dim % 2 != 0 || d->head_dim > 128)
+    return fail(TLM_ERR_INVALID, "TLMAttention: head_dim %d must be even and <= 128", d->head_dim);
   if (d->rotary_dim < 0 || d->rotary_dim > d->head_dim || d->rotary_dim % 2 != 0)
     return fail(TLM_ERR_INVALID, "TLMAttention: invalid rotary dimension %d", d->rotary_dim);
   if (d->rotary_dim > 0 && !d->inv_freq) return fail(TLM_ERR_INVALID, "TLMAttention: missing inv_freq");
@@ -474,7 +470,8 @@ static int attn_init(tlm_ctx* ctx, const tlm_attn_desc* d, tlm_attn* A, bool own
   if (A->G > 16) return fail(TLM_ERR_INVALID, "TLMAttention: more than 16 query heads per kv head");
   A->gmax = A->G <= 1 ? 1 : A->G <= 2 ? 2 : A->G <= 4 ? 4 : A->G <= 8 ? 8 : 16;
   A->scale = (float)(d->attn_scale > 0 ? d->attn_scale : 1.0 / sqrt((double)d->head_dim));
-  if (attn_smem_bytes(A->G, d->head_dim) > 65536)
+  A->lpp = attn_lpp(d->head_dim, d->kv_fmt == TLM_FMT_F32);
+  if (attn_smem_bytes(A->gmax, d->head_dim, A->lpp) > 65536)
     return fail(TLM_ERR_INVALID, "TLMAttention: %d heads per kv head x head_dim %d exceed the LDS budget", A->G,
                 d->head_dim);
   A->chmin = 32;
@@ -494,8 +491,6 @@ static int attn_init(tlm_ctx* ctx, const tlm_attn_desc* d, tlm_attn* A, bool own
   HIP_TRY(hipMemcpy(A->rope_sin, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice));
   HIP_TRY(hipMalloc(&A->pacc, sizeof(float) * (size_t)d->heads * A->nsplit * D));
   HIP_TRY(hipMalloc(&A->pml, sizeof(float) * (size_t)d->heads * A->nsplit * 2));
-  HIP_TRY(hipMalloc(&A->ticket, sizeof(int) * d->kv_heads));
-  HIP_TRY(hipMemset(A->ticket, 0, sizeof(int) * d->kv_heads));
   if (own_cache) {
     const size_t cache = (size_t)d->kv_heads * d->max_tokens * D * esz;
     HIP_TRY(hipMalloc(&A->kc, cache));
@@ -513,7 +508,6 @@ static void attn_free(tlm_attn* A, bool own_cache) {
   hipFree(A->rope_sin);
   hipFree(A->pacc);
   hipFree(A->pml);
-  hipFree(A->ticket);
   if (own_cache) {
     hipFree(A->kc);
     hipFree(A->vc);
@@ -537,7 +531,6 @@ static AttnArgs attn_args(const tlm_attn* A, const float* src, int n_src, int st
   a.out = out;
   a.pacc = A->pacc;
   a.pml = A->pml;
-  a.ticket = A->ticket;
   a.Hq = A->d.heads;
   a.Hkv = A->d.kv_heads;
   a.D = A->d.head_dim;
@@ -547,6 +540,7 @@ static AttnArgs attn_args(const tlm_attn* A, const float* src, int n_src, int st
   a.window = A->d.sliding_window;
   a.nsplit = A->nsplit;
   a.chmin = A->chmin;
+  a.lpp = A->lpp;
   a.scale = A->scale;
   return a;
 }
@@ -579,7 +573,7 @@ int tlm_op_attention(tlm_attn* A, const float* qkv, int position, float* out) {
   launch_set_ctrl(A->ctrl, 0, position, 0, 0, 0, st);
   const int total = (A->d.heads + 2 * A->d.kv_heads) * A->d.head_dim;
   AttnArgs a = attn_args(A, qkv, 1, total, nullptr, A->ctrl, A->kc, A->vc, out);
-  if (!launch_attention(A->d.kv_fmt == TLM_FMT_F32, A->gmax, a, st))
+  if (!launch_attention(A->d.kv_fmt == TLM_FMT_F32, A->gmax, a, true, st))
     return fail(TLM_ERR_STATE, "TLMAttention: no kernel variant for this shape");
   CHECK_LAUNCH("TLMAttention");
   return TLM_OK;
@@ -653,15 +647,12 @@ int tlm_op_logits(tlm_linear* head, const float* x, float* logits, int32_t* toke
   a.logits = logits;
   a.arg_val = ctx->arg_val;
   a.arg_idx = ctx->arg_idx;
-  a.ticket = ctx->ticket;
-  // a scratch ctrl block: the sampled token lands in ctrl[C_TOKEN]
-  a.ctrl = token;
-  a.advance = 0;
-  a.tokens_out = nullptr;
   if (gemv_smem_bytes(wfmt(head->fmt), p.cps, p.waves) > 65536)
     return fail(TLM_ERR_INVALID, "TLMLogits: hidden size %d too large for one block", head->K);
   if (!launch_lm_head(wfmt(head->fmt), p.waves, dim3(p.gx), a, ctx->stream))
     return fail(TLM_ERR_STATE, "TLMLogits: no kernel variant for this shape");
+  // the sampled token lands in token[0] (the merge's ctrl[C_TOKEN])
+  launch_argmax_merge(ctx->arg_val, ctx->arg_idx, p.gx, token, nullptr, 0, 0, ctx->stream);
   CHECK_LAUNCH("TLMLogits");
   return TLM_OK;
 }
@@ -669,7 +660,7 @@ int tlm_op_logits(tlm_linear* head, const float* x, float* logits, int32_t* toke
 int tlm_op_argmax(tlm_ctx* ctx, const float* logits, int n, int32_t* token) {
   if (!ctx || !logits || !token || n <= 0) return fail(TLM_ERR_INVALID, "TLMLogits: invalid argmax argument");
   const int blocks = std::max(1, std::min(1024, (n + 1023) / 1024));
-  launch_argmax(logits, n, ctx->arg_val, ctx->arg_idx, ctx->ticket + 1, token, blocks, ctx->stream);
+  launch_argmax(logits, n, ctx->arg_val, ctx->arg_idx, token, blocks, ctx->stream);
   CHECK_LAUNCH("TLMLogits");
   return TLM_OK;
 }
@@ -691,6 +682,7 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
   if (d->hidden_size <= 0 || d->intermediate_size <= 0 || d->num_layers <= 0 || d->vocab_size <= 0 ||
       d->max_tokens <= 0)
     return fail(TLM_ERR_INVALID, "TLMModel: invalid dimensions");
+  if (d->hidden_size > 4096) return fail(TLM_ERR_INVALID, "TLMModel: hidden size above 4096 is not supported");
   if (d->linear_fmt != TLM_FMT_Q4 && d->linear_fmt != TLM_FMT_F16)
     return fail(TLM_ERR_INVALID, "TLMModel: linear_fmt must be q4 or fp16");
   if (d->embed_fmt != TLM_FMT_F16 && d->embed_fmt != TLM_FMT_F32)
@@ -760,7 +752,6 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
   M_TRY(model_alloc((void**)&m->logits, sizeof(float) * d->vocab_size));
   M_TRY(model_alloc((void**)&m->arg_val, sizeof(float) * 4096));
   M_TRY(model_alloc((void**)&m->arg_idx, sizeof(int) * 4096));
-  M_TRY(model_alloc((void**)&m->ticket, sizeof(int) * 4));
 #undef M_TRY
   if (rc) {
     std::string msg = g_error;
@@ -793,7 +784,7 @@ void tlm_model_destroy(tlm_model* m) {
   tlm_linear_destroy(m->head);
   attn_free(&m->attn, false);
   void* bufs[] = {m->emb, m->final_norm, m->ctrl, m->tokens_out, m->prompt, m->xa, m->xb, m->xf, m->attn_out,
-                  m->pq, m->po, m->pgu, m->pd, m->logits, m->arg_val, m->arg_idx, m->ticket};
+                  m->pq, m->po, m->pgu, m->pd, m->logits, m->arg_val, m->arg_idx};
   for (void* p : bufs) hipFree(p);
   delete m;
 }
@@ -896,14 +887,21 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which) {
   // 2. RoPE + KV append + split-K attention
   if (which < 0 || which == 1) {
     AttnArgs a = attn_args(&m->attn, m->pq, L.qkv->plan.splits, m->Nqkv, L.bqkv, m->ctrl, L.kc, L.vc, m->attn_out);
-    ok &= launch_attention(d.kv_fmt == TLM_FMT_F32, m->attn.gmax, a, st);
+    ok &= launch_attention(d.kv_fmt == TLM_FMT_F32, m->attn.gmax, a, false, st);
   }
-  // 3. O projection
+  // 3. O projection; its prologue combines the attention chunk partials
   if (which < 0 || which == 5) {
     GemvArgs a;
     fill_gemv_args(a, L.o, m->po);
-    a.in = m->attn_out;
-    ok &= launch_gemv(wfmt(L.o->fmt), PRO_COPY, L.o->plan.waves, dim3(L.o->plan.gx, L.o->plan.splits), a, st);
+    a.ctrl = m->ctrl;
+    a.pacc = m->attn.pacc;
+    a.pml = m->attn.pml;
+    a.att_D = d.head_dim;
+    a.att_nsplit = m->attn.nsplit;
+    a.att_chmin = m->attn.chmin;
+    a.att_window = d.sliding_window;
+    a.att_max_tokens = d.max_tokens;
+    ok &= launch_gemv(wfmt(L.o->fmt), PRO_ATTN, L.o->plan.waves, dim3(L.o->plan.gx, L.o->plan.splits), a, st);
   }
   // 4. x_mid = x + O partials; RMSNorm; gate|up GEMV
   if (which < 0 || which == 2) {
@@ -946,12 +944,10 @@ static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, bool final_
   a.logits = m->logits;
   a.arg_val = m->arg_val;
   a.arg_idx = m->arg_idx;
-  a.ticket = m->ticket;
-  a.ctrl = m->ctrl;
-  a.tokens_out = advance ? m->tokens_out : nullptr;
-  a.advance = advance ? 1 : 0;
-  a.max_steps = d.max_tokens;
-  return launch_lm_head(wfmt(m->head->fmt), m->lm_plan.waves, dim3(m->lm_plan.gx), a, st);
+  if (!launch_lm_head(wfmt(m->head->fmt), m->lm_plan.waves, dim3(m->lm_plan.gx), a, st)) return false;
+  launch_argmax_merge(m->arg_val, m->arg_idx, m->lm_plan.gx, m->ctrl, advance ? m->tokens_out : nullptr,
+                      advance ? 1 : 0, d.max_tokens, st);
+  return true;
 }
 
 static int capture(tlm_model* m, bool logits, hipGraph_t* g, hipGraphExec_t* ge) {
@@ -975,10 +971,34 @@ int tlm_model_finalize(tlm_model* m) {
   if (!m) return fail(TLM_ERR_INVALID, "TLMModel: null model");
   if (m->finalized) return TLM_OK;
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  const char* env = getenv("TLM_GRAPHS");
+  m->use_graphs = !(env && env[0] == '0');
+  if (!m->use_graphs) {
+    m->finalized = true;
+    return TLM_OK;
+  }
   int rc = capture(m, true, &m->graph_logits, &m->g_logits);
   if (rc == TLM_OK) rc = capture(m, false, &m->graph_prefill, &m->g_prefill);
   if (rc) return rc;
   m->finalized = true;
+  return TLM_OK;
+}
+
+// One token of the schedule: the captured graph, or the same kernels enqueued directly.
+static int run_token(tlm_model* m, bool logits) {
+  hipStream_t st = m->ctx->stream;
+  if (m->use_graphs) {
+    HIP_TRY(hipGraphLaunch(logits ? m->g_logits : m->g_prefill, st));
+    return TLM_OK;
+  }
+  bool ok = true;
+  for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1);
+  if (logits)
+    ok &= enqueue_head(m, st, true, true);
+  else
+    launch_prefill_advance(m->ctrl, m->prompt, st);
+  if (!ok) return fail(TLM_ERR_STATE, "TLMModel: no kernel variant for a stage of this model");
+  CHECK_LAUNCH("TLMModel");
   return TLM_OK;
 }
 
@@ -999,8 +1019,7 @@ int tlm_compute_token(tlm_model* m, int32_t token, int32_t position, int flags) 
   hipStream_t st = m->ctx->stream;
   launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, st);
   CHECK_LAUNCH("TLMModel");
-  HIP_TRY(hipGraphLaunch((flags & TLM_LOGITS) ? m->g_logits : m->g_prefill, st));
-  return TLM_OK;
+  return run_token(m, (flags & TLM_LOGITS) != 0);
 }
 
 int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end) {
@@ -1018,7 +1037,10 @@ int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end)
   HIP_TRY(hipMemcpy(m->prompt, tokens + start, sizeof(int32_t) * (end - start), hipMemcpyHostToDevice));
   launch_set_ctrl(m->ctrl, tokens[start], start, 0, start, end - start, st);
   CHECK_LAUNCH("TLMModel");
-  for (int i = start; i < end; i++) HIP_TRY(hipGraphLaunch(m->g_prefill, st));
+  for (int i = start; i < end; i++) {
+    rc = run_token(m, false);
+    if (rc) return rc;
+  }
   return TLM_OK;
 }
 
@@ -1055,7 +1077,10 @@ int tlm_decode_greedy(tlm_model* m, int32_t token, int32_t position, int n, int3
   hipStream_t st = m->ctx->stream;
   launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, st);
   CHECK_LAUNCH("TLMModel");
-  for (int i = 0; i < n; i++) HIP_TRY(hipGraphLaunch(m->g_logits, st));
+  for (int i = 0; i < n; i++) {
+    rc = run_token(m, true);
+    if (rc) return rc;
+  }
   HIP_TRY(hipStreamSynchronize(st));
   if (n > 0) HIP_TRY(hipMemcpy(out, m->tokens_out, sizeof(int32_t) * n, hipMemcpyDeviceToHost));
   return TLM_OK;
@@ -1126,13 +1151,19 @@ int tlm_time_decode(tlm_model* m, int32_t token, int32_t position, int warmup, i
   if (rc) return rc;
   hipStream_t st = m->ctx->stream;
   launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, st);
-  for (int i = 0; i < warmup; i++) HIP_TRY(hipGraphLaunch(m->g_logits, st));
+  for (int i = 0; i < warmup; i++) {
+    rc = run_token(m, true);
+    if (rc) return rc;
+  }
   hipEvent_t e0, e1;
   HIP_TRY(hipEventCreate(&e0));
   HIP_TRY(hipEventCreate(&e1));
   HIP_TRY(hipStreamSynchronize(st));
   HIP_TRY(hipEventRecord(e0, st));
-  for (int i = 0; i < n; i++) HIP_TRY(hipGraphLaunch(m->g_logits, st));
+  for (int i = 0; i < n; i++) {
+    rc = run_token(m, true);
+    if (rc) return rc;
+  }
   HIP_TRY(hipEventRecord(e1, st));
   HIP_TRY(hipEventSynchronize(e1));
   float f = 0.f;

@@ -7,6 +7,7 @@ namespace tlm {
 
 constexpr int kTile = 64;      // output rows per tile: one row per lane of a wave64
 constexpr int kMaxChunks = 8;  // 16-byte chunks a wave keeps in flight per batch
+constexpr int kMaxPart = 12;   // partial vectors a consumer folds in with one round trip
 
 enum WeightFmt { WF_F16 = 1, WF_Q4 = 2 };
 
@@ -15,7 +16,22 @@ enum Prologue {
   PRO_COPY = 0,    // x = in
   PRO_RMS = 1,     // x = rmsnorm(base + sum_j pin[j]) * w   (base: fp32 vector or embedding row)
   PRO_SWIGLU = 2,  // x = silu(sum_j pin[j][k]) * (sum_j pin[j][up_off + k])
+  PRO_ATTN = 3,    // x = flash-decoding combine of the attention chunk partials
 };
+
+// Split of the attention window [first, pos] into chunks; identical on host and device.
+struct ChunkPlan {
+  int first, n, chunk, nact;
+};
+__host__ __device__ inline ChunkPlan chunk_plan(int pos, int window, int nsplit, int chmin) {
+  ChunkPlan p;
+  p.first = window > 0 ? (pos - window + 1 > 0 ? pos - window + 1 : 0) : 0;
+  p.n = pos - p.first + 1;
+  const int c = (p.n + nsplit - 1) / nsplit;
+  p.chunk = c > chmin ? c : chmin;
+  p.nact = (p.n + p.chunk - 1) / p.chunk;
+  return p;
+}
 
 // ctrl block (device int32[8]): per-token state read by every kernel so that one
 // captured graph serves every position.
@@ -40,11 +56,14 @@ struct GemvArgs {
   float eps;
   float* xout;         // block (0,0) stores base + sum pin here (residual stream)
   int up_off;          // SWIGLU: offset of the up rows in pin
+  // PRO_ATTN: chunk partials of the attention kernel
+  const float* pacc;   // [Hq][nsplit][D]
+  const float* pml;    // [Hq][nsplit][2]
+  int att_D, att_nsplit, att_chmin, att_window, att_max_tokens;
   // LM head epilogue
   float* logits;       // full logits (may be null)
   float* arg_val;      // per-block argmax partials
   int* arg_idx;
-  int* ticket;         // arrival counter (zero between launches)
   int* tokens_out;     // greedy stream (indexed by ctrl[C_STEP]), may be null
   int advance;         // 1: last block advances ctrl (token <- argmax, pos++, step++)
   int max_steps;
@@ -59,11 +78,11 @@ struct AttnArgs {
   void* vc;
   const float* rope_cos;  // [max_tokens][rd/2], attention factor folded in
   const float* rope_sin;
-  float* out;           // [Hq D]
-  float* pacc;          // [Hq][nsplit][D]
-  float* pml;           // [Hq][nsplit][2] (m, l)
-  int* ticket;          // [Hkv]
+  float* out;           // [Hq D] (combine kernel)
+  float* pacc;          // [Hq][nsplit][D] unnormalised chunk outputs
+  float* pml;           // [Hq][nsplit][2] (max score, sum of exp)
   int Hq, Hkv, D, G, rd, max_tokens, window, nsplit, chmin;
+  int lpp;              // lanes per position in the score pass (1, 2 or 4)
   float scale;
 };
 
@@ -71,21 +90,25 @@ struct AttnArgs {
 // launchers return false when no compiled variant matches (nothing is launched)
 bool launch_gemv(int fmt, int pro, int waves, dim3 grid, const GemvArgs& a, hipStream_t st);
 bool launch_lm_head(int fmt, int waves, dim3 grid, const GemvArgs& a, hipStream_t st);
-bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, hipStream_t st);
+// attention chunk partials; with `combine` also the combine kernel writing a.out
+bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, bool combine, hipStream_t st);
 size_t gemv_smem_bytes(int fmt, int cps, int waves);
 void launch_final_norm(const float* base, const float* pin, int n_pin, int pin_stride, const float* w, int n,
                        float eps, float* y, hipStream_t st);
 void launch_rmsnorm(const float* x, const float* w, int n, float eps, int offset, float* y, hipStream_t st);
 void launch_silu_mul(const float* g, const float* u, int n, float* out, hipStream_t st);
 void launch_reduce(const float* part, int n_part, int stride, const float* bias, int n, float* y, hipStream_t st);
-void launch_argmax(const float* logits, int n, float* pval, int* pidx, int* ticket, int* token, int blocks,
-                   hipStream_t st);
+void launch_argmax(const float* logits, int n, float* pval, int* pidx, int* token, int blocks, hipStream_t st);
+// second pass of the greedy sampler; `ctrl` receives the token at ctrl[C_TOKEN]
+void launch_argmax_merge(const float* pval, const int* pidx, int n, int* ctrl, int* tokens_out, int advance,
+                         int max_steps, hipStream_t st);
 void launch_set_ctrl(int* ctrl, int token, int pos, int step, int base, int len, hipStream_t st);
 void launch_prefill_advance(int* ctrl, const int* prompt, hipStream_t st);
 void launch_dequant(int fmt, const uint4* w, const uint16_t* s, int N, int T, int C, int K, float* out,
                     hipStream_t st);
 void launch_kv_fill(void* kc, void* vc, bool f32, size_t heads_stride, int Hkv, int max_tokens, int D, int count,
                     uint64_t seed, hipStream_t st);
-size_t attn_smem_bytes(int G, int D);
+size_t attn_smem_bytes(int gmax, int D, int lpp);
+int attn_lpp(int D, bool kv_f32);
 
 }  // namespace tlm

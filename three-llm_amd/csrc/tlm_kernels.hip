@@ -11,6 +11,8 @@
 //   partial sums    [S][N] fp32: split-K GEMVs leave S partial vectors that the
 //                   consuming kernel folds into its prologue.
 #include <float.h>
+
+#include <algorithm>
 #include <hip/hip_fp16.h>
 
 #include "tlm_kernels.h"
@@ -73,46 +75,116 @@ __device__ void wave_argmax(float& v, int& i) {
 
 // ------------------------------------------------------------------ GEMV --
 
+// Sum of n <= kMaxPart partial vectors at element k.  The loads are
+// unconditional (indices clamped to valid rows) and only the adds are masked,
+// so all of them are in flight before the first use: a consumer pays one
+// memory round trip however many splits its producer used.  n == 0 reads nothing.
+__device__ __forceinline__ float sum_parts(const float* p, int n, int stride, int k) {
+  if (n <= 0) return 0.f;
+  float v[kMaxPart];
+#pragma unroll
+  for (int j = 0; j < kMaxPart; j++) v[j] = p[(size_t)min(j, n - 1) * stride + k];
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMaxPart; j++) s += j < n ? v[j] : 0.f;
+  return s;
+}
+
+// Flash-decoding combine of one output element (query head `row`, dim d) over
+// the attention chunk partials, 16 chunks per round trip (nact >= 1).
+__device__ float attn_combine_elem(const float* pacc, const float* pml, int row, int d, int D, int nsplit, int nact) {
+  const float* ml = pml + (size_t)row * nsplit * 2;
+  const float* ac = pacc + (size_t)row * nsplit * D + d;
+  float M = -INFINITY, L = 0.f, O = 0.f;
+  for (int jb = 0; jb < nact; jb += 16) {
+    float mm[16], ll[16], aa[16];
+#pragma unroll
+    for (int u = 0; u < 16; u++) {
+      const int j = min(jb + u, nact - 1);
+      mm[u] = ml[2 * j];
+      ll[u] = ml[2 * j + 1];
+      aa[u] = ac[(size_t)j * D];
+    }
+    float Mb = M;
+#pragma unroll
+    for (int u = 0; u < 16; u++) Mb = fmaxf(Mb, mm[u]);
+    const float sc = M == -INFINITY ? 0.f : __expf(M - Mb);
+    L *= sc;
+    O *= sc;
+#pragma unroll
+    for (int u = 0; u < 16; u++) {
+      const float e = (jb + u < nact && mm[u] != -INFINITY) ? __expf(mm[u] - Mb) : 0.f;
+      L = fmaf(ll[u], e, L);
+      O = fmaf(aa[u], e, O);
+    }
+    M = Mb;
+  }
+  return O / L;
+}
+
+// Elements handled per thread in one round trip by the prologues.
+constexpr int kEpt = 4;
+
 template <int PRO>
 __device__ void gemv_prologue(const GemvArgs& a, float* xl, float* scratch, int k0, int k1, int klen_pad) {
   const int tid = threadIdx.x, nt = blockDim.x;
   if (PRO == PRO_COPY) {
     for (int i = tid; i < klen_pad; i += nt) {
       const int k = k0 + i;
-      xl[i] = k < a.K ? a.in[k] : 0.f;
+      const float v = a.in[min(k, a.K - 1)];
+      xl[i] = k < a.K ? v : 0.f;
     }
   } else if (PRO == PRO_SWIGLU) {
     // silu(gate) * up of TSLSiLUMul.ts:15-29 on the summed gate/up partials
-    for (int i = tid; i < klen_pad; i += nt) {
-      const int k = k0 + i;
-      float v = 0.f;
-      if (k < a.K) {
-        float g = 0.f, u = 0.f;
-        for (int j = 0; j < a.n_pin; j++) {
-          g += a.pin[(size_t)j * a.pin_stride + k];
-          u += a.pin[(size_t)j * a.pin_stride + a.up_off + k];
-        }
-        v = g / (1.f + __expf(-g)) * u;
+    for (int ib = 0; ib < klen_pad; ib += kEpt * nt) {
+      float g[kEpt], u[kEpt];
+#pragma unroll
+      for (int e = 0; e < kEpt; e++) {
+        const int k = min(k0 + ib + tid + e * nt, a.K - 1);
+        g[e] = sum_parts(a.pin, a.n_pin, a.pin_stride, k);
+        u[e] = sum_parts(a.pin + a.up_off, a.n_pin, a.pin_stride, k);
       }
-      xl[i] = v;
+#pragma unroll
+      for (int e = 0; e < kEpt; e++) {
+        const int i = ib + tid + e * nt;
+        if (i < klen_pad) xl[i] = k0 + i < a.K ? g[e] / (1.f + __expf(-g[e])) * u[e] : 0.f;
+      }
+    }
+  } else if (PRO == PRO_ATTN) {
+    const ChunkPlan cp = chunk_plan(a.ctrl[C_POS], a.att_window, a.att_nsplit, a.att_chmin);
+    for (int i = tid; i < klen_pad; i += nt) {
+      const int k = min(k0 + i, a.K - 1);
+      const float v = attn_combine_elem(a.pacc, a.pml, k / a.att_D, k % a.att_D, a.att_D, a.att_nsplit, cp.nact);
+      xl[i] = k0 + i < a.K ? v : 0.f;
     }
   } else {
-    // residual stream x = base + sum(pin), then TSLRMSNorm.ts:50-74 on all K
+    // residual stream x = base + sum(pin), then TSLRMSNorm.ts:50-74 over all K
     const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && a.xout != nullptr;
     const int tok = a.base ? 0 : a.ctrl[C_TOKEN];
     float ss = 0.f;
-    for (int k = tid; k < a.K; k += nt) {
-      float v;
-      if (a.base)
-        v = a.base[k];
-      else if (a.emb_f32)
-        v = ((const float*)a.emb)[(size_t)tok * a.K + k];
-      else
-        v = h2f(((const uint16_t*)a.emb)[(size_t)tok * a.K + k]);
-      for (int j = 0; j < a.n_pin; j++) v += a.pin[(size_t)j * a.pin_stride + k];
-      ss = fmaf(v, v, ss);
-      if (writer) a.xout[k] = v;
-      if (k >= k0 && k < k1) xl[k - k0] = v;
+    for (int kb = 0; kb < a.K; kb += kEpt * nt) {
+      float v[kEpt];
+#pragma unroll
+      for (int e = 0; e < kEpt; e++) {
+        const int k = min(kb + tid + e * nt, a.K - 1);
+        float x;
+        if (a.base)
+          x = a.base[k];
+        else if (a.emb_f32)
+          x = ((const float*)a.emb)[(size_t)tok * a.K + k];
+        else
+          x = h2f(((const uint16_t*)a.emb)[(size_t)tok * a.K + k]);
+        v[e] = x + sum_parts(a.pin, a.n_pin, a.pin_stride, k);
+      }
+#pragma unroll
+      for (int e = 0; e < kEpt; e++) {
+        const int k = kb + tid + e * nt;
+        if (k < a.K) {
+          ss = fmaf(v[e], v[e], ss);
+          if (writer) a.xout[k] = v[e];
+          if (k >= k0 && k < k1) xl[k - k0] = v[e];
+        }
+      }
     }
     for (int i = (k1 - k0) + tid; i < klen_pad; i += nt) xl[i] = 0.f;
     const float tot = block_sum(ss, scratch);  // its barriers also publish xl
@@ -167,17 +239,16 @@ struct GemvCore {
   uint4 d[kMaxChunks];
   uint16_t sc[kMaxChunks];
 
+  // Loads of batch b: unconditional (chunk index clamped to this wave's last
+  // chunk), so the whole batch is in flight at once.  nw >= 1.
   __device__ __forceinline__ void load(const GemvArgs& a, int t, int c0, int wave, int W, int nw, int b) {
     const int lane = threadIdx.x & 63;
     const uint4* wt = a.w + (size_t)t * a.C * kTile;
 #pragma unroll
     for (int u = 0; u < kMaxChunks; u++) {
-      const int i = b + u;
-      if (i < nw) {
-        const int c = c0 + wave + i * W;
-        d[u] = wt[(size_t)c * kTile + lane];
-        if (FMT == WF_Q4) sc[u] = a.s[((size_t)t * a.C + c) * kTile + lane];
-      }
+      const int c = c0 + wave + min(b + u, nw - 1) * W;
+      d[u] = wt[(size_t)c * kTile + lane];
+      if (FMT == WF_Q4) sc[u] = a.s[((size_t)t * a.C + c) * kTile + lane];
     }
   }
 
@@ -185,9 +256,8 @@ struct GemvCore {
     float acc = 0.f;
 #pragma unroll
     for (int u = 0; u < kMaxChunks; u++) {
-      const int i = b + u;
-      if (i < nw) {
-        const int cl = wave + i * W;
+      if (b + u < nw) {  // wave-uniform
+        const int cl = wave + (b + u) * W;
         if (FMT == WF_Q4)
           acc += dot_q4(d[u], xl + cl * CK, xsum[cl], h2f(sc[u]));
         else
@@ -217,7 +287,7 @@ template <int FMT, int PRO, int W>
 __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvArgs a) {
   extern __shared__ float sm[];
   constexpr int CK = GemvCore<FMT>::CK;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int s = blockIdx.y;
   const int c0 = s * a.cps, c1 = min(a.C, c0 + a.cps);
   const int ncl = c1 - c0;
@@ -227,7 +297,7 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvArgs a) {
 
   GemvCore<FMT> core;
   int t = blockIdx.x;
-  if (t < a.T) core.load(a, t, c0, wave, W, nw, 0);  // weights in flight during the prologue
+  if (t < a.T && nw > 0) core.load(a, t, c0, wave, W, nw, 0);  // weights in flight during the prologue
   gemv_prologue<PRO>(a, L.xl, L.scratch, k0, k1, ncl * CK);
   __syncthreads();
   if (FMT == WF_Q4) {
@@ -260,23 +330,21 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvArgs a) {
   }
 }
 
-// LM head: GEMV over the vocabulary (PRO_COPY input) with the greedy sampler
-// fused in.  Each block keeps its best (score, id); the last block to finish
-// merges all partials (TSLLogits.ts:201-274 as one launch) and, in the decode
-// graph, advances the token/position state for the next step.
+// LM head: GEMV over the vocabulary (PRO_COPY input) with the first pass of
+// the greedy sampler fused in (createChunkPartialMaxNode, TSLLogits.ts:201-248):
+// each block keeps its best (score, id) over its tiles.
 template <int FMT, int W>
 __global__ __launch_bounds__(W * 64) void lm_head_kernel(GemvArgs a) {
   extern __shared__ float sm[];
   constexpr int CK = GemvCore<FMT>::CK;
-  __shared__ int is_last;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ncl = a.C;
   GemvSmem L(sm, a.cps, CK, W);
   const int nw = wave < ncl ? (ncl - wave + W - 1) / W : 0;
 
   GemvCore<FMT> core;
   int t = blockIdx.x;
-  if (t < a.T) core.load(a, t, 0, wave, W, nw, 0);
+  if (t < a.T && nw > 0) core.load(a, t, 0, wave, W, nw, 0);
   gemv_prologue<PRO_COPY>(a, L.xl, L.scratch, 0, a.K, ncl * CK);
   __syncthreads();
   if (FMT == WF_Q4) {
@@ -319,50 +387,54 @@ __global__ __launch_bounds__(W * 64) void lm_head_kernel(GemvArgs a) {
       a.arg_idx[blockIdx.x] = best_i;
     }
   }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) is_last = atomicAdd(a.ticket, 1) == (int)gridDim.x - 1;
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
+}
+
+// Second pass of the greedy sampler (createGreedyMergeNode, TSLLogits.ts:250-274):
+// one block reduces the per-block partials; a separate launch, so the kernel
+// boundary (not a device-scope fence per block) publishes the partials.  In the
+// decode graph it also advances the token/position state for the next step.
+__global__ __launch_bounds__(1024) void argmax_merge_kernel(const float* pval, const int* pidx, int n, int* ctrl,
+                                                            int* tokens_out, int advance, int max_steps) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   float bv = kLowest;
   int bi = 0x7fffffff;
-  for (int i = threadIdx.x; i < (int)gridDim.x; i += blockDim.x) {
-    const float v = a.arg_val[i];
-    const int ix = a.arg_idx[i];
-    if (better(v, ix, bv, bi)) {
-      bv = v;
-      bi = ix;
+  for (int i = threadIdx.x; i < n; i += blockDim.x)
+    if (better(pval[i], pidx[i], bv, bi)) {
+      bv = pval[i];
+      bi = pidx[i];
     }
-  }
   wave_argmax(bv, bi);
-  float* sv = L.red;
-  int* si = reinterpret_cast<int*>(L.red + 64);
   if (lane == 0) {
     sv[wave] = bv;
     si[wave] = bi;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < W; w++)
+    for (int w = 1; w < nw; w++)
       if (better(sv[w], si[w], bv, bi)) {
         bv = sv[w];
         bi = si[w];
       }
-    // createGreedyMergeNode starts from (LOWEST, 0): nothing above LOWEST -> token 0
+    // the merge starts from (LOWEST, 0): nothing above LOWEST -> token 0
     const int token = bv > kLowest ? bi : 0;
-    int* ctrl = const_cast<int*>(a.ctrl);
-    if (a.tokens_out) {
+    if (tokens_out) {
       const int step = ctrl[C_STEP];
-      if (step >= 0 && step < a.max_steps) a.tokens_out[step] = token;
+      if (step >= 0 && step < max_steps) tokens_out[step] = token;
     }
     ctrl[C_TOKEN] = token;
-    if (a.advance) {
+    if (advance) {
       ctrl[C_POS] += 1;
       ctrl[C_STEP] += 1;
     }
-    *a.ticket = 0;
   }
+}
+
+void launch_argmax_merge(const float* pval, const int* pidx, int n, int* ctrl, int* tokens_out, int advance,
+                         int max_steps, hipStream_t st) {
+  hipLaunchKernelGGL(argmax_merge_kernel, dim3(1), dim3(1024), 0, st, pval, pidx, n, ctrl, tokens_out, advance,
+                     max_steps);
 }
 
 size_t gemv_smem_bytes(int fmt, int cps, int waves) {
@@ -381,6 +453,8 @@ bool launch_gemv(int fmt, int pro, int waves, dim3 grid, const GemvArgs& a, hipS
   GEMV_W(WF_Q4, PRO_COPY)
   GEMV_W(WF_Q4, PRO_RMS)
   GEMV_W(WF_Q4, PRO_SWIGLU)
+  GEMV_W(WF_Q4, PRO_ATTN)
+  GEMV_W(WF_F16, PRO_ATTN)
   GEMV_W(WF_F16, PRO_COPY)
   GEMV_W(WF_F16, PRO_RMS)
   GEMV_W(WF_F16, PRO_SWIGLU)
@@ -437,60 +511,168 @@ __device__ __forceinline__ void kv_load8<float>(const float* p, float* o) {
   o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
 }
 
-size_t attn_smem_bytes(int G, int D) {
-  const int HD = D / 2, NS = 256 / HD;
-  const size_t q = (size_t)G * D, kvn = 2 * (size_t)D, p = (size_t)G * 256 + D;
-  const size_t red = (size_t)NS * G * D;
-  return sizeof(float) * (q + kvn + p + red + 64);
+// Lanes per position in the score pass: each lane keeps at most 128 bytes of
+// a K row in registers.  Rows of more than 64 bytes are split over at least two
+// lanes, which also keeps the q reads lane-varying (one lane per position made
+// them wave-uniform and the compiler promoted all of them to scalar registers).
+int attn_lpp(int D, bool kv_f32) {
+  const int bytes = (D <= 32 ? 32 : D) * (kv_f32 ? 4 : 2);
+  return bytes <= 64 ? 1 : bytes <= 256 ? 2 : 4;
 }
 
-// One block = one KV head x one chunk of positions (split-K over the
-// sequence).  It forms q (and, for the chunk holding `pos`, the new k/v) from
-// the QKV partial sums + bias, applies RoPE (TSLAttention.ts:168-250), appends
-// k/v to the cache (:252-286), computes scores and an online softmax over
-// sub-tiles of 256 positions for all G query heads of its KV head (GQA), and
-// writes (m, l, acc).  The last block of a head merges the chunks.
-template <typename KT, int GMAX>
+// Compiled head dimension of attn_kernel: 64 and 128 exactly, 32 covers any
+// even head_dim <= 32 through runtime bounds.
+static int attn_dt(int D) { return D <= 32 ? 32 : D; }
+
+// Bytes of the V tile a block stages per pass (256 / lpp positions).
+static constexpr int kVTileBytes = 32768;
+
+// LDS of attn_kernel: q, new k/v, per-wave probabilities, a region shared by
+// the V tile (during the passes), the RoPE scratch and the P.V reduction (after
+// them), and per-wave softmax statistics.
+size_t attn_smem_bytes(int gmax, int D, int lpp) {
+  const int HD = D / 2, NSW = 64 / HD, PW = 64 / lpp;
+  const size_t red = std::max({(size_t)4 * NSW * gmax * D, (size_t)gmax * D + D, (size_t)kVTileBytes / 4});
+  return sizeof(float) * ((size_t)gmax * D + 2 * D + 4 * (size_t)gmax * PW + red + 8 * gmax);
+}
+
+// Global loads of one attention pass, held in registers: this lane's K-row
+// slice and its share of the coalesced V tile.  All loads are unconditional
+// (rows clamped to t1 - 1), so a pass costs one memory round trip.
+template <typename KT, int WPR, int VCH, bool GEN, int DLM>
+struct AttnLoads {
+  static constexpr int ESZ = sizeof(KT);
+  uint32_t kw[WPR];
+  uint4 vst[VCH];
+
+  __device__ __forceinline__ void issue(const KT* kh, const KT* vh, int tb, int t1, int prow, int qpart, int D,
+                                        int DL, int tid) {
+    const int t = min(tb + prow, t1 - 1);
+    if (!GEN) {
+      const uint4* krow = reinterpret_cast<const uint4*>(kh + (size_t)t * D + qpart * DL);
+#pragma unroll
+      for (int j = 0; j < WPR / 4; j++) {
+        const uint4 q = krow[j];
+        kw[4 * j] = q.x;
+        kw[4 * j + 1] = q.y;
+        kw[4 * j + 2] = q.z;
+        kw[4 * j + 3] = q.w;
+      }
+    } else {
+      const KT* kr = kh + (size_t)t * D + qpart * DL;
+#pragma unroll
+      for (int e = 0; e < DLM; e++) {
+        const uint32_t v = ESZ == 2 ? (uint32_t)((const uint16_t*)kr)[min(e, DL - 1)]
+                                    : ((const uint32_t*)kr)[min(e, DL - 1)];
+        if (ESZ == 2) {
+          if (e & 1) kw[e >> 1] |= v << 16; else kw[e >> 1] = v;
+        } else {
+          kw[e] = v;
+        }
+      }
+    }
+    const int row_bytes = D * ESZ;
+#pragma unroll
+    for (int j = 0; j < VCH; j++) {
+      const int off = (j * 256 + tid) * 16;
+      const int r = min(tb + off / row_bytes, t1 - 1);
+      vst[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(vh + (size_t)r * D) + off % row_bytes);
+    }
+  }
+
+  // registers -> LDS V tile, then the fresh row (not in the cache yet) from vn
+  __device__ __forceinline__ void stage_v(KT* vt, const float* vn, int tb, bool own, int pos, int D, int SUB, int tid) {
+#pragma unroll
+    for (int j = 0; j < VCH; j++) reinterpret_cast<uint4*>(vt)[j * 256 + tid] = vst[j];
+    __syncthreads();
+    if (own && pos >= tb && pos < tb + SUB)
+      for (int d = tid; d < D; d += 256) vt[(size_t)(pos - tb) * D + d] = kv_store<KT>(vn[d]);
+    __syncthreads();
+  }
+
+  __device__ __forceinline__ float kelem(int e) const {
+    if (ESZ == 2) return h2f((kw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+    return __uint_as_float(kw[e]);
+  }
+};
+
+// One block = one KV head x one chunk of positions (split-K over the sequence,
+// flash-decoding).  Each block:
+//   * issues its K-row and V loads for the first pass before anything else
+//     (unconditional loads with clamped rows: one memory round trip),
+//   * forms q (and, in the chunk holding `pos`, the new k/v) from the QKV
+//     partial sums + bias, applies RoPE (TSLAttention.ts:168-250) and appends
+//     k/v to the cache (:252-286),
+//   * scores its positions for all G query heads sharing the KV head (GQA)
+//     with a per-wave online softmax (wave shuffles only) and accumulates P.V
+//     per wave,
+//   * merges its waves and writes (max, sum, unnormalised output) per query
+//     head for the combine (attn_combine_elem).
+template <typename KT, int GMAX, int DT>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   extern __shared__ float sm[];
-  __shared__ int is_last;
-  const int h = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
-  const int D = a.D, G = a.G;
+  constexpr int ESZ = sizeof(KT);
+  constexpr int LPP = DT * ESZ <= 64 ? 1 : DT * ESZ <= 256 ? 2 : 4;  // as attn_lpp
+  constexpr bool GEN = DT == 32;  // runtime head_dim <= 32
+  constexpr int SUB = 256 / LPP;  // positions per pass
+  constexpr int PW = 64 / LPP;    // positions per wave per pass
+  constexpr int DLM = DT / LPP;   // K elements per lane (compiled bound)
+  constexpr int WPR = DLM * ESZ / 4;  // 32-bit words of K per lane
+  const int h = blockIdx.x, c = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int D = GEN ? a.D : DT, G = a.G;
   const int pos = a.ctrl[C_POS];
   if (pos < 0 || pos >= a.max_tokens) return;
-  const int first = a.window > 0 ? max(0, pos - a.window + 1) : 0;
-  const int n = pos - first + 1;
-  const int chunk = max(a.chmin, (n + a.nsplit - 1) / a.nsplit);
-  const int nact = (n + chunk - 1) / chunk;
-  if (c >= nact) return;
-  const int t0 = first + c * chunk, t1 = min(t0 + chunk, pos + 1);
+  const ChunkPlan cp = chunk_plan(pos, a.window, a.nsplit, a.chmin);
+  if (c >= cp.nact) return;
+  const int t0 = cp.first + c * cp.chunk, t1 = min(t0 + cp.chunk, pos + 1);
   const bool own = pos >= t0 && pos < t1;
-  const int HD = D / 2, NS = 256 / HD;
+  const int DL = D / LPP;
+  const int HD = D / 2, NSW = 64 / HD;
+  const int dp = lane % HD, slot = min(lane / HD, NSW - 1);  // PV role (lanes past NSW*HD duplicate slot NSW-1)
+  const bool pv_lane = lane < NSW * HD;
+  const int pl = lane / LPP, qpart = lane % LPP;
   float* q_l = sm;
-  float* kn = q_l + G * D;
+  float* kn = q_l + GMAX * D;
   float* vn = kn + D;
-  float* p_l = vn + D;
-  float* red = p_l + G * 256 + D;
-  float* bscr = red + NS * G * D;
-  const int QS = a.Hq * D, KS = a.Hkv * D;
+  float* p_l = vn + D;                                         // [4][GMAX][PW]
+  float* red = p_l + 4 * GMAX * PW;                            // [4][NSW][GMAX][D], or the V tile
+  KT* vt = reinterpret_cast<KT*>(red);                         // [SUB][D] during the passes
+  float* ml_l = red + max(max(4 * NSW * GMAX * D, GMAX * D + D), kVTileBytes / 4);  // [4][GMAX][2]
+  constexpr int VCH = kVTileBytes / 16 / 256;                  // 16-byte V chunks per thread
+  const KT* kh = reinterpret_cast<const KT*>(a.kc) + (size_t)h * a.max_tokens * D;
+  const KT* vh = reinterpret_cast<const KT*>(a.vc) + (size_t)h * a.max_tokens * D;
 
-  // 1. q, new k, new v = sum of partials + bias
-  for (int i = tid; i < G * D; i += 256) {
-    const int col = h * G * D + i;
-    float v = a.bias ? a.bias[col] : 0.f;
-    for (int j = 0; j < a.n_src; j++) v += a.src[(size_t)j * a.src_stride + col];
-    q_l[i] = v;
-  }
-  if (own)
-    for (int i = tid; i < 2 * D; i += 256) {
-      const int col = i < D ? QS + h * D + i : QS + KS + h * D + (i - D);
-      float v = a.bias ? a.bias[col] : 0.f;
-      for (int j = 0; j < a.n_src; j++) v += a.src[(size_t)j * a.src_stride + col];
-      (i < D ? kn[i] : vn[i - D]) = v;
+  AttnLoads<KT, WPR, VCH, GEN, DLM> ld;
+  ld.issue(kh, vh, t0, t1, wave * PW + pl, qpart, D, DL, tid);
+
+  // q, new k, new v = sum of partials + bias (loads in flight with the K/V above)
+  {
+    const int nq = G * D, ntot = nq + (own ? 2 * D : 0);
+    const int QS = a.Hq * D, KS = a.Hkv * D;
+    for (int ib = 0; ib < ntot; ib += kEpt * 256) {
+      float v[kEpt];
+#pragma unroll
+      for (int e = 0; e < kEpt; e++) {
+        const int i = min(ib + tid + e * 256, ntot - 1);
+        const int col = i < nq ? h * G * D + i : (i - nq < D ? QS + h * D + (i - nq) : QS + KS + h * D + (i - nq - D));
+        v[e] = (a.bias ? a.bias[col] : 0.f) + sum_parts(a.src, a.n_src, a.src_stride, col);
+      }
+#pragma unroll
+      for (int e = 0; e < kEpt; e++) {
+        const int i = ib + tid + e * 256;
+        if (i < nq)
+          q_l[i] = v[e];
+        else if (i < ntot)
+          (i - nq < D ? kn[i - nq] : vn[i - nq - D]) = v[e];
+      }
     }
+    // rows G..GMAX-1 stay zero: the score and P.V loops run over GMAX heads without guards
+    for (int i = nq + tid; i < GMAX * D; i += 256) q_l[i] = 0.f;
+  }
   __syncthreads();
 
-  // 2. RoPE (rotate-half) on q and the new k; cos/sin already carry the attention factor
+  // RoPE (rotate-half) on q and the new k; the tables carry the attention factor
   if (a.rd > 0) {
     const int half = a.rd / 2;
     const float* cs = a.rope_cos + (size_t)pos * half;
@@ -505,196 +687,184 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         const float partner = d < half ? -v[d + half] : v[d - half];
         r = v[d] * cs[j] + partner * sn[j];
       }
-      p_l[i] = r;
+      red[i] = r;
     }
     __syncthreads();
     for (int i = tid; i < nrot; i += 256) {
       if (i < G * D)
-        q_l[i] = p_l[i];
+        q_l[i] = red[i];
       else
-        kn[i - G * D] = p_l[i];
+        kn[i - G * D] = red[i];
     }
     __syncthreads();
   }
-
-  KT* kh = reinterpret_cast<KT*>(a.kc) + (size_t)h * a.max_tokens * D;
-  KT* vh = reinterpret_cast<KT*>(a.vc) + (size_t)h * a.max_tokens * D;
-  // 3. KV append at pos (the cache keeps the rounded value; so does this block)
+  // KV append at pos; this block keeps the rounded values the cache will hold
   if (own) {
+    KT* kc = reinterpret_cast<KT*>(a.kc) + (size_t)h * a.max_tokens * D;
+    KT* vc = reinterpret_cast<KT*>(a.vc) + (size_t)h * a.max_tokens * D;
     for (int i = tid; i < D; i += 256) {
       const KT kq = kv_store<KT>(kn[i]), vq = kv_store<KT>(vn[i]);
-      kh[(size_t)pos * D + i] = kq;
-      vh[(size_t)pos * D + i] = vq;
+      kc[(size_t)pos * D + i] = kq;
+      vc[(size_t)pos * D + i] = vq;
       kn[i] = kv_load<KT>(&kq);
       vn[i] = kv_load<KT>(&vq);
     }
     __syncthreads();
   }
 
-  // 4. scores + online softmax + PV over sub-tiles of 256 positions
-  float m_run[GMAX], l_run[GMAX], acc0[GMAX], acc1[GMAX];
+  float m_w[GMAX], l_w[GMAX], acc0[GMAX], acc1[GMAX];
 #pragma unroll
   for (int g = 0; g < GMAX; g++) {
-    m_run[g] = -INFINITY;
-    l_run[g] = 0.f;
+    m_w[g] = -INFINITY;
+    l_w[g] = 0.f;
     acc0[g] = 0.f;
     acc1[g] = 0.f;
   }
-  const int dp = tid % HD, ts = tid / HD;
-  for (int tb = t0; tb < t1; tb += 256) {
-    const int T = min(256, t1 - tb);
-    float sc[GMAX];
+  for (int tb = t0; tb < t1; tb += SUB) {
+    if (tb != t0) ld.issue(kh, vh, tb, t1, wave * PW + pl, qpart, D, DL, tid);
+    ld.stage_v(vt, vn, tb, own, pos, D, SUB, tid);
+    // scores of this lane's position (partial dot over its K slice)
+    const int t = tb + wave * PW + pl;
+    const bool valid = t < t1;
+    if (own && t == pos) {  // the fresh row is not in the cache yet: take it from LDS
 #pragma unroll
-    for (int g = 0; g < GMAX; g++) sc[g] = -INFINITY;
-    if (tid < T) {
-      const int t = tb + tid;
-#pragma unroll
-      for (int g = 0; g < GMAX; g++) sc[g] = 0.f;
-      if (own && t == pos) {
-        for (int d = 0; d < D; d++) {
-          const float kd = kn[d];
-#pragma unroll
-          for (int g = 0; g < GMAX; g++)
-            if (g < G) sc[g] = fmaf(q_l[g * D + d], kd, sc[g]);
-        }
-      } else if ((D & 7) == 0) {
-        const KT* row = kh + (size_t)t * D;
-        for (int d = 0; d < D; d += 8) {
-          float k8[8];
-          kv_load8<KT>(row + d, k8);
-#pragma unroll
-          for (int g = 0; g < GMAX; g++)
-            if (g < G) {
-              const float* q = q_l + g * D + d;
-#pragma unroll
-              for (int e = 0; e < 8; e++) sc[g] = fmaf(q[e], k8[e], sc[g]);
-            }
-        }
-      } else {
-        const KT* row = kh + (size_t)t * D;
-        for (int d = 0; d < D; d++) {
-          const float kd = kv_load<KT>(row + d);
-#pragma unroll
-          for (int g = 0; g < GMAX; g++)
-            if (g < G) sc[g] = fmaf(q_l[g * D + d], kd, sc[g]);
+      for (int e = 0; e < DLM; e++) {
+        const uint32_t b = ESZ == 2 ? (uint32_t)__half_as_ushort(__float2half_rn(kn[qpart * DL + min(e, DL - 1)]))
+                                    : __float_as_uint(kn[qpart * DL + min(e, DL - 1)]);
+        if (ESZ == 2) {
+          if (e & 1) ld.kw[e >> 1] = (ld.kw[e >> 1] & 0xFFFFu) | (b << 16); else ld.kw[e >> 1] = (ld.kw[e >> 1] & 0xFFFF0000u) | b;
+        } else {
+          ld.kw[e] = b;
         }
       }
-#pragma unroll
-      for (int g = 0; g < GMAX; g++) sc[g] *= a.scale;
     }
-    float corr[GMAX];
+    float s[GMAX];
+#pragma unroll
+    for (int g = 0; g < GMAX; g++) s[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < DLM; e++) {
+      if (!GEN || e < DL) {
+        const float kd = ld.kelem(e);
+        const float* qd = q_l + qpart * DL + e;
+#pragma unroll
+        for (int g = 0; g < GMAX; g++) s[g] = fmaf(qd[g * D], kd, s[g]);
+      }
+      // keep the scheduler from hoisting every q read of the unrolled loop
+      // (register pressure): one block of 8 K elements at a time
+      if ((e & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int g = 0; g < GMAX; g++) {
-      corr[g] = 1.f;
-      if (g < G) {
-        const float mt = block_max(sc[g], bscr);
-        const float mn = fmaxf(m_run[g], mt);
-        const float p = tid < T ? __expf(sc[g] - mn) : 0.f;
-        p_l[g * 256 + tid] = p;
-        const float lt = block_sum(p, bscr);
-        corr[g] = __expf(m_run[g] - mn);
-        l_run[g] = l_run[g] * corr[g] + lt;
-        m_run[g] = mn;
+      if (LPP > 1) s[g] += __shfl_xor(s[g], 1, 64);
+      if (LPP > 2) s[g] += __shfl_xor(s[g], 2, 64);
+      s[g] = valid ? s[g] * a.scale : -INFINITY;
+    }
+    // per-wave online softmax
+#pragma unroll
+    for (int g = 0; g < GMAX; g++) {
+      float p = 0.f;
+      if (g < G) {  // wave-uniform, once per head
+        const float mt = wave_max(s[g]);
+        const float mn = fmaxf(m_w[g], mt);
+        p = (valid && mn != -INFINITY) ? __expf(s[g] - mn) : 0.f;
+        const float lt = wave_sum(qpart == 0 ? p : 0.f);
+        const float corr = m_w[g] == -INFINITY ? 0.f : __expf(m_w[g] - mn);
+        l_w[g] = l_w[g] * corr + lt;
+        acc0[g] *= corr;
+        acc1[g] *= corr;
+        m_w[g] = mn;
       }
+      if (qpart == 0) p_l[(wave * GMAX + g) * PW + pl] = p;
     }
     __syncthreads();
-    if (ts < NS) {
+    // P.V over this wave's positions; lane = (d pair, slot)
+    if (pv_lane) {
+      for (int pw = slot; pw < PW; pw += NSW) {
+        const int r = wave * PW + pw;  // row of the V tile
+        if (tb + r >= t1) break;
+        const float v0 = kv_load<KT>(vt + (size_t)r * D + 2 * dp);
+        const float v1 = kv_load<KT>(vt + (size_t)r * D + 2 * dp + 1);
+        const float* pp = p_l + wave * GMAX * PW + pw;
 #pragma unroll
-      for (int g = 0; g < GMAX; g++) {
-        acc0[g] *= corr[g];
-        acc1[g] *= corr[g];
-      }
-      for (int tt = ts; tt < T; tt += NS) {
-        const int t = tb + tt;
-        float v0, v1;
-        if (own && t == pos) {
-          v0 = vn[2 * dp];
-          v1 = vn[2 * dp + 1];
-        } else {
-          v0 = kv_load<KT>(vh + (size_t)t * D + 2 * dp);
-          v1 = kv_load<KT>(vh + (size_t)t * D + 2 * dp + 1);
+        for (int g = 0; g < GMAX; g++) {
+          acc0[g] = fmaf(pp[g * PW], v0, acc0[g]);
+          acc1[g] = fmaf(pp[g * PW], v1, acc1[g]);
         }
-#pragma unroll
-        for (int g = 0; g < GMAX; g++)
-          if (g < G) {
-            const float p = p_l[g * 256 + tt];
-            acc0[g] = fmaf(p, v0, acc0[g]);
-            acc1[g] = fmaf(p, v1, acc1[g]);
-          }
       }
     }
     __syncthreads();
   }
 
-  // 5. reduce the PV slots, write the chunk result
-  if (ts < NS) {
+  // merge waves and slots of the block; write the chunk partial
+  if (pv_lane) {
 #pragma unroll
-    for (int g = 0; g < GMAX; g++)
-      if (g < G) {
-        red[(ts * G + g) * D + 2 * dp] = acc0[g];
-        red[(ts * G + g) * D + 2 * dp + 1] = acc1[g];
-      }
+    for (int g = 0; g < GMAX; g++) {
+      red[((wave * NSW + slot) * GMAX + g) * D + 2 * dp] = acc0[g];
+      red[((wave * NSW + slot) * GMAX + g) * D + 2 * dp + 1] = acc1[g];
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < GMAX; g++) {
+      ml_l[(wave * GMAX + g) * 2] = m_w[g];
+      ml_l[(wave * GMAX + g) * 2 + 1] = l_w[g];
+    }
   }
   __syncthreads();
   for (int i = tid; i < G * D; i += 256) {
     const int g = i / D, d = i % D;
-    float o = 0.f;
-    for (int s2 = 0; s2 < NS; s2++) o += red[(s2 * G + g) * D + d];
-    float l = 0.f;
-#pragma unroll
-    for (int gg = 0; gg < GMAX; gg++)
-      if (gg == g) l = l_run[gg];
-    const int row = h * G + g;
-    if (nact == 1)
-      a.out[(size_t)row * D + d] = o / l;
-    else
-      a.pacc[((size_t)row * a.nsplit + c) * D + d] = o;
-  }
-  if (nact == 1) return;
-#pragma unroll
-  for (int g = 0; g < GMAX; g++)
-    if (g < G && tid == g) {
-      a.pml[((size_t)(h * G + g) * a.nsplit + c) * 2] = m_run[g];
-      a.pml[((size_t)(h * G + g) * a.nsplit + c) * 2 + 1] = l_run[g];
-    }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) is_last = atomicAdd(&a.ticket[h], 1) == nact - 1;
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  // 6. merge chunks (flash-decoding combine)
-  for (int i = tid; i < G * D; i += 256) {
-    const int g = i / D, d = i % D, row = h * G + g;
-    const float* ml = a.pml + (size_t)row * a.nsplit * 2;
     float M = -INFINITY;
-    for (int j = 0; j < nact; j++) M = fmaxf(M, ml[2 * j]);
-    float Lsum = 0.f, O = 0.f;
-    for (int j = 0; j < nact; j++) {
-      const float e = __expf(ml[2 * j] - M);
-      Lsum = fmaf(ml[2 * j + 1], e, Lsum);
-      O = fmaf(a.pacc[((size_t)row * a.nsplit + j) * D + d], e, O);
+    for (int w = 0; w < 4; w++) M = fmaxf(M, ml_l[(w * GMAX + g) * 2]);
+    float L = 0.f, O = 0.f;
+    for (int w = 0; w < 4; w++) {
+      const float mw = ml_l[(w * GMAX + g) * 2];
+      const float e = mw == -INFINITY ? 0.f : __expf(mw - M);
+      L = fmaf(ml_l[(w * GMAX + g) * 2 + 1], e, L);
+      float o = 0.f;
+      for (int sl = 0; sl < NSW; sl++) o += red[((w * NSW + sl) * GMAX + g) * D + d];
+      O = fmaf(o, e, O);
     }
-    a.out[(size_t)row * D + d] = O / Lsum;
+    const int row = h * G + g;
+    a.pacc[((size_t)row * a.nsplit + c) * D + d] = O;
+    if (d == 0) {
+      a.pml[((size_t)row * a.nsplit + c) * 2] = M;
+      a.pml[((size_t)row * a.nsplit + c) * 2 + 1] = L;
+    }
   }
-  if (tid == 0) a.ticket[h] = 0;
 }
 
-bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, hipStream_t st) {
+// Combine of the chunk partials into the attention output (op-level path; the
+// decode graph folds this into the O projection's prologue instead).
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+  const int row = blockIdx.x;
+  const int pos = a.ctrl[C_POS];
+  if (pos < 0 || pos >= a.max_tokens) return;
+  const ChunkPlan cp = chunk_plan(pos, a.window, a.nsplit, a.chmin);
+  for (int d = threadIdx.x; d < a.D; d += blockDim.x)
+    a.out[(size_t)row * a.D + d] = attn_combine_elem(a.pacc, a.pml, row, d, a.D, a.nsplit, cp.nact);
+}
+
+bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, bool combine, hipStream_t st) {
   const dim3 grid(a.Hkv, a.nsplit);
-  const size_t smem = attn_smem_bytes(a.G, a.D);
-#define ATT_CASE(KT, GM)                                                            \
-  if (gmax == GM) {                                                                 \
-    hipLaunchKernelGGL((attn_kernel<KT, GM>), grid, dim3(256), smem, st, a);        \
-    return true;                                                                    \
+  const size_t smem = attn_smem_bytes(gmax, a.D, a.lpp);
+  const int dt = attn_dt(a.D);
+  if (dt != 32 && dt != 64 && dt != 128) return false;
+  bool ok = false;
+#define ATT_CASE(KT, GM, DTV)                                                         \
+  if (!ok && gmax == GM && dt == DTV) {                                               \
+    hipLaunchKernelGGL((attn_kernel<KT, GM, DTV>), grid, dim3(256), smem, st, a);     \
+    ok = true;                                                                        \
   }
+#define ATT_G(KT, DTV) ATT_CASE(KT, 1, DTV) ATT_CASE(KT, 2, DTV) ATT_CASE(KT, 4, DTV) ATT_CASE(KT, 8, DTV) ATT_CASE(KT, 16, DTV)
   if (kv_f32) {
-    ATT_CASE(float, 1) ATT_CASE(float, 2) ATT_CASE(float, 4) ATT_CASE(float, 8) ATT_CASE(float, 16)
+    ATT_G(float, 32) ATT_G(float, 64) ATT_G(float, 128)
   } else {
-    ATT_CASE(uint16_t, 1) ATT_CASE(uint16_t, 2) ATT_CASE(uint16_t, 4) ATT_CASE(uint16_t, 8) ATT_CASE(uint16_t, 16)
+    ATT_G(uint16_t, 32) ATT_G(uint16_t, 64) ATT_G(uint16_t, 128)
   }
+#undef ATT_G
 #undef ATT_CASE
-  return false;
+  if (ok && combine) hipLaunchKernelGGL(attn_combine_kernel, dim3(a.Hq), dim3(128), 0, st, a);
+  return ok;
 }
 
 // --------------------------------------------------------- small kernels --
@@ -703,17 +873,20 @@ bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, hipStream_t st) 
 __global__ __launch_bounds__(1024) void final_norm_kernel(const float* base, const float* pin, int n_pin,
                                                           int pin_stride, const float* w, int n, float eps, float* y) {
   __shared__ float scratch[16];
+  // n <= 4 * blockDim.x: every element is loaded in one round trip and kept in registers
+  float v[kEpt];
   float ss = 0.f;
-  for (int k = threadIdx.x; k < n; k += blockDim.x) {
-    float v = base[k];
-    for (int j = 0; j < n_pin; j++) v += pin[(size_t)j * pin_stride + k];
-    ss = fmaf(v, v, ss);
+#pragma unroll
+  for (int e = 0; e < kEpt; e++) {
+    const int k = threadIdx.x + e * blockDim.x;
+    v[e] = k < n ? base[k] + sum_parts(pin, n_pin, pin_stride, k) : 0.f;
+    ss = fmaf(v[e], v[e], ss);
   }
   const float inv = rsqrtf(block_sum(ss, scratch) / (float)n + eps);
-  for (int k = threadIdx.x; k < n; k += blockDim.x) {
-    float v = base[k];
-    for (int j = 0; j < n_pin; j++) v += pin[(size_t)j * pin_stride + k];
-    y[k] = v * inv * w[k];
+#pragma unroll
+  for (int e = 0; e < kEpt; e++) {
+    const int k = threadIdx.x + e * blockDim.x;
+    if (k < n) y[k] = v[e] * inv * w[k];
   }
 }
 
@@ -759,12 +932,10 @@ void launch_reduce(const float* part, int n_part, int stride, const float* bias,
   hipLaunchKernelGGL(reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, st, part, n_part, stride, bias, n, y);
 }
 
-// Greedy argmax of an fp32 vector: block partials + last-block merge.
-__global__ __launch_bounds__(256) void argmax_kernel(const float* logits, int n, float* pval, int* pidx, int* ticket,
-                                                     int* token) {
+// Greedy argmax of an fp32 vector: block partials, then argmax_merge_kernel.
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* logits, int n, float* pval, int* pidx) {
   __shared__ float sv[4];
   __shared__ int si[4];
-  __shared__ int is_last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float bv = kLowest;
   int bi = 0x7fffffff;
@@ -773,48 +944,26 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* logits, int n,
       bv = logits[i];
       bi = i;
     }
-  for (int pass = 0; pass < 2; pass++) {
-    wave_argmax(bv, bi);
-    if (lane == 0) {
-      sv[wave] = bv;
-      si[wave] = bi;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0)
-      for (int w = 1; w < 4; w++)
-        if (better(sv[w], si[w], bv, bi)) {
-          bv = sv[w];
-          bi = si[w];
-        }
-    if (pass == 1) break;
-    if (threadIdx.x == 0) {
-      pval[blockIdx.x] = bv;
-      pidx[blockIdx.x] = bi;
-    }
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) is_last = atomicAdd(ticket, 1) == (int)gridDim.x - 1;
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    bv = kLowest;
-    bi = 0x7fffffff;
-    for (int i = threadIdx.x; i < (int)gridDim.x; i += blockDim.x)
-      if (better(pval[i], pidx[i], bv, bi)) {
-        bv = pval[i];
-        bi = pidx[i];
-      }
-    __syncthreads();
+  wave_argmax(bv, bi);
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
   }
+  __syncthreads();
   if (threadIdx.x == 0) {
-    *token = bv > kLowest ? bi : 0;
-    *ticket = 0;
+    for (int w = 1; w < 4; w++)
+      if (better(sv[w], si[w], bv, bi)) {
+        bv = sv[w];
+        bi = si[w];
+      }
+    pval[blockIdx.x] = bv;
+    pidx[blockIdx.x] = bi;
   }
 }
 
-void launch_argmax(const float* logits, int n, float* pval, int* pidx, int* ticket, int* token, int blocks,
-                   hipStream_t st) {
-  hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(256), 0, st, logits, n, pval, pidx, ticket, token);
+void launch_argmax(const float* logits, int n, float* pval, int* pidx, int* token, int blocks, hipStream_t st) {
+  hipLaunchKernelGGL(argmax_partial_kernel, dim3(blocks), dim3(256), 0, st, logits, n, pval, pidx);
+  launch_argmax_merge(pval, pidx, blocks, token, nullptr, 0, 0, st);
 }
 
 __global__ void set_ctrl_kernel(int* ctrl, int token, int pos, int step, int base, int len) {
