@@ -107,6 +107,7 @@ struct tlm_model {
   int* tokens_out = nullptr;
   int* prompt = nullptr;
   float *xa = nullptr, *xb = nullptr, *xf = nullptr, *attn_out = nullptr;
+  float* x0 = nullptr;  // embedding row of the current token (staged by the control kernels)
   float *pq = nullptr, *po = nullptr, *pgu = nullptr, *pd = nullptr;
   float* logits = nullptr;
   float* arg_val = nullptr;
@@ -155,6 +156,12 @@ static GemvPlan plan_gemv(int T, int C, int cus, int CK, bool single_split) {
   p.gx = T;
   if (p.waves > cps) p.waves = cps >= 8 ? 8 : cps >= 4 ? 4 : cps >= 2 ? 2 : 1;
   return p;
+}
+
+// A GEMV whose prologue RMS-normalises the whole input row keeps 8 elements
+// of it per thread: K <= 512 * waves.
+static void rms_waves(tlm_linear* L) {
+  while (L->plan.waves < 8 && L->K > 512 * L->plan.waves) L->plan.waves *= 2;
 }
 
 // Host repack of canonical rows [r0, r0 + rows) into the device tile layout.
@@ -471,7 +478,7 @@ static int attn_init(tlm_ctx* ctx, const tlm_attn_desc* d, tlm_attn* A, bool own
   A->gmax = A->G <= 1 ? 1 : A->G <= 2 ? 2 : A->G <= 4 ? 4 : A->G <= 8 ? 8 : 16;
   A->scale = (float)(d->attn_scale > 0 ? d->attn_scale : 1.0 / sqrt((double)d->head_dim));
   A->lpp = attn_lpp(d->head_dim, d->kv_fmt == TLM_FMT_F32);
-  if (attn_smem_bytes(A->gmax, d->head_dim, A->lpp) > 65536)
+  if (attn_smem_bytes(A->gmax, d->head_dim, d->kv_fmt == TLM_FMT_F32) > 65536)
     return fail(TLM_ERR_INVALID, "TLMAttention: %d heads per kv head x head_dim %d exceed the LDS budget", A->G,
                 d->head_dim);
   A->chmin = 32;
@@ -570,7 +577,7 @@ int tlm_op_attention(tlm_attn* A, const float* qkv, int position, float* out) {
   if (position < 0 || position >= A->d.max_tokens)
     return fail(TLM_ERR_RANGE, "TLMAttention: position %d outside [0, %d)", position, A->d.max_tokens);
   hipStream_t st = A->ctx->stream;
-  launch_set_ctrl(A->ctrl, 0, position, 0, 0, 0, st);
+  launch_set_ctrl(A->ctrl, 0, position, 0, 0, 0, EmbStage{}, st);
   const int total = (A->d.heads + 2 * A->d.kv_heads) * A->d.head_dim;
   AttnArgs a = attn_args(A, qkv, 1, total, nullptr, A->ctrl, A->kc, A->vc, out);
   if (!launch_attention(A->d.kv_fmt == TLM_FMT_F32, A->gmax, a, true, st))
@@ -652,7 +659,7 @@ int tlm_op_logits(tlm_linear* head, const float* x, float* logits, int32_t* toke
   if (!launch_lm_head(wfmt(head->fmt), p.waves, dim3(p.gx), a, ctx->stream))
     return fail(TLM_ERR_STATE, "TLMLogits: no kernel variant for this shape");
   // the sampled token lands in token[0] (the merge's ctrl[C_TOKEN])
-  launch_argmax_merge(ctx->arg_val, ctx->arg_idx, p.gx, token, nullptr, 0, 0, ctx->stream);
+  launch_argmax_merge(ctx->arg_val, ctx->arg_idx, p.gx, token, nullptr, 0, 0, EmbStage{}, ctx->stream);
   CHECK_LAUNCH("TLMLogits");
   return TLM_OK;
 }
@@ -691,6 +698,8 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
     return fail(TLM_ERR_INVALID, "TLMModel: a tied head needs an fp16 embedding table");
   if (!d->tied && d->head_fmt != TLM_FMT_F16 && d->head_fmt != TLM_FMT_Q4)
     return fail(TLM_ERR_INVALID, "TLMModel: head_fmt must be fp16 or q4");
+  if (d->hidden_size % 4 != 0)
+    return fail(TLM_ERR_INVALID, "TLMModel: hidden_size %d must be a multiple of 4", d->hidden_size);
   tlm_model* m = new tlm_model();
   m->ctx = ctx;
   m->d = *d;
@@ -722,6 +731,10 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
     M_TRY(linear_alloc(ctx, lf, H, m->QS, false, &L.o));
     M_TRY(linear_alloc(ctx, lf, 2 * I, H, false, &L.gu));
     M_TRY(linear_alloc(ctx, lf, H, I, false, &L.down));
+    if (rc == TLM_OK) {
+      rms_waves(L.qkv);
+      rms_waves(L.gu);
+    }
     M_TRY(model_alloc((void**)&L.attn_norm, sizeof(float) * H));
     M_TRY(model_alloc((void**)&L.ffn_norm, sizeof(float) * H));
     if (d->qkv_bias) M_TRY(model_alloc((void**)&L.bqkv, sizeof(float) * m->Nqkv));
@@ -735,6 +748,7 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
   M_TRY(model_alloc((void**)&m->tokens_out, sizeof(int) * d->max_tokens));
   M_TRY(model_alloc((void**)&m->prompt, sizeof(int) * d->max_tokens));
   M_TRY(model_alloc((void**)&m->xa, sizeof(float) * H));
+  M_TRY(model_alloc((void**)&m->x0, sizeof(float) * H));
   M_TRY(model_alloc((void**)&m->xb, sizeof(float) * H));
   M_TRY(model_alloc((void**)&m->xf, sizeof(float) * H));
   M_TRY(model_alloc((void**)&m->attn_out, sizeof(float) * m->QS));
@@ -783,7 +797,7 @@ void tlm_model_destroy(tlm_model* m) {
   }
   tlm_linear_destroy(m->head);
   attn_free(&m->attn, false);
-  void* bufs[] = {m->emb, m->final_norm, m->ctrl, m->tokens_out, m->prompt, m->xa, m->xb, m->xf, m->attn_out,
+  void* bufs[] = {m->emb, m->final_norm, m->ctrl, m->tokens_out, m->prompt, m->xa, m->x0, m->xb, m->xf, m->attn_out,
                   m->pq, m->po, m->pgu, m->pd, m->logits, m->arg_val, m->arg_idx};
   for (void* p : bufs) hipFree(p);
   delete m;
@@ -856,6 +870,10 @@ int tlm_model_upload(tlm_model* m, int tensor, int layer, const void* host, size
 
 // ----------------------------------------------------- the per-token schedule
 
+static EmbStage emb_stage(const tlm_model* m) {
+  return EmbStage{m->emb, m->d.embed_fmt == TLM_FMT_F32 ? 1 : 0, m->d.hidden_size, m->x0};
+}
+
 // Kernels of one layer.  which: -1 all; otherwise a single stage (timing).
 static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which) {
   bool ok = true;
@@ -868,10 +886,10 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which) {
     GemvArgs a;
     fill_gemv_args(a, L.qkv, m->pq);
     if (l == 0) {
-      a.base = nullptr;
-      a.emb = m->emb;
-      a.emb_f32 = d.embed_fmt == TLM_FMT_F32;
+      a.base = m->x0;
+      a.pin = m->x0;  // never summed (n_pin 0), but loaded: must be a valid vector
       a.n_pin = 0;
+      a.pin_stride = H;
     } else {
       a.base = m->xb;
       a.pin = m->pd;
@@ -946,7 +964,7 @@ static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, bool final_
   a.arg_idx = m->arg_idx;
   if (!launch_lm_head(wfmt(m->head->fmt), m->lm_plan.waves, dim3(m->lm_plan.gx), a, st)) return false;
   launch_argmax_merge(m->arg_val, m->arg_idx, m->lm_plan.gx, m->ctrl, advance ? m->tokens_out : nullptr,
-                      advance ? 1 : 0, d.max_tokens, st);
+                      advance ? 1 : 0, d.max_tokens, emb_stage(m), st);
   return true;
 }
 
@@ -958,7 +976,7 @@ static int capture(tlm_model* m, bool logits, hipGraph_t* g, hipGraphExec_t* ge)
   if (logits)
     ok &= enqueue_head(m, st, true, true);
   else
-    launch_prefill_advance(m->ctrl, m->prompt, st);
+    launch_prefill_advance(m->ctrl, m->prompt, emb_stage(m), st);
   hipError_t le = hipGetLastError();
   HIP_TRY(hipStreamEndCapture(st, g));
   if (le != hipSuccess) return fail(TLM_ERR_HIP, "TLMModel: launch during capture failed: %s", hipGetErrorString(le));
@@ -996,7 +1014,7 @@ static int run_token(tlm_model* m, bool logits) {
   if (logits)
     ok &= enqueue_head(m, st, true, true);
   else
-    launch_prefill_advance(m->ctrl, m->prompt, st);
+    launch_prefill_advance(m->ctrl, m->prompt, emb_stage(m), st);
   if (!ok) return fail(TLM_ERR_STATE, "TLMModel: no kernel variant for a stage of this model");
   CHECK_LAUNCH("TLMModel");
   return TLM_OK;
@@ -1017,7 +1035,7 @@ int tlm_compute_token(tlm_model* m, int32_t token, int32_t position, int flags) 
   rc = tlm_model_finalize(m);
   if (rc) return rc;
   hipStream_t st = m->ctx->stream;
-  launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, st);
+  launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
   CHECK_LAUNCH("TLMModel");
   return run_token(m, (flags & TLM_LOGITS) != 0);
 }
@@ -1035,7 +1053,7 @@ int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end)
   hipStream_t st = m->ctx->stream;
   HIP_TRY(hipStreamSynchronize(st));
   HIP_TRY(hipMemcpy(m->prompt, tokens + start, sizeof(int32_t) * (end - start), hipMemcpyHostToDevice));
-  launch_set_ctrl(m->ctrl, tokens[start], start, 0, start, end - start, st);
+  launch_set_ctrl(m->ctrl, tokens[start], start, 0, start, end - start, emb_stage(m), st);
   CHECK_LAUNCH("TLMModel");
   for (int i = start; i < end; i++) {
     rc = run_token(m, false);
@@ -1075,7 +1093,7 @@ int tlm_decode_greedy(tlm_model* m, int32_t token, int32_t position, int n, int3
   rc = tlm_model_finalize(m);
   if (rc) return rc;
   hipStream_t st = m->ctx->stream;
-  launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, st);
+  launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
   CHECK_LAUNCH("TLMModel");
   for (int i = 0; i < n; i++) {
     rc = run_token(m, true);
@@ -1150,7 +1168,7 @@ int tlm_time_decode(tlm_model* m, int32_t token, int32_t position, int warmup, i
   rc = tlm_model_finalize(m);
   if (rc) return rc;
   hipStream_t st = m->ctx->stream;
-  launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, st);
+  launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
   for (int i = 0; i < warmup; i++) {
     rc = run_token(m, true);
     if (rc) return rc;

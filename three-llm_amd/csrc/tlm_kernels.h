@@ -7,16 +7,17 @@ namespace tlm {
 
 constexpr int kTile = 64;      // output rows per tile: one row per lane of a wave64
 constexpr int kMaxChunks = 8;  // 16-byte chunks a wave keeps in flight per batch
-constexpr int kMaxPart = 12;   // partial vectors a consumer folds in with one round trip
+constexpr int kMaxPart = 8;    // partial vectors a consumer folds in with one round trip
 
 enum WeightFmt { WF_F16 = 1, WF_Q4 = 2 };
 
 // GEMV prologues: how the input slice x[k0, k1) is formed in LDS.
 enum Prologue {
   PRO_COPY = 0,    // x = in
-  PRO_RMS = 1,     // x = rmsnorm(base + sum_j pin[j]) * w   (base: fp32 vector or embedding row)
+  PRO_RMS = 1,     // x = rmsnorm(base + sum_j pin[j]) * w
   PRO_SWIGLU = 2,  // x = silu(sum_j pin[j][k]) * (sum_j pin[j][up_off + k])
   PRO_ATTN = 3,    // x = flash-decoding combine of the attention chunk partials
+  PRO_RMS2 = 4,    // PRO_RMS for K up to 8 elements per thread (chosen by launch_gemv)
 };
 
 // Split of the attention window [first, pos] into chunks; identical on host and device.
@@ -37,6 +38,16 @@ __host__ __device__ inline ChunkPlan chunk_plan(int pos, int window, int nsplit,
 // captured graph serves every position.
 enum Ctrl { C_TOKEN = 0, C_POS = 1, C_STEP = 2, C_BASE = 3, C_LEN = 4 };
 
+// Embedding row staging: the kernels that choose the next token (set_ctrl,
+// prefill_advance, argmax_merge) also copy its embedding row to x0, the
+// residual base of layer 0.  x0 == null disables the copy.
+struct EmbStage {
+  const void* emb;  // [V][H] fp16 or fp32
+  int f32;
+  int H;
+  float* x0;
+};
+
 struct GemvArgs {
   const uint4* w;      // [T][C][64] 16-byte chunks (q4: 32 k, fp16: 8 k)
   const uint16_t* s;   // q4 scales [T][C][64] (fp16 bits)
@@ -46,9 +57,7 @@ struct GemvArgs {
   // PRO_COPY
   const float* in;
   // PRO_RMS
-  const float* base;   // fp32 [K] residual, or null to gather the embedding row
-  const void* emb;     // embedding table [V][K] when base == null
-  int emb_f32;
+  const float* base;   // fp32 [K] residual stream (layer 0: the staged embedding row)
   const int* ctrl;
   const float* pin;    // partials to add (RMS) / gate|up partials (SWIGLU)
   int n_pin, pin_stride;
@@ -101,14 +110,15 @@ void launch_reduce(const float* part, int n_part, int stride, const float* bias,
 void launch_argmax(const float* logits, int n, float* pval, int* pidx, int* token, int blocks, hipStream_t st);
 // second pass of the greedy sampler; `ctrl` receives the token at ctrl[C_TOKEN]
 void launch_argmax_merge(const float* pval, const int* pidx, int n, int* ctrl, int* tokens_out, int advance,
-                         int max_steps, hipStream_t st);
-void launch_set_ctrl(int* ctrl, int token, int pos, int step, int base, int len, hipStream_t st);
-void launch_prefill_advance(int* ctrl, const int* prompt, hipStream_t st);
+                         int max_steps, const EmbStage& es, hipStream_t st);
+void launch_set_ctrl(int* ctrl, int token, int pos, int step, int base, int len, const EmbStage& es,
+                     hipStream_t st);
+void launch_prefill_advance(int* ctrl, const int* prompt, const EmbStage& es, hipStream_t st);
 void launch_dequant(int fmt, const uint4* w, const uint16_t* s, int N, int T, int C, int K, float* out,
                     hipStream_t st);
 void launch_kv_fill(void* kc, void* vc, bool f32, size_t heads_stride, int Hkv, int max_tokens, int D, int count,
                     uint64_t seed, hipStream_t st);
-size_t attn_smem_bytes(int gmax, int D, int lpp);
+size_t attn_smem_bytes(int gmax, int D, bool kv_f32);
 int attn_lpp(int D, bool kv_f32);
 
 }  // namespace tlm

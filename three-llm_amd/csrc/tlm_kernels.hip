@@ -90,6 +90,8 @@ __device__ __forceinline__ float sum_parts(const float* p, int n, int stride, in
   return s;
 }
 
+__device__ __forceinline__ float4 f4add(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
+
 // Flash-decoding combine of one output element (query head `row`, dim d) over
 // the attention chunk partials, 16 chunks per round trip (nact >= 1).
 __device__ float attn_combine_elem(const float* pacc, const float* pml, int row, int d, int D, int nsplit, int nact) {
@@ -122,76 +124,196 @@ __device__ float attn_combine_elem(const float* pacc, const float* pml, int row,
   return O / L;
 }
 
-// Elements handled per thread in one round trip by the prologues.
+// Elements handled per thread in one round trip by the attention gather.
 constexpr int kEpt = 4;
 
-template <int PRO>
-__device__ void gemv_prologue(const GemvArgs& a, float* xl, float* scratch, int k0, int k1, int klen_pad) {
-  const int tid = threadIdx.x, nt = blockDim.x;
-  if (PRO == PRO_COPY) {
-    for (int i = tid; i < klen_pad; i += nt) {
-      const int k = k0 + i;
-      const float v = a.in[min(k, a.K - 1)];
-      xl[i] = k < a.K ? v : 0.f;
-    }
-  } else if (PRO == PRO_SWIGLU) {
-    // silu(gate) * up of TSLSiLUMul.ts:15-29 on the summed gate/up partials
-    for (int ib = 0; ib < klen_pad; ib += kEpt * nt) {
-      float g[kEpt], u[kEpt];
-#pragma unroll
-      for (int e = 0; e < kEpt; e++) {
-        const int k = min(k0 + ib + tid + e * nt, a.K - 1);
-        g[e] = sum_parts(a.pin, a.n_pin, a.pin_stride, k);
-        u[e] = sum_parts(a.pin + a.up_off, a.n_pin, a.pin_stride, k);
-      }
-#pragma unroll
-      for (int e = 0; e < kEpt; e++) {
-        const int i = ib + tid + e * nt;
-        if (i < klen_pad) xl[i] = k0 + i < a.K ? g[e] / (1.f + __expf(-g[e])) * u[e] : 0.f;
-      }
-    }
-  } else if (PRO == PRO_ATTN) {
-    const ChunkPlan cp = chunk_plan(a.ctrl[C_POS], a.att_window, a.att_nsplit, a.att_chmin);
-    for (int i = tid; i < klen_pad; i += nt) {
-      const int k = min(k0 + i, a.K - 1);
-      const float v = attn_combine_elem(a.pacc, a.pml, k / a.att_D, k % a.att_D, a.att_D, a.att_nsplit, cp.nact);
-      xl[i] = k0 + i < a.K ? v : 0.f;
-    }
-  } else {
-    // residual stream x = base + sum(pin), then TSLRMSNorm.ts:50-74 over all K
-    const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && a.xout != nullptr;
-    const int tok = a.base ? 0 : a.ctrl[C_TOKEN];
-    float ss = 0.f;
-    for (int kb = 0; kb < a.K; kb += kEpt * nt) {
-      float v[kEpt];
-#pragma unroll
-      for (int e = 0; e < kEpt; e++) {
-        const int k = min(kb + tid + e * nt, a.K - 1);
-        float x;
-        if (a.base)
-          x = a.base[k];
-        else if (a.emb_f32)
-          x = ((const float*)a.emb)[(size_t)tok * a.K + k];
-        else
-          x = h2f(((const uint16_t*)a.emb)[(size_t)tok * a.K + k]);
-        v[e] = x + sum_parts(a.pin, a.n_pin, a.pin_stride, k);
-      }
-#pragma unroll
-      for (int e = 0; e < kEpt; e++) {
-        const int k = kb + tid + e * nt;
-        if (k < a.K) {
-          ss = fmaf(v[e], v[e], ss);
-          if (writer) a.xout[k] = v[e];
-          if (k >= k0 && k < k1) xl[k - k0] = v[e];
-        }
-      }
-    }
-    for (int i = (k1 - k0) + tid; i < klen_pad; i += nt) xl[i] = 0.f;
-    const float tot = block_sum(ss, scratch);  // its barriers also publish xl
-    const float inv = rsqrtf(tot / (float)a.K + a.eps);
-    for (int i = tid; i < k1 - k0; i += nt) xl[i] = xl[i] * inv * a.norm_w[k0 + i];
+// Stores 4 prologue outputs at slice offset i (a multiple of 4) and, for q4,
+// adds them into the group sums sum_k x_k of the 32-element groups: the 8
+// lanes covering a group reduce with shuffles.  Every lane of the wave must
+// call it (in_slice false contributes nothing).
+template <int FMT>
+__device__ __forceinline__ void put4(float* xl, float* xsum, int i, float4 y, bool in_slice) {
+  if (in_slice) *reinterpret_cast<float4*>(xl + i) = y;
+  if (FMT == WF_Q4) {
+    float g = in_slice ? (y.x + y.y) + (y.z + y.w) : 0.f;
+    g += __shfl_xor(g, 1, 64);
+    g += __shfl_xor(g, 2, 64);
+    g += __shfl_xor(g, 4, 64);
+    if (in_slice && (i & 31) == 0) xsum[i >> 5] = g;
   }
 }
+
+// Input slice x[k0, k1) of a GEMV in LDS (xl, zero-padded to klen_pad) plus,
+// for q4, its 32-element group sums.  Each thread owns 4 consecutive elements
+// (K % 4 == 0).  issue() puts the thread's first loads in flight and runs
+// before the kernel issues its weight loads: a wave's loads complete in issue
+// order, so the prologue's data (split-K partials of the previous kernel,
+// L2/MALL-resident) must not queue behind the weights streamed from HBM.
+// Every load in issue() is unconditional (indices clamped, results masked
+// arithmetically) so the compiler can wait for exactly the prologue's loads
+// while the weight loads stay outstanding.
+template <int PRO, int FMT>
+struct GemvPrologue {
+  static constexpr bool kRms = PRO == PRO_RMS || PRO == PRO_RMS2;
+  static constexpr int R = PRO == PRO_RMS2 ? 2 : 1;  // float4s of the residual row per thread
+  float4 x[R], w[R];
+  float4 p[2][kMaxPart];  // RMS: partials per float4 (R rows); SWIGLU: [0] gate, [1] up partials
+  float2 ml[8];           // ATTN: (m, l) and accumulators of the first 8 chunks
+  float4 ac[8];
+  int nact;
+  bool fast;  // float4 path (else element-wise, for odd fp16 shapes)
+
+  __device__ __forceinline__ void load_parts(const float* base, int n, int stride, int k, float4* dst) {
+#pragma unroll
+    for (int j = 0; j < kMaxPart; j++)
+      dst[j] = *reinterpret_cast<const float4*>(base + (size_t)max(min(j, n - 1), 0) * stride + k);
+  }
+  __device__ __forceinline__ float4 sum_loaded(const float4* src, int n) {
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < kMaxPart; j++) {
+      const float m = j < n ? 1.f : 0.f;
+      s = make_float4(fmaf(src[j].x, m, s.x), fmaf(src[j].y, m, s.y), fmaf(src[j].z, m, s.z), fmaf(src[j].w, m, s.w));
+    }
+    return s;
+  }
+  // Loads of the float4 at slice index f (clamped into the slice and the
+  // input); ATTN: chunks [jb, jb + 8), clamped to `lim` chunks.
+  __device__ __forceinline__ void load_slice4(const GemvArgs& a, int f, int k0, int n4, int jb, int lim) {
+    const int kc = min(k0 + 4 * min(f, n4 - 1), a.K - 4);
+    if (PRO == PRO_COPY) {
+      x[0] = *reinterpret_cast<const float4*>(a.in + kc);
+    } else if (PRO == PRO_SWIGLU) {
+      load_parts(a.pin, a.n_pin, a.pin_stride, kc, p[0]);
+      load_parts(a.pin + a.up_off, a.n_pin, a.pin_stride, kc, p[1]);
+    } else if (PRO == PRO_ATTN) {
+      const int row = kc / a.att_D, d = kc % a.att_D;
+      const float* mlp = a.pml + (size_t)row * a.att_nsplit * 2;
+      const float* acp = a.pacc + (size_t)row * a.att_nsplit * a.att_D + d;
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int j = min(jb + u, lim - 1);
+        ml[u] = *reinterpret_cast<const float2*>(mlp + 2 * j);
+        ac[u] = *reinterpret_cast<const float4*>(acp + (size_t)j * a.att_D);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void issue(const GemvArgs& a, int k0, int klen_pad) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    fast = (a.K & 3) == 0 && (PRO != PRO_ATTN || (a.att_D & 3) == 0);
+    if (kRms) {
+      const int K4 = a.K >> 2;
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const int f = min(tid + r * nt, K4 - 1);
+        w[r] = *reinterpret_cast<const float4*>(a.norm_w + 4 * f);
+        x[r] = *reinterpret_cast<const float4*>(a.base + 4 * f);
+        load_parts(a.pin, a.n_pin, a.pin_stride, 4 * f, p[r]);
+      }
+    } else if (fast) {
+      // ATTN: the first 8 chunk slots are read before the position is known
+      // (slots past the active count are masked in value4)
+      load_slice4(a, tid, k0, klen_pad / 4, 0, a.att_nsplit);
+    }
+  }
+
+  // silu(gate) * up (TSLSiLUMul.ts:15-29) or the flash-decoding combine of the
+  // attention chunk partials for the float4 loaded by load_slice4.
+  __device__ __forceinline__ float4 value4(const GemvArgs& a, int f, int k0, int n4) {
+    if (PRO == PRO_COPY) return x[0];
+    if (PRO == PRO_SWIGLU) {
+      const float4 g = sum_loaded(p[0], a.n_pin), u = sum_loaded(p[1], a.n_pin);
+      return make_float4(g.x / (1.f + __expf(-g.x)) * u.x, g.y / (1.f + __expf(-g.y)) * u.y,
+                         g.z / (1.f + __expf(-g.z)) * u.z, g.w / (1.f + __expf(-g.w)) * u.w);
+    }
+    float M = -INFINITY, L = 0.f;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int jb = 0; jb < nact; jb += 8) {
+      if (jb > 0) load_slice4(a, f, k0, n4, jb, nact);
+      float Mb = M;
+#pragma unroll
+      for (int u = 0; u < 8; u++) Mb = jb + u < nact ? fmaxf(Mb, ml[u].x) : Mb;
+      const float sc = M == -INFINITY ? 0.f : __expf(M - Mb);
+      L *= sc;
+      O = make_float4(O.x * sc, O.y * sc, O.z * sc, O.w * sc);
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        // selects, not products: slots past nact may hold anything
+        const bool use = jb + u < nact && ml[u].x != -INFINITY;
+        const float e = use ? __expf(ml[u].x - Mb) : 0.f;
+        L = use ? fmaf(ml[u].y, e, L) : L;
+        O.x = use ? fmaf(ac[u].x, e, O.x) : O.x;
+        O.y = use ? fmaf(ac[u].y, e, O.y) : O.y;
+        O.z = use ? fmaf(ac[u].z, e, O.z) : O.z;
+        O.w = use ? fmaf(ac[u].w, e, O.w) : O.w;
+      }
+      M = Mb;
+    }
+    const float il = 1.f / L;
+    return make_float4(O.x * il, O.y * il, O.z * il, O.w * il);
+  }
+
+  __device__ void finish(const GemvArgs& a, float* xl, float* xsum, float* scratch, int k0, int k1, int klen_pad) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    // the position is read here, after the weight loads are issued
+    if (PRO == PRO_ATTN) nact = chunk_plan(a.ctrl[C_POS], a.att_window, a.att_nsplit, a.att_chmin).nact;
+    if (kRms) {
+      // residual stream x = base + sum(pin), then TSLRMSNorm.ts:50-74 over all K
+      const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && a.xout != nullptr;
+      const int K4 = a.K >> 2;
+      float4 v[R];
+      float ss = 0.f;
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const int f = tid + r * nt;
+        v[r] = f4add(x[r], sum_loaded(p[r], a.n_pin));
+        const float m = f < K4 ? 1.f : 0.f;
+        ss = fmaf(v[r].x * m, v[r].x, ss);
+        ss = fmaf(v[r].y * m, v[r].y, ss);
+        ss = fmaf(v[r].z * m, v[r].z, ss);
+        ss = fmaf(v[r].w * m, v[r].w, ss);
+        if (writer && f < K4) *reinterpret_cast<float4*>(a.xout + 4 * f) = v[r];
+      }
+      const float inv = rsqrtf(block_sum(ss, scratch) / (float)a.K + a.eps);
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const int k = 4 * (tid + r * nt);
+        const float4 y = make_float4(v[r].x * inv * w[r].x, v[r].y * inv * w[r].y, v[r].z * inv * w[r].z,
+                                     v[r].w * inv * w[r].w);
+        put4<FMT>(xl, xsum, k - k0, y, k >= k0 && k < k1);
+      }
+      for (int i = (k1 - k0) + tid; i < klen_pad; i += nt) xl[i] = 0.f;  // slice padding past K
+    } else if (!fast) {
+      // element-wise path for shapes the float4 path cannot cover (fp16 weights
+      // only: q4 needs K % 32 == 0, so no group sums here)
+      for (int i = tid; i < klen_pad; i += nt) {
+        const int k = k0 + i;
+        float y = 0.f;
+        if (k < a.K) {
+          if (PRO == PRO_COPY) {
+            y = a.in[k];
+          } else if (PRO == PRO_SWIGLU) {
+            const float g = sum_parts(a.pin, a.n_pin, a.pin_stride, k);
+            y = g / (1.f + __expf(-g)) * sum_parts(a.pin + a.up_off, a.n_pin, a.pin_stride, k);
+          } else {
+            y = attn_combine_elem(a.pacc, a.pml, k / a.att_D, k % a.att_D, a.att_D, a.att_nsplit, nact);
+          }
+        }
+        xl[i] = y;
+      }
+    } else {
+      const int n4 = klen_pad / 4;
+      for (int fb = 0; fb < n4; fb += nt) {
+        const int f = fb + tid;
+        if (fb > 0) load_slice4(a, f, k0, n4, 0, PRO == PRO_ATTN ? nact : 1);
+        float4 y = value4(a, f, k0, n4);
+        if (!(f < n4 && k0 + 4 * f < a.K)) y = make_float4(0.f, 0.f, 0.f, 0.f);
+        put4<FMT>(xl, xsum, 4 * f, y, f < n4);
+      }
+    }
+  }
+};
 
 // 32 q4 weights of one row (one 16-byte chunk) against x[0..32).
 // sum_k s*(n_k - 8)*x_k = s*(sum_k n_k x_k - 8*sum_k x_k); n_k in [0,15] via
@@ -240,13 +362,15 @@ struct GemvCore {
   uint16_t sc[kMaxChunks];
 
   // Loads of batch b: unconditional (chunk index clamped to this wave's last
-  // chunk), so the whole batch is in flight at once.  nw >= 1.
-  __device__ __forceinline__ void load(const GemvArgs& a, int t, int c0, int wave, int W, int nw, int b) {
+  // chunk, or to the slice's last chunk for a wave without chunks), so the
+  // whole batch is in flight at once and the compiler can count exactly which
+  // loads each use waits for.
+  __device__ __forceinline__ void load(const GemvArgs& a, int t, int c0, int ncl, int wave, int W, int nw, int b) {
     const int lane = threadIdx.x & 63;
     const uint4* wt = a.w + (size_t)t * a.C * kTile;
 #pragma unroll
     for (int u = 0; u < kMaxChunks; u++) {
-      const int c = c0 + wave + min(b + u, nw - 1) * W;
+      const int c = c0 + min(wave + min(b + u, max(nw, 1) - 1) * W, ncl - 1);
       d[u] = wt[(size_t)c * kTile + lane];
       if (FMT == WF_Q4) sc[u] = a.s[((size_t)t * a.C + c) * kTile + lane];
     }
@@ -295,23 +419,18 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvArgs a) {
   GemvSmem L(sm, a.cps, CK, W);
   const int nw = wave < ncl ? (ncl - wave + W - 1) / W : 0;
 
+  GemvPrologue<PRO, FMT> pro;
+  pro.issue(a, k0, ncl * CK);
   GemvCore<FMT> core;
   int t = blockIdx.x;
-  if (t < a.T && nw > 0) core.load(a, t, c0, wave, W, nw, 0);  // weights in flight during the prologue
-  gemv_prologue<PRO>(a, L.xl, L.scratch, k0, k1, ncl * CK);
+  core.load(a, t, c0, ncl, wave, W, nw, 0);  // weights in flight during the prologue (t < T: gridDim.x <= T)
+  __builtin_amdgcn_sched_barrier(0);  // keep every load issued before the prologue's first wait
+  pro.finish(a, L.xl, L.xsum, L.scratch, k0, k1, ncl * CK);
   __syncthreads();
-  if (FMT == WF_Q4) {
-    for (int i = threadIdx.x; i < ncl; i += blockDim.x) {
-      float v = 0.f;
-      for (int j = 0; j < 32; j++) v += L.xl[i * 32 + j];
-      L.xsum[i] = v;
-    }
-    __syncthreads();
-  }
   for (; t < a.T; t += gridDim.x) {
     float acc = 0.f;
     for (int b = 0; b < nw; b += kMaxChunks) {
-      if (b > 0 || t != (int)blockIdx.x) core.load(a, t, c0, wave, W, nw, b);
+      if (b > 0 || t != (int)blockIdx.x) core.load(a, t, c0, ncl, wave, W, nw, b);
       acc += core.compute(L.xl, L.xsum, wave, W, nw, b);
     }
     L.red[wave * kTile + lane] = acc;
@@ -342,25 +461,20 @@ __global__ __launch_bounds__(W * 64) void lm_head_kernel(GemvArgs a) {
   GemvSmem L(sm, a.cps, CK, W);
   const int nw = wave < ncl ? (ncl - wave + W - 1) / W : 0;
 
+  GemvPrologue<PRO_COPY, FMT> pro;
+  pro.issue(a, 0, ncl * CK);
   GemvCore<FMT> core;
   int t = blockIdx.x;
-  if (t < a.T && nw > 0) core.load(a, t, 0, wave, W, nw, 0);
-  gemv_prologue<PRO_COPY>(a, L.xl, L.scratch, 0, a.K, ncl * CK);
+  core.load(a, t, 0, ncl, wave, W, nw, 0);  // gridDim.x <= T
+  __builtin_amdgcn_sched_barrier(0);
+  pro.finish(a, L.xl, L.xsum, L.scratch, 0, a.K, ncl * CK);
   __syncthreads();
-  if (FMT == WF_Q4) {
-    for (int i = threadIdx.x; i < ncl; i += blockDim.x) {
-      float v = 0.f;
-      for (int j = 0; j < 32; j++) v += L.xl[i * 32 + j];
-      L.xsum[i] = v;
-    }
-    __syncthreads();
-  }
   float best_v = kLowest;
   int best_i = 0x7fffffff;
   for (; t < a.T; t += gridDim.x) {
     float acc = 0.f;
     for (int b = 0; b < nw; b += kMaxChunks) {
-      if (b > 0 || t != (int)blockIdx.x) core.load(a, t, 0, wave, W, nw, b);
+      if (b > 0 || t != (int)blockIdx.x) core.load(a, t, 0, ncl, wave, W, nw, b);
       acc += core.compute(L.xl, L.xsum, wave, W, nw, b);
     }
     L.red[wave * kTile + lane] = acc;
@@ -393,10 +507,20 @@ __global__ __launch_bounds__(W * 64) void lm_head_kernel(GemvArgs a) {
 // one block reduces the per-block partials; a separate launch, so the kernel
 // boundary (not a device-scope fence per block) publishes the partials.  In the
 // decode graph it also advances the token/position state for the next step.
+// Copies the embedding row of `token` to es.x0 (all threads of the block take part).
+__device__ __forceinline__ void stage_embedding(const EmbStage& es, int token) {
+  if (!es.x0) return;
+  for (int i = threadIdx.x; i < es.H; i += blockDim.x)
+    es.x0[i] = es.f32 ? ((const float*)es.emb)[(size_t)token * es.H + i]
+                      : h2f(((const uint16_t*)es.emb)[(size_t)token * es.H + i]);
+}
+
 __global__ __launch_bounds__(1024) void argmax_merge_kernel(const float* pval, const int* pidx, int n, int* ctrl,
-                                                            int* tokens_out, int advance, int max_steps) {
+                                                            int* tokens_out, int advance, int max_steps,
+                                                            EmbStage es) {
   __shared__ float sv[16];
   __shared__ int si[16];
+  __shared__ int tok_s;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   float bv = kLowest;
   int bi = 0x7fffffff;
@@ -428,13 +552,16 @@ __global__ __launch_bounds__(1024) void argmax_merge_kernel(const float* pval, c
       ctrl[C_POS] += 1;
       ctrl[C_STEP] += 1;
     }
+    tok_s = token;
   }
+  __syncthreads();
+  stage_embedding(es, tok_s);
 }
 
 void launch_argmax_merge(const float* pval, const int* pidx, int n, int* ctrl, int* tokens_out, int advance,
-                         int max_steps, hipStream_t st) {
+                         int max_steps, const EmbStage& es, hipStream_t st) {
   hipLaunchKernelGGL(argmax_merge_kernel, dim3(1), dim3(1024), 0, st, pval, pidx, n, ctrl, tokens_out, advance,
-                     max_steps);
+                     max_steps, es);
 }
 
 size_t gemv_smem_bytes(int fmt, int cps, int waves) {
@@ -444,19 +571,25 @@ size_t gemv_smem_bytes(int fmt, int cps, int waves) {
 
 bool launch_gemv(int fmt, int pro, int waves, dim3 grid, const GemvArgs& a, hipStream_t st) {
   const size_t smem = gemv_smem_bytes(fmt, a.cps, waves);
+  // the RMS prologue keeps one (PRO_RMS) or two (PRO_RMS2) float4s of the
+  // residual row per thread
+  if (pro == PRO_RMS && a.K > 4 * 64 * waves) pro = PRO_RMS2;
+  if (pro == PRO_RMS2 && a.K > 8 * 64 * waves) return false;
 #define GEMV_CASE(F, P, Wv)                                                           \
   if (fmt == F && pro == P && waves == Wv) {                                          \
     hipLaunchKernelGGL((gemv_kernel<F, P, Wv>), grid, dim3(Wv * 64), smem, st, a);    \
     return true;                                                                      \
   }
-#define GEMV_W(F, P) GEMV_CASE(F, P, 1) GEMV_CASE(F, P, 2) GEMV_CASE(F, P, 4) GEMV_CASE(F, P, 8) GEMV_CASE(F, P, 16)
+#define GEMV_W(F, P) GEMV_CASE(F, P, 1) GEMV_CASE(F, P, 2) GEMV_CASE(F, P, 4) GEMV_CASE(F, P, 8)
   GEMV_W(WF_Q4, PRO_COPY)
   GEMV_W(WF_Q4, PRO_RMS)
+  GEMV_W(WF_Q4, PRO_RMS2)
   GEMV_W(WF_Q4, PRO_SWIGLU)
   GEMV_W(WF_Q4, PRO_ATTN)
   GEMV_W(WF_F16, PRO_ATTN)
   GEMV_W(WF_F16, PRO_COPY)
   GEMV_W(WF_F16, PRO_RMS)
+  GEMV_W(WF_F16, PRO_RMS2)
   GEMV_W(WF_F16, PRO_SWIGLU)
 #undef GEMV_W
 #undef GEMV_CASE
@@ -511,29 +644,34 @@ __device__ __forceinline__ void kv_load8<float>(const float* p, float* o) {
   o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
 }
 
-// Lanes per position in the score pass: each lane keeps at most 128 bytes of
-// a K row in registers.  Rows of more than 64 bytes are split over at least two
-// lanes, which also keeps the q reads lane-varying (one lane per position made
-// them wave-uniform and the compiler promoted all of them to scalar registers).
-int attn_lpp(int D, bool kv_f32) {
-  const int bytes = (D <= 32 ? 32 : D) * (kv_f32 ? 4 : 2);
-  return bytes <= 64 ? 1 : bytes <= 256 ? 2 : 4;
+// Attention tiling shared by the host (LDS size) and the kernel.
+struct AttnTiling {
+  int lpp, sub, gpw, vt_bytes;
+};
+static constexpr __host__ __device__ inline AttnTiling attn_tiling(int dt, int esz, int gmax) {
+  AttnTiling t{};
+  t.lpp = dt * esz <= 64 ? 1 : dt * esz <= 256 ? 2 : 4;  // lanes per position: <= 128 B of K per lane
+  t.sub = 64 / t.lpp;                                    // positions per pass (all waves see all of them)
+  t.gpw = gmax >= 4 ? gmax / 4 : 1;                      // query heads per wave
+  t.vt_bytes = t.sub * dt * esz;                         // V tile of one pass
+  return t;
 }
 
 // Compiled head dimension of attn_kernel: 64 and 128 exactly, 32 covers any
 // even head_dim <= 32 through runtime bounds.
 static int attn_dt(int D) { return D <= 32 ? 32 : D; }
 
-// Bytes of the V tile a block stages per pass (256 / lpp positions).
-static constexpr int kVTileBytes = 32768;
+int attn_lpp(int D, bool kv_f32) { return attn_tiling(attn_dt(D), kv_f32 ? 4 : 2, 1).lpp; }
 
-// LDS of attn_kernel: q, new k/v, per-wave probabilities, a region shared by
-// the V tile (during the passes), the RoPE scratch and the P.V reduction (after
-// them), and per-wave softmax statistics.
-size_t attn_smem_bytes(int gmax, int D, int lpp) {
-  const int HD = D / 2, NSW = 64 / HD, PW = 64 / lpp;
-  const size_t red = std::max({(size_t)4 * NSW * gmax * D, (size_t)gmax * D + D, (size_t)kVTileBytes / 4});
-  return sizeof(float) * ((size_t)gmax * D + 2 * D + 4 * (size_t)gmax * PW + red + 8 * gmax);
+// LDS of attn_kernel: q (padded to gmax heads), new k/v, per-wave
+// probabilities, and one region used in turn as RoPE scratch, V tile and the
+// P.V slot reduction.
+size_t attn_smem_bytes(int gmax, int D, bool kv_f32) {
+  const AttnTiling t = attn_tiling(attn_dt(D), kv_f32 ? 4 : 2, gmax);
+  const int NSW = 64 / (D / 2);
+  const size_t region = std::max({(size_t)t.vt_bytes, sizeof(float) * ((size_t)gmax * D + D),
+                                  sizeof(float) * 4 * (size_t)NSW * t.gpw * D});
+  return sizeof(float) * ((size_t)gmax * D + 2 * D + 4 * (size_t)t.gpw * t.sub) + region;
 }
 
 // Global loads of one attention pass, held in registers: this lane's K-row
@@ -558,6 +696,13 @@ struct AttnLoads {
         kw[4 * j + 2] = q.z;
         kw[4 * j + 3] = q.w;
       }
+      const int row_bytes = D * ESZ;  // a multiple of 16
+#pragma unroll
+      for (int j = 0; j < VCH; j++) {
+        const int off = (j * 256 + tid) * 16;
+        const int r = min(tb + off / row_bytes, t1 - 1);
+        vst[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(vh + (size_t)r * D) + off % row_bytes);
+      }
     } else {
       const KT* kr = kh + (size_t)t * D + qpart * DL;
 #pragma unroll
@@ -571,21 +716,20 @@ struct AttnLoads {
         }
       }
     }
-    const int row_bytes = D * ESZ;
-#pragma unroll
-    for (int j = 0; j < VCH; j++) {
-      const int off = (j * 256 + tid) * 16;
-      const int r = min(tb + off / row_bytes, t1 - 1);
-      vst[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(vh + (size_t)r * D) + off % row_bytes);
-    }
   }
 
-  // registers -> LDS V tile, then the fresh row (not in the cache yet) from vn
-  __device__ __forceinline__ void stage_v(KT* vt, const float* vn, int tb, bool own, int pos, int D, int SUB, int tid) {
+  // V rows [tb, tb + sub) into the LDS tile (the generic small-D path loads
+  // them here element by element), then the fresh row from vn.
+  __device__ __forceinline__ void stage_v(KT* vt, const KT* vh, const float* vn, int tb, int t1, bool own, int pos,
+                                          int D, int sub, int tid) {
+    if (!GEN) {
 #pragma unroll
-    for (int j = 0; j < VCH; j++) reinterpret_cast<uint4*>(vt)[j * 256 + tid] = vst[j];
+      for (int j = 0; j < VCH; j++) reinterpret_cast<uint4*>(vt)[j * 256 + tid] = vst[j];
+    } else {
+      for (int i = tid; i < sub * D; i += 256) vt[i] = vh[(size_t)min(tb + i / D, t1 - 1) * D + i % D];
+    }
     __syncthreads();
-    if (own && pos >= tb && pos < tb + SUB)
+    if (own && pos >= tb && pos < tb + sub)
       for (int d = tid; d < D; d += 256) vt[(size_t)(pos - tb) * D + d] = kv_store<KT>(vn[d]);
     __syncthreads();
   }
@@ -597,27 +741,28 @@ struct AttnLoads {
 };
 
 // One block = one KV head x one chunk of positions (split-K over the sequence,
-// flash-decoding).  Each block:
-//   * issues its K-row and V loads for the first pass before anything else
-//     (unconditional loads with clamped rows: one memory round trip),
+// flash-decoding).  The block's 4 waves share the KV head's G query heads
+// (GQA), gpw heads each, and all of the chunk's positions, in passes of `sub`
+// positions.  Each block:
+//   * issues the first pass's K-row and V loads before anything else,
 //   * forms q (and, in the chunk holding `pos`, the new k/v) from the QKV
 //     partial sums + bias, applies RoPE (TSLAttention.ts:168-250) and appends
 //     k/v to the cache (:252-286),
-//   * scores its positions for all G query heads sharing the KV head (GQA)
-//     with a per-wave online softmax (wave shuffles only) and accumulates P.V
-//     per wave,
-//   * merges its waves and writes (max, sum, unnormalised output) per query
-//     head for the combine (attn_combine_elem).
+//   * per pass: stages V in LDS, scores its positions for its heads, issues
+//     the next pass's loads, runs a per-wave online softmax (wave shuffles)
+//     and accumulates P.V,
+//   * writes (max, sum, unnormalised output) per query head for the combine
+//     (attn_combine_elem).
 template <typename KT, int GMAX, int DT>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   extern __shared__ float sm[];
   constexpr int ESZ = sizeof(KT);
-  constexpr int LPP = DT * ESZ <= 64 ? 1 : DT * ESZ <= 256 ? 2 : 4;  // as attn_lpp
+  constexpr AttnTiling TL = attn_tiling(DT, ESZ, GMAX);
+  constexpr int LPP = TL.lpp, SUB = TL.sub, GPW = TL.gpw;
   constexpr bool GEN = DT == 32;  // runtime head_dim <= 32
-  constexpr int SUB = 256 / LPP;  // positions per pass
-  constexpr int PW = 64 / LPP;    // positions per wave per pass
   constexpr int DLM = DT / LPP;   // K elements per lane (compiled bound)
-  constexpr int WPR = DLM * ESZ / 4;  // 32-bit words of K per lane
+  constexpr int WPR = DLM * ESZ / 4;
+  constexpr int VCH = TL.vt_bytes >= 4096 ? TL.vt_bytes / 4096 : 1;
   const int h = blockIdx.x, c = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int D = GEN ? a.D : DT, G = a.G;
@@ -629,22 +774,22 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   const bool own = pos >= t0 && pos < t1;
   const int DL = D / LPP;
   const int HD = D / 2, NSW = 64 / HD;
-  const int dp = lane % HD, slot = min(lane / HD, NSW - 1);  // PV role (lanes past NSW*HD duplicate slot NSW-1)
+  const int dp = lane % HD, slot = min(lane / HD, NSW - 1);
   const bool pv_lane = lane < NSW * HD;
   const int pl = lane / LPP, qpart = lane % LPP;
-  float* q_l = sm;
+  const int g0 = wave * GPW;            // this wave's first query head
+  const bool busy = g0 < G;             // wave-uniform
+  float* q_l = sm;                      // [GMAX][D]
   float* kn = q_l + GMAX * D;
   float* vn = kn + D;
-  float* p_l = vn + D;                                         // [4][GMAX][PW]
-  float* red = p_l + 4 * GMAX * PW;                            // [4][NSW][GMAX][D], or the V tile
-  KT* vt = reinterpret_cast<KT*>(red);                         // [SUB][D] during the passes
-  float* ml_l = red + max(max(4 * NSW * GMAX * D, GMAX * D + D), kVTileBytes / 4);  // [4][GMAX][2]
-  constexpr int VCH = kVTileBytes / 16 / 256;                  // 16-byte V chunks per thread
+  float* p_l = vn + D;                  // [4][GPW][SUB]
+  float* region = p_l + 4 * GPW * SUB;  // RoPE scratch / V tile / slot reduction
+  KT* vt = reinterpret_cast<KT*>(region);
   const KT* kh = reinterpret_cast<const KT*>(a.kc) + (size_t)h * a.max_tokens * D;
   const KT* vh = reinterpret_cast<const KT*>(a.vc) + (size_t)h * a.max_tokens * D;
 
   AttnLoads<KT, WPR, VCH, GEN, DLM> ld;
-  ld.issue(kh, vh, t0, t1, wave * PW + pl, qpart, D, DL, tid);
+  ld.issue(kh, vh, t0, t1, pl, qpart, D, DL, tid);
 
   // q, new k, new v = sum of partials + bias (loads in flight with the K/V above)
   {
@@ -667,8 +812,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
           (i - nq < D ? kn[i - nq] : vn[i - nq - D]) = v[e];
       }
     }
-    // rows G..GMAX-1 stay zero: the score and P.V loops run over GMAX heads without guards
-    for (int i = nq + tid; i < GMAX * D; i += 256) q_l[i] = 0.f;
+    for (int i = nq + tid; i < GMAX * D; i += 256) q_l[i] = 0.f;  // padded heads
   }
   __syncthreads();
 
@@ -687,14 +831,14 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         const float partner = d < half ? -v[d + half] : v[d - half];
         r = v[d] * cs[j] + partner * sn[j];
       }
-      red[i] = r;
+      region[i] = r;
     }
     __syncthreads();
     for (int i = tid; i < nrot; i += 256) {
       if (i < G * D)
-        q_l[i] = red[i];
+        q_l[i] = region[i];
       else
-        kn[i - G * D] = red[i];
+        kn[i - G * D] = region[i];
     }
     __syncthreads();
   }
@@ -712,25 +856,24 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     __syncthreads();
   }
 
-  float m_w[GMAX], l_w[GMAX], acc0[GMAX], acc1[GMAX];
+  float m_w[GPW], l_w[GPW], acc0[GPW], acc1[GPW];
 #pragma unroll
-  for (int g = 0; g < GMAX; g++) {
-    m_w[g] = -INFINITY;
-    l_w[g] = 0.f;
-    acc0[g] = 0.f;
-    acc1[g] = 0.f;
+  for (int j = 0; j < GPW; j++) {
+    m_w[j] = -INFINITY;
+    l_w[j] = 0.f;
+    acc0[j] = 0.f;
+    acc1[j] = 0.f;
   }
+  const float* qw = q_l + g0 * D + qpart * DL;
   for (int tb = t0; tb < t1; tb += SUB) {
-    if (tb != t0) ld.issue(kh, vh, tb, t1, wave * PW + pl, qpart, D, DL, tid);
-    ld.stage_v(vt, vn, tb, own, pos, D, SUB, tid);
-    // scores of this lane's position (partial dot over its K slice)
-    const int t = tb + wave * PW + pl;
+    ld.stage_v(vt, vh, vn, tb, t1, own, pos, D, SUB, tid);
+    const int t = tb + pl;
     const bool valid = t < t1;
     if (own && t == pos) {  // the fresh row is not in the cache yet: take it from LDS
 #pragma unroll
       for (int e = 0; e < DLM; e++) {
-        const uint32_t b = ESZ == 2 ? (uint32_t)__half_as_ushort(__float2half_rn(kn[qpart * DL + min(e, DL - 1)]))
-                                    : __float_as_uint(kn[qpart * DL + min(e, DL - 1)]);
+        const float x = kn[qpart * DL + min(e, DL - 1)];
+        const uint32_t b = ESZ == 2 ? (uint32_t)__half_as_ushort(__float2half_rn(x)) : __float_as_uint(x);
         if (ESZ == 2) {
           if (e & 1) ld.kw[e >> 1] = (ld.kw[e >> 1] & 0xFFFFu) | (b << 16); else ld.kw[e >> 1] = (ld.kw[e >> 1] & 0xFFFF0000u) | b;
         } else {
@@ -738,97 +881,82 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         }
       }
     }
-    float s[GMAX];
+    float s[GPW];
 #pragma unroll
-    for (int g = 0; g < GMAX; g++) s[g] = 0.f;
+    for (int j = 0; j < GPW; j++) s[j] = 0.f;
+    if (busy) {
 #pragma unroll
-    for (int e = 0; e < DLM; e++) {
-      if (!GEN || e < DL) {
-        const float kd = ld.kelem(e);
-        const float* qd = q_l + qpart * DL + e;
+      for (int e = 0; e < DLM; e++) {
+        if (!GEN || e < DL) {
+          const float kd = ld.kelem(e);
 #pragma unroll
-        for (int g = 0; g < GMAX; g++) s[g] = fmaf(qd[g * D], kd, s[g]);
+          for (int j = 0; j < GPW; j++) s[j] = fmaf(qw[j * D + e], kd, s[j]);
+        }
+        if ((e & 7) == 7) __builtin_amdgcn_sched_barrier(0);
       }
-      // keep the scheduler from hoisting every q read of the unrolled loop
-      // (register pressure): one block of 8 K elements at a time
-      if ((e & 7) == 7) __builtin_amdgcn_sched_barrier(0);
     }
+    // the next pass's loads overlap this pass's softmax and P.V
+    if (tb + SUB < t1) ld.issue(kh, vh, tb + SUB, t1, pl, qpart, D, DL, tid);
+    if (busy) {
 #pragma unroll
-    for (int g = 0; g < GMAX; g++) {
-      if (LPP > 1) s[g] += __shfl_xor(s[g], 1, 64);
-      if (LPP > 2) s[g] += __shfl_xor(s[g], 2, 64);
-      s[g] = valid ? s[g] * a.scale : -INFINITY;
-    }
-    // per-wave online softmax
-#pragma unroll
-    for (int g = 0; g < GMAX; g++) {
-      float p = 0.f;
-      if (g < G) {  // wave-uniform, once per head
-        const float mt = wave_max(s[g]);
-        const float mn = fmaxf(m_w[g], mt);
-        p = (valid && mn != -INFINITY) ? __expf(s[g] - mn) : 0.f;
+      for (int j = 0; j < GPW; j++) {
+        if (LPP > 1) s[j] += __shfl_xor(s[j], 1, 64);
+        if (LPP > 2) s[j] += __shfl_xor(s[j], 2, 64);
+        const float sc = valid ? s[j] * a.scale : -INFINITY;
+        const float mn = fmaxf(m_w[j], wave_max(sc));
+        const float p = (valid && mn != -INFINITY) ? __expf(sc - mn) : 0.f;
         const float lt = wave_sum(qpart == 0 ? p : 0.f);
-        const float corr = m_w[g] == -INFINITY ? 0.f : __expf(m_w[g] - mn);
-        l_w[g] = l_w[g] * corr + lt;
-        acc0[g] *= corr;
-        acc1[g] *= corr;
-        m_w[g] = mn;
+        const float corr = m_w[j] == -INFINITY ? 0.f : __expf(m_w[j] - mn);
+        l_w[j] = l_w[j] * corr + lt;
+        acc0[j] *= corr;
+        acc1[j] *= corr;
+        m_w[j] = mn;
+        if (qpart == 0) p_l[(wave * GPW + j) * SUB + pl] = p;
       }
-      if (qpart == 0) p_l[(wave * GMAX + g) * PW + pl] = p;
     }
     __syncthreads();
-    // P.V over this wave's positions; lane = (d pair, slot)
-    if (pv_lane) {
-      for (int pw = slot; pw < PW; pw += NSW) {
-        const int r = wave * PW + pw;  // row of the V tile
-        if (tb + r >= t1) break;
-        const float v0 = kv_load<KT>(vt + (size_t)r * D + 2 * dp);
-        const float v1 = kv_load<KT>(vt + (size_t)r * D + 2 * dp + 1);
-        const float* pp = p_l + wave * GMAX * PW + pw;
+    if (busy && pv_lane) {
+      for (int pw = slot; pw < SUB; pw += NSW) {
+        if (tb + pw >= t1) break;
+        const float v0 = kv_load<KT>(vt + (size_t)pw * D + 2 * dp);
+        const float v1 = kv_load<KT>(vt + (size_t)pw * D + 2 * dp + 1);
 #pragma unroll
-        for (int g = 0; g < GMAX; g++) {
-          acc0[g] = fmaf(pp[g * PW], v0, acc0[g]);
-          acc1[g] = fmaf(pp[g * PW], v1, acc1[g]);
+        for (int j = 0; j < GPW; j++) {
+          const float p = p_l[(wave * GPW + j) * SUB + pw];
+          acc0[j] = fmaf(p, v0, acc0[j]);
+          acc1[j] = fmaf(p, v1, acc1[j]);
         }
       }
     }
     __syncthreads();
   }
 
-  // merge waves and slots of the block; write the chunk partial
-  if (pv_lane) {
+  // reduce the P.V slots of each wave; write this chunk's partial per head
+  float* red = region;  // [4][NSW][GPW][D]
+  if (busy && pv_lane) {
 #pragma unroll
-    for (int g = 0; g < GMAX; g++) {
-      red[((wave * NSW + slot) * GMAX + g) * D + 2 * dp] = acc0[g];
-      red[((wave * NSW + slot) * GMAX + g) * D + 2 * dp + 1] = acc1[g];
-    }
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int g = 0; g < GMAX; g++) {
-      ml_l[(wave * GMAX + g) * 2] = m_w[g];
-      ml_l[(wave * GMAX + g) * 2 + 1] = l_w[g];
+    for (int j = 0; j < GPW; j++) {
+      red[((wave * NSW + slot) * GPW + j) * D + 2 * dp] = acc0[j];
+      red[((wave * NSW + slot) * GPW + j) * D + 2 * dp + 1] = acc1[j];
     }
   }
   __syncthreads();
-  for (int i = tid; i < G * D; i += 256) {
-    const int g = i / D, d = i % D;
-    float M = -INFINITY;
-    for (int w = 0; w < 4; w++) M = fmaxf(M, ml_l[(w * GMAX + g) * 2]);
-    float L = 0.f, O = 0.f;
-    for (int w = 0; w < 4; w++) {
-      const float mw = ml_l[(w * GMAX + g) * 2];
-      const float e = mw == -INFINITY ? 0.f : __expf(mw - M);
-      L = fmaf(ml_l[(w * GMAX + g) * 2 + 1], e, L);
-      float o = 0.f;
-      for (int sl = 0; sl < NSW; sl++) o += red[((w * NSW + sl) * GMAX + g) * D + d];
-      O = fmaf(o, e, O);
-    }
-    const int row = h * G + g;
-    a.pacc[((size_t)row * a.nsplit + c) * D + d] = O;
-    if (d == 0) {
-      a.pml[((size_t)row * a.nsplit + c) * 2] = M;
-      a.pml[((size_t)row * a.nsplit + c) * 2 + 1] = L;
+  if (busy) {
+#pragma unroll
+    for (int j = 0; j < GPW; j++) {
+      const int g = g0 + j;
+      if (g < G) {
+        const int row = h * G + g;
+        for (int d = lane; d < D; d += 64) {
+          float o = 0.f;
+          for (int sl = 0; sl < NSW; sl++) o += red[((wave * NSW + sl) * GPW + j) * D + d];
+          a.pacc[((size_t)row * a.nsplit + c) * D + d] = o;
+        }
+        if (lane == 0) {
+          a.pml[((size_t)row * a.nsplit + c) * 2] = m_w[j];
+          a.pml[((size_t)row * a.nsplit + c) * 2 + 1] = l_w[j];
+        }
+      }
     }
   }
 }
@@ -846,7 +974,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 
 bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, bool combine, hipStream_t st) {
   const dim3 grid(a.Hkv, a.nsplit);
-  const size_t smem = attn_smem_bytes(gmax, a.D, a.lpp);
+  const size_t smem = attn_smem_bytes(gmax, a.D, kv_f32);
   const int dt = attn_dt(a.D);
   if (dt != 32 && dt != 64 && dt != 128) return false;
   bool ok = false;
@@ -963,32 +1091,42 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* logits
 
 void launch_argmax(const float* logits, int n, float* pval, int* pidx, int* token, int blocks, hipStream_t st) {
   hipLaunchKernelGGL(argmax_partial_kernel, dim3(blocks), dim3(256), 0, st, logits, n, pval, pidx);
-  launch_argmax_merge(pval, pidx, blocks, token, nullptr, 0, 0, st);
+  launch_argmax_merge(pval, pidx, blocks, token, nullptr, 0, 0, EmbStage{}, st);
 }
 
-__global__ void set_ctrl_kernel(int* ctrl, int token, int pos, int step, int base, int len) {
-  ctrl[C_TOKEN] = token;
-  ctrl[C_POS] = pos;
-  ctrl[C_STEP] = step;
-  ctrl[C_BASE] = base;
-  ctrl[C_LEN] = len;
+__global__ void set_ctrl_kernel(int* ctrl, int token, int pos, int step, int base, int len, EmbStage es) {
+  if (threadIdx.x == 0) {
+    ctrl[C_TOKEN] = token;
+    ctrl[C_POS] = pos;
+    ctrl[C_STEP] = step;
+    ctrl[C_BASE] = base;
+    ctrl[C_LEN] = len;
+  }
+  stage_embedding(es, token);
 }
 
-void launch_set_ctrl(int* ctrl, int token, int pos, int step, int base, int len, hipStream_t st) {
-  hipLaunchKernelGGL(set_ctrl_kernel, dim3(1), dim3(1), 0, st, ctrl, token, pos, step, base, len);
+void launch_set_ctrl(int* ctrl, int token, int pos, int step, int base, int len, const EmbStage& es,
+                     hipStream_t st) {
+  hipLaunchKernelGGL(set_ctrl_kernel, dim3(1), dim3(256), 0, st, ctrl, token, pos, step, base, len, es);
 }
 
 // prefillChunkComputeNodes' advance node (DecoderTSLRunner.ts:216-225): next
 // position, next prompt token.
-__global__ void prefill_advance_kernel(int* ctrl, const int* prompt) {
+__global__ void prefill_advance_kernel(int* ctrl, const int* prompt, EmbStage es) {
   const int pos = ctrl[C_POS] + 1;
-  ctrl[C_POS] = pos;
   const int i = pos - ctrl[C_BASE];
-  if (i >= 0 && i < ctrl[C_LEN]) ctrl[C_TOKEN] = prompt[i];
+  const bool next = i >= 0 && i < ctrl[C_LEN];
+  const int token = next ? prompt[i] : 0;
+  __syncthreads();  // every thread has read ctrl before thread 0 updates it
+  if (threadIdx.x == 0) {
+    ctrl[C_POS] = pos;
+    if (next) ctrl[C_TOKEN] = token;
+  }
+  if (next) stage_embedding(es, token);
 }
 
-void launch_prefill_advance(int* ctrl, const int* prompt, hipStream_t st) {
-  hipLaunchKernelGGL(prefill_advance_kernel, dim3(1), dim3(1), 0, st, ctrl, prompt);
+void launch_prefill_advance(int* ctrl, const int* prompt, const EmbStage& es, hipStream_t st) {
+  hipLaunchKernelGGL(prefill_advance_kernel, dim3(1), dim3(256), 0, st, ctrl, prompt, es);
 }
 
 __global__ void dequant_kernel(int fmt, const uint4* w, const uint16_t* s, int N, int C, int K, float* out) {
