@@ -79,6 +79,7 @@ struct tlm_attn {
   float* rope_sin = nullptr;
   float* pacc = nullptr;
   float* pml = nullptr;
+  float* zero_bias = nullptr;  // stands in for an absent QKV bias
   int* ctrl = nullptr;
 };
 
@@ -491,13 +492,16 @@ static int attn_init(tlm_ctx* ctx, const tlm_attn_desc* d, tlm_attn* A, bool own
   std::vector<float> cs, sn;
   const int half = std::max(1, d->rotary_dim / 2);
   if (d->rotary_dim > 0) rope_tables(d->max_tokens, d->rotary_dim, d->inv_freq, d->attention_factor, cs, sn);
-  else cs.assign(half, 0.f), sn.assign(half, 0.f);
+  else cs.assign((size_t)d->max_tokens * half, 0.f), sn.assign((size_t)d->max_tokens * half, 0.f);
   HIP_TRY(hipMalloc(&A->rope_cos, cs.size() * sizeof(float)));
   HIP_TRY(hipMalloc(&A->rope_sin, sn.size() * sizeof(float)));
   HIP_TRY(hipMemcpy(A->rope_cos, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice));
   HIP_TRY(hipMemcpy(A->rope_sin, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice));
   HIP_TRY(hipMalloc(&A->pacc, sizeof(float) * (size_t)d->heads * A->nsplit * D));
   HIP_TRY(hipMalloc(&A->pml, sizeof(float) * (size_t)d->heads * A->nsplit * 2));
+  const size_t nqkv = (size_t)(d->heads + 2 * d->kv_heads) * D;
+  HIP_TRY(hipMalloc(&A->zero_bias, sizeof(float) * nqkv));
+  HIP_TRY(hipMemset(A->zero_bias, 0, sizeof(float) * nqkv));
   if (own_cache) {
     const size_t cache = (size_t)d->kv_heads * d->max_tokens * D * esz;
     HIP_TRY(hipMalloc(&A->kc, cache));
@@ -515,6 +519,7 @@ static void attn_free(tlm_attn* A, bool own_cache) {
   hipFree(A->rope_sin);
   hipFree(A->pacc);
   hipFree(A->pml);
+  hipFree(A->zero_bias);
   if (own_cache) {
     hipFree(A->kc);
     hipFree(A->vc);
@@ -529,7 +534,7 @@ static AttnArgs attn_args(const tlm_attn* A, const float* src, int n_src, int st
   a.src = src;
   a.n_src = n_src;
   a.src_stride = stride;
-  a.bias = bias;
+  a.bias = bias ? bias : A->zero_bias;
   a.ctrl = ctrl;
   a.kc = kc;
   a.vc = vc;

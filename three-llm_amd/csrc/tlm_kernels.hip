@@ -23,23 +23,54 @@ static constexpr float kLowest = -3.4028234663852886e38f;  // TSLLogits.ts:21 LO
 
 __device__ __forceinline__ float h2f(uint32_t bits) { return __half2float(__ushort_as_half((unsigned short)bits)); }
 
+// Cross-lane moves through DPP (data-parallel primitives: a VALU operand
+// modifier, no LDS round trip).  Every reduction below pairs lanes
+// symmetrically, so all lanes of a group end with the same bits.
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within each 8 lanes
+constexpr int kDppMirror = 0x140;     // lane i <-> 15 - i within each 16 lanes
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float readlane(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Sum over each aligned group of 8 lanes, in every lane of the group.
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  return v + dpp<kDppHalfMirror>(v);
+}
+
+// Sum / max over the 64 lanes of a wave (wave-uniform result).
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v = sum8(v);
+  v += dpp<kDppMirror>(v);
+  return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  v = fmaxf(v, dpp<kDppXor2>(v));
+  v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp<kDppMirror>(v));
+  return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
 }
 
-// Block-wide reductions (blockDim.x a multiple of 64); every thread gets the result.
+// Block-wide sum (blockDim.x a multiple of 64); every thread gets the result.
+// scratch holds one float per wave and must not be in use by another
+// reduction of the same kernel (each kernel calls this once per scratch).
 __device__ float block_sum(float v, float* scratch) {
   v = wave_sum(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  __syncthreads();
   if (lane == 0) scratch[wave] = v;
   __syncthreads();
   float r = 0.f;
@@ -47,30 +78,40 @@ __device__ float block_sum(float v, float* scratch) {
   return r;
 }
 
-__device__ float block_max(float v, float* scratch) {
-  v = wave_max(v);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  __syncthreads();
-  if (lane == 0) scratch[wave] = v;
-  __syncthreads();
-  float r = -INFINITY;
-  for (int i = 0; i < nw; i++) r = fmaxf(r, scratch[i]);
-  return r;
-}
-
 // Greedy order of TSLLogits.ts:228-229: higher score, ties to the lower id.
+// A strict total order on (score, id) for non-NaN scores; lanes start from
+// (LOWEST, INT_MAX) and only take better candidates, so NaN never enters.
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
 
+template <int CTRL>
+__device__ __forceinline__ void argmax_step(float& v, int& i) {
+  const float ov = dpp<CTRL>(v);
+  const int oi = dpp<CTRL>(i);
+  if (better(ov, oi, v, i)) {
+    v = ov;
+    i = oi;
+  }
+}
+
+// Best (score, id) of the wave, in every lane.
 __device__ void wave_argmax(float& v, int& i) {
+  argmax_step<kDppXor1>(v, i);
+  argmax_step<kDppXor2>(v, i);
+  argmax_step<kDppHalfMirror>(v, i);
+  argmax_step<kDppMirror>(v, i);
+  float bv = readlane(v, 0);
+  int bi = __builtin_amdgcn_readlane(i, 0);
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float ov = __shfl_xor(v, o, 64);
-    int oi = __shfl_xor(i, o, 64);
-    if (better(ov, oi, v, i)) {
-      v = ov;
-      i = oi;
+  for (int r = 16; r < 64; r += 16) {
+    const float rv = readlane(v, r);
+    const int ri = __builtin_amdgcn_readlane(i, r);
+    if (better(rv, ri, bv, bi)) {
+      bv = rv;
+      bi = ri;
     }
   }
+  v = bv;
+  i = bi;
 }
 
 // ------------------------------------------------------------------ GEMV --
@@ -135,10 +176,7 @@ template <int FMT>
 __device__ __forceinline__ void put4(float* xl, float* xsum, int i, float4 y, bool in_slice) {
   if (in_slice) *reinterpret_cast<float4*>(xl + i) = y;
   if (FMT == WF_Q4) {
-    float g = in_slice ? (y.x + y.y) + (y.z + y.w) : 0.f;
-    g += __shfl_xor(g, 1, 64);
-    g += __shfl_xor(g, 2, 64);
-    g += __shfl_xor(g, 4, 64);
+    const float g = sum8(in_slice ? (y.x + y.y) + (y.z + y.w) : 0.f);
     if (in_slice && (i & 31) == 0) xsum[i >> 5] = g;
   }
 }
@@ -740,6 +778,81 @@ struct AttnLoads {
   }
 };
 
+// q heads and the new k, v rows of one KV head: QKV split-K partial sums +
+// bias, with RoPE (rotate-half, TSLAttention.ts:168-250) applied in registers.
+// Row r < G is query head h*G + r, row G the new k, row G + 1 the new v; item j
+// of a row covers the element pair (j, j + rd/2) when j < rd/2 on a rotated
+// row, else (2j, 2j + 1).  Loads are unconditional (item index clamped; bias
+// and RoPE tables are always valid buffers) so issue() can run ahead of the
+// K/V loads and be waited for alone.
+template <int IT>
+struct AttnGather {
+  float p0[IT][kMaxPart], p1[IT][kMaxPart];
+  float b0[IT], b1[IT], c[IT], sn[IT];
+
+  struct Item {
+    int row, e0, e1, col, j;
+    bool rot;
+  };
+  __device__ __forceinline__ static Item item(const AttnArgs& a, int idx, int h) {
+    const int D = a.D, HD = D / 2;
+    Item it;
+    it.row = idx / HD;
+    it.j = idx % HD;
+    const int hf = (a.rd > 0 && it.row <= a.G) ? a.rd / 2 : 0;
+    it.rot = it.j < hf;
+    it.e0 = it.rot ? it.j : 2 * it.j;
+    it.e1 = it.rot ? it.j + hf : 2 * it.j + 1;
+    const int QS = a.Hq * D, KS = a.Hkv * D;
+    it.col = it.row < a.G ? (h * a.G + it.row) * D : it.row == a.G ? QS + h * D : QS + KS + h * D;
+    return it;
+  }
+
+  __device__ __forceinline__ void issue(const AttnArgs& a, int h, int pos, int ib, int nit) {
+    const int half = a.rd > 0 ? a.rd / 2 : 1;  // RoPE table row width
+#pragma unroll
+    for (int u = 0; u < IT; u++) {
+      const Item it = item(a, min(ib + (int)threadIdx.x + 256 * u, nit - 1), h);
+#pragma unroll
+      for (int q = 0; q < kMaxPart; q++) {
+        const float* src = a.src + (size_t)max(min(q, a.n_src - 1), 0) * a.src_stride + it.col;
+        p0[u][q] = src[it.e0];
+        p1[u][q] = src[it.e1];
+      }
+      b0[u] = a.bias[it.col + it.e0];
+      b1[u] = a.bias[it.col + it.e1];
+      const int tj = (size_t)pos * half + min(it.j, half - 1);
+      c[u] = a.rope_cos[tj];
+      sn[u] = a.rope_sin[tj];
+    }
+  }
+
+  __device__ __forceinline__ void finish(const AttnArgs& a, int h, int ib, int nit, float* q_l, float* kn, float* vn) {
+#pragma unroll
+    for (int u = 0; u < IT; u++) {
+      const int idx = ib + (int)threadIdx.x + 256 * u;
+      const Item it = item(a, min(idx, nit - 1), h);
+      float x0 = b0[u], x1 = b1[u];
+#pragma unroll
+      for (int q = 0; q < kMaxPart; q++) {
+        const float m = q < a.n_src ? 1.f : 0.f;
+        x0 = fmaf(p0[u][q], m, x0);
+        x1 = fmaf(p1[u][q], m, x1);
+      }
+      float y0 = x0, y1 = x1;
+      if (it.rot) {
+        y0 = x0 * c[u] + (-x1) * sn[u];
+        y1 = x1 * c[u] + x0 * sn[u];
+      }
+      if (idx < nit) {
+        float* dst = it.row < a.G ? q_l + it.row * a.D : it.row == a.G ? kn : vn;
+        dst[it.e0] = y0;
+        dst[it.e1] = y1;
+      }
+    }
+  }
+};
+
 // One block = one KV head x one chunk of positions (split-K over the sequence,
 // flash-decoding).  The block's 4 waves share the KV head's G query heads
 // (GQA), gpw heads each, and all of the chunk's positions, in passes of `sub`
@@ -788,60 +901,22 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   const KT* kh = reinterpret_cast<const KT*>(a.kc) + (size_t)h * a.max_tokens * D;
   const KT* vh = reinterpret_cast<const KT*>(a.vc) + (size_t)h * a.max_tokens * D;
 
+  // q, new k, new v (+ RoPE) first: their loads are issued ahead of the K/V
+  // loads, which are only needed after them
+  constexpr int GIT = (GMAX + 2) * DT / 2 > 256 ? 2 : 1;  // items per thread pre-issued
+  const int nit = (G + 2) * (D / 2);
+  AttnGather<GIT> ga;
+  ga.issue(a, h, pos, 0, nit);
   AttnLoads<KT, WPR, VCH, GEN, DLM> ld;
   ld.issue(kh, vh, t0, t1, pl, qpart, D, DL, tid);
-
-  // q, new k, new v = sum of partials + bias (loads in flight with the K/V above)
-  {
-    const int nq = G * D, ntot = nq + (own ? 2 * D : 0);
-    const int QS = a.Hq * D, KS = a.Hkv * D;
-    for (int ib = 0; ib < ntot; ib += kEpt * 256) {
-      float v[kEpt];
-#pragma unroll
-      for (int e = 0; e < kEpt; e++) {
-        const int i = min(ib + tid + e * 256, ntot - 1);
-        const int col = i < nq ? h * G * D + i : (i - nq < D ? QS + h * D + (i - nq) : QS + KS + h * D + (i - nq - D));
-        v[e] = (a.bias ? a.bias[col] : 0.f) + sum_parts(a.src, a.n_src, a.src_stride, col);
-      }
-#pragma unroll
-      for (int e = 0; e < kEpt; e++) {
-        const int i = ib + tid + e * 256;
-        if (i < nq)
-          q_l[i] = v[e];
-        else if (i < ntot)
-          (i - nq < D ? kn[i - nq] : vn[i - nq - D]) = v[e];
-      }
-    }
-    for (int i = nq + tid; i < GMAX * D; i += 256) q_l[i] = 0.f;  // padded heads
+  __builtin_amdgcn_sched_barrier(0);
+  ga.finish(a, h, 0, nit, q_l, kn, vn);
+  for (int ib = 256 * GIT; ib < nit; ib += 256 * GIT) {
+    ga.issue(a, h, pos, ib, nit);
+    ga.finish(a, h, ib, nit, q_l, kn, vn);
   }
+  for (int i = G * D + tid; i < GMAX * D; i += 256) q_l[i] = 0.f;  // padded heads
   __syncthreads();
-
-  // RoPE (rotate-half) on q and the new k; the tables carry the attention factor
-  if (a.rd > 0) {
-    const int half = a.rd / 2;
-    const float* cs = a.rope_cos + (size_t)pos * half;
-    const float* sn = a.rope_sin + (size_t)pos * half;
-    const int nrot = G * D + (own ? D : 0);
-    for (int i = tid; i < nrot; i += 256) {
-      const float* v = i < G * D ? q_l + (i / D) * D : kn;
-      const int d = i < G * D ? i % D : i - G * D;
-      float r = v[d];
-      if (d < a.rd) {
-        const int j = d < half ? d : d - half;
-        const float partner = d < half ? -v[d + half] : v[d - half];
-        r = v[d] * cs[j] + partner * sn[j];
-      }
-      region[i] = r;
-    }
-    __syncthreads();
-    for (int i = tid; i < nrot; i += 256) {
-      if (i < G * D)
-        q_l[i] = region[i];
-      else
-        kn[i - G * D] = region[i];
-    }
-    __syncthreads();
-  }
   // KV append at pos; this block keeps the rounded values the cache will hold
   if (own) {
     KT* kc = reinterpret_cast<KT*>(a.kc) + (size_t)h * a.max_tokens * D;
@@ -900,8 +975,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     if (busy) {
 #pragma unroll
       for (int j = 0; j < GPW; j++) {
-        if (LPP > 1) s[j] += __shfl_xor(s[j], 1, 64);
-        if (LPP > 2) s[j] += __shfl_xor(s[j], 2, 64);
+        if (LPP > 1) s[j] += dpp<kDppXor1>(s[j]);
+        if (LPP > 2) s[j] += dpp<kDppXor2>(s[j]);
         const float sc = valid ? s[j] * a.scale : -INFINITY;
         const float mn = fmaxf(m_w[j], wave_max(sc));
         const float p = (valid && mn != -INFINITY) ? __expf(sc - mn) : 0.f;
@@ -916,8 +991,9 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     }
     __syncthreads();
     if (busy && pv_lane) {
+      // rows past t1 hold clamped copies of valid rows and have p == 0
+#pragma unroll 8
       for (int pw = slot; pw < SUB; pw += NSW) {
-        if (tb + pw >= t1) break;
         const float v0 = kv_load<KT>(vt + (size_t)pw * D + 2 * dp);
         const float v1 = kv_load<KT>(vt + (size_t)pw * D + 2 * dp + 1);
 #pragma unroll
