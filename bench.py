@@ -64,8 +64,11 @@ def bytes_per_token(hw, position: int, kv_first: int = 0) -> float:
 
 
 def lm_head_bytes(hw) -> float:
+    """Algorithmic bytes of one LM head launch: fp16 head rows, the normed
+    hidden vector, the logits and the per-block argmax partials."""
     r = hw.recipe
-    return r.vocab_size * r.hidden_size * 2.0 + r.hidden_size * 4 + r.vocab_size * 4
+    blocks = min((r.vocab_size + 63) // 64, 4096)
+    return r.vocab_size * r.hidden_size * 2.0 + r.hidden_size * 4 + r.vocab_size * 4 + blocks * 8
 
 
 def read_traffic(kernel: str):
@@ -105,14 +108,29 @@ def main():
     ap.add_argument("--workload", default="qwen2.5-0.5b")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work (0 disables)")
     ap.add_argument("--kernel-iters", type=int, default=50)
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="only run a plain device-to-device copy of this many MiB, 5 times (the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings), then exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; the multi-GPU (tensor-parallel) decode path is a design "
-              "only (see DESIGN.md), so --gpus must be 1", file=sys.stderr)
+              "only, so --gpus must be 1", file=sys.stderr)
         sys.exit(2)
 
     pkg = _package()
     W, R, tlm = pkg.weights, pkg.runner, pkg.tlm
+    if args.copy_mib:
+        ctx = tlm.Context(0)
+        n = args.copy_mib << 20
+        src, dst = ctx.buffer(n), ctx.buffer(n)
+        for _ in range(5):
+            dst.copy_from(src)
+        ctx.sync()
+        log(f"[bench] copied {args.copy_mib} MiB device-to-device 5 times")
+        src.free()
+        dst.free()
+        ctx.close()
+        return
     wl = W.WORKLOADS[args.workload]
     t0 = time.perf_counter()
     hw = W.synthetic(wl)
@@ -152,15 +170,17 @@ def main():
     ms_step = wall * 1e3 / steps
     mean_bytes = sum(bytes_per_token(hw, pos0 + i, 0) for i in range(steps)) / steps
     hbm_frac = mean_bytes * toks / HBM_PEAK
-    # dominant kernel: the LM head (HIP events on the model stream)
-    lm_ms = runner.model.time_kernel(0, args.kernel_iters)
+    # dominant kernel: the LM head, timed inside decode steps over the same
+    # positions (a pair of HIP events on the model stream around each launch)
+    lm_ms = runner.model.time_head(last, pos0, min(steps, args.kernel_iters))
     lm_bytes = lm_head_bytes(hw)
     lm_bw = lm_bytes / (lm_ms * 1e-3)
     stage_ms = {name: runner.model.time_kernel(k, args.kernel_iters)
                 for name, k in (("qkv", 4), ("attention", 1), ("o", 5), ("gate_up", 2), ("down", 3))}
     log(f"[bench] decode {toks:.1f} tok/s ({ms_step * 1e3:.1f} us/token wall, {ev_ms * 1e3 / steps:.1f} us/token "
         f"events), {mean_bytes / 1e6:.2f} MB/token -> {hbm_frac * 100:.1f}% of HBM roofline")
-    log(f"[bench] LM head {lm_ms * 1e3:.1f} us/launch = {lm_bw / 1e9:.0f} GB/s; per-launch stage times (us): "
+    log(f"[bench] LM head {lm_ms * 1e3:.1f} us/launch in decode steps = {lm_bw / 1e9:.0f} GB/s; stage times, "
+        f"back-to-back launches of layer 0 (us): "
         + ", ".join(f"{k} {v * 1e3:.1f}" for k, v in stage_ms.items()))
     log(f"[bench] prefill {prefill_n} tokens in {prefill_s * 1e3:.1f} ms; first tokens {list(tokens[:8])}")
     cpu = None

@@ -68,6 +68,11 @@ int tlm_alloc(tlm_ctx* ctx, size_t bytes, void** dptr);
 int tlm_free(tlm_ctx* ctx, void* dptr);
 int tlm_upload(tlm_ctx* ctx, void* dst, const void* src, size_t bytes);   /* blocking */
 int tlm_download(tlm_ctx* ctx, void* dst, const void* src, size_t bytes); /* waits for the stream */
+/* Device-to-device copy enqueued on the context stream (bytes % 16 == 0): a
+ * plain streaming kernel of known size.  A utility with no reference
+ * counterpart (the reference copies through WebGPU buffers); it also scales
+ * hardware byte counters against a known transfer. */
+int tlm_copy(tlm_ctx* ctx, void* dst, const void* src, size_t bytes);
 
 /* ------------------------------------------------------------------ linear
  * TSLLinear (tsl/TSLLinear.ts:13-82): y[n] = b[n] + sum_k W[n][k] x[k].
@@ -201,6 +206,11 @@ int tlm_read_hidden(tlm_model* model, float* out, size_t n);
  * 4 = QKV of layer 0, 5 = O of layer 0) over iters launches. */
 int tlm_time_decode(tlm_model* model, int32_t token, int32_t position, int warmup, int n, double* ms);
 int tlm_time_kernel(tlm_model* model, int which, int iters, double* avg_ms);
+/* tlm_time_head: n greedy decode steps from (token, position), each the layer
+ * graph then the LM head bracketed by its own pair of events; average ms of
+ * the LM head launch inside a real step (its weights cold in the caches, as in
+ * decode).  Leaves the cache and ctrl state advanced like tlm_decode_greedy. */
+int tlm_time_head(tlm_model* model, int32_t token, int32_t position, int n, double* avg_ms);
 /* Launch layout chosen for the model (for reports): per-stage grid sizes. */
 int tlm_model_describe(tlm_model* model, char* out, size_t len);
 

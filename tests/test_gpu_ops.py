@@ -193,6 +193,20 @@ def test_attention_long_fp16_cache(ctx, heads, kv, D, theta, steps, window):
     A.close()
 
 
+def test_device_copy_is_exact(ctx):
+    """tlm_copy: byte-exact device-to-device copy; sizes not a multiple of 16 are rejected."""
+    rng = np.random.default_rng(7)
+    a = rng.integers(0, 256, size=(1 << 20) + 48, dtype=np.uint8)
+    src, dst = ctx.buffer(a.nbytes), ctx.buffer(a.nbytes)
+    src.write(a)
+    dst.copy_from(src)
+    assert np.array_equal(dst.read(np.uint8), a)
+    with pytest.raises(tlm.TlmError):
+        dst.copy_from(src, 8)
+    src.free()
+    dst.free()
+
+
 # ------------------------------------------------------------------ logits --
 
 def test_argmax_known_answers(ctx):

@@ -56,6 +56,7 @@ struct tlm_ctx {
 
 struct GemvPlan {
   int waves = 4, cps = 1, splits = 1, gx = 1;
+  int nch = 1;  // chunks per wave per load batch
 };
 
 struct tlm_linear {
@@ -116,8 +117,8 @@ struct tlm_model {
   // attention (shared by the layers; they run one after another)
   tlm_attn attn;
   GemvPlan lm_plan;
-  hipGraphExec_t g_logits = nullptr, g_prefill = nullptr;
-  hipGraph_t graph_logits = nullptr, graph_prefill = nullptr;
+  hipGraphExec_t g_logits = nullptr, g_prefill = nullptr, g_layers = nullptr;
+  hipGraph_t graph_logits = nullptr, graph_prefill = nullptr, graph_layers = nullptr;
   bool finalized = false;
   bool use_graphs = true;  // TLM_GRAPHS=0 enqueues the same kernels directly (profilers, debugging)
 };
@@ -126,6 +127,13 @@ struct tlm_model {
 
 // Chunks per row: 16-byte units of 32 q4 weights or 8 fp16 weights.
 static int chunk_k(int fmt) { return fmt == TLM_FMT_Q4 ? 32 : 8; }
+
+// Chunks a wave loads per batch: its chunk count rounded up to a power of two
+// (at most kMaxChunks; more chunks run in several batches).
+static void set_nch(GemvPlan& p) {
+  const int per_wave = (p.cps + p.waves - 1) / p.waves;
+  p.nch = per_wave <= 1 ? 1 : per_wave <= 2 ? 2 : per_wave <= 4 ? 4 : 8;
+}
 
 // Split-K plan for one GEMV: enough waves to keep every CU busy on a latency-
 // bound batch-1 product, at least one 16-byte chunk per wave, and few partial
@@ -137,6 +145,7 @@ static GemvPlan plan_gemv(int T, int C, int cus, int CK, bool single_split) {
     p.cps = C;
     p.splits = 1;
     p.gx = T;
+    set_nch(p);
     return p;
   }
   const long units = (long)T * C;
@@ -155,7 +164,8 @@ static GemvPlan plan_gemv(int T, int C, int cus, int CK, bool single_split) {
   p.cps = cps;
   p.splits = S;
   p.gx = T;
-  if (p.waves > cps) p.waves = cps >= 8 ? 8 : cps >= 4 ? 4 : cps >= 2 ? 2 : 1;
+  if (p.waves > cps) p.waves = cps >= 8 ? 8 : 4;
+  set_nch(p);
   return p;
 }
 
@@ -163,6 +173,7 @@ static GemvPlan plan_gemv(int T, int C, int cus, int CK, bool single_split) {
 // of it per thread: K <= 512 * waves.
 static void rms_waves(tlm_linear* L) {
   while (L->plan.waves < 8 && L->K > 512 * L->plan.waves) L->plan.waves *= 2;
+  set_nch(L->plan);
 }
 
 // Host repack of canonical rows [r0, r0 + rows) into the device tile layout.
@@ -258,6 +269,11 @@ static void fill_gemv_args(GemvArgs& a, const tlm_linear* L, float* out) {
 
 static int wfmt(int fmt) { return fmt == TLM_FMT_Q4 ? WF_Q4 : WF_F16; }
 
+// One GEMV launch of a linear with its split-K plan.
+static bool launch_linear(const tlm_linear* L, int pro, const GemvArgs& a, hipStream_t st) {
+  return launch_gemv(wfmt(L->fmt), pro, L->plan.waves, L->plan.nch, dim3(L->plan.gx, L->plan.splits), a, st);
+}
+
 // ------------------------------------------------------------------ context --
 
 extern "C" {
@@ -341,6 +357,15 @@ int tlm_download(tlm_ctx* ctx, void* dst, const void* src, size_t bytes) {
   return TLM_OK;
 }
 
+int tlm_copy(tlm_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(TLM_ERR_INVALID, "TLMBuffer: null argument");
+  if (bytes % 16 != 0) return fail(TLM_ERR_INVALID, "TLMBuffer: copy size %zu is not a multiple of 16", bytes);
+  if (bytes == 0) return TLM_OK;
+  launch_copy(static_cast<uint4*>(dst), static_cast<const uint4*>(src), bytes / 16, ctx->stream);
+  CHECK_LAUNCH("TLMBuffer");
+  return TLM_OK;
+}
+
 // ------------------------------------------------------------------ linear --
 
 int tlm_linear_create(tlm_ctx* ctx, int fmt, int n_out, int k_in, const void* weights, const uint16_t* scales,
@@ -391,7 +416,7 @@ int tlm_op_linear(tlm_linear* L, const float* x, const float* bias, float* y) {
   fill_gemv_args(a, L, direct ? y : L->part);
   a.in = x;
   a.bias = direct ? bias : nullptr;
-  if (!launch_gemv(wfmt(L->fmt), PRO_COPY, L->plan.waves, dim3(L->plan.gx, L->plan.splits), a, L->ctx->stream))
+  if (!launch_linear(L, PRO_COPY, a, L->ctx->stream))
     return fail(TLM_ERR_STATE, "TLMLinear: no kernel variant for this shape");
   CHECK_LAUNCH("TLMLinear");
   if (!direct) {
@@ -426,7 +451,7 @@ int tlm_op_gated_mlp(tlm_linear* gu, tlm_linear* down, const float* x, float* y)
   GemvArgs a;
   fill_gemv_args(a, gu, gu->part);
   a.in = x;
-  if (!launch_gemv(wfmt(gu->fmt), PRO_COPY, gu->plan.waves, dim3(gu->plan.gx, gu->plan.splits), a, st))
+  if (!launch_linear(gu, PRO_COPY, a, st))
     return fail(TLM_ERR_STATE, "TLMGatedMLP: no kernel variant for this shape");
   CHECK_LAUNCH("TLMGatedMLP");
   GemvArgs b;
@@ -436,7 +461,7 @@ int tlm_op_gated_mlp(tlm_linear* gu, tlm_linear* down, const float* x, float* y)
   b.n_pin = gu->plan.splits;
   b.pin_stride = gu->N;
   b.up_off = down->K;
-  if (!launch_gemv(wfmt(down->fmt), PRO_SWIGLU, down->plan.waves, dim3(down->plan.gx, down->plan.splits), b, st))
+  if (!launch_linear(down, PRO_SWIGLU, b, st))
     return fail(TLM_ERR_STATE, "TLMGatedMLP: no kernel variant for this shape");
   CHECK_LAUNCH("TLMGatedMLP");
   if (!direct) {
@@ -661,7 +686,7 @@ int tlm_op_logits(tlm_linear* head, const float* x, float* logits, int32_t* toke
   a.arg_idx = ctx->arg_idx;
   if (gemv_smem_bytes(wfmt(head->fmt), p.cps, p.waves) > 65536)
     return fail(TLM_ERR_INVALID, "TLMLogits: hidden size %d too large for one block", head->K);
-  if (!launch_lm_head(wfmt(head->fmt), p.waves, dim3(p.gx), a, ctx->stream))
+  if (!launch_lm_head(wfmt(head->fmt), p.waves, p.nch, dim3(p.gx), a, ctx->stream))
     return fail(TLM_ERR_STATE, "TLMLogits: no kernel variant for this shape");
   // the sampled token lands in token[0] (the merge's ctrl[C_TOKEN])
   launch_argmax_merge(ctx->arg_val, ctx->arg_idx, p.gx, token, nullptr, 0, 0, EmbStage{}, ctx->stream);
@@ -787,6 +812,8 @@ void tlm_model_destroy(tlm_model* m) {
   hipStreamSynchronize(m->ctx->stream);
   if (m->g_logits) hipGraphExecDestroy(m->g_logits);
   if (m->g_prefill) hipGraphExecDestroy(m->g_prefill);
+  if (m->g_layers) hipGraphExecDestroy(m->g_layers);
+  if (m->graph_layers) hipGraphDestroy(m->graph_layers);
   if (m->graph_logits) hipGraphDestroy(m->graph_logits);
   if (m->graph_prefill) hipGraphDestroy(m->graph_prefill);
   for (auto& L : m->layers) {
@@ -905,7 +932,7 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which) {
     a.norm_w = L.attn_norm;
     a.eps = (float)d.rms_eps;
     a.xout = m->xa;
-    ok &= launch_gemv(wfmt(L.qkv->fmt), PRO_RMS, L.qkv->plan.waves, dim3(L.qkv->plan.gx, L.qkv->plan.splits), a, st);
+    ok &= launch_linear(L.qkv, PRO_RMS, a, st);
   }
   // 2. RoPE + KV append + split-K attention
   if (which < 0 || which == 1) {
@@ -924,7 +951,7 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which) {
     a.att_chmin = m->attn.chmin;
     a.att_window = d.sliding_window;
     a.att_max_tokens = d.max_tokens;
-    ok &= launch_gemv(wfmt(L.o->fmt), PRO_ATTN, L.o->plan.waves, dim3(L.o->plan.gx, L.o->plan.splits), a, st);
+    ok &= launch_linear(L.o, PRO_ATTN, a, st);
   }
   // 4. x_mid = x + O partials; RMSNorm; gate|up GEMV
   if (which < 0 || which == 2) {
@@ -938,7 +965,7 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which) {
     a.eps = (float)d.rms_eps;
     a.xout = m->xb;
     a.ctrl = m->ctrl;
-    ok &= launch_gemv(wfmt(L.gu->fmt), PRO_RMS, L.gu->plan.waves, dim3(L.gu->plan.gx, L.gu->plan.splits), a, st);
+    ok &= launch_linear(L.gu, PRO_RMS, a, st);
   }
   // 5. silu(gate) * up folded into the down GEMV
   if (which < 0 || which == 3) {
@@ -948,18 +975,22 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which) {
     a.n_pin = L.gu->plan.splits;
     a.pin_stride = 2 * I;
     a.up_off = I;
-    ok &= launch_gemv(wfmt(L.down->fmt), PRO_SWIGLU, L.down->plan.waves,
-                      dim3(L.down->plan.gx, L.down->plan.splits), a, st);
+    ok &= launch_linear(L.down, PRO_SWIGLU, a, st);
   }
   return ok;
 }
 
-static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, bool final_norm) {
+static void enqueue_final_norm(tlm_model* m, hipStream_t st) {
   const tlm_model_desc& d = m->d;
-  const Layer& last = m->layers.back();
-  if (final_norm)
-    launch_final_norm(m->xb, m->pd, last.down->plan.splits, d.hidden_size, m->final_norm, d.hidden_size,
-                      (float)d.rms_eps, m->xf, st);
+  launch_final_norm(m->xb, m->pd, m->layers.back().down->plan.splits, d.hidden_size, m->final_norm, d.hidden_size,
+                    (float)d.rms_eps, m->xf, st);
+}
+
+// Final norm (optional), LM head with the fused first argmax pass, argmax
+// merge.  `ev` (optional) brackets the LM head kernel with two events.
+static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, bool final_norm, hipEvent_t* ev = nullptr) {
+  const tlm_model_desc& d = m->d;
+  if (final_norm) enqueue_final_norm(m, st);
   GemvArgs a;
   fill_gemv_args(a, m->head, nullptr);
   a.cps = m->lm_plan.cps;
@@ -967,21 +998,29 @@ static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, bool final_
   a.logits = m->logits;
   a.arg_val = m->arg_val;
   a.arg_idx = m->arg_idx;
-  if (!launch_lm_head(wfmt(m->head->fmt), m->lm_plan.waves, dim3(m->lm_plan.gx), a, st)) return false;
+  if (ev) hipEventRecord(ev[0], st);
+  if (!launch_lm_head(wfmt(m->head->fmt), m->lm_plan.waves, m->lm_plan.nch, dim3(m->lm_plan.gx), a, st)) return false;
+  if (ev) hipEventRecord(ev[1], st);
   launch_argmax_merge(m->arg_val, m->arg_idx, m->lm_plan.gx, m->ctrl, advance ? m->tokens_out : nullptr,
                       advance ? 1 : 0, d.max_tokens, emb_stage(m), st);
   return true;
 }
 
-static int capture(tlm_model* m, bool logits, hipGraph_t* g, hipGraphExec_t* ge) {
+// Graph tails: the decode/logits step, the prefill step, or the layers and
+// final norm alone (LM head timing).
+enum GraphTail { TAIL_PREFILL = 0, TAIL_LOGITS = 1, TAIL_NORM = 2 };
+
+static int capture(tlm_model* m, int tail, hipGraph_t* g, hipGraphExec_t* ge) {
   hipStream_t st = m->ctx->stream;
   HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
   bool ok = true;
   for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1);
-  if (logits)
+  if (tail == TAIL_LOGITS)
     ok &= enqueue_head(m, st, true, true);
-  else
+  else if (tail == TAIL_PREFILL)
     launch_prefill_advance(m->ctrl, m->prompt, emb_stage(m), st);
+  else
+    enqueue_final_norm(m, st);
   hipError_t le = hipGetLastError();
   HIP_TRY(hipStreamEndCapture(st, g));
   if (le != hipSuccess) return fail(TLM_ERR_HIP, "TLMModel: launch during capture failed: %s", hipGetErrorString(le));
@@ -1000,8 +1039,8 @@ int tlm_model_finalize(tlm_model* m) {
     m->finalized = true;
     return TLM_OK;
   }
-  int rc = capture(m, true, &m->graph_logits, &m->g_logits);
-  if (rc == TLM_OK) rc = capture(m, false, &m->graph_prefill, &m->g_prefill);
+  int rc = capture(m, TAIL_LOGITS, &m->graph_logits, &m->g_logits);
+  if (rc == TLM_OK) rc = capture(m, TAIL_PREFILL, &m->graph_prefill, &m->g_prefill);
   if (rc) return rc;
   m->finalized = true;
   return TLM_OK;
@@ -1194,6 +1233,45 @@ int tlm_time_decode(tlm_model* m, int32_t token, int32_t position, int warmup, i
   hipEventDestroy(e0);
   hipEventDestroy(e1);
   *ms = f;
+  return TLM_OK;
+}
+
+int tlm_time_head(tlm_model* m, int32_t token, int32_t position, int n, double* avg_ms) {
+  if (!m || !avg_ms || n <= 0) return fail(TLM_ERR_INVALID, "TLMModel: invalid timing argument");
+  int rc = check_token(m, token, position);
+  if (rc) return rc;
+  if ((long)position + n > m->d.max_tokens) return fail(TLM_ERR_RANGE, "TLMModel: timed decode passes max_tokens");
+  rc = tlm_model_finalize(m);
+  if (rc) return rc;
+  hipStream_t st = m->ctx->stream;
+  if (m->use_graphs && !m->g_layers) {
+    rc = capture(m, TAIL_NORM, &m->graph_layers, &m->g_layers);
+    if (rc) return rc;
+  }
+  std::vector<hipEvent_t> ev(2 * (size_t)n, nullptr);
+  for (auto& e : ev) HIP_TRY(hipEventCreate(&e));
+  launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
+  bool ok = true;
+  for (int i = 0; i < n && ok; i++) {
+    if (m->use_graphs) {
+      HIP_TRY(hipGraphLaunch(m->g_layers, st));
+    } else {
+      for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1);
+      enqueue_final_norm(m, st);
+    }
+    ok &= enqueue_head(m, st, true, false, &ev[2 * (size_t)i]);
+  }
+  if (!ok) return fail(TLM_ERR_STATE, "TLMModel: no kernel variant for a stage of this model");
+  CHECK_LAUNCH("TLMModel");
+  HIP_TRY(hipStreamSynchronize(st));
+  double total = 0.0;
+  for (int i = 0; i < n; i++) {
+    float f = 0.f;
+    HIP_TRY(hipEventElapsedTime(&f, ev[2 * i], ev[2 * i + 1]));
+    total += f;
+  }
+  for (auto& e : ev) hipEventDestroy(e);
+  *avg_ms = total / n;
   return TLM_OK;
 }
 

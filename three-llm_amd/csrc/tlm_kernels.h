@@ -6,7 +6,7 @@
 namespace tlm {
 
 constexpr int kTile = 64;      // output rows per tile: one row per lane of a wave64
-constexpr int kMaxChunks = 8;  // 16-byte chunks a wave keeps in flight per batch
+constexpr int kMaxChunks = 8;  // most 16-byte chunks a wave keeps in flight per batch
 constexpr int kMaxPart = 8;    // partial vectors a consumer folds in with one round trip
 
 enum WeightFmt { WF_F16 = 1, WF_Q4 = 2 };
@@ -97,8 +97,9 @@ struct AttnArgs {
 
 // launchers (stream-ordered, graph-capturable: no memset, no host sync)
 // launchers return false when no compiled variant matches (nothing is launched)
-bool launch_gemv(int fmt, int pro, int waves, dim3 grid, const GemvArgs& a, hipStream_t st);
-bool launch_lm_head(int fmt, int waves, dim3 grid, const GemvArgs& a, hipStream_t st);
+// waves in {4, 8}; nch in {1, 2, 4, 8}: chunks per wave and load batch
+bool launch_gemv(int fmt, int pro, int waves, int nch, dim3 grid, const GemvArgs& a, hipStream_t st);
+bool launch_lm_head(int fmt, int waves, int nch, dim3 grid, const GemvArgs& a, hipStream_t st);
 // attention chunk partials; with `combine` also the combine kernel writing a.out
 bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, bool combine, hipStream_t st);
 size_t gemv_smem_bytes(int fmt, int cps, int waves);
@@ -114,6 +115,7 @@ void launch_argmax_merge(const float* pval, const int* pidx, int n, int* ctrl, i
 void launch_set_ctrl(int* ctrl, int token, int pos, int step, int base, int len, const EmbStage& es,
                      hipStream_t st);
 void launch_prefill_advance(int* ctrl, const int* prompt, const EmbStage& es, hipStream_t st);
+void launch_copy(uint4* dst, const uint4* src, size_t n16, hipStream_t st);
 void launch_dequant(int fmt, const uint4* w, const uint16_t* s, int N, int T, int C, int K, float* out,
                     hipStream_t st);
 void launch_kv_fill(void* kc, void* vc, bool f32, size_t heads_stride, int Hkv, int max_tokens, int D, int count,

@@ -393,11 +393,13 @@ __device__ __forceinline__ float dot_f16(const uint4 d, const float* __restrict_
   return a0 + a1;
 }
 
-template <int FMT>
+// NCH: chunks a wave keeps in flight per batch (>= its chunk count when that
+// fits, so no load is a clamped duplicate).
+template <int FMT, int NCH>
 struct GemvCore {
   static constexpr int CK = FMT == WF_Q4 ? 32 : 8;  // k per 16-byte chunk
-  uint4 d[kMaxChunks];
-  uint16_t sc[kMaxChunks];
+  uint4 d[NCH];
+  uint16_t sc[NCH];
 
   // Loads of batch b: unconditional (chunk index clamped to this wave's last
   // chunk, or to the slice's last chunk for a wave without chunks), so the
@@ -407,7 +409,7 @@ struct GemvCore {
     const int lane = threadIdx.x & 63;
     const uint4* wt = a.w + (size_t)t * a.C * kTile;
 #pragma unroll
-    for (int u = 0; u < kMaxChunks; u++) {
+    for (int u = 0; u < NCH; u++) {
       const int c = c0 + min(wave + min(b + u, max(nw, 1) - 1) * W, ncl - 1);
       d[u] = wt[(size_t)c * kTile + lane];
       if (FMT == WF_Q4) sc[u] = a.s[((size_t)t * a.C + c) * kTile + lane];
@@ -417,7 +419,7 @@ struct GemvCore {
   __device__ __forceinline__ float compute(const float* xl, const float* xsum, int wave, int W, int nw, int b) const {
     float acc = 0.f;
 #pragma unroll
-    for (int u = 0; u < kMaxChunks; u++) {
+    for (int u = 0; u < NCH; u++) {
       if (b + u < nw) {  // wave-uniform
         const int cl = wave + (b + u) * W;
         if (FMT == WF_Q4)
@@ -445,10 +447,10 @@ struct GemvSmem {
   }
 };
 
-template <int FMT, int PRO, int W>
+template <int FMT, int PRO, int W, int NCH>
 __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvArgs a) {
   extern __shared__ float sm[];
-  constexpr int CK = GemvCore<FMT>::CK;
+  constexpr int CK = GemvCore<FMT, NCH>::CK;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int s = blockIdx.y;
   const int c0 = s * a.cps, c1 = min(a.C, c0 + a.cps);
@@ -459,7 +461,7 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvArgs a) {
 
   GemvPrologue<PRO, FMT> pro;
   pro.issue(a, k0, ncl * CK);
-  GemvCore<FMT> core;
+  GemvCore<FMT, NCH> core;
   int t = blockIdx.x;
   core.load(a, t, c0, ncl, wave, W, nw, 0);  // weights in flight during the prologue (t < T: gridDim.x <= T)
   __builtin_amdgcn_sched_barrier(0);  // keep every load issued before the prologue's first wait
@@ -467,7 +469,7 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvArgs a) {
   __syncthreads();
   for (; t < a.T; t += gridDim.x) {
     float acc = 0.f;
-    for (int b = 0; b < nw; b += kMaxChunks) {
+    for (int b = 0; b < nw; b += NCH) {
       if (b > 0 || t != (int)blockIdx.x) core.load(a, t, c0, ncl, wave, W, nw, b);
       acc += core.compute(L.xl, L.xsum, wave, W, nw, b);
     }
@@ -490,10 +492,10 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvArgs a) {
 // LM head: GEMV over the vocabulary (PRO_COPY input) with the first pass of
 // the greedy sampler fused in (createChunkPartialMaxNode, TSLLogits.ts:201-248):
 // each block keeps its best (score, id) over its tiles.
-template <int FMT, int W>
+template <int FMT, int W, int NCH>
 __global__ __launch_bounds__(W * 64) void lm_head_kernel(GemvArgs a) {
   extern __shared__ float sm[];
-  constexpr int CK = GemvCore<FMT>::CK;
+  constexpr int CK = GemvCore<FMT, NCH>::CK;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ncl = a.C;
   GemvSmem L(sm, a.cps, CK, W);
@@ -501,7 +503,7 @@ __global__ __launch_bounds__(W * 64) void lm_head_kernel(GemvArgs a) {
 
   GemvPrologue<PRO_COPY, FMT> pro;
   pro.issue(a, 0, ncl * CK);
-  GemvCore<FMT> core;
+  GemvCore<FMT, NCH> core;
   int t = blockIdx.x;
   core.load(a, t, 0, ncl, wave, W, nw, 0);  // gridDim.x <= T
   __builtin_amdgcn_sched_barrier(0);
@@ -511,7 +513,7 @@ __global__ __launch_bounds__(W * 64) void lm_head_kernel(GemvArgs a) {
   int best_i = 0x7fffffff;
   for (; t < a.T; t += gridDim.x) {
     float acc = 0.f;
-    for (int b = 0; b < nw; b += kMaxChunks) {
+    for (int b = 0; b < nw; b += NCH) {
       if (b > 0 || t != (int)blockIdx.x) core.load(a, t, 0, ncl, wave, W, nw, b);
       acc += core.compute(L.xl, L.xsum, wave, W, nw, b);
     }
@@ -607,18 +609,19 @@ size_t gemv_smem_bytes(int fmt, int cps, int waves) {
   return sizeof(float) * ((size_t)cps * CK + cps + waves * kTile + 64);
 }
 
-bool launch_gemv(int fmt, int pro, int waves, dim3 grid, const GemvArgs& a, hipStream_t st) {
+bool launch_gemv(int fmt, int pro, int waves, int nch, dim3 grid, const GemvArgs& a, hipStream_t st) {
   const size_t smem = gemv_smem_bytes(fmt, a.cps, waves);
   // the RMS prologue keeps one (PRO_RMS) or two (PRO_RMS2) float4s of the
   // residual row per thread
   if (pro == PRO_RMS && a.K > 4 * 64 * waves) pro = PRO_RMS2;
   if (pro == PRO_RMS2 && a.K > 8 * 64 * waves) return false;
-#define GEMV_CASE(F, P, Wv)                                                           \
-  if (fmt == F && pro == P && waves == Wv) {                                          \
-    hipLaunchKernelGGL((gemv_kernel<F, P, Wv>), grid, dim3(Wv * 64), smem, st, a);    \
-    return true;                                                                      \
+#define GEMV_CASE(F, P, Wv, N)                                                          \
+  if (fmt == F && pro == P && waves == Wv && nch == N) {                                \
+    hipLaunchKernelGGL((gemv_kernel<F, P, Wv, N>), grid, dim3(Wv * 64), smem, st, a);   \
+    return true;                                                                        \
   }
-#define GEMV_W(F, P) GEMV_CASE(F, P, 1) GEMV_CASE(F, P, 2) GEMV_CASE(F, P, 4) GEMV_CASE(F, P, 8)
+#define GEMV_N(F, P, Wv) GEMV_CASE(F, P, Wv, 1) GEMV_CASE(F, P, Wv, 2) GEMV_CASE(F, P, Wv, 4) GEMV_CASE(F, P, Wv, 8)
+#define GEMV_W(F, P) GEMV_N(F, P, 4) GEMV_N(F, P, 8)
   GEMV_W(WF_Q4, PRO_COPY)
   GEMV_W(WF_Q4, PRO_RMS)
   GEMV_W(WF_Q4, PRO_RMS2)
@@ -630,18 +633,21 @@ bool launch_gemv(int fmt, int pro, int waves, dim3 grid, const GemvArgs& a, hipS
   GEMV_W(WF_F16, PRO_RMS2)
   GEMV_W(WF_F16, PRO_SWIGLU)
 #undef GEMV_W
+#undef GEMV_N
 #undef GEMV_CASE
   return false;
 }
 
-bool launch_lm_head(int fmt, int waves, dim3 grid, const GemvArgs& a, hipStream_t st) {
+bool launch_lm_head(int fmt, int waves, int nch, dim3 grid, const GemvArgs& a, hipStream_t st) {
   const size_t smem = gemv_smem_bytes(fmt, a.cps, waves);
-#define LM_CASE(F, Wv)                                                                \
-  if (fmt == F && waves == Wv) {                                                      \
-    hipLaunchKernelGGL((lm_head_kernel<F, Wv>), grid, dim3(Wv * 64), smem, st, a);    \
-    return true;                                                                      \
+#define LM_CASE(F, Wv, N)                                                               \
+  if (fmt == F && waves == Wv && nch == N) {                                            \
+    hipLaunchKernelGGL((lm_head_kernel<F, Wv, N>), grid, dim3(Wv * 64), smem, st, a);   \
+    return true;                                                                        \
   }
-  LM_CASE(WF_F16, 4) LM_CASE(WF_F16, 8) LM_CASE(WF_Q4, 4) LM_CASE(WF_Q4, 8)
+#define LM_N(F, Wv) LM_CASE(F, Wv, 1) LM_CASE(F, Wv, 2) LM_CASE(F, Wv, 4) LM_CASE(F, Wv, 8)
+  LM_N(WF_F16, 4) LM_N(WF_F16, 8) LM_N(WF_Q4, 4) LM_N(WF_Q4, 8)
+#undef LM_N
 #undef LM_CASE
   return false;
 }
@@ -1203,6 +1209,17 @@ __global__ void prefill_advance_kernel(int* ctrl, const int* prompt, EmbStage es
 
 void launch_prefill_advance(int* ctrl, const int* prompt, const EmbStage& es, hipStream_t st) {
   hipLaunchKernelGGL(prefill_advance_kernel, dim3(1), dim3(256), 0, st, ctrl, prompt, es);
+}
+
+// Streaming copy, 16 bytes per lane per iteration.
+__global__ __launch_bounds__(256) void copy_kernel(uint4* __restrict__ dst, const uint4* __restrict__ src, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
+void launch_copy(uint4* dst, const uint4* src, size_t n16, hipStream_t st) {
+  const size_t blocks = std::min<size_t>((n16 + 255) / 256, 8192);
+  hipLaunchKernelGGL(copy_kernel, dim3((unsigned)blocks), dim3(256), 0, st, dst, src, n16);
 }
 
 __global__ void dequant_kernel(int fmt, const uint4* w, const uint16_t* s, int N, int C, int K, float* out) {

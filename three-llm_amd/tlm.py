@@ -22,12 +22,12 @@ LOGITS = 1
 # exported symbols (checked by the CPU test suite against include/tlm.h)
 EXPORTS = [
     "tlm_abi_version", "tlm_last_error", "tlm_open", "tlm_close", "tlm_sync", "tlm_device_info", "tlm_alloc",
-    "tlm_free", "tlm_upload", "tlm_download", "tlm_linear_create", "tlm_linear_destroy", "tlm_linear_dequant",
+    "tlm_free", "tlm_upload", "tlm_download", "tlm_copy", "tlm_linear_create", "tlm_linear_destroy", "tlm_linear_dequant",
     "tlm_op_linear", "tlm_op_rmsnorm", "tlm_op_silu_mul", "tlm_op_gated_mlp", "tlm_attn_create", "tlm_attn_destroy",
     "tlm_op_attention", "tlm_attn_reset", "tlm_attn_read_cache", "tlm_op_logits", "tlm_op_argmax",
     "tlm_model_create", "tlm_model_destroy", "tlm_model_upload", "tlm_model_finalize", "tlm_compute_token",
     "tlm_prefill", "tlm_read_logits", "tlm_read_token", "tlm_decode_greedy", "tlm_reset_cache", "tlm_kv_write",
-    "tlm_kv_read", "tlm_kv_fill_normal", "tlm_read_hidden", "tlm_time_decode", "tlm_time_kernel",
+    "tlm_kv_read", "tlm_kv_fill_normal", "tlm_read_hidden", "tlm_time_decode", "tlm_time_kernel", "tlm_time_head",
     "tlm_model_describe", "tlm_synth_normal", "tlm_synth_tokens", "tlm_quantize_q4", "tlm_f32_to_f16",
 ]
 
@@ -79,6 +79,7 @@ def lib():
             "tlm_free": ([VP, VP], ctypes.c_int),
             "tlm_upload": ([VP, VP, VP, sz], ctypes.c_int),
             "tlm_download": ([VP, VP, VP, sz], ctypes.c_int),
+            "tlm_copy": ([VP, VP, VP, sz], ctypes.c_int),
             "tlm_linear_create": ([VP, ctypes.c_int, ctypes.c_int, ctypes.c_int, VP, VP, ctypes.POINTER(VP)],
                                   ctypes.c_int),
             "tlm_linear_destroy": ([VP], None),
@@ -110,6 +111,7 @@ def lib():
             "tlm_read_hidden": ([VP, VP, sz], ctypes.c_int),
             "tlm_time_decode": ([VP, i32, i32, ctypes.c_int, ctypes.c_int, ctypes.POINTER(dbl)], ctypes.c_int),
             "tlm_time_kernel": ([VP, ctypes.c_int, ctypes.c_int, ctypes.POINTER(dbl)], ctypes.c_int),
+            "tlm_time_head": ([VP, i32, i32, ctypes.c_int, ctypes.POINTER(dbl)], ctypes.c_int),
             "tlm_model_describe": ([VP, ctypes.c_char_p, sz], ctypes.c_int),
             "tlm_synth_normal": ([u64, u64, sz, ctypes.c_float, VP], ctypes.c_int),
             "tlm_synth_tokens": ([u64, u64, sz, i32, VP], ctypes.c_int),
@@ -192,6 +194,12 @@ class Buffer:
         out = np.empty(n, dtype)
         check(lib().tlm_download(self.ctx.ptr, _ptr(out), self.ptr, out.nbytes))
         return out
+
+    def copy_from(self, src: "Buffer", nbytes: Optional[int] = None) -> "Buffer":
+        """Device-to-device copy on the context stream (asynchronous)."""
+        n = min(self.nbytes, src.nbytes) if nbytes is None else nbytes
+        check(lib().tlm_copy(self.ctx.ptr, self.ptr, src.ptr, n))
+        return self
 
     def free(self):
         if self.ptr:
@@ -391,6 +399,12 @@ class Model:
     def time_decode(self, token: int, position: int, warmup: int, n: int) -> float:
         ms = ctypes.c_double()
         check(lib().tlm_time_decode(self.ptr, int(token), int(position), warmup, n, ctypes.byref(ms)))
+        return ms.value
+
+    def time_head(self, token: int, position: int, n: int) -> float:
+        """Average ms of the LM head kernel inside n real decode steps."""
+        ms = ctypes.c_double()
+        check(lib().tlm_time_head(self.ptr, int(token), int(position), n, ctypes.byref(ms)))
         return ms.value
 
     def time_kernel(self, which: int, iters: int) -> float:
