@@ -175,6 +175,16 @@ def main():
     lm_ms = runner.model.time_head(last, pos0, min(steps, args.kernel_iters))
     lm_bytes = lm_head_bytes(hw)
     lm_bw = lm_bytes / (lm_ms * 1e-3)
+    # host-driven loop (computeToken + sampleToken per token: one 4-byte
+    # device-to-host read and one stream sync per token over PCIe)
+    n_host = min(steps, 64)
+    tok = last
+    ctx.sync()
+    th = time.perf_counter()
+    for i in range(n_host):
+        runner.computeToken(int(tok), pos0 + i, True)
+        tok = runner.sampleToken(1, {"temperature": 0})
+    host_tok_s = n_host / (time.perf_counter() - th)
     stage_ms = {name: runner.model.time_kernel(k, args.kernel_iters)
                 for name, k in (("qkv", 4), ("attention", 1), ("o", 5), ("gate_up", 2), ("down", 3))}
     log(f"[bench] decode {toks:.1f} tok/s ({ms_step * 1e3:.1f} us/token wall, {ev_ms * 1e3 / steps:.1f} us/token "
@@ -182,6 +192,7 @@ def main():
     log(f"[bench] LM head {lm_ms * 1e3:.1f} us/launch in decode steps = {lm_bw / 1e9:.0f} GB/s; stage times, "
         f"back-to-back launches of layer 0 (us): "
         + ", ".join(f"{k} {v * 1e3:.1f}" for k, v in stage_ms.items()))
+    log(f"[bench] host-driven loop (token read back every step): {host_tok_s:.1f} tok/s")
     log(f"[bench] prefill {prefill_n} tokens in {prefill_s * 1e3:.1f} ms; first tokens {list(tokens[:8])}")
     cpu = None
     if args.cpu_budget > 0:
@@ -208,6 +219,7 @@ def main():
         "hbm_roofline_frac": round(hbm_frac, 4),
         "bytes_per_token": round(mean_bytes),
         "prefill_tok_s": round(prefill_n / prefill_s, 1) if prefill_n > 0 and prefill_s > 0 else None,
+        "host_loop_tok_s": round(host_tok_s, 1),
         "config": {"workload": wl.name, "prompt": wl.prompt_len, "decode": steps, "batch": 1,
                    "linears": wl.storage.linear + (" g32 fp16 scales" if wl.storage.linear == "q4" else ""),
                    "head": "fp16 tied" if hw.recipe.tied_embeddings else wl.storage.head, "kv": wl.storage.kv,
