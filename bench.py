@@ -186,7 +186,7 @@ def main():
         tok = runner.sampleToken(1, {"temperature": 0})
     host_tok_s = n_host / (time.perf_counter() - th)
     stage_ms = {name: runner.model.time_kernel(k, args.kernel_iters)
-                for name, k in (("qkv", 4), ("attention", 1), ("o", 5), ("gate_up", 2), ("down", 3))}
+                for name, k in (("qkv", 4), ("attention", 1), ("o", 5), ("mlp", 2))}
     log(f"[bench] decode {toks:.1f} tok/s ({ms_step * 1e3:.1f} us/token wall, {ev_ms * 1e3 / steps:.1f} us/token "
         f"events), {mean_bytes / 1e6:.2f} MB/token -> {hbm_frac * 100:.1f}% of HBM roofline")
     log(f"[bench] LM head {lm_ms * 1e3:.1f} us/launch in decode steps = {lm_bw / 1e9:.0f} GB/s; stage times, "

@@ -202,8 +202,10 @@ int tlm_read_hidden(tlm_model* model, float* out, size_t n);
 /* Timing with HIP events on the model stream.  tlm_time_decode: greedy
  * decode of n tokens after `warmup` untimed ones, from `position`; ms total.
  * tlm_time_kernel: average ms of one launch of kernel `which` (0 = LM head,
- * 1 = attention of layer 0, 2 = gate/up of layer 0, 3 = down of layer 0,
- * 4 = QKV of layer 0, 5 = O of layer 0) over iters launches. */
+ * 1 = attention of layer 0, 2 = fused gate|up/SwiGLU/down MLP of layer 0,
+ * 4 = QKV of layer 0, 5 = O of layer 0) over iters back-to-back launches;
+ * afterwards the residual accumulators are cleared (the next token starts
+ * from the cache and ctrl state as left). */
 int tlm_time_decode(tlm_model* model, int32_t token, int32_t position, int warmup, int n, double* ms);
 int tlm_time_kernel(tlm_model* model, int which, int iters, double* avg_ms);
 /* tlm_time_head: n greedy decode steps from (token, position), each the layer

@@ -67,7 +67,17 @@ struct tlm_linear {
   uint16_t* s = nullptr;
   GemvPlan plan;
   float* part = nullptr;  // op-level partials [splits][N]
+  // paired layout (fused MLP gate|up, N = 2I): canonical gate row i sits in
+  // tile i / 32, lane i % 32; up row I + i in the same tile, lane 32 + i % 32
+  int pair_half = 0;  // I when paired, else 0
 };
+
+// Physical row of canonical row r.
+static int phys_row(const tlm_linear* L, int r) {
+  if (!L->pair_half) return r;
+  const int I = L->pair_half, up = r >= I, i = up ? r - I : r;
+  return (i / 32) * kTile + (up ? 32 : 0) + i % 32;
+}
 
 struct tlm_attn {
   tlm_ctx* ctx = nullptr;
@@ -108,9 +118,13 @@ struct tlm_model {
   int* ctrl = nullptr;
   int* tokens_out = nullptr;
   int* prompt = nullptr;
-  float *xa = nullptr, *xb = nullptr, *xf = nullptr, *attn_out = nullptr;
-  float* x0 = nullptr;  // embedding row of the current token (staged by the control kernels)
-  float *pq = nullptr, *po = nullptr, *pgu = nullptr, *pd = nullptr;
+  float *xa = nullptr, *xf = nullptr, *attn_out = nullptr;
+  // residual accumulators (fixed point, kRep replicas of H): x0 holds the
+  // current token's embedding row (staged by the control kernels), rb[l] the
+  // residual after layer l's MLP
+  unsigned long long *x0 = nullptr, *rb = nullptr;
+  float *pq = nullptr, *po = nullptr;
+  int mlp_nch = 1, mlp_ndb = 1;
   float* logits = nullptr;
   float* arg_val = nullptr;
   int* arg_idx = nullptr;
@@ -180,10 +194,12 @@ static void rms_waves(tlm_linear* L) {
 // Tiles shared with rows outside the range are read back first.
 static int linear_write_rows(tlm_linear* L, int r0, int rows, const void* data, const uint16_t* scales) {
   if (rows <= 0) return TLM_OK;
-  const int t0 = r0 / kTile, t1 = (r0 + rows - 1) / kTile + 1;
+  int t0 = r0 / kTile, t1 = (r0 + rows - 1) / kTile + 1;
+  if (L->pair_half) t0 = 0, t1 = L->T;
   const size_t tiles = (size_t)(t1 - t0);
   const size_t chunk_elems = (size_t)L->C * kTile;  // chunks per tile
-  const bool aligned = (r0 % kTile == 0) && ((r0 + rows) % kTile == 0 || r0 + rows == L->N);
+  const bool aligned =
+      !L->pair_half && (r0 % kTile == 0) && ((r0 + rows) % kTile == 0 || r0 + rows == L->N);
   hipStream_t st = L->ctx->stream;
   HIP_TRY(hipStreamSynchronize(st));
   if (data) {
@@ -193,7 +209,8 @@ static int linear_write_rows(tlm_linear* L, int r0, int rows, const void* data, 
     const int CK = chunk_k(L->fmt);
     const int Kc = L->fmt == TLM_FMT_Q4 ? L->K / 2 : L->K;  // canonical row length in units
     for (int r = r0; r < r0 + rows; r++) {
-      const int t = r / kTile - t0, lane = r % kTile;
+      const int pr = phys_row(L, r);
+      const int t = pr / kTile - t0, lane = pr % kTile;
       for (int c = 0; c < L->C; c++) {
         uint4 v = {0, 0, 0, 0};
         if (L->fmt == TLM_FMT_Q4) {
@@ -219,7 +236,8 @@ static int linear_write_rows(tlm_linear* L, int r0, int rows, const void* data, 
     if (!aligned) HIP_TRY(hipMemcpy(host.data(), dst, host.size() * sizeof(uint16_t), hipMemcpyDeviceToHost));
     const int G = L->K / 32;
     for (int r = r0; r < r0 + rows; r++) {
-      const int t = r / kTile - t0, lane = r % kTile;
+      const int pr = phys_row(L, r);
+      const int t = pr / kTile - t0, lane = pr % kTile;
       for (int c = 0; c < L->C; c++)
         host[((size_t)t * L->C + c) * kTile + lane] = c < G ? scales[(size_t)(r - r0) * G + c] : 0;
     }
@@ -228,7 +246,8 @@ static int linear_write_rows(tlm_linear* L, int r0, int rows, const void* data, 
   return TLM_OK;
 }
 
-static int linear_alloc(tlm_ctx* ctx, int fmt, int N, int K, bool single_split, tlm_linear** out) {
+static int linear_alloc(tlm_ctx* ctx, int fmt, int N, int K, bool single_split, tlm_linear** out,
+                        bool paired = false) {
   if (fmt != TLM_FMT_F16 && fmt != TLM_FMT_Q4) return fail(TLM_ERR_INVALID, "TLMLinear: unsupported format %d", fmt);
   if (N <= 0 || K <= 0) return fail(TLM_ERR_INVALID, "TLMLinear: invalid shape %dx%d", N, K);
   if (fmt == TLM_FMT_Q4 && K % 32 != 0) return fail(TLM_ERR_INVALID, "TLMLinear: q4 needs K %% 32 == 0 (K=%d)", K);
@@ -238,6 +257,10 @@ static int linear_alloc(tlm_ctx* ctx, int fmt, int N, int K, bool single_split, 
   L->N = N;
   L->K = K;
   L->T = (N + kTile - 1) / kTile;
+  if (paired) {
+    L->pair_half = N / 2;
+    L->T = (N / 2 + 31) / 32;
+  }
   L->C = (K + chunk_k(fmt) - 1) / chunk_k(fmt);
   L->plan = plan_gemv(L->T, L->C, ctx->cus, chunk_k(fmt), single_split);
   const size_t chunks = (size_t)L->T * L->C * kTile;
@@ -759,12 +782,9 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
   for (auto& L : m->layers) {
     M_TRY(linear_alloc(ctx, lf, m->Nqkv, H, false, &L.qkv));
     M_TRY(linear_alloc(ctx, lf, H, m->QS, false, &L.o));
-    M_TRY(linear_alloc(ctx, lf, 2 * I, H, false, &L.gu));
+    M_TRY(linear_alloc(ctx, lf, 2 * I, H, false, &L.gu, true));
     M_TRY(linear_alloc(ctx, lf, H, I, false, &L.down));
-    if (rc == TLM_OK) {
-      rms_waves(L.qkv);
-      rms_waves(L.gu);
-    }
+    if (rc == TLM_OK) rms_waves(L.qkv);
     M_TRY(model_alloc((void**)&L.attn_norm, sizeof(float) * H));
     M_TRY(model_alloc((void**)&L.ffn_norm, sizeof(float) * H));
     if (d->qkv_bias) M_TRY(model_alloc((void**)&L.bqkv, sizeof(float) * m->Nqkv));
@@ -778,16 +798,22 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
   M_TRY(model_alloc((void**)&m->tokens_out, sizeof(int) * d->max_tokens));
   M_TRY(model_alloc((void**)&m->prompt, sizeof(int) * d->max_tokens));
   M_TRY(model_alloc((void**)&m->xa, sizeof(float) * H));
-  M_TRY(model_alloc((void**)&m->x0, sizeof(float) * H));
-  M_TRY(model_alloc((void**)&m->xb, sizeof(float) * H));
+  M_TRY(model_alloc((void**)&m->x0, sizeof(unsigned long long) * kRep * H));
+  M_TRY(model_alloc((void**)&m->rb, sizeof(unsigned long long) * kRep * H * d->num_layers));
   M_TRY(model_alloc((void**)&m->xf, sizeof(float) * H));
   M_TRY(model_alloc((void**)&m->attn_out, sizeof(float) * m->QS));
   if (rc == TLM_OK) {
     const Layer& L0 = m->layers[0];
     M_TRY(model_alloc((void**)&m->pq, sizeof(float) * L0.qkv->plan.splits * m->Nqkv));
     M_TRY(model_alloc((void**)&m->po, sizeof(float) * L0.o->plan.splits * H));
-    M_TRY(model_alloc((void**)&m->pgu, sizeof(float) * L0.gu->plan.splits * 2 * I));
-    M_TRY(model_alloc((void**)&m->pd, sizeof(float) * L0.down->plan.splits * H));
+    // fused MLP: 8 waves; gate|up chunks and down (tile, chunk) items per wave
+    const int per = (L0.gu->C + kMlpWaves - 1) / kMlpWaves;
+    m->mlp_nch = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : 8;
+    const int items = L0.down->T * (32 / chunk_k(lf));
+    const int dper = (items + kMlpWaves - 1) / kMlpWaves;
+    m->mlp_ndb = dper <= 1 ? 1 : dper <= 2 ? 2 : 4;
+    if (mlp_smem_bytes(wfmt(lf), L0.gu->C, H) > 65536)
+      rc = fail(TLM_ERR_INVALID, "TLMModel: hidden size %d too large for the fused MLP block", H);
     m->lm_plan = plan_gemv(m->head->T, m->head->C, ctx->cus, chunk_k(m->head->fmt), true);
     m->lm_plan.gx = std::min(m->head->T, 4096);
     if (gemv_smem_bytes(wfmt(m->head->fmt), m->lm_plan.cps, m->lm_plan.waves) > 65536)
@@ -829,8 +855,8 @@ void tlm_model_destroy(tlm_model* m) {
   }
   tlm_linear_destroy(m->head);
   attn_free(&m->attn, false);
-  void* bufs[] = {m->emb, m->final_norm, m->ctrl, m->tokens_out, m->prompt, m->xa, m->x0, m->xb, m->xf, m->attn_out,
-                  m->pq, m->po, m->pgu, m->pd, m->logits, m->arg_val, m->arg_idx};
+  void* bufs[] = {m->emb, m->final_norm, m->ctrl, m->tokens_out, m->prompt, m->xa, m->x0, m->xf, m->attn_out,
+                  m->pq, m->po, m->rb, m->logits, m->arg_val, m->arg_idx};
   for (void* p : bufs) hipFree(p);
   delete m;
 }
@@ -912,27 +938,19 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which) {
   const tlm_model_desc& d = m->d;
   const int H = d.hidden_size, I = d.intermediate_size;
   Layer& L = m->layers[l];
-  const Layer& P = m->layers[l > 0 ? l - 1 : 0];
-  // 1. x = (layer 0: embedding row; else x_mid + down partials); RMSNorm; QKV GEMV
+  const int nl = d.num_layers;
+  const size_t rstride = (size_t)kRep * H;
+  // 1. x = residual accumulator (layer 0: the staged embedding row); RMSNorm;
+  //    QKV GEMV.  Block (0,0) stores x for the MLP.
   if (which < 0 || which == 4) {
     GemvArgs a;
     fill_gemv_args(a, L.qkv, m->pq);
-    if (l == 0) {
-      a.base = m->x0;
-      a.pin = m->x0;  // never summed (n_pin 0), but loaded: must be a valid vector
-      a.n_pin = 0;
-      a.pin_stride = H;
-    } else {
-      a.base = m->xb;
-      a.pin = m->pd;
-      a.n_pin = P.down->plan.splits;
-      a.pin_stride = H;
-    }
+    a.acc_in = l == 0 ? m->x0 : m->rb + (size_t)(l - 1) * rstride;
     a.ctrl = m->ctrl;
     a.norm_w = L.attn_norm;
     a.eps = (float)d.rms_eps;
     a.xout = m->xa;
-    ok &= launch_linear(L.qkv, PRO_RMS, a, st);
+    ok &= launch_linear(L.qkv, PRO_RMSF, a, st);
   }
   // 2. RoPE + KV append + split-K attention
   if (which < 0 || which == 1) {
@@ -951,38 +969,39 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which) {
     a.att_chmin = m->attn.chmin;
     a.att_window = d.sliding_window;
     a.att_max_tokens = d.max_tokens;
+    // the accumulator layer l - 1 produced was last read by this layer's QKV
+    // (layer 0: the previous token's final norm): clear it for its next use
+    a.zero_ptr = m->rb + (size_t)((l + nl - 1) % nl) * rstride;
+    a.zero_n = (int)rstride;
     ok &= launch_linear(L.o, PRO_ATTN, a, st);
   }
-  // 4. x_mid = x + O partials; RMSNorm; gate|up GEMV
+  // 4. x_mid = x + O partials; RMSNorm; gate|up; SwiGLU; down, accumulated
+  //    with x_mid into rb[l]
   if (which < 0 || which == 2) {
-    GemvArgs a;
-    fill_gemv_args(a, L.gu, m->pgu);
-    a.base = m->xa;
-    a.pin = m->po;
-    a.n_pin = L.o->plan.splits;
-    a.pin_stride = H;
-    a.norm_w = L.ffn_norm;
-    a.eps = (float)d.rms_eps;
-    a.xout = m->xb;
-    a.ctrl = m->ctrl;
-    ok &= launch_linear(L.gu, PRO_RMS, a, st);
+    MlpArgs a;
+    fill_gemv_args(a.g, L.gu, nullptr);
+    a.g.base = m->xa;
+    a.g.pin = m->po;
+    a.g.n_pin = L.o->plan.splits;
+    a.g.pin_stride = H;
+    a.g.norm_w = L.ffn_norm;
+    a.g.eps = (float)d.rms_eps;
+    a.g.ctrl = m->ctrl;
+    a.wd = L.down->w;
+    a.sd = L.down->s;
+    a.Td = L.down->T;
+    a.Cd = L.down->C;
+    a.H = H;
+    a.acc = m->rb + (size_t)l * rstride;
+    ok &= launch_mlp(wfmt(L.gu->fmt), m->mlp_nch, m->mlp_ndb, L.gu->T, a, st);
   }
-  // 5. silu(gate) * up folded into the down GEMV
-  if (which < 0 || which == 3) {
-    GemvArgs a;
-    fill_gemv_args(a, L.down, m->pd);
-    a.pin = m->pgu;
-    a.n_pin = L.gu->plan.splits;
-    a.pin_stride = 2 * I;
-    a.up_off = I;
-    ok &= launch_linear(L.down, PRO_SWIGLU, a, st);
-  }
+  (void)I;
   return ok;
 }
 
 static void enqueue_final_norm(tlm_model* m, hipStream_t st) {
   const tlm_model_desc& d = m->d;
-  launch_final_norm(m->xb, m->pd, m->layers.back().down->plan.splits, d.hidden_size, m->final_norm, d.hidden_size,
+  launch_final_norm(m->rb + (size_t)(d.num_layers - 1) * kRep * d.hidden_size, m->final_norm, d.hidden_size,
                     (float)d.rms_eps, m->xf, st);
 }
 
@@ -1276,7 +1295,7 @@ int tlm_time_head(tlm_model* m, int32_t token, int32_t position, int n, double* 
 }
 
 int tlm_time_kernel(tlm_model* m, int which, int iters, double* avg_ms) {
-  if (!m || !avg_ms || iters <= 0 || which < 0 || which > 5)
+  if (!m || !avg_ms || iters <= 0 || which < 0 || which > 5 || which == 3)
     return fail(TLM_ERR_INVALID, "TLMModel: invalid kernel timing argument");
   int rc = tlm_model_finalize(m);
   if (rc) return rc;
@@ -1298,6 +1317,10 @@ int tlm_time_kernel(tlm_model* m, int which, int iters, double* avg_ms) {
   hipEventDestroy(e0);
   hipEventDestroy(e1);
   *avg_ms = f / iters;
+  // repeated single stages break the accumulators' zero-before-use order:
+  // clear them (the cache and ctrl state are left as the stages wrote them)
+  HIP_TRY(hipMemsetAsync(m->rb, 0, sizeof(unsigned long long) * kRep * m->d.hidden_size * m->d.num_layers, st));
+  HIP_TRY(hipStreamSynchronize(st));
   return TLM_OK;
 }
 
@@ -1310,7 +1333,10 @@ int tlm_model_describe(tlm_model* m, char* out, size_t len) {
              x->plan.cps, x->plan.splits);
     return std::string(b);
   };
-  std::string s = "qkv[" + p(L.qkv) + "] o[" + p(L.o) + "] gate_up[" + p(L.gu) + "] down[" + p(L.down) + "] head[" +
+  char mlp[160];
+  snprintf(mlp, sizeof mlp, "gate|up %dx%d paired, down %dx%d; %d blocks x %d waves, %d+%d chunks/wave",
+           L.gu->N, L.gu->K, L.down->N, L.down->K, L.gu->T, kMlpWaves, m->mlp_nch, m->mlp_ndb);
+  std::string s = "qkv[" + p(L.qkv) + "] o[" + p(L.o) + "] mlp[" + mlp + "] head[" +
                   p(m->head) + " grid=" + std::to_string(m->lm_plan.gx) + " waves=" +
                   std::to_string(m->lm_plan.waves) + "] attn[nsplit=" + std::to_string(m->attn.nsplit) +
                   " G=" + std::to_string(m->attn.G) + "]";

@@ -8,6 +8,13 @@ namespace tlm {
 constexpr int kTile = 64;      // output rows per tile: one row per lane of a wave64
 constexpr int kMaxChunks = 8;  // most 16-byte chunks a wave keeps in flight per batch
 constexpr int kMaxPart = 8;    // partial vectors a consumer folds in with one round trip
+// Residual stream accumulators: kRep replicas of an int64 fixed-point vector
+// (value * 2^32).  Producers add into replica (block % kRep) with device-scope
+// atomics; integer addition is associative, so the sum is exact and the same
+// in every run.  Readers add the replicas.
+constexpr int kRep = 4;
+constexpr float kFxScale = 4294967296.0f;        // 2^32
+constexpr float kFxInv = 2.3283064365386963e-10f;  // 2^-32
 
 enum WeightFmt { WF_F16 = 1, WF_Q4 = 2 };
 
@@ -18,6 +25,8 @@ enum Prologue {
   PRO_SWIGLU = 2,  // x = silu(sum_j pin[j][k]) * (sum_j pin[j][up_off + k])
   PRO_ATTN = 3,    // x = flash-decoding combine of the attention chunk partials
   PRO_RMS2 = 4,    // PRO_RMS for K up to 8 elements per thread (chosen by launch_gemv)
+  PRO_RMSF = 5,    // x = rmsnorm(sum of the kRep fixed-point replicas acc_in) * w
+  PRO_RMSF2 = 6,   // PRO_RMSF for K up to 8 elements per thread (chosen by launch_gemv)
 };
 
 // Split of the attention window [first, pos] into chunks; identical on host and device.
@@ -39,13 +48,14 @@ __host__ __device__ inline ChunkPlan chunk_plan(int pos, int window, int nsplit,
 enum Ctrl { C_TOKEN = 0, C_POS = 1, C_STEP = 2, C_BASE = 3, C_LEN = 4 };
 
 // Embedding row staging: the kernels that choose the next token (set_ctrl,
-// prefill_advance, argmax_merge) also copy its embedding row to x0, the
-// residual base of layer 0.  x0 == null disables the copy.
+// prefill_advance, argmax_merge) also write its embedding row, in fixed point,
+// to replica 0 of x0, the residual accumulator layer 0 reads (replicas 1..3
+// stay zero).  x0 == null disables the copy.
 struct EmbStage {
   const void* emb;  // [V][H] fp16 or fp32
   int f32;
   int H;
-  float* x0;
+  unsigned long long* x0;
 };
 
 struct GemvArgs {
@@ -57,7 +67,10 @@ struct GemvArgs {
   // PRO_COPY
   const float* in;
   // PRO_RMS
-  const float* base;   // fp32 [K] residual stream (layer 0: the staged embedding row)
+  const float* base;   // fp32 [K] residual stream
+  const unsigned long long* acc_in;  // PRO_RMSF: [kRep][K] fixed-point residual
+  unsigned long long* zero_ptr;      // optional: the grid zeroes zero_ptr[0, zero_n)
+  int zero_n;
   const int* ctrl;
   const float* pin;    // partials to add (RMS) / gate|up partials (SWIGLU)
   int n_pin, pin_stride;
@@ -76,6 +89,18 @@ struct GemvArgs {
   int* tokens_out;     // greedy stream (indexed by ctrl[C_STEP]), may be null
   int advance;         // 1: last block advances ctrl (token <- argmax, pos++, step++)
   int max_steps;
+};
+
+// Fused gate|up -> SwiGLU -> down of one 32-index slice of the intermediate
+// dimension per block.  The gate|up linear is stored in row pairs: tile t holds
+// gate rows 32t..32t+31 in lanes 0..31 and the matching up rows in lanes 32..63.
+struct MlpArgs {
+  GemvArgs g;               // gate|up (K = H) and the PRO_RMS prologue inputs
+  const uint4* wd;          // down linear tiles [Td][Cd][64]
+  const uint16_t* sd;       // q4 scales of the down linear
+  int Td, Cd;               // down tiles (ceil(H / 64)) and chunks per row
+  int H;                    // output rows
+  unsigned long long* acc;  // [kRep][H] fixed-point accumulator, zero on entry
 };
 
 struct AttnArgs {
@@ -99,12 +124,17 @@ struct AttnArgs {
 // launchers return false when no compiled variant matches (nothing is launched)
 // waves in {4, 8}; nch in {1, 2, 4, 8}: chunks per wave and load batch
 bool launch_gemv(int fmt, int pro, int waves, int nch, dim3 grid, const GemvArgs& a, hipStream_t st);
+// fused MLP: 8 waves, one block per 32 intermediate indices; nch: gate|up
+// chunks per wave, ndb: down (tile, chunk) items per wave per batch (1, 2, 4)
+bool launch_mlp(int fmt, int nch, int ndb, int blocks, const MlpArgs& a, hipStream_t st);
+size_t mlp_smem_bytes(int fmt, int C, int K);
+constexpr int kMlpWaves = 8;
 bool launch_lm_head(int fmt, int waves, int nch, dim3 grid, const GemvArgs& a, hipStream_t st);
 // attention chunk partials; with `combine` also the combine kernel writing a.out
 bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, bool combine, hipStream_t st);
 size_t gemv_smem_bytes(int fmt, int cps, int waves);
-void launch_final_norm(const float* base, const float* pin, int n_pin, int pin_stride, const float* w, int n,
-                       float eps, float* y, hipStream_t st);
+// y = rmsnorm(sum of the kRep replicas of acc) * w, n <= 4096
+void launch_final_norm(const unsigned long long* acc, const float* w, int n, float eps, float* y, hipStream_t st);
 void launch_rmsnorm(const float* x, const float* w, int n, float eps, int offset, float* y, hipStream_t st);
 void launch_silu_mul(const float* g, const float* u, int n, float* out, hipStream_t st);
 void launch_reduce(const float* part, int n_part, int stride, const float* bias, int n, float* y, hipStream_t st);

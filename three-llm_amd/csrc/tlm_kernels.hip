@@ -23,6 +23,12 @@ static constexpr float kLowest = -3.4028234663852886e38f;  // TSLLogits.ts:21 LO
 
 __device__ __forceinline__ float h2f(uint32_t bits) { return __half2float(__ushort_as_half((unsigned short)bits)); }
 
+// Fixed-point residual values (x * 2^32 as a two's-complement int64).
+__device__ __forceinline__ unsigned long long to_fx(float v) {
+  return (unsigned long long)__float2ll_rn(v * kFxScale);
+}
+__device__ __forceinline__ float from_fx(unsigned long long s) { return __ll2float_rn((long long)s) * kFxInv; }
+
 // Cross-lane moves through DPP (data-parallel primitives: a VALU operand
 // modifier, no LDS round trip).  Every reduction below pairs lanes
 // symmetrically, so all lanes of a group end with the same bits.
@@ -192,9 +198,11 @@ __device__ __forceinline__ void put4(float* xl, float* xsum, int i, float4 y, bo
 // while the weight loads stay outstanding.
 template <int PRO, int FMT>
 struct GemvPrologue {
-  static constexpr bool kRms = PRO == PRO_RMS || PRO == PRO_RMS2;
-  static constexpr int R = PRO == PRO_RMS2 ? 2 : 1;  // float4s of the residual row per thread
+  static constexpr bool kRmsF = PRO == PRO_RMSF || PRO == PRO_RMSF2;
+  static constexpr bool kRms = PRO == PRO_RMS || PRO == PRO_RMS2 || kRmsF;
+  static constexpr int R = (PRO == PRO_RMS2 || PRO == PRO_RMSF2) ? 2 : 1;  // float4s of the residual row per thread
   float4 x[R], w[R];
+  ulonglong2 fx[kRmsF ? R : 1][kRep][2];  // RMSF: the 4 elements' replicas
   float4 p[2][kMaxPart];  // RMS: partials per float4 (R rows); SWIGLU: [0] gate, [1] up partials
   float2 ml[8];           // ATTN: (m, l) and accumulators of the first 8 chunks
   float4 ac[8];
@@ -246,8 +254,17 @@ struct GemvPrologue {
       for (int r = 0; r < R; r++) {
         const int f = min(tid + r * nt, K4 - 1);
         w[r] = *reinterpret_cast<const float4*>(a.norm_w + 4 * f);
-        x[r] = *reinterpret_cast<const float4*>(a.base + 4 * f);
-        load_parts(a.pin, a.n_pin, a.pin_stride, 4 * f, p[r]);
+        if (kRmsF) {
+#pragma unroll
+          for (int q = 0; q < kRep; q++) {
+            const ulonglong2* src = reinterpret_cast<const ulonglong2*>(a.acc_in + (size_t)q * a.K + 4 * f);
+            fx[kRmsF ? r : 0][q][0] = src[0];
+            fx[kRmsF ? r : 0][q][1] = src[1];
+          }
+        } else {
+          x[r] = *reinterpret_cast<const float4*>(a.base + 4 * f);
+          load_parts(a.pin, a.n_pin, a.pin_stride, 4 * f, p[r]);
+        }
       }
     } else if (fast) {
       // ATTN: the first 8 chunk slots are read before the position is known
@@ -292,7 +309,25 @@ struct GemvPrologue {
     return make_float4(O.x * il, O.y * il, O.z * il, O.w * il);
   }
 
-  __device__ void finish(const GemvArgs& a, float* xl, float* xsum, float* scratch, int k0, int k1, int klen_pad) {
+  // Residual row float4 r: base + partials, or the sum of the fixed-point replicas.
+  __device__ __forceinline__ float4 residual4(const GemvArgs& a, int r) {
+    if (kRmsF) {
+      unsigned long long s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+#pragma unroll
+      for (int q = 0; q < kRep; q++) {
+        s0 += fx[kRmsF ? r : 0][q][0].x;
+        s1 += fx[kRmsF ? r : 0][q][0].y;
+        s2 += fx[kRmsF ? r : 0][q][1].x;
+        s3 += fx[kRmsF ? r : 0][q][1].y;
+      }
+      return make_float4(from_fx(s0), from_fx(s1), from_fx(s2), from_fx(s3));
+    }
+    return f4add(x[r], sum_loaded(p[r], a.n_pin));
+  }
+
+  // xm (optional, RMS prologues): receives the un-normalised residual row.
+  __device__ void finish(const GemvArgs& a, float* xl, float* xsum, float* scratch, int k0, int k1, int klen_pad,
+                         float* xm = nullptr) {
     const int tid = threadIdx.x, nt = blockDim.x;
     // the position is read here, after the weight loads are issued
     if (PRO == PRO_ATTN) nact = chunk_plan(a.ctrl[C_POS], a.att_window, a.att_nsplit, a.att_chmin).nact;
@@ -305,13 +340,14 @@ struct GemvPrologue {
 #pragma unroll
       for (int r = 0; r < R; r++) {
         const int f = tid + r * nt;
-        v[r] = f4add(x[r], sum_loaded(p[r], a.n_pin));
+        v[r] = residual4(a, r);
         const float m = f < K4 ? 1.f : 0.f;
         ss = fmaf(v[r].x * m, v[r].x, ss);
         ss = fmaf(v[r].y * m, v[r].y, ss);
         ss = fmaf(v[r].z * m, v[r].z, ss);
         ss = fmaf(v[r].w * m, v[r].w, ss);
         if (writer && f < K4) *reinterpret_cast<float4*>(a.xout + 4 * f) = v[r];
+        if (xm && f < K4) *reinterpret_cast<float4*>(xm + 4 * f) = v[r];
       }
       const float inv = rsqrtf(block_sum(ss, scratch) / (float)a.K + a.eps);
 #pragma unroll
@@ -463,6 +499,11 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvArgs a) {
   pro.issue(a, k0, ncl * CK);
   GemvCore<FMT, NCH> core;
   int t = blockIdx.x;
+  if (a.zero_ptr) {  // clears an accumulator for a later kernel: each block a slice
+    const int nb = gridDim.x * gridDim.y, bid = blockIdx.y * gridDim.x + blockIdx.x;
+    const int per = (a.zero_n + nb - 1) / nb;
+    for (int i = bid * per + threadIdx.x; i < min(a.zero_n, (bid + 1) * per); i += blockDim.x) a.zero_ptr[i] = 0ull;
+  }
   core.load(a, t, c0, ncl, wave, W, nw, 0);  // weights in flight during the prologue (t < T: gridDim.x <= T)
   __builtin_amdgcn_sched_barrier(0);  // keep every load issued before the prologue's first wait
   pro.finish(a, L.xl, L.xsum, L.scratch, k0, k1, ncl * CK);
@@ -547,12 +588,13 @@ __global__ __launch_bounds__(W * 64) void lm_head_kernel(GemvArgs a) {
 // one block reduces the per-block partials; a separate launch, so the kernel
 // boundary (not a device-scope fence per block) publishes the partials.  In the
 // decode graph it also advances the token/position state for the next step.
-// Copies the embedding row of `token` to es.x0 (all threads of the block take part).
+// Writes the embedding row of `token`, in fixed point, to replica 0 of es.x0
+// (all threads of the block take part).
 __device__ __forceinline__ void stage_embedding(const EmbStage& es, int token) {
   if (!es.x0) return;
   for (int i = threadIdx.x; i < es.H; i += blockDim.x)
-    es.x0[i] = es.f32 ? ((const float*)es.emb)[(size_t)token * es.H + i]
-                      : h2f(((const uint16_t*)es.emb)[(size_t)token * es.H + i]);
+    es.x0[i] = to_fx(es.f32 ? ((const float*)es.emb)[(size_t)token * es.H + i]
+                            : h2f(((const uint16_t*)es.emb)[(size_t)token * es.H + i]));
 }
 
 __global__ __launch_bounds__(1024) void argmax_merge_kernel(const float* pval, const int* pidx, int n, int* ctrl,
@@ -613,8 +655,9 @@ bool launch_gemv(int fmt, int pro, int waves, int nch, dim3 grid, const GemvArgs
   const size_t smem = gemv_smem_bytes(fmt, a.cps, waves);
   // the RMS prologue keeps one (PRO_RMS) or two (PRO_RMS2) float4s of the
   // residual row per thread
-  if (pro == PRO_RMS && a.K > 4 * 64 * waves) pro = PRO_RMS2;
-  if (pro == PRO_RMS2 && a.K > 8 * 64 * waves) return false;
+  if (pro == PRO_RMSF && a.K > 4 * 64 * waves) pro = PRO_RMSF2;
+  if (pro == PRO_RMSF2 && a.K > 8 * 64 * waves) return false;
+  if (pro == PRO_RMS || pro == PRO_RMS2) return false;  // residual + partials: the fused MLP kernel only
 #define GEMV_CASE(F, P, Wv, N)                                                          \
   if (fmt == F && pro == P && waves == Wv && nch == N) {                                \
     hipLaunchKernelGGL((gemv_kernel<F, P, Wv, N>), grid, dim3(Wv * 64), smem, st, a);   \
@@ -623,14 +666,14 @@ bool launch_gemv(int fmt, int pro, int waves, int nch, dim3 grid, const GemvArgs
 #define GEMV_N(F, P, Wv) GEMV_CASE(F, P, Wv, 1) GEMV_CASE(F, P, Wv, 2) GEMV_CASE(F, P, Wv, 4) GEMV_CASE(F, P, Wv, 8)
 #define GEMV_W(F, P) GEMV_N(F, P, 4) GEMV_N(F, P, 8)
   GEMV_W(WF_Q4, PRO_COPY)
-  GEMV_W(WF_Q4, PRO_RMS)
-  GEMV_W(WF_Q4, PRO_RMS2)
+  GEMV_W(WF_Q4, PRO_RMSF)
+  GEMV_W(WF_Q4, PRO_RMSF2)
   GEMV_W(WF_Q4, PRO_SWIGLU)
   GEMV_W(WF_Q4, PRO_ATTN)
   GEMV_W(WF_F16, PRO_ATTN)
   GEMV_W(WF_F16, PRO_COPY)
-  GEMV_W(WF_F16, PRO_RMS)
-  GEMV_W(WF_F16, PRO_RMS2)
+  GEMV_W(WF_F16, PRO_RMSF)
+  GEMV_W(WF_F16, PRO_RMSF2)
   GEMV_W(WF_F16, PRO_SWIGLU)
 #undef GEMV_W
 #undef GEMV_N
@@ -649,6 +692,131 @@ bool launch_lm_head(int fmt, int waves, int nch, dim3 grid, const GemvArgs& a, h
   LM_N(WF_F16, 4) LM_N(WF_F16, 8) LM_N(WF_Q4, 4) LM_N(WF_Q4, 8)
 #undef LM_N
 #undef LM_CASE
+  return false;
+}
+
+// ------------------------------------------------------------------- MLP --
+
+// Down-projection slice of one block: (tile, chunk) items over the block's 32
+// intermediate indices; item = tile * CPG + chunk, this wave's items are
+// wave, wave + W, ...  Loads are unconditional (items clamped).
+template <int FMT, int DB>
+struct MlpDown {
+  static constexpr int CK = FMT == WF_Q4 ? 32 : 8;
+  static constexpr int CPG = 32 / CK;  // chunks per 32-index group
+  uint4 d[DB];
+  uint16_t sc[DB];
+  __device__ __forceinline__ void load(const MlpArgs& m, int blk, int wave, int W, int nd, int nitems, int ib) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int u = 0; u < DB; u++) {
+      const int item = min(wave + min(ib + u, max(nd, 1) - 1) * W, nitems - 1);
+      const int td = item / CPG, c = min(blk * CPG + item % CPG, m.Cd - 1);
+      const size_t at = ((size_t)td * m.Cd + c) * kTile + lane;
+      d[u] = m.wd[at];
+      if (FMT == WF_Q4) sc[u] = m.sd[at];
+    }
+  }
+};
+
+// One block per 32 intermediate indices i0 = 32 * blockIdx.x:
+//   x_mid = base + sum of the O partials (TSLAdd.ts:10-33), RMSNorm
+//   (TSLRMSNorm.ts:50-74), [g | u] = rows of the paired gate|up tile,
+//   h = silu(g) * u (TSLSiLUMul.ts:15-29), then the down columns i0..i0+31:
+//   y[n] += sum_i Wd[n][i0 + i] h[i], added in fixed point to replica
+//   (block % kRep) of the accumulator; block 0 also adds x_mid (the residual).
+// TSLGatedMLP.ts:17-90 computes the same product as three dispatches.
+template <int FMT, int PRO, int NCH, int DB>
+__global__ __launch_bounds__(kMlpWaves * 64) void mlp_kernel(MlpArgs m) {
+  extern __shared__ float sm[];
+  constexpr int W = kMlpWaves;
+  constexpr int CK = GemvCore<FMT, NCH>::CK;
+  using Down = MlpDown<FMT, DB>;
+  const GemvArgs& a = m.g;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int blk = blockIdx.x, C = a.C;
+  float* xl = sm;               // [C * CK] normed x
+  float* xsum = xl + C * CK;    // [C] q4 group sums
+  float* red = xsum + ((C + 3) & ~3);  // [W][64] (keeps h and xm 16-byte aligned)
+  float* scratch = red + W * kTile;
+  float* h = scratch + 64;      // [32] silu(g) * u, then their sum
+  float* xm = h + 64;           // [K] x_mid (block 0)
+  const int nw = wave < C ? (C - wave + W - 1) / W : 0;
+  const int nitems = m.Td * Down::CPG;
+  const int nd = wave < nitems ? (nitems - wave + W - 1) / W : 0;
+
+  GemvPrologue<PRO, FMT> pro;
+  pro.issue(a, 0, C * CK);
+  GemvCore<FMT, NCH> core;
+  core.load(a, blk, 0, C, wave, W, nw, 0);
+  Down dn;
+  dn.load(m, blk, wave, W, nd, nitems, 0);
+  __builtin_amdgcn_sched_barrier(0);  // every load issued before the prologue's first wait
+  pro.finish(a, xl, xsum, scratch, 0, a.K, C * CK, blk == 0 ? xm : nullptr);
+  __syncthreads();
+
+  float acc = 0.f;
+  for (int b = 0; b < nw; b += NCH) {
+    if (b > 0) core.load(a, blk, 0, C, wave, W, nw, b);
+    acc += core.compute(xl, xsum, wave, W, nw, b);
+  }
+  red[wave * kTile + lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; w++) v += red[w * kTile + lane];
+    // lanes 0..31 hold g, lanes 32..63 the matching u: h = silu(g) * u in
+    // lanes 32..63 (padded indices have zero rows, so their h is 0)
+    const float g = __shfl(v, lane & 31, 64);
+    const float hv = g / (1.f + __expf(-g)) * v;
+    if (lane >= 32) h[lane - 32] = hv;
+    const float hs = wave_sum(lane >= 32 ? hv : 0.f);
+    if (lane == 0) h[32] = hs;
+  }
+  __syncthreads();
+
+  const float hsum = h[32];
+  for (int ib = 0; ib < nd; ib += DB) {
+    if (ib > 0) dn.load(m, blk, wave, W, nd, nitems, ib);
+#pragma unroll
+    for (int u = 0; u < DB; u++) {
+      if (ib + u < nd) {  // wave-uniform
+        const int item = wave + (ib + u) * W;
+        const int td = item / Down::CPG, cc = item % Down::CPG;
+        const float p = FMT == WF_Q4 ? dot_q4(dn.d[u], h, hsum, h2f(dn.sc[u])) : dot_f16(dn.d[u], h + cc * CK);
+        const int n = td * kTile + lane;
+        if (n < m.H) atomicAdd(m.acc + (size_t)(blk % kRep) * m.H + n, to_fx(p));
+      }
+    }
+  }
+  if (blk == 0)
+    for (int n = threadIdx.x; n < m.H; n += blockDim.x) atomicAdd(m.acc + n, to_fx(xm[n]));
+}
+
+size_t mlp_smem_bytes(int fmt, int C, int K) {
+  const int CK = fmt == WF_Q4 ? 32 : 8;
+  return sizeof(float) * ((size_t)C * CK + ((C + 3) & ~3) + kMlpWaves * kTile + 64 + 64 + K);
+}
+
+bool launch_mlp(int fmt, int nch, int ndb, int blocks, const MlpArgs& m, hipStream_t st) {
+  const size_t smem = mlp_smem_bytes(fmt, m.g.C, m.g.K);
+  int pro = m.g.K > 4 * 64 * kMlpWaves ? PRO_RMS2 : PRO_RMS;
+  if (m.g.K > 8 * 64 * kMlpWaves) return false;
+#define MLP_CASE(F, P, N, D)                                                                          \
+  if (fmt == F && pro == P && nch == N && ndb == D) {                                                 \
+    hipLaunchKernelGGL((mlp_kernel<F, P, N, D>), dim3(blocks), dim3(kMlpWaves * 64), smem, st, m);    \
+    return true;                                                                                      \
+  }
+#define MLP_D(F, P, N) MLP_CASE(F, P, N, 1) MLP_CASE(F, P, N, 2) MLP_CASE(F, P, N, 4)
+#define MLP_N(F, P) MLP_D(F, P, 1) MLP_D(F, P, 2) MLP_D(F, P, 4) MLP_D(F, P, 8)
+  MLP_N(WF_Q4, PRO_RMS)
+  MLP_N(WF_Q4, PRO_RMS2)
+  MLP_N(WF_F16, PRO_RMS)
+  MLP_N(WF_F16, PRO_RMS2)
+#undef MLP_N
+#undef MLP_D
+#undef MLP_CASE
   return false;
 }
 
@@ -1080,16 +1248,26 @@ bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, bool combine, hi
 // --------------------------------------------------------- small kernels --
 
 // Final norm: x = base + sum(pin); y = rmsnorm(x) * w (one block).
-__global__ __launch_bounds__(1024) void final_norm_kernel(const float* base, const float* pin, int n_pin,
-                                                          int pin_stride, const float* w, int n, float eps, float* y) {
+__global__ __launch_bounds__(1024) void final_norm_kernel(const unsigned long long* acc, const float* w, int n,
+                                                          float eps, float* y) {
   __shared__ float scratch[16];
   // n <= 4 * blockDim.x: every element is loaded in one round trip and kept in registers
+  unsigned long long q[kEpt][kRep];
+#pragma unroll
+  for (int e = 0; e < kEpt; e++) {
+    const int k = min(threadIdx.x + e * blockDim.x, n - 1);
+#pragma unroll
+    for (int r = 0; r < kRep; r++) q[e][r] = acc[(size_t)r * n + k];
+  }
   float v[kEpt];
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < kEpt; e++) {
     const int k = threadIdx.x + e * blockDim.x;
-    v[e] = k < n ? base[k] + sum_parts(pin, n_pin, pin_stride, k) : 0.f;
+    unsigned long long s = 0;
+#pragma unroll
+    for (int r = 0; r < kRep; r++) s += q[e][r];
+    v[e] = k < n ? from_fx(s) : 0.f;
     ss = fmaf(v[e], v[e], ss);
   }
   const float inv = rsqrtf(block_sum(ss, scratch) / (float)n + eps);
@@ -1100,9 +1278,8 @@ __global__ __launch_bounds__(1024) void final_norm_kernel(const float* base, con
   }
 }
 
-void launch_final_norm(const float* base, const float* pin, int n_pin, int pin_stride, const float* w, int n,
-                       float eps, float* y, hipStream_t st) {
-  hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, st, base, pin, n_pin, pin_stride, w, n, eps, y);
+void launch_final_norm(const unsigned long long* acc, const float* w, int n, float eps, float* y, hipStream_t st) {
+  hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, st, acc, w, n, eps, y);
 }
 
 __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* x, const float* w, int n, float eps, int offset,
