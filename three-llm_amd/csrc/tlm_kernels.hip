@@ -835,92 +835,67 @@ __device__ __forceinline__ uint16_t kv_store<uint16_t>(float v) { return __half_
 template <>
 __device__ __forceinline__ float kv_store<float>(float v) { return v; }
 
-// Eight consecutive cache elements starting at p (16-byte aligned for fp16, 32 for fp32).
-template <typename KT>
-__device__ __forceinline__ void kv_load8(const KT* p, float* o);
-template <>
-__device__ __forceinline__ void kv_load8<uint16_t>(const uint16_t* p, float* o) {
-  const uint4 d = *reinterpret_cast<const uint4*>(p);
-  const uint32_t wv[4] = {d.x, d.y, d.z, d.w};
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    o[2 * j] = h2f(wv[j] & 0xFFFFu);
-    o[2 * j + 1] = h2f(wv[j] >> 16);
-  }
-}
-template <>
-__device__ __forceinline__ void kv_load8<float>(const float* p, float* o) {
-  const float4 a = *reinterpret_cast<const float4*>(p);
-  const float4 b = *reinterpret_cast<const float4*>(p + 4);
-  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
-  o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
-}
-
-// Attention tiling shared by the host (LDS size) and the kernel.
-struct AttnTiling {
-  int lpp, sub, gpw, vt_bytes;
+// Tiling of head_kernel: LPP lanes per cached position, so each lane holds 64
+// bytes of a K row; SUB = 64 / LPP positions per pass; the V rows of a pass
+// (always 4 KiB) are staged in LDS with 64 bytes per lane.
+struct HeadTiling {
+  int lpp, sub, dl;
 };
-static constexpr __host__ __device__ inline AttnTiling attn_tiling(int dt, int esz, int gmax) {
-  AttnTiling t{};
-  t.lpp = dt * esz <= 64 ? 1 : dt * esz <= 256 ? 2 : 4;  // lanes per position: <= 128 B of K per lane
-  t.sub = 64 / t.lpp;                                    // positions per pass (all waves see all of them)
-  t.gpw = gmax >= 4 ? gmax / 4 : 1;                      // query heads per wave
-  t.vt_bytes = t.sub * dt * esz;                         // V tile of one pass
+static constexpr __host__ __device__ inline HeadTiling head_tiling(int dt, int esz) {
+  HeadTiling t{};
+  t.lpp = dt * esz <= 64 ? 1 : dt * esz / 64;
+  t.sub = 64 / t.lpp;
+  t.dl = dt / t.lpp;  // K elements per lane
   return t;
 }
 
-// Compiled head dimension of attn_kernel: 64 and 128 exactly, 32 covers any
-// even head_dim <= 32 through runtime bounds.
+// Compiled head dimension: 64 and 128 exactly; 32 covers any even head_dim
+// <= 32 through runtime bounds (element-wise, clamped loads).
 static int attn_dt(int D) { return D <= 32 ? 32 : D; }
 
-int attn_lpp(int D, bool kv_f32) { return attn_tiling(attn_dt(D), kv_f32 ? 4 : 2, 1).lpp; }
+int attn_lpp(int D, bool kv_f32) { return head_tiling(attn_dt(D), kv_f32 ? 4 : 2).lpp; }
 
-// LDS of attn_kernel: q (padded to gmax heads), new k/v, per-wave
-// probabilities, and one region used in turn as RoPE scratch, V tile and the
-// P.V slot reduction.
+// LDS of head_kernel: q, the new k and v, their pre-RoPE values, the pass's
+// probabilities and the V tile.
 size_t attn_smem_bytes(int gmax, int D, bool kv_f32) {
-  const AttnTiling t = attn_tiling(attn_dt(D), kv_f32 ? 4 : 2, gmax);
-  const int NSW = 64 / (D / 2);
-  const size_t region = std::max({(size_t)t.vt_bytes, sizeof(float) * ((size_t)gmax * D + D),
-                                  sizeof(float) * 4 * (size_t)NSW * t.gpw * D});
-  return sizeof(float) * ((size_t)gmax * D + 2 * D + 4 * (size_t)t.gpw * t.sub) + region;
+  (void)gmax;
+  const HeadTiling t = head_tiling(attn_dt(D), kv_f32 ? 4 : 2);
+  return sizeof(float) * (6 * (size_t)attn_dt(D) + t.sub) + 4096;
 }
 
-// Global loads of one attention pass, held in registers: this lane's K-row
-// slice and its share of the coalesced V tile.  All loads are unconditional
-// (rows clamped to t1 - 1), so a pass costs one memory round trip.
-template <typename KT, int WPR, int VCH, bool GEN, int DLM>
-struct AttnLoads {
+// Global loads of one head_kernel pass, held in registers: this lane's K-row
+// slice (DL elements) and its 64 bytes of the pass's V rows.  Unconditional:
+// rows are clamped to t1 - 1.
+template <typename KT, int KW, bool GEN, int DL>
+struct HeadLoads {
   static constexpr int ESZ = sizeof(KT);
-  uint32_t kw[WPR];
-  uint4 vst[VCH];
-
-  __device__ __forceinline__ void issue(const KT* kh, const KT* vh, int tb, int t1, int prow, int qpart, int D,
-                                        int DL, int tid) {
-    const int t = min(tb + prow, t1 - 1);
+  uint32_t kw[KW];
+  uint4 vs[4];
+  __device__ __forceinline__ void issue(const KT* kh, const KT* vh, int tb, int t1, int pl, int part, int D,
+                                        int row_bytes, int lane) {
+    const int t = min(tb + pl, t1 - 1);
     if (!GEN) {
-      const uint4* krow = reinterpret_cast<const uint4*>(kh + (size_t)t * D + qpart * DL);
+      const uint4* kr = reinterpret_cast<const uint4*>(kh + (size_t)t * D + part * DL);
 #pragma unroll
-      for (int j = 0; j < WPR / 4; j++) {
-        const uint4 q = krow[j];
-        kw[4 * j] = q.x;
-        kw[4 * j + 1] = q.y;
-        kw[4 * j + 2] = q.z;
-        kw[4 * j + 3] = q.w;
+      for (int j = 0; j < KW / 4; j++) {
+        const uint4 v = kr[j];
+        kw[4 * j] = v.x;
+        kw[4 * j + 1] = v.y;
+        kw[4 * j + 2] = v.z;
+        kw[4 * j + 3] = v.w;
       }
-      const int row_bytes = D * ESZ;  // a multiple of 16
 #pragma unroll
-      for (int j = 0; j < VCH; j++) {
-        const int off = (j * 256 + tid) * 16;
+      for (int j = 0; j < 4; j++) {
+        const int off = (j * 64 + lane) * 16;  // byte offset in the [SUB][D] tile
         const int r = min(tb + off / row_bytes, t1 - 1);
-        vst[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(vh + (size_t)r * D) + off % row_bytes);
+        vs[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(vh + (size_t)r * D) + off % row_bytes);
       }
     } else {
-      const KT* kr = kh + (size_t)t * D + qpart * DL;
+      const KT* kr = kh + (size_t)t * D;
 #pragma unroll
-      for (int e = 0; e < DLM; e++) {
-        const uint32_t v = ESZ == 2 ? (uint32_t)((const uint16_t*)kr)[min(e, DL - 1)]
-                                    : ((const uint32_t*)kr)[min(e, DL - 1)];
+      for (int e = 0; e < DL; e++) {
+        const int k = min(part * DL + e, D - 1);
+        const uint32_t v = ESZ == 2 ? (uint32_t)((const uint16_t*)kr)[k] : ((const uint32_t*)kr)[k];
         if (ESZ == 2) {
           if (e & 1) kw[e >> 1] |= v << 16; else kw[e >> 1] = v;
         } else {
@@ -929,290 +904,180 @@ struct AttnLoads {
       }
     }
   }
-
-  // V rows [tb, tb + sub) into the LDS tile (the generic small-D path loads
-  // them here element by element), then the fresh row from vn.
-  __device__ __forceinline__ void stage_v(KT* vt, const KT* vh, const float* vn, int tb, int t1, bool own, int pos,
-                                          int D, int sub, int tid) {
-    if (!GEN) {
-#pragma unroll
-      for (int j = 0; j < VCH; j++) reinterpret_cast<uint4*>(vt)[j * 256 + tid] = vst[j];
-    } else {
-      for (int i = tid; i < sub * D; i += 256) vt[i] = vh[(size_t)min(tb + i / D, t1 - 1) * D + i % D];
-    }
-    __syncthreads();
-    if (own && pos >= tb && pos < tb + sub)
-      for (int d = tid; d < D; d += 256) vt[(size_t)(pos - tb) * D + d] = kv_store<KT>(vn[d]);
-    __syncthreads();
-  }
-
-  __device__ __forceinline__ float kelem(int e) const {
-    if (ESZ == 2) return h2f((kw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
-    return __uint_as_float(kw[e]);
-  }
 };
 
-// q heads and the new k, v rows of one KV head: QKV split-K partial sums +
-// bias, with RoPE (rotate-half, TSLAttention.ts:168-250) applied in registers.
-// Row r < G is query head h*G + r, row G the new k, row G + 1 the new v; item j
-// of a row covers the element pair (j, j + rd/2) when j < rd/2 on a rotated
-// row, else (2j, 2j + 1).  Loads are unconditional (item index clamped; bias
-// and RoPE tables are always valid buffers) so issue() can run ahead of the
-// K/V loads and be waited for alone.
-template <int IT>
-struct AttnGather {
-  float p0[IT][kMaxPart], p1[IT][kMaxPart];
-  float b0[IT], b1[IT], c[IT], sn[IT];
-
-  struct Item {
-    int row, e0, e1, col, j;
-    bool rot;
-  };
-  __device__ __forceinline__ static Item item(const AttnArgs& a, int idx, int h) {
-    const int D = a.D, HD = D / 2;
-    Item it;
-    it.row = idx / HD;
-    it.j = idx % HD;
-    const int hf = (a.rd > 0 && it.row <= a.G) ? a.rd / 2 : 0;
-    it.rot = it.j < hf;
-    it.e0 = it.rot ? it.j : 2 * it.j;
-    it.e1 = it.rot ? it.j + hf : 2 * it.j + 1;
-    const int QS = a.Hq * D, KS = a.Hkv * D;
-    it.col = it.row < a.G ? (h * a.G + it.row) * D : it.row == a.G ? QS + h * D : QS + KS + h * D;
-    return it;
-  }
-
-  __device__ __forceinline__ void issue(const AttnArgs& a, int h, int pos, int ib, int nit) {
-    const int half = a.rd > 0 ? a.rd / 2 : 1;  // RoPE table row width
-#pragma unroll
-    for (int u = 0; u < IT; u++) {
-      const Item it = item(a, min(ib + (int)threadIdx.x + 256 * u, nit - 1), h);
-#pragma unroll
-      for (int q = 0; q < kMaxPart; q++) {
-        const float* src = a.src + (size_t)max(min(q, a.n_src - 1), 0) * a.src_stride + it.col;
-        p0[u][q] = src[it.e0];
-        p1[u][q] = src[it.e1];
-      }
-      b0[u] = a.bias[it.col + it.e0];
-      b1[u] = a.bias[it.col + it.e1];
-      const int tj = (size_t)pos * half + min(it.j, half - 1);
-      c[u] = a.rope_cos[tj];
-      sn[u] = a.rope_sin[tj];
-    }
-  }
-
-  __device__ __forceinline__ void finish(const AttnArgs& a, int h, int ib, int nit, float* q_l, float* kn, float* vn) {
-#pragma unroll
-    for (int u = 0; u < IT; u++) {
-      const int idx = ib + (int)threadIdx.x + 256 * u;
-      const Item it = item(a, min(idx, nit - 1), h);
-      float x0 = b0[u], x1 = b1[u];
-#pragma unroll
-      for (int q = 0; q < kMaxPart; q++) {
-        const float m = q < a.n_src ? 1.f : 0.f;
-        x0 = fmaf(p0[u][q], m, x0);
-        x1 = fmaf(p1[u][q], m, x1);
-      }
-      float y0 = x0, y1 = x1;
-      if (it.rot) {
-        y0 = x0 * c[u] + (-x1) * sn[u];
-        y1 = x1 * c[u] + x0 * sn[u];
-      }
-      if (idx < nit) {
-        float* dst = it.row < a.G ? q_l + it.row * a.D : it.row == a.G ? kn : vn;
-        dst[it.e0] = y0;
-        dst[it.e1] = y1;
-      }
-    }
-  }
-};
-
-// One block = one KV head x one chunk of positions (split-K over the sequence,
-// flash-decoding).  The block's 4 waves share the KV head's G query heads
-// (GQA), gpw heads each, and all of the chunk's positions, in passes of `sub`
-// positions.  Each block:
-//   * issues the first pass's K-row and V loads before anything else,
-//   * forms q (and, in the chunk holding `pos`, the new k/v) from the QKV
-//     partial sums + bias, applies RoPE (TSLAttention.ts:168-250) and appends
-//     k/v to the cache (:252-286),
-//   * per pass: stages V in LDS, scores its positions for its heads, issues
-//     the next pass's loads, runs a per-wave online softmax (wave shuffles)
-//     and accumulates P.V,
-//   * writes (max, sum, unnormalised output) per query head for the combine
-//     (attn_combine_elem).
-template <typename KT, int GMAX, int DT>
-__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+// One wave = one query head x one chunk of positions (split-K over the
+// sequence, flash decoding; TSLAttention.ts:306-428 computes the same scores
+// and softmax over the whole window).  The wave
+//   * forms its q head and the KV head's new k and v from the QKV partial sums
+//     + bias and applies RoPE (rotate-half, TSLAttention.ts:168-250),
+//   * in the chunk holding `pos`, appends k and v to the cache (head g == 0 of
+//     the group writes; TSLAttention.ts:252-286) and uses the rounded row,
+//   * per pass of SUB positions: scores from the K rows in registers, an online
+//     softmax with DPP wave reductions, P.V from the V rows staged in LDS,
+//   * writes (max, sum, unnormalised output) for the combine.
+// All global loads of the first pass are unconditional and issued before the
+// first use; a one-wave block needs no barrier beyond wave-level LDS order.
+template <typename KT, int DT>
+__global__ __launch_bounds__(64) void head_kernel(AttnArgs a) {
   extern __shared__ float sm[];
   constexpr int ESZ = sizeof(KT);
-  constexpr AttnTiling TL = attn_tiling(DT, ESZ, GMAX);
-  constexpr int LPP = TL.lpp, SUB = TL.sub, GPW = TL.gpw;
+  constexpr HeadTiling TL = head_tiling(DT, ESZ);
+  constexpr int LPP = TL.lpp, SUB = TL.sub, DL = TL.dl;
   constexpr bool GEN = DT == 32;  // runtime head_dim <= 32
-  constexpr int DLM = DT / LPP;   // K elements per lane (compiled bound)
-  constexpr int WPR = DLM * ESZ / 4;
-  constexpr int VCH = TL.vt_bytes >= 4096 ? TL.vt_bytes / 4096 : 1;
-  const int h = blockIdx.x, c = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int D = GEN ? a.D : DT, G = a.G;
+  constexpr int EPL = DT > 64 ? DT / 64 : 1;  // q/k/v elements per lane (d = lane + 64 e)
+  constexpr int KW = DL * ESZ / 4;            // K dwords per lane
+  const int h = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
+  const int D = GEN ? a.D : DT, G = a.G, hk = h / G, g = h % G;
   const int pos = a.ctrl[C_POS];
   if (pos < 0 || pos >= a.max_tokens) return;
   const ChunkPlan cp = chunk_plan(pos, a.window, a.nsplit, a.chmin);
   if (c >= cp.nact) return;
   const int t0 = cp.first + c * cp.chunk, t1 = min(t0 + cp.chunk, pos + 1);
   const bool own = pos >= t0 && pos < t1;
-  const int DL = D / LPP;
-  const int HD = D / 2, NSW = 64 / HD;
-  const int dp = lane % HD, slot = min(lane / HD, NSW - 1);
-  const bool pv_lane = lane < NSW * HD;
-  const int pl = lane / LPP, qpart = lane % LPP;
-  const int g0 = wave * GPW;            // this wave's first query head
-  const bool busy = g0 < G;             // wave-uniform
-  float* q_l = sm;                      // [GMAX][D]
-  float* kn = q_l + GMAX * D;
-  float* vn = kn + D;
-  float* p_l = vn + D;                  // [4][GPW][SUB]
-  float* region = p_l + 4 * GPW * SUB;  // RoPE scratch / V tile / slot reduction
-  KT* vt = reinterpret_cast<KT*>(region);
-  const KT* kh = reinterpret_cast<const KT*>(a.kc) + (size_t)h * a.max_tokens * D;
-  const KT* vh = reinterpret_cast<const KT*>(a.vc) + (size_t)h * a.max_tokens * D;
+  float* q_l = sm;            // [DT]
+  float* kn = q_l + DT;       // [DT] new k (rounded like the cache)
+  float* vn = kn + DT;        // [DT]
+  float* raw = vn + DT;       // [3][DT] pre-RoPE q, k, v
+  float* p_l = raw + 3 * DT;  // [SUB]
+  KT* vt = reinterpret_cast<KT*>(p_l + SUB);  // [SUB][DT] V rows of the pass (4 KiB)
+  const KT* kh = reinterpret_cast<const KT*>(a.kc) + (size_t)hk * a.max_tokens * D;
+  const KT* vh = reinterpret_cast<const KT*>(a.vc) + (size_t)hk * a.max_tokens * D;
+  const int pl = lane / LPP, part = lane % LPP;
+  const int half = a.rd > 0 ? a.rd / 2 : 1;  // RoPE table row width
 
-  // q, new k, new v (+ RoPE) first: their loads are issued ahead of the K/V
-  // loads, which are only needed after them
-  constexpr int GIT = (GMAX + 2) * DT / 2 > 256 ? 2 : 1;  // items per thread pre-issued
-  const int nit = (G + 2) * (D / 2);
-  AttnGather<GIT> ga;
-  ga.issue(a, h, pos, 0, nit);
-  AttnLoads<KT, WPR, VCH, GEN, DLM> ld;
-  ld.issue(kh, vh, t0, t1, pl, qpart, D, DL, tid);
-  __builtin_amdgcn_sched_barrier(0);
-  ga.finish(a, h, 0, nit, q_l, kn, vn);
-  for (int ib = 256 * GIT; ib < nit; ib += 256 * GIT) {
-    ga.issue(a, h, pos, ib, nit);
-    ga.finish(a, h, ib, nit, q_l, kn, vn);
-  }
-  for (int i = G * D + tid; i < GMAX * D; i += 256) q_l[i] = 0.f;  // padded heads
-  __syncthreads();
-  // KV append at pos; this block keeps the rounded values the cache will hold
-  if (own) {
-    KT* kc = reinterpret_cast<KT*>(a.kc) + (size_t)h * a.max_tokens * D;
-    KT* vc = reinterpret_cast<KT*>(a.vc) + (size_t)h * a.max_tokens * D;
-    for (int i = tid; i < D; i += 256) {
-      const KT kq = kv_store<KT>(kn[i]), vq = kv_store<KT>(vn[i]);
-      kc[(size_t)pos * D + i] = kq;
-      vc[(size_t)pos * D + i] = vq;
-      kn[i] = kv_load<KT>(&kq);
-      vn[i] = kv_load<KT>(&vq);
-    }
-    __syncthreads();
-  }
-
-  float m_w[GPW], l_w[GPW], acc0[GPW], acc1[GPW];
+  // q (row 0), new k (row 1), new v (row 2): partial sums + bias, element d = lane + 64 e
+  const int QS = a.Hq * D, KS = a.Hkv * D;
+  float gp[3][EPL][kMaxPart], gb[3][EPL];
 #pragma unroll
-  for (int j = 0; j < GPW; j++) {
-    m_w[j] = -INFINITY;
-    l_w[j] = 0.f;
-    acc0[j] = 0.f;
-    acc1[j] = 0.f;
+  for (int r = 0; r < 3; r++) {
+    const int base = r == 0 ? h * D : r == 1 ? QS + hk * D : QS + KS + hk * D;
+#pragma unroll
+    for (int e = 0; e < EPL; e++) {
+      const int col = base + min(lane + 64 * e, D - 1);
+#pragma unroll
+      for (int j = 0; j < kMaxPart; j++)
+        gp[r][e][j] = a.src[(size_t)max(min(j, a.n_src - 1), 0) * a.src_stride + col];
+      gb[r][e] = a.bias[col];
+    }
   }
-  const float* qw = q_l + g0 * D + qpart * DL;
+  float rc[EPL], rs[EPL];  // cos / sin of element d's rotation pair
+#pragma unroll
+  for (int e = 0; e < EPL; e++) {
+    const int d = min(lane + 64 * e, D - 1);
+    const int j = d < half ? d : d - half;
+    rc[e] = a.rope_cos[(size_t)pos * half + min(j, half - 1)];
+    rs[e] = a.rope_sin[(size_t)pos * half + min(j, half - 1)];
+  }
+  // first pass: this lane's K slice and its 64 bytes of the V rows
+  HeadLoads<KT, KW, GEN, DL> ld;
+  const int row_bytes = D * ESZ;
+  ld.issue(kh, vh, t0, t1, pl, part, D, row_bytes, lane);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // finish q/k/v: sums, RoPE through LDS pairs, cache rounding
+#pragma unroll
+  for (int r = 0; r < 3; r++)
+#pragma unroll
+    for (int e = 0; e < EPL; e++) {
+      float s = gb[r][e];
+#pragma unroll
+      for (int j = 0; j < kMaxPart; j++) s = fmaf(gp[r][e][j], j < a.n_src ? 1.f : 0.f, s);
+      const int d = lane + 64 * e;
+      if (d < D) raw[r * DT + d] = s;
+    }
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < EPL; e++) {
+    const int d = lane + 64 * e;
+    if (d < D) {
+      float qv = raw[d], kv = raw[DT + d];
+      if (d < a.rd) {
+        const int pd = d < half ? d + half : d - half;
+        const float sg = d < half ? -1.f : 1.f;
+        qv = raw[d] * rc[e] + sg * raw[pd] * rs[e];
+        kv = raw[DT + d] * rc[e] + sg * raw[DT + pd] * rs[e];
+      }
+      q_l[d] = qv;
+      const KT kq = kv_store<KT>(kv), vq = kv_store<KT>(raw[2 * DT + d]);
+      kn[d] = kv_load<KT>(&kq);
+      vn[d] = kv_load<KT>(&vq);
+      if (own && g == 0) {
+        reinterpret_cast<KT*>(a.kc)[((size_t)hk * a.max_tokens + pos) * D + d] = kq;
+        reinterpret_cast<KT*>(a.vc)[((size_t)hk * a.max_tokens + pos) * D + d] = vq;
+      }
+    }
+  }
+  for (int d = D + lane; d < DT; d += 64) q_l[d] = kn[d] = 0.f;  // padded dims (generic path)
+  __syncthreads();
+
+  float m = -INFINITY, l = 0.f, o[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; e++) o[e] = 0.f;
+  float qr[DL];
+#pragma unroll
+  for (int e = 0; e < DL; e++) qr[e] = q_l[part * DL + e];
   for (int tb = t0; tb < t1; tb += SUB) {
-    ld.stage_v(vt, vh, vn, tb, t1, own, pos, D, SUB, tid);
+    // V rows to LDS (the fresh row from vn), K slice of this lane (fresh row from kn)
+    if (!GEN) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) reinterpret_cast<uint4*>(vt)[j * 64 + lane] = ld.vs[j];
+    } else {
+      for (int i = lane; i < SUB * D; i += 64) vt[i] = vh[(size_t)min(tb + i / D, t1 - 1) * D + i % D];
+    }
     const int t = tb + pl;
     const bool valid = t < t1;
-    if (own && t == pos) {  // the fresh row is not in the cache yet: take it from LDS
+    float kf[DL];
 #pragma unroll
-      for (int e = 0; e < DLM; e++) {
-        const float x = kn[qpart * DL + min(e, DL - 1)];
-        const uint32_t b = ESZ == 2 ? (uint32_t)__half_as_ushort(__float2half_rn(x)) : __float_as_uint(x);
-        if (ESZ == 2) {
-          if (e & 1) ld.kw[e >> 1] = (ld.kw[e >> 1] & 0xFFFFu) | (b << 16); else ld.kw[e >> 1] = (ld.kw[e >> 1] & 0xFFFF0000u) | b;
-        } else {
-          ld.kw[e] = b;
-        }
-      }
-    }
-    float s[GPW];
+    for (int e = 0; e < DL; e++)
+      kf[e] = ESZ == 2 ? h2f((ld.kw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) : __uint_as_float(ld.kw[e]);
+    if (own && t == pos) {
 #pragma unroll
-    for (int j = 0; j < GPW; j++) s[j] = 0.f;
-    if (busy) {
-#pragma unroll
-      for (int e = 0; e < DLM; e++) {
-        if (!GEN || e < DL) {
-          const float kd = ld.kelem(e);
-#pragma unroll
-          for (int j = 0; j < GPW; j++) s[j] = fmaf(qw[j * D + e], kd, s[j]);
-        }
-        if ((e & 7) == 7) __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    // the next pass's loads overlap this pass's softmax and P.V
-    if (tb + SUB < t1) ld.issue(kh, vh, tb + SUB, t1, pl, qpart, D, DL, tid);
-    if (busy) {
-#pragma unroll
-      for (int j = 0; j < GPW; j++) {
-        if (LPP > 1) s[j] += dpp<kDppXor1>(s[j]);
-        if (LPP > 2) s[j] += dpp<kDppXor2>(s[j]);
-        const float sc = valid ? s[j] * a.scale : -INFINITY;
-        const float mn = fmaxf(m_w[j], wave_max(sc));
-        const float p = (valid && mn != -INFINITY) ? __expf(sc - mn) : 0.f;
-        const float lt = wave_sum(qpart == 0 ? p : 0.f);
-        const float corr = m_w[j] == -INFINITY ? 0.f : __expf(m_w[j] - mn);
-        l_w[j] = l_w[j] * corr + lt;
-        acc0[j] *= corr;
-        acc1[j] *= corr;
-        m_w[j] = mn;
-        if (qpart == 0) p_l[(wave * GPW + j) * SUB + pl] = p;
-      }
+      for (int e = 0; e < DL; e++) kf[e] = kn[min(part * DL + e, DT - 1)];
     }
     __syncthreads();
-    if (busy && pv_lane) {
-      // rows past t1 hold clamped copies of valid rows and have p == 0
+    if (own && pos >= tb && pos < tb + SUB)
+      for (int d = lane; d < D; d += 64) vt[(size_t)(pos - tb) * D + d] = kv_store<KT>(vn[d]);
+    // the next pass's loads overlap this pass's math
+    if (tb + SUB < t1) ld.issue(kh, vh, tb + SUB, t1, pl, part, D, row_bytes, lane);
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < DL; e++) s = fmaf(qr[e], kf[e], s);
+    if (LPP > 1) s += dpp<kDppXor1>(s);
+    if (LPP > 2) s += dpp<kDppXor2>(s);
+    if (LPP > 4) s += __shfl_xor(s, 4, 64);
+    const float sc = valid ? s * a.scale : -INFINITY;
+    const float mn = fmaxf(m, wave_max(sc));
+    const float p = (valid && mn != -INFINITY) ? __expf(sc - mn) : 0.f;
+    const float corr = m == -INFINITY ? 0.f : __expf(m - mn);
+    l = l * corr + wave_sum(part == 0 ? p : 0.f);
+    m = mn;
+    if (part == 0) p_l[pl] = p;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < EPL; e++) {
+      const int d = lane + 64 * e;
+      float acc = o[e] * corr;
+      if (d < D) {
 #pragma unroll 8
-      for (int pw = slot; pw < SUB; pw += NSW) {
-        const float v0 = kv_load<KT>(vt + (size_t)pw * D + 2 * dp);
-        const float v1 = kv_load<KT>(vt + (size_t)pw * D + 2 * dp + 1);
-#pragma unroll
-        for (int j = 0; j < GPW; j++) {
-          const float p = p_l[(wave * GPW + j) * SUB + pw];
-          acc0[j] = fmaf(p, v0, acc0[j]);
-          acc1[j] = fmaf(p, v1, acc1[j]);
-        }
+        for (int u = 0; u < SUB; u++) acc = fmaf(p_l[u], kv_load<KT>(vt + (size_t)u * D + d), acc);
       }
+      o[e] = acc;
     }
     __syncthreads();
   }
-
-  // reduce the P.V slots of each wave; write this chunk's partial per head
-  float* red = region;  // [4][NSW][GPW][D]
-  if (busy && pv_lane) {
+  const size_t row = (size_t)h * a.nsplit + c;
 #pragma unroll
-    for (int j = 0; j < GPW; j++) {
-      red[((wave * NSW + slot) * GPW + j) * D + 2 * dp] = acc0[j];
-      red[((wave * NSW + slot) * GPW + j) * D + 2 * dp + 1] = acc1[j];
-    }
+  for (int e = 0; e < EPL; e++) {
+    const int d = lane + 64 * e;
+    if (d < D) a.pacc[row * D + d] = o[e];
   }
-  __syncthreads();
-  if (busy) {
-#pragma unroll
-    for (int j = 0; j < GPW; j++) {
-      const int g = g0 + j;
-      if (g < G) {
-        const int row = h * G + g;
-        for (int d = lane; d < D; d += 64) {
-          float o = 0.f;
-          for (int sl = 0; sl < NSW; sl++) o += red[((wave * NSW + sl) * GPW + j) * D + d];
-          a.pacc[((size_t)row * a.nsplit + c) * D + d] = o;
-        }
-        if (lane == 0) {
-          a.pml[((size_t)row * a.nsplit + c) * 2] = m_w[j];
-          a.pml[((size_t)row * a.nsplit + c) * 2 + 1] = l_w[j];
-        }
-      }
-    }
+  if (lane == 0) {
+    a.pml[row * 2] = m;
+    a.pml[row * 2 + 1] = l;
   }
 }
 
-// Combine of the chunk partials into the attention output (op-level path; the
-// decode graph folds this into the O projection's prologue instead).
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   const int row = blockIdx.x;
   const int pos = a.ctrl[C_POS];
@@ -1223,24 +1088,22 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 }
 
 bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, bool combine, hipStream_t st) {
-  const dim3 grid(a.Hkv, a.nsplit);
+  (void)gmax;
+  const dim3 grid(a.Hq, a.nsplit);
   const size_t smem = attn_smem_bytes(gmax, a.D, kv_f32);
   const int dt = attn_dt(a.D);
-  if (dt != 32 && dt != 64 && dt != 128) return false;
-  bool ok = false;
-#define ATT_CASE(KT, GM, DTV)                                                         \
-  if (!ok && gmax == GM && dt == DTV) {                                               \
-    hipLaunchKernelGGL((attn_kernel<KT, GM, DTV>), grid, dim3(256), smem, st, a);     \
-    ok = true;                                                                        \
-  }
-#define ATT_G(KT, DTV) ATT_CASE(KT, 1, DTV) ATT_CASE(KT, 2, DTV) ATT_CASE(KT, 4, DTV) ATT_CASE(KT, 8, DTV) ATT_CASE(KT, 16, DTV)
+  bool ok = true;
   if (kv_f32) {
-    ATT_G(float, 32) ATT_G(float, 64) ATT_G(float, 128)
+    if (dt == 32) hipLaunchKernelGGL((head_kernel<float, 32>), grid, dim3(64), smem, st, a);
+    else if (dt == 64) hipLaunchKernelGGL((head_kernel<float, 64>), grid, dim3(64), smem, st, a);
+    else if (dt == 128) hipLaunchKernelGGL((head_kernel<float, 128>), grid, dim3(64), smem, st, a);
+    else ok = false;
   } else {
-    ATT_G(uint16_t, 32) ATT_G(uint16_t, 64) ATT_G(uint16_t, 128)
+    if (dt == 32) hipLaunchKernelGGL((head_kernel<uint16_t, 32>), grid, dim3(64), smem, st, a);
+    else if (dt == 64) hipLaunchKernelGGL((head_kernel<uint16_t, 64>), grid, dim3(64), smem, st, a);
+    else if (dt == 128) hipLaunchKernelGGL((head_kernel<uint16_t, 128>), grid, dim3(64), smem, st, a);
+    else ok = false;
   }
-#undef ATT_G
-#undef ATT_CASE
   if (ok && combine) hipLaunchKernelGGL(attn_combine_kernel, dim3(a.Hq), dim3(128), 0, st, a);
   return ok;
 }
