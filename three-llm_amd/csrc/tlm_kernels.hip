@@ -204,8 +204,10 @@ struct GemvPrologue {
   float4 x[R], w[R];
   ulonglong2 fx[kRmsF ? R : 1][kRep][2];  // RMSF: the 4 elements' replicas
   float4 p[2][kMaxPart];  // RMS: partials per float4 (R rows); SWIGLU: [0] gate, [1] up partials
-  float2 ml[8];           // ATTN: (m, l) and accumulators of the first 8 chunks
-  float4 ac[8];
+  static constexpr int kSlotLanes = 8;  // ATTN: lanes sharing one float4, splitting its chunk slots
+  static constexpr int kSlotsPerLane = 2;
+  float2 ml[kSlotsPerLane];  // ATTN: (m, l) and accumulators of this lane's chunk slots
+  float4 ac[kSlotsPerLane];
   int nact;
   bool fast;  // float4 path (else element-wise, for odd fp16 shapes)
 
@@ -233,12 +235,14 @@ struct GemvPrologue {
       load_parts(a.pin, a.n_pin, a.pin_stride, kc, p[0]);
       load_parts(a.pin + a.up_off, a.n_pin, a.pin_stride, kc, p[1]);
     } else if (PRO == PRO_ATTN) {
+      // slots jb + (lane & 7) + 8u of the float4 at f
       const int row = kc / a.att_D, d = kc % a.att_D;
       const float* mlp = a.pml + (size_t)row * a.att_nsplit * 2;
       const float* acp = a.pacc + (size_t)row * a.att_nsplit * a.att_D + d;
+      const int sl = threadIdx.x & (kSlotLanes - 1);
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const int j = min(jb + u, lim - 1);
+      for (int u = 0; u < kSlotsPerLane; u++) {
+        const int j = min(jb + sl + kSlotLanes * u, lim - 1);
         ml[u] = *reinterpret_cast<const float2*>(mlp + 2 * j);
         ac[u] = *reinterpret_cast<const float4*>(acp + (size_t)j * a.att_D);
       }
@@ -267,9 +271,9 @@ struct GemvPrologue {
         }
       }
     } else if (fast) {
-      // ATTN: the first 8 chunk slots are read before the position is known
-      // (slots past the active count are masked in value4)
-      load_slice4(a, tid, k0, klen_pad / 4, 0, a.att_nsplit);
+      // ATTN: the first chunk slots are read before the position is known
+      // (slots past the active count are masked in attn_finish)
+      load_slice4(a, PRO == PRO_ATTN ? tid / kSlotLanes : tid, k0, klen_pad / 4, 0, a.att_nsplit);
     }
   }
 
@@ -282,31 +286,63 @@ struct GemvPrologue {
       return make_float4(g.x / (1.f + __expf(-g.x)) * u.x, g.y / (1.f + __expf(-g.y)) * u.y,
                          g.z / (1.f + __expf(-g.z)) * u.z, g.w / (1.f + __expf(-g.w)) * u.w);
     }
-    float M = -INFINITY, L = 0.f;
-    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int jb = 0; jb < nact; jb += 8) {
-      if (jb > 0) load_slice4(a, f, k0, n4, jb, nact);
-      float Mb = M;
+    return x[0];  // not reached for PRO_ATTN (attn_finish)
+  }
+
+  // Flash-decoding combine of the attention chunk partials: eight lanes share
+  // one float4 (4 dims of one head) and split its active chunk slots; each
+  // lane merges its slots online, then the eight merge with DPP (max, then the
+  // rescaled sums).  Every lane of the wave takes part.
+  __device__ __forceinline__ void attn_finish(const GemvArgs& a, float* xl, float* xsum, int k0, int klen_pad) {
+    const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, sl = tid & (kSlotLanes - 1);
+    const int n4 = klen_pad / 4, per = nt / kSlotLanes;
+    constexpr int SB = kSlotLanes * kSlotsPerLane;  // slots per batch
+    for (int fb = 0; fb < n4; fb += per) {
+      const int f = fb + tid / kSlotLanes;
+      if (fb > 0) load_slice4(a, f, k0, n4, 0, a.att_nsplit);
+      float M = -INFINITY, L = 0.f;
+      float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int jb = 0; jb < nact; jb += SB) {
+        if (jb > 0) load_slice4(a, f, k0, n4, jb, nact);
+        float Mb = M;
 #pragma unroll
-      for (int u = 0; u < 8; u++) Mb = jb + u < nact ? fmaxf(Mb, ml[u].x) : Mb;
-      const float sc = M == -INFINITY ? 0.f : __expf(M - Mb);
-      L *= sc;
-      O = make_float4(O.x * sc, O.y * sc, O.z * sc, O.w * sc);
+        for (int u = 0; u < kSlotsPerLane; u++)
+          Mb = jb + sl + kSlotLanes * u < nact ? fmaxf(Mb, ml[u].x) : Mb;
+        const float sc = M == -INFINITY ? 0.f : __expf(M - Mb);
+        L *= sc;
+        O = make_float4(O.x * sc, O.y * sc, O.z * sc, O.w * sc);
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
-        // selects, not products: slots past nact may hold anything
-        const bool use = jb + u < nact && ml[u].x != -INFINITY;
-        const float e = use ? __expf(ml[u].x - Mb) : 0.f;
-        L = use ? fmaf(ml[u].y, e, L) : L;
-        O.x = use ? fmaf(ac[u].x, e, O.x) : O.x;
-        O.y = use ? fmaf(ac[u].y, e, O.y) : O.y;
-        O.z = use ? fmaf(ac[u].z, e, O.z) : O.z;
-        O.w = use ? fmaf(ac[u].w, e, O.w) : O.w;
+        for (int u = 0; u < kSlotsPerLane; u++) {
+          // selects, not products: slots past nact may hold anything
+          const bool use = jb + sl + kSlotLanes * u < nact && ml[u].x != -INFINITY;
+          const float e = use ? __expf(ml[u].x - Mb) : 0.f;
+          L = use ? fmaf(ml[u].y, e, L) : L;
+          O.x = use ? fmaf(ac[u].x, e, O.x) : O.x;
+          O.y = use ? fmaf(ac[u].y, e, O.y) : O.y;
+          O.z = use ? fmaf(ac[u].z, e, O.z) : O.z;
+          O.w = use ? fmaf(ac[u].w, e, O.w) : O.w;
+        }
+        M = Mb;
       }
-      M = Mb;
+      // merge the eight lanes of the float4
+      float Mg = fmaxf(M, dpp<kDppXor1>(M));
+      Mg = fmaxf(Mg, dpp<kDppXor2>(Mg));
+      Mg = fmaxf(Mg, dpp<kDppHalfMirror>(Mg));
+      const float sc = M == -INFINITY ? 0.f : __expf(M - Mg);
+      const float Lg = sum8(L * sc);
+      float4 y = make_float4(sum8(O.x * sc), sum8(O.y * sc), sum8(O.z * sc), sum8(O.w * sc));
+      const float il = 1.f / Lg;
+      y = make_float4(y.x * il, y.y * il, y.z * il, y.w * il);
+      const bool valid = f < n4 && k0 + 4 * f < a.K;
+      if (!valid) y = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (sl == 0 && f < n4) *reinterpret_cast<float4*>(xl + 4 * f) = y;
+      if (FMT == WF_Q4) {
+        // a wave's eight float4s are one aligned 32-element group
+        const float gsum = wave_sum(sl == 0 ? (y.x + y.y) + (y.z + y.w) : 0.f);
+        const int f0 = fb + (tid >> 6) * (64 / kSlotLanes);
+        if (lane == 0 && f0 < n4) xsum[f0 / 8] = gsum;
+      }
     }
-    const float il = 1.f / L;
-    return make_float4(O.x * il, O.y * il, O.z * il, O.w * il);
   }
 
   // Residual row float4 r: base + partials, or the sum of the fixed-point replicas.
@@ -376,11 +412,13 @@ struct GemvPrologue {
         }
         xl[i] = y;
       }
+    } else if (PRO == PRO_ATTN) {
+      attn_finish(a, xl, xsum, k0, klen_pad);
     } else {
       const int n4 = klen_pad / 4;
       for (int fb = 0; fb < n4; fb += nt) {
         const int f = fb + tid;
-        if (fb > 0) load_slice4(a, f, k0, n4, 0, PRO == PRO_ATTN ? nact : 1);
+        if (fb > 0) load_slice4(a, f, k0, n4, 0, 1);
         float4 y = value4(a, f, k0, n4);
         if (!(f < n4 && k0 + 4 * f < a.K)) y = make_float4(0.f, 0.f, 0.f, 0.f);
         put4<FMT>(xl, xsum, 4 * f, y, f < n4);
