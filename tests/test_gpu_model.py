@@ -131,6 +131,30 @@ def test_qwen_shape_q4_against_oracle(ctx, layers):
     om.close()
 
 
+def _reduced(name, layers, prompt_len=8):
+    wl = W.WORKLOADS[name]
+    cfg = dict(wl.config, num_hidden_layers=layers)
+    return W.Workload(wl.name + f"-{layers}l", cfg, wl.storage, prompt_len, 6, 512, qkv_bias=wl.qkv_bias)
+
+
+@pytest.mark.parametrize("name", ["llama-3.2-1b", "llama-3.2-3b"])
+def test_llama_shapes_q4_against_oracle(ctx, name):
+    """Llama-3.2-1B (hidden 2048, 32/8 heads, head_dim 64) and 3B (hidden 3072,
+    24/8 heads, head_dim 128) shapes with 2 layers: q4 linears, fp16 tied head,
+    fp16 cache; logits within 2e-2/1e-2 and the greedy stream equal."""
+    wl = _reduced(name, 2)
+    hw = W.synthetic(wl)
+    hw.keep = True
+    runner = R.DecoderHIPRunner(hw, {"maxTokens": wl.max_tokens}, ctx=ctx)
+    om = oracle_model(hw, wl.max_tokens, kv_f16=True, threads=16)
+    prompt = W.prompt_tokens(wl)
+    dev, ref, gaps = greedy_against_oracle(runner, om, prompt, 6)
+    print(name, "device:", dev, "oracle:", ref)
+    assert_streams_match(dev, ref, gaps)
+    runner.close()
+    om.close()
+
+
 def test_device_loop_equals_host_loop(ctx):
     wl = W.WORKLOADS["tiny"]
     hw = W.synthetic(wl)
