@@ -709,7 +709,7 @@ int tlm_op_logits(tlm_linear* head, const float* x, float* logits, int32_t* toke
   a.arg_idx = ctx->arg_idx;
   if (gemv_smem_bytes(wfmt(head->fmt), p.cps, p.waves) > 65536)
     return fail(TLM_ERR_INVALID, "TLMLogits: hidden size %d too large for one block", head->K);
-  if (!launch_lm_head(wfmt(head->fmt), p.waves, p.nch, dim3(p.gx), a, ctx->stream))
+  if (!launch_lm_head(wfmt(head->fmt), PRO_COPY, p.waves, p.nch, dim3(p.gx), a, ctx->stream))
     return fail(TLM_ERR_STATE, "TLMLogits: no kernel variant for this shape");
   // the sampled token lands in token[0] (the merge's ctrl[C_TOKEN])
   launch_argmax_merge(ctx->arg_val, ctx->arg_idx, p.gx, token, nullptr, 0, 0, EmbStage{}, ctx->stream);
@@ -816,6 +816,10 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
       rc = fail(TLM_ERR_INVALID, "TLMModel: hidden size %d too large for the fused MLP block", H);
     m->lm_plan = plan_gemv(m->head->T, m->head->C, ctx->cus, chunk_k(m->head->fmt), true);
     m->lm_plan.gx = std::min(m->head->T, 4096);
+    {  // every chunk of a wave's row slice in flight at once (up to 16)
+      const int per = (m->head->C + m->lm_plan.waves - 1) / m->lm_plan.waves;
+      m->lm_plan.nch = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : 16;
+    }
     if (gemv_smem_bytes(wfmt(m->head->fmt), m->lm_plan.cps, m->lm_plan.waves) > 65536)
       rc = fail(TLM_ERR_INVALID, "TLMModel: hidden size %d too large for one LM head block", H);
   }
@@ -999,35 +1003,34 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which) {
   return ok;
 }
 
-static void enqueue_final_norm(tlm_model* m, hipStream_t st) {
+// LM head with the final RMSNorm in its prologue (every block normalises the
+// last layer's residual accumulator; block 0 stores the result for
+// readHidden) and the first argmax pass fused in, then the argmax merge.
+// `ev` (optional) brackets the LM head kernel with two events.
+static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, hipEvent_t* ev = nullptr) {
   const tlm_model_desc& d = m->d;
-  launch_final_norm(m->rb + (size_t)(d.num_layers - 1) * kRep * d.hidden_size, m->final_norm, d.hidden_size,
-                    (float)d.rms_eps, m->xf, st);
-}
-
-// Final norm (optional), LM head with the fused first argmax pass, argmax
-// merge.  `ev` (optional) brackets the LM head kernel with two events.
-static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, bool final_norm, hipEvent_t* ev = nullptr) {
-  const tlm_model_desc& d = m->d;
-  if (final_norm) enqueue_final_norm(m, st);
   GemvArgs a;
   fill_gemv_args(a, m->head, nullptr);
   a.cps = m->lm_plan.cps;
-  a.in = m->xf;
+  a.acc_in = m->rb + (size_t)(d.num_layers - 1) * kRep * d.hidden_size;
+  a.norm_w = m->final_norm;
+  a.eps = (float)d.rms_eps;
+  a.xnorm = m->xf;
   a.logits = m->logits;
   a.arg_val = m->arg_val;
   a.arg_idx = m->arg_idx;
   if (ev) hipEventRecord(ev[0], st);
-  if (!launch_lm_head(wfmt(m->head->fmt), m->lm_plan.waves, m->lm_plan.nch, dim3(m->lm_plan.gx), a, st)) return false;
+  if (!launch_lm_head(wfmt(m->head->fmt), PRO_RMSF, m->lm_plan.waves, m->lm_plan.nch, dim3(m->lm_plan.gx), a, st))
+    return false;
   if (ev) hipEventRecord(ev[1], st);
   launch_argmax_merge(m->arg_val, m->arg_idx, m->lm_plan.gx, m->ctrl, advance ? m->tokens_out : nullptr,
                       advance ? 1 : 0, d.max_tokens, emb_stage(m), st);
   return true;
 }
 
-// Graph tails: the decode/logits step, the prefill step, or the layers and
-// final norm alone (LM head timing).
-enum GraphTail { TAIL_PREFILL = 0, TAIL_LOGITS = 1, TAIL_NORM = 2 };
+// Graph tails: the decode/logits step, the prefill step, or the layers alone
+// (LM head timing).
+enum GraphTail { TAIL_PREFILL = 0, TAIL_LOGITS = 1, TAIL_NONE = 2 };
 
 static int capture(tlm_model* m, int tail, hipGraph_t* g, hipGraphExec_t* ge) {
   hipStream_t st = m->ctx->stream;
@@ -1035,11 +1038,9 @@ static int capture(tlm_model* m, int tail, hipGraph_t* g, hipGraphExec_t* ge) {
   bool ok = true;
   for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1);
   if (tail == TAIL_LOGITS)
-    ok &= enqueue_head(m, st, true, true);
+    ok &= enqueue_head(m, st, true);
   else if (tail == TAIL_PREFILL)
     launch_prefill_advance(m->ctrl, m->prompt, emb_stage(m), st);
-  else
-    enqueue_final_norm(m, st);
   hipError_t le = hipGetLastError();
   HIP_TRY(hipStreamEndCapture(st, g));
   if (le != hipSuccess) return fail(TLM_ERR_HIP, "TLMModel: launch during capture failed: %s", hipGetErrorString(le));
@@ -1075,7 +1076,7 @@ static int run_token(tlm_model* m, bool logits) {
   bool ok = true;
   for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1);
   if (logits)
-    ok &= enqueue_head(m, st, true, true);
+    ok &= enqueue_head(m, st, true);
   else
     launch_prefill_advance(m->ctrl, m->prompt, emb_stage(m), st);
   if (!ok) return fail(TLM_ERR_STATE, "TLMModel: no kernel variant for a stage of this model");
@@ -1264,7 +1265,7 @@ int tlm_time_head(tlm_model* m, int32_t token, int32_t position, int n, double* 
   if (rc) return rc;
   hipStream_t st = m->ctx->stream;
   if (m->use_graphs && !m->g_layers) {
-    rc = capture(m, TAIL_NORM, &m->graph_layers, &m->g_layers);
+    rc = capture(m, TAIL_NONE, &m->graph_layers, &m->g_layers);
     if (rc) return rc;
   }
   std::vector<hipEvent_t> ev(2 * (size_t)n, nullptr);
@@ -1276,9 +1277,8 @@ int tlm_time_head(tlm_model* m, int32_t token, int32_t position, int n, double* 
       HIP_TRY(hipGraphLaunch(m->g_layers, st));
     } else {
       for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1);
-      enqueue_final_norm(m, st);
     }
-    ok &= enqueue_head(m, st, true, false, &ev[2 * (size_t)i]);
+    ok &= enqueue_head(m, st, true, &ev[2 * (size_t)i]);
   }
   if (!ok) return fail(TLM_ERR_STATE, "TLMModel: no kernel variant for a stage of this model");
   CHECK_LAUNCH("TLMModel");
@@ -1303,7 +1303,7 @@ int tlm_time_kernel(tlm_model* m, int which, int iters, double* avg_ms) {
   hipEvent_t e0, e1;
   HIP_TRY(hipEventCreate(&e0));
   HIP_TRY(hipEventCreate(&e1));
-  auto one = [&]() { return which == 0 ? enqueue_head(m, st, false, false) : enqueue_layer(m, 0, st, which); };
+  auto one = [&]() { return which == 0 ? enqueue_head(m, st, false) : enqueue_layer(m, 0, st, which); };
   if (!one()) return fail(TLM_ERR_STATE, "TLMModel: no kernel variant for stage %d", which);  // warm
   CHECK_LAUNCH("TLMModel");
   HIP_TRY(hipStreamSynchronize(st));

@@ -82,7 +82,8 @@ struct GemvArgs {
   const float* pacc;   // [Hq][nsplit][D]
   const float* pml;    // [Hq][nsplit][2]
   int att_D, att_nsplit, att_chmin, att_window, att_max_tokens;
-  // LM head epilogue
+  // LM head
+  float* xnorm;        // with an RMS prologue: block 0 stores the normalised input here (may be null)
   float* logits;       // full logits (may be null)
   float* arg_val;      // per-block argmax partials
   int* arg_idx;
@@ -129,12 +130,11 @@ bool launch_gemv(int fmt, int pro, int waves, int nch, dim3 grid, const GemvArgs
 bool launch_mlp(int fmt, int nch, int ndb, int blocks, const MlpArgs& a, hipStream_t st);
 size_t mlp_smem_bytes(int fmt, int C, int K);
 constexpr int kMlpWaves = 8;
-bool launch_lm_head(int fmt, int waves, int nch, dim3 grid, const GemvArgs& a, hipStream_t st);
+// pro: PRO_COPY (input a.in) or PRO_RMSF (the final norm fused in); nch up to 16
+bool launch_lm_head(int fmt, int pro, int waves, int nch, dim3 grid, const GemvArgs& a, hipStream_t st);
 // attention chunk partials; with `combine` also the combine kernel writing a.out
 bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, bool combine, hipStream_t st);
 size_t gemv_smem_bytes(int fmt, int cps, int waves);
-// y = rmsnorm(sum of the kRep replicas of acc) * w, n <= 4096
-void launch_final_norm(const unsigned long long* acc, const float* w, int n, float eps, float* y, hipStream_t st);
 void launch_rmsnorm(const float* x, const float* w, int n, float eps, int offset, float* y, hipStream_t st);
 void launch_silu_mul(const float* g, const float* u, int n, float* out, hipStream_t st);
 void launch_reduce(const float* part, int n_part, int stride, const float* bias, int n, float* y, hipStream_t st);

@@ -571,7 +571,7 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvArgs a) {
 // LM head: GEMV over the vocabulary (PRO_COPY input) with the first pass of
 // the greedy sampler fused in (createChunkPartialMaxNode, TSLLogits.ts:201-248):
 // each block keeps its best (score, id) over its tiles.
-template <int FMT, int W, int NCH>
+template <int FMT, int PRO, int W, int NCH>
 __global__ __launch_bounds__(W * 64) void lm_head_kernel(GemvArgs a) {
   extern __shared__ float sm[];
   constexpr int CK = GemvCore<FMT, NCH>::CK;
@@ -580,7 +580,7 @@ __global__ __launch_bounds__(W * 64) void lm_head_kernel(GemvArgs a) {
   GemvSmem L(sm, a.cps, CK, W);
   const int nw = wave < ncl ? (ncl - wave + W - 1) / W : 0;
 
-  GemvPrologue<PRO_COPY, FMT> pro;
+  GemvPrologue<PRO, FMT> pro;
   pro.issue(a, 0, ncl * CK);
   GemvCore<FMT, NCH> core;
   int t = blockIdx.x;
@@ -588,6 +588,8 @@ __global__ __launch_bounds__(W * 64) void lm_head_kernel(GemvArgs a) {
   __builtin_amdgcn_sched_barrier(0);
   pro.finish(a, L.xl, L.xsum, L.scratch, 0, a.K, ncl * CK);
   __syncthreads();
+  if (a.xnorm && blockIdx.x == 0)  // the final hidden state (readHidden)
+    for (int k = threadIdx.x; k < a.K; k += blockDim.x) a.xnorm[k] = L.xl[k];
   float best_v = kLowest;
   int best_i = 0x7fffffff;
   for (; t < a.T; t += gridDim.x) {
@@ -719,15 +721,20 @@ bool launch_gemv(int fmt, int pro, int waves, int nch, dim3 grid, const GemvArgs
   return false;
 }
 
-bool launch_lm_head(int fmt, int waves, int nch, dim3 grid, const GemvArgs& a, hipStream_t st) {
+bool launch_lm_head(int fmt, int pro, int waves, int nch, dim3 grid, const GemvArgs& a, hipStream_t st) {
   const size_t smem = gemv_smem_bytes(fmt, a.cps, waves);
-#define LM_CASE(F, Wv, N)                                                               \
-  if (fmt == F && waves == Wv && nch == N) {                                            \
-    hipLaunchKernelGGL((lm_head_kernel<F, Wv, N>), grid, dim3(Wv * 64), smem, st, a);   \
-    return true;                                                                        \
+  if (pro == PRO_RMSF && a.K > 4 * 64 * waves) pro = PRO_RMSF2;
+  if (pro == PRO_RMSF2 && a.K > 8 * 64 * waves) return false;
+#define LM_CASE(F, P, Wv, N)                                                               \
+  if (fmt == F && pro == P && waves == Wv && nch == N) {                                   \
+    hipLaunchKernelGGL((lm_head_kernel<F, P, Wv, N>), grid, dim3(Wv * 64), smem, st, a);   \
+    return true;                                                                           \
   }
-#define LM_N(F, Wv) LM_CASE(F, Wv, 1) LM_CASE(F, Wv, 2) LM_CASE(F, Wv, 4) LM_CASE(F, Wv, 8)
-  LM_N(WF_F16, 4) LM_N(WF_F16, 8) LM_N(WF_Q4, 4) LM_N(WF_Q4, 8)
+#define LM_N(F, P, Wv) LM_CASE(F, P, Wv, 1) LM_CASE(F, P, Wv, 2) LM_CASE(F, P, Wv, 4) LM_CASE(F, P, Wv, 8) \
+  LM_CASE(F, P, Wv, 16)
+#define LM_P(F, Wv) LM_N(F, PRO_COPY, Wv) LM_N(F, PRO_RMSF, Wv) LM_N(F, PRO_RMSF2, Wv)
+  LM_P(WF_F16, 4) LM_P(WF_F16, 8) LM_P(WF_Q4, 4) LM_P(WF_Q4, 8)
+#undef LM_P
 #undef LM_N
 #undef LM_CASE
   return false;
@@ -1149,40 +1156,6 @@ bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, bool combine, hi
 // --------------------------------------------------------- small kernels --
 
 // Final norm: x = base + sum(pin); y = rmsnorm(x) * w (one block).
-__global__ __launch_bounds__(1024) void final_norm_kernel(const unsigned long long* acc, const float* w, int n,
-                                                          float eps, float* y) {
-  __shared__ float scratch[16];
-  // n <= 4 * blockDim.x: every element is loaded in one round trip and kept in registers
-  unsigned long long q[kEpt][kRep];
-#pragma unroll
-  for (int e = 0; e < kEpt; e++) {
-    const int k = min(threadIdx.x + e * blockDim.x, n - 1);
-#pragma unroll
-    for (int r = 0; r < kRep; r++) q[e][r] = acc[(size_t)r * n + k];
-  }
-  float v[kEpt];
-  float ss = 0.f;
-#pragma unroll
-  for (int e = 0; e < kEpt; e++) {
-    const int k = threadIdx.x + e * blockDim.x;
-    unsigned long long s = 0;
-#pragma unroll
-    for (int r = 0; r < kRep; r++) s += q[e][r];
-    v[e] = k < n ? from_fx(s) : 0.f;
-    ss = fmaf(v[e], v[e], ss);
-  }
-  const float inv = rsqrtf(block_sum(ss, scratch) / (float)n + eps);
-#pragma unroll
-  for (int e = 0; e < kEpt; e++) {
-    const int k = threadIdx.x + e * blockDim.x;
-    if (k < n) y[k] = v[e] * inv * w[k];
-  }
-}
-
-void launch_final_norm(const unsigned long long* acc, const float* w, int n, float eps, float* y, hipStream_t st) {
-  hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, st, acc, w, n, eps, y);
-}
-
 __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* x, const float* w, int n, float eps, int offset,
                                                        float* y) {
   __shared__ float scratch[16];
