@@ -86,6 +86,12 @@ void tlm_linear_destroy(tlm_linear* lin);
 int tlm_linear_dequant(tlm_linear* lin, float* host_out);
 /* y = bias + W x.  x: fp32[K] device, bias: fp32[N] device or NULL, y: fp32[N] device. */
 int tlm_op_linear(tlm_linear* lin, const float* x, const float* bias, float* y);
+/* The same linear over `rows` tokens at once, as one MFMA GEMM (the batched
+ * prefill's linear; the reference applies TSLLinear once per replayed token,
+ * DecoderTSLRunner.ts:472-480).  x: fp16 bits device [rows][K] (K % 32 == 0),
+ * y: fp32 device [rows][N].  W is dequantised to fp16 ((code - 8) * s rounded
+ * once), products accumulate in fp32.  Enqueue only. */
+int tlm_op_linear_rows(tlm_linear* lin, const uint16_t* x, int32_t rows, const float* bias, float* y);
 
 /* ----------------------------------------------------------- element ops */
 /* TSLRMSNorm (tsl/TSLRMSNorm.ts:18-81): y = x * rsqrt(mean(x^2) + eps) * (offset ? 1 + w : w). */
@@ -117,6 +123,13 @@ void tlm_attn_destroy(tlm_attn* attn);
 /* qkv: fp32 device [(heads + 2 kv_heads) * head_dim] (packed Q|K|V, pre-RoPE);
  * out: fp32 device [heads * head_dim]. */
 int tlm_op_attention(tlm_attn* attn, const float* qkv, int position, float* out);
+/* `rows` consecutive positions position0.. at once (the batched prefill's
+ * attention; the reference runs TSLAttention once per replayed token): qkv fp32
+ * device [rows][(heads + 2 kv_heads) * head_dim], bias included; RoPE, the K/V
+ * rows appended to the cache, causal attention of each row over
+ * [max(0, pos - W + 1), pos] on MFMA; out: fp16 bits device [rows][heads * head_dim].
+ * Needs an fp16 cache and head_dim 64 or 128.  Waits for the stream. */
+int tlm_op_attention_rows(tlm_attn* attn, const float* qkv, int32_t rows, int32_t position0, uint16_t* out);
 int tlm_attn_reset(tlm_attn* attn);
 /* Cache rows [0, count) as fp32 [count][kv_heads*head_dim] (host). */
 int tlm_attn_read_cache(tlm_attn* attn, int count, float* k_out, float* v_out);
@@ -179,6 +192,15 @@ int tlm_model_finalize(tlm_model* model);
 int tlm_compute_token(tlm_model* model, int32_t token, int32_t position, int flags);
 /* prefillTokens (DecoderTSLRunner.ts:504-530): positions [start, end), no logits. */
 int tlm_prefill(tlm_model* model, const int32_t* tokens, int32_t start, int32_t end);
+/* Batched prefill control: tlm_prefill runs chunks of up to `chunk` positions
+ * with at least `min_rows` positions (default 64, chunk 2048) as row batches
+ * (MFMA GEMMs and flash attention per layer, tlm_op_linear_rows /
+ * tlm_op_attention_rows) and replays the decode graph per position below
+ * that, as the reference always does (DecoderTSLRunner.ts:472-480).
+ * min_rows <= 0 turns the batched path off; TLM_ERR_INVALID names why a model
+ * cannot use it (fp32 cache, head_dim other than 64/128, sizes not multiples
+ * of 32, a q4 scale above 8188). */
+int tlm_model_set_prefill(tlm_model* model, int32_t min_rows, int32_t chunk);
 /* readLogits (DecoderTSLRunner.ts:532-535): waits, copies n <= vocab floats. */
 int tlm_read_logits(tlm_model* model, float* out, size_t n);
 /* sampleToken greedy (TSLLogits.ts:359-361): waits, returns the argmax. */

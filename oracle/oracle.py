@@ -244,6 +244,12 @@ class Model:
             raise ValueError("oracle: token or position out of range")
         return (logits, hidden) if want_hidden else logits
 
+    def prefill(self, token, position):
+        """One prompt position without the LM head (prefillTokens computes no
+        logits, DecoderTSLRunner.ts:504-530)."""
+        if lib().orc_forward_token(self.ptr, int(token), int(position), None, None) != 0:
+            raise ValueError("oracle: token or position out of range")
+
     def close(self):
         if self.ptr:
             lib().orc_model_free(self.ptr)

@@ -17,7 +17,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libtlm.so"
-SOURCES = ["tlm_api.hip", "tlm_kernels.hip", "tlm_host.cpp"]
+SOURCES = ["tlm_api.hip", "tlm_kernels.hip", "tlm_prefill.hip", "tlm_host.cpp"]
 ARCH = os.environ.get("TLM_OFFLOAD_ARCH", "gfx950")
 
 

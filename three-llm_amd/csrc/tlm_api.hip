@@ -70,6 +70,7 @@ struct tlm_linear {
   // paired layout (fused MLP gate|up, N = 2I): canonical gate row i sits in
   // tile i / 32, lane i % 32; up row I + i in the same tile, lane 32 + i % 32
   int pair_half = 0;  // I when paired, else 0
+  uint16_t smax = 0;  // q4: largest scale magnitude uploaded (fp16 bits)
 };
 
 // Physical row of canonical row r.
@@ -131,6 +132,12 @@ struct tlm_model {
   // attention (shared by the layers; they run one after another)
   tlm_attn attn;
   GemvPlan lm_plan;
+  // batched prefill: chunks of at least pf_min_rows positions (0: off) run as
+  // MFMA GEMMs over pf_chunk rows at a time; row buffers for pf_cap rows are
+  // allocated on first use
+  int pf_min_rows = 64, pf_chunk = 2048, pf_cap = 0;
+  float *pf_x = nullptr, *pf_qkv = nullptr;
+  uint16_t *pf_xn = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_h = nullptr;
   hipGraphExec_t g_logits = nullptr, g_prefill = nullptr, g_layers = nullptr;
   hipGraph_t graph_logits = nullptr, graph_prefill = nullptr, graph_layers = nullptr;
   bool finalized = false;
@@ -238,8 +245,11 @@ static int linear_write_rows(tlm_linear* L, int r0, int rows, const void* data, 
     for (int r = r0; r < r0 + rows; r++) {
       const int pr = phys_row(L, r);
       const int t = pr / kTile - t0, lane = pr % kTile;
-      for (int c = 0; c < L->C; c++)
-        host[((size_t)t * L->C + c) * kTile + lane] = c < G ? scales[(size_t)(r - r0) * G + c] : 0;
+      for (int c = 0; c < L->C; c++) {
+        const uint16_t sv = c < G ? scales[(size_t)(r - r0) * G + c] : 0;
+        host[((size_t)t * L->C + c) * kTile + lane] = sv;
+        L->smax = std::max<uint16_t>(L->smax, sv & 0x7fff);
+      }
     }
     HIP_TRY(hipMemcpy(dst, host.data(), host.size() * sizeof(uint16_t), hipMemcpyHostToDevice));
   }
@@ -449,6 +459,30 @@ int tlm_op_linear(tlm_linear* L, const float* x, const float* bias, float* y) {
   return TLM_OK;
 }
 
+int tlm_op_linear_rows(tlm_linear* L, const uint16_t* x, int32_t rows, const float* bias, float* y) {
+  if (!L || !x || !y || rows <= 0) return fail(TLM_ERR_INVALID, "TLMLinear: invalid argument");
+  if (L->pair_half) return fail(TLM_ERR_INVALID, "TLMLinear: paired layout");
+  GemmArgs g;
+  memset(&g, 0, sizeof g);
+  g.A = x;
+  g.lda = L->K;
+  g.M = rows;
+  g.N = L->N;
+  g.K = L->K;
+  g.w = L->w;
+  g.s = L->s;
+  g.C = L->C;
+  g.bias = bias;
+  g.Cf = y;
+  g.ldc = L->N;
+  if (L->fmt == TLM_FMT_Q4 && L->smax > 0x6FFF)
+    return fail(TLM_ERR_INVALID, "TLMLinear: q4 scale above 8188 overflows the fp16 GEMM operand");
+  if (!launch_gemm(wfmt(L->fmt), GEMM_STORE, g, L->ctx->stream))
+    return fail(TLM_ERR_INVALID, "TLMLinear: batched rows need K %% 32 == 0 (K = %d)", L->K);
+  CHECK_LAUNCH("TLMLinear");
+  return TLM_OK;
+}
+
 // -------------------------------------------------------------- element ops --
 
 int tlm_op_rmsnorm(tlm_ctx* ctx, const float* x, const float* w, int n, double eps, int offset, float* y) {
@@ -636,6 +670,57 @@ int tlm_op_attention(tlm_attn* A, const float* qkv, int position, float* out) {
   if (!launch_attention(A->d.kv_fmt == TLM_FMT_F32, A->gmax, a, true, st))
     return fail(TLM_ERR_STATE, "TLMAttention: no kernel variant for this shape");
   CHECK_LAUNCH("TLMAttention");
+  return TLM_OK;
+}
+
+int tlm_op_attention_rows(tlm_attn* A, const float* qkv, int32_t rows, int32_t position0, uint16_t* out) {
+  if (!A || !qkv || !out || rows <= 0) return fail(TLM_ERR_INVALID, "TLMAttention: invalid argument");
+  const tlm_attn_desc& d = A->d;
+  if (position0 < 0 || position0 + rows > d.max_tokens)
+    return fail(TLM_ERR_RANGE, "TLMAttention: rows [%d, %d) outside [0, %d)", position0, position0 + rows,
+                d.max_tokens);
+  if (d.kv_fmt == TLM_FMT_F32 || (d.head_dim != 64 && d.head_dim != 128))
+    return fail(TLM_ERR_INVALID, "TLMAttention: batched rows need an fp16 cache and head_dim 64 or 128");
+  hipStream_t st = A->ctx->stream;
+  uint16_t* q = nullptr;
+  const size_t qn = (size_t)rows * d.heads * d.head_dim;
+  HIP_TRY(hipMalloc(&q, 2 * qn));
+  RopeKvArgs r;
+  memset(&r, 0, sizeof r);
+  r.qkv = qkv;
+  r.M = rows;
+  r.p0 = position0;
+  r.Hq = d.heads;
+  r.Hkv = d.kv_heads;
+  r.D = d.head_dim;
+  r.rd = d.rotary_dim;
+  r.max_tokens = d.max_tokens;
+  r.rope_cos = A->rope_cos;
+  r.rope_sin = A->rope_sin;
+  r.q = q;
+  r.kc = A->kc;
+  r.vc = A->vc;
+  launch_rope_kv(r, st);
+  PrefillAttnArgs pa;
+  memset(&pa, 0, sizeof pa);
+  pa.q = q;
+  pa.kc = A->kc;
+  pa.vc = A->vc;
+  pa.out = out;
+  pa.M = rows;
+  pa.p0 = position0;
+  pa.Hq = d.heads;
+  pa.Hkv = d.kv_heads;
+  pa.D = d.head_dim;
+  pa.G = A->G;
+  pa.max_tokens = d.max_tokens;
+  pa.window = d.sliding_window;
+  pa.scale_log2 = A->scale * 1.4426950408889634f;
+  launch_prefill_attention(pa, st);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  hipFree(q);
+  if (e != hipSuccess) return fail(TLM_ERR_HIP, "TLMAttention: batched rows failed: %s", hipGetErrorString(e));
   return TLM_OK;
 }
 
@@ -860,7 +945,8 @@ void tlm_model_destroy(tlm_model* m) {
   tlm_linear_destroy(m->head);
   attn_free(&m->attn, false);
   void* bufs[] = {m->emb, m->final_norm, m->ctrl, m->tokens_out, m->prompt, m->xa, m->x0, m->xf, m->attn_out,
-                  m->pq, m->po, m->rb, m->logits, m->arg_val, m->arg_idx};
+                  m->pq, m->po, m->rb, m->logits, m->arg_val, m->arg_idx, m->pf_x, m->pf_qkv, m->pf_xn,
+                  m->pf_q, m->pf_att, m->pf_h};
   for (void* p : bufs) hipFree(p);
   delete m;
 }
@@ -1104,6 +1190,142 @@ int tlm_compute_token(tlm_model* m, int32_t token, int32_t position, int flags) 
   return run_token(m, (flags & TLM_LOGITS) != 0);
 }
 
+// Why the batched prefill cannot serve this model (null: it can).
+static const char* prefill_unsupported(const tlm_model* m) {
+  const tlm_model_desc& d = m->d;
+  const int H = d.hidden_size, I = d.intermediate_size;
+  if (d.linear_fmt != TLM_FMT_Q4 && d.linear_fmt != TLM_FMT_F16) return "linears are neither q4 nor fp16";
+  if (d.kv_fmt == TLM_FMT_F32) return "the fp32 KV cache";
+  if (d.head_dim != 64 && d.head_dim != 128) return "head_dim other than 64 or 128";
+  if (H % 32 || I % 32 || m->QS % 32) return "hidden, intermediate and q sizes must be multiples of 32";
+  // fp16 dequantised weights: (code - 8) * s must stay finite, 8 s <= 65504
+  for (const Layer& L : m->layers)
+    for (const tlm_linear* lin : {L.qkv, L.o, L.gu, L.down})
+      if (lin->fmt == TLM_FMT_Q4 && lin->smax > 0x6FFF) return "a q4 scale above 8188 (fp16 overflow)";
+  return nullptr;
+}
+
+static int prefill_alloc(tlm_model* m, int rows) {
+  if (m->pf_cap >= rows) return TLM_OK;
+  rows = std::max(rows, m->pf_chunk);  // one allocation serves every later chunk
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  void* bufs[] = {m->pf_x, m->pf_qkv, m->pf_xn, m->pf_q, m->pf_att, m->pf_h};
+  for (void* p : bufs) hipFree(p);
+  m->pf_x = m->pf_qkv = nullptr;
+  m->pf_xn = m->pf_q = m->pf_att = m->pf_h = nullptr;
+  m->pf_cap = 0;
+  const size_t R = (size_t)rows, H = m->d.hidden_size, I = m->d.intermediate_size;
+  int rc = TLM_OK;
+  if (!rc) rc = model_alloc((void**)&m->pf_x, sizeof(float) * R * H);
+  if (!rc) rc = model_alloc((void**)&m->pf_qkv, sizeof(float) * R * m->Nqkv);
+  if (!rc) rc = model_alloc((void**)&m->pf_xn, 2 * R * H);
+  if (!rc) rc = model_alloc((void**)&m->pf_q, 2 * R * m->QS);
+  if (!rc) rc = model_alloc((void**)&m->pf_att, 2 * R * m->QS);
+  if (!rc) rc = model_alloc((void**)&m->pf_h, 2 * R * I);
+  if (!rc) m->pf_cap = rows;
+  return rc;
+}
+
+static GemmArgs gemm_args(const tlm_linear* L, const uint16_t* A, int lda, int M) {
+  GemmArgs g;
+  memset(&g, 0, sizeof g);
+  g.A = A;
+  g.lda = lda;
+  g.M = M;
+  g.N = L->N;
+  g.K = L->K;
+  g.w = L->w;
+  g.s = L->s;
+  g.C = L->C;
+  return g;
+}
+
+// Positions [p0, p0 + M) through every layer as row batches; the K and V rows
+// land in the cache, nothing else of the model's decode state changes.
+// tokens: device array of the M token ids.
+static int prefill_rows(tlm_model* m, const int* tokens, int p0, int M) {
+  int rc = prefill_alloc(m, M);
+  if (rc) return rc;
+  const tlm_model_desc& d = m->d;
+  const int H = d.hidden_size, I = d.intermediate_size, D = d.head_dim;
+  const int lf = wfmt(d.linear_fmt);
+  hipStream_t st = m->ctx->stream;
+  launch_embed_rows(tokens, M, m->emb, d.embed_fmt == TLM_FMT_F32, H, m->pf_x, st);
+  for (int l = 0; l < d.num_layers; l++) {
+    const Layer& L = m->layers[l];
+    bool ok = true;
+    launch_rms_rows(m->pf_x, M, H, L.attn_norm, (float)d.rms_eps, m->pf_xn, st);
+    GemmArgs g = gemm_args(L.qkv, m->pf_xn, H, M);
+    g.bias = L.bqkv;
+    g.Cf = m->pf_qkv;
+    g.ldc = m->Nqkv;
+    ok = ok && launch_gemm(lf, GEMM_STORE, g, st);
+    RopeKvArgs r;
+    memset(&r, 0, sizeof r);
+    r.qkv = m->pf_qkv;
+    r.M = M;
+    r.p0 = p0;
+    r.Hq = d.num_heads;
+    r.Hkv = d.num_kv_heads;
+    r.D = D;
+    r.rd = d.rotary_dim;
+    r.max_tokens = d.max_tokens;
+    r.rope_cos = m->attn.rope_cos;
+    r.rope_sin = m->attn.rope_sin;
+    r.q = m->pf_q;
+    r.kc = L.kc;
+    r.vc = L.vc;
+    r.kv_f32 = 0;
+    launch_rope_kv(r, st);
+    PrefillAttnArgs pa;
+    memset(&pa, 0, sizeof pa);
+    pa.q = m->pf_q;
+    pa.kc = L.kc;
+    pa.vc = L.vc;
+    pa.out = m->pf_att;
+    pa.M = M;
+    pa.p0 = p0;
+    pa.Hq = d.num_heads;
+    pa.Hkv = d.num_kv_heads;
+    pa.D = D;
+    pa.G = m->attn.G;
+    pa.max_tokens = d.max_tokens;
+    pa.window = d.sliding_window;
+    pa.scale_log2 = m->attn.scale * 1.4426950408889634f;
+    ok = ok && launch_prefill_attention(pa, st);
+    g = gemm_args(L.o, m->pf_att, m->QS, M);
+    g.Cf = m->pf_x;
+    g.ldc = H;
+    ok = ok && launch_gemm(lf, GEMM_ADD, g, st);
+    launch_rms_rows(m->pf_x, M, H, L.ffn_norm, (float)d.rms_eps, m->pf_xn, st);
+    g = gemm_args(L.gu, m->pf_xn, H, M);
+    g.N = L.gu->T * kTile;
+    g.Ch = m->pf_h;
+    g.ldc = I;
+    g.n_out = I;
+    ok = ok && launch_gemm(lf, GEMM_SWIGLU, g, st);
+    g = gemm_args(L.down, m->pf_h, I, M);
+    g.Cf = m->pf_x;
+    g.ldc = H;
+    ok = ok && launch_gemm(lf, GEMM_ADD, g, st);
+    if (!ok) return fail(TLM_ERR_STATE, "TLMModel: no batched prefill kernel for layer %d", l);
+    CHECK_LAUNCH("TLMModel");
+  }
+  return TLM_OK;
+}
+
+int tlm_model_set_prefill(tlm_model* m, int32_t min_rows, int32_t chunk) {
+  if (!m) return fail(TLM_ERR_INVALID, "TLMModel: null model");
+  if (chunk < 1) return fail(TLM_ERR_INVALID, "TLMModel: prefill chunk %d must be positive", chunk);
+  if (min_rows > 0) {
+    const char* why = prefill_unsupported(m);
+    if (why) return fail(TLM_ERR_INVALID, "TLMModel: batched prefill unavailable: %s", why);
+  }
+  m->pf_min_rows = std::max(0, min_rows);
+  m->pf_chunk = std::min(chunk, m->d.max_tokens);
+  return TLM_OK;
+}
+
 int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end) {
   if (!m || (!tokens && end > start)) return fail(TLM_ERR_INVALID, "TLMModel: null argument");
   if (start < 0 || end > m->d.max_tokens || start > end)
@@ -1117,11 +1339,18 @@ int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end)
   hipStream_t st = m->ctx->stream;
   HIP_TRY(hipStreamSynchronize(st));
   HIP_TRY(hipMemcpy(m->prompt, tokens + start, sizeof(int32_t) * (end - start), hipMemcpyHostToDevice));
-  launch_set_ctrl(m->ctrl, tokens[start], start, 0, start, end - start, emb_stage(m), st);
-  CHECK_LAUNCH("TLMModel");
-  for (int i = start; i < end; i++) {
-    rc = run_token(m, false);
+  const bool batched = m->pf_min_rows > 0 && !prefill_unsupported(m);
+  for (int p = start; p < end;) {
+    const int n = std::min(end - p, batched ? m->pf_chunk : end - p);
+    if (batched && n >= m->pf_min_rows) {
+      rc = prefill_rows(m, m->prompt + (p - start), p, n);
+    } else {  // the decode graph replayed per position
+      launch_set_ctrl(m->ctrl, tokens[p], p, 0, start, end - start, emb_stage(m), st);
+      CHECK_LAUNCH("TLMModel");
+      for (int i = 0; i < n && !rc; i++) rc = run_token(m, false);
+    }
     if (rc) return rc;
+    p += n;
   }
   return TLM_OK;
 }

@@ -153,4 +153,49 @@ void launch_kv_fill(void* kc, void* vc, bool f32, size_t heads_stride, int Hkv, 
 size_t attn_smem_bytes(int gmax, int D, bool kv_f32);
 int attn_lpp(int D, bool kv_f32);
 
+// ------------------------------------------------------------ batched prefill --
+// A chunk of M prompt positions per pass: row-major activations, linears as
+// MFMA GEMMs C[M][N] = A[M][K] * W^T over the tiled weight layout.
+enum GemmEpi {
+  GEMM_STORE = 0,   // Cf[m][n] = acc + bias[n]
+  GEMM_ADD = 1,     // Cf[m][n] += acc (residual stream)
+  GEMM_SWIGLU = 2,  // Ch[m][i] = fp16(silu(gate) * up), paired gate|up weight rows
+};
+struct GemmArgs {
+  const uint16_t* A;   // fp16 [M][lda]
+  int lda, M, N, K;    // N: physical weight rows (64 per tile)
+  const uint4* w;      // [T][C][64] 16-byte chunks
+  const uint16_t* s;   // q4 scales [T][C][64]
+  int C;               // chunks per row in the weight layout
+  const float* bias;   // GEMM_STORE, may be null
+  float* Cf;           // fp32 [M][ldc]
+  uint16_t* Ch;        // GEMM_SWIGLU: fp16 [M][ldc]
+  int ldc;
+  int n_out;           // GEMM_SWIGLU: intermediate size I (outputs i < n_out)
+};
+struct PrefillAttnArgs {
+  const uint16_t* q;    // fp16 [M][Hq D], RoPE applied
+  const void* kc;       // fp16 [Hkv][max_tokens][D] (this layer)
+  const void* vc;
+  uint16_t* out;        // fp16 [M][Hq D]
+  int M, p0, Hq, Hkv, D, G, max_tokens, window;
+  float scale_log2;     // softmax scale * log2(e)
+};
+struct RopeKvArgs {
+  const float* qkv;     // fp32 [M][Nqkv] (bias included)
+  int M, p0, Hq, Hkv, D, rd, max_tokens;
+  const float* rope_cos;  // [max_tokens][rd / 2]
+  const float* rope_sin;
+  uint16_t* q;          // fp16 [M][Hq D]
+  void* kc;             // [Hkv][max_tokens][D]
+  void* vc;
+  int kv_f32;
+};
+bool launch_gemm(int fmt, int epi, const GemmArgs& g, hipStream_t st);
+void launch_embed_rows(const int* tokens, int M, const void* emb, int f32, int H, float* X, hipStream_t st);
+void launch_rms_rows(const float* X, int M, int H, const float* w, float eps, uint16_t* Y, hipStream_t st);
+void launch_rope_kv(const RopeKvArgs& a, hipStream_t st);
+bool launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t st);
+void launch_rows_to_f16(const float* x, size_t n, uint16_t* y, hipStream_t st);
+
 }  // namespace tlm

@@ -1,0 +1,415 @@
+// Batched prefill: M prompt positions per layer pass.  The reference replays
+// its one-token decode graph once per prompt position (DecoderTSLRunner.ts:
+// 472-480, 504-530); here the linears of all M positions run as one q4 x fp16
+// GEMM on MFMA (v_mfma_f32_32x32x16_f16) and causal attention as one MFMA
+// flash-attention pass, which gives the token-by-token result up to fp16
+// rounding of the activations.
+#include "tlm_kernels.h"
+#include <hip/hip_fp16.h>
+#include <math.h>
+
+namespace tlm {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+namespace {
+
+// 8 q4 codes of one dword (k order: low then high nibble of each byte) as
+// fp16 (code - 8) * s.  The fp16 bit pattern 0x6400 | n is 1024 + n, so
+// subtracting 1032 gives n - 8 exactly; the product with s rounds once.
+__device__ __forceinline__ half8_t dequant8(uint32_t w, half2_t s2) {
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+  half8_t r;
+#pragma unroll
+  for (int b = 0; b < 4; b++) {
+    // byte 0 <- lo byte b, byte 2 <- hi byte b, bytes 1 and 3 <- 0 (selector 0x0c)
+    const uint32_t sel = 0x0c000c00u | (uint32_t)b | ((uint32_t)(4 + b) << 16);
+    const uint32_t bits = __builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u;
+    half2_t v = __builtin_bit_cast(half2_t, bits);
+    v = (v - (half2_t){(_Float16)1032.f, (_Float16)1032.f}) * s2;
+    r[2 * b] = v[0];
+    r[2 * b + 1] = v[1];
+  }
+  return r;
+}
+
+__device__ __forceinline__ half8_t as_half8(uint4 v) { return __builtin_bit_cast(half8_t, v); }
+
+__device__ __forceinline__ float block_sum_f(float v, float* scratch) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  float s = 0.f;
+  for (int i = 0; i < nw; i++) s += scratch[i];
+  return s;
+}
+
+}  // namespace
+
+// Global loads of one 32-k step: the thread's A pieces and the lane's weight
+// chunks (q4: one 16-byte chunk + scale; fp16: the two 8-k chunks of its half).
+template <int FMT, int MT, int NB>
+struct GemmLoads {
+  static constexpr int NW = FMT == WF_Q4 ? 1 : 2;
+  const uint16_t* asrc[MT];
+  const uint4* wp[NB];
+  const uint16_t* sp[NB];
+  uint4 areg[MT], wreg[NB][NW];
+  uint16_t sreg[NB];
+  __device__ __forceinline__ void load(int c, int kh) {
+#pragma unroll
+    for (int u = 0; u < MT; u++) areg[u] = *reinterpret_cast<const uint4*>(asrc[u] + c * 32);
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      if (FMT == WF_Q4) {
+        wreg[j][0] = wp[j][(size_t)c * kTile];
+        sreg[j] = sp[j][(size_t)c * kTile];
+      } else {
+#pragma unroll
+        for (int e = 0; e < NW; e++) wreg[j][e] = wp[j][(size_t)(4 * c + 2 * e + kh) * kTile];
+      }
+    }
+  }
+};
+
+// ----------------------------------------------------------------- GEMM --
+// C = A W^T.  Block: 4 waves as 2 (rows) x 2 (columns); a wave owns 32 MT rows
+// x 32 NB columns as MT x NB MFMA tiles of 32 x 32.  Per 32-k step the block's
+// A rows [64 MT][32] go through LDS (double buffered, one barrier per step)
+// and each lane forms its column's B operand in registers: q4 codes
+// dequantised once per step, fp16 rows loaded as they are.  The next step's
+// A and W loads are issued before this step's MFMAs.
+// MFMA 32x32x16 f16 lane layouts: A: lane l holds A[l % 32][8 (l / 32) + 0..7];
+// B: B[8 (l / 32) + 0..7][l % 32]; D: register v of lane l holds
+// D[8 (v / 4) + 4 (l / 32) + v % 4][l % 32].
+// Columns are physical weight rows: with NB = 2 a wave's two groups are the
+// two halves of one 64-row tile, which for the paired gate|up layout are the
+// gate rows 32t.. and the matching up rows, so GEMM_SWIGLU finishes in-lane.
+template <int FMT, int MT, int NB, int EPI>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+  constexpr int BM = 64 * MT;
+  constexpr int LS = 40;       // LDS halves per A row (32 + 8: conflict-free 16-byte reads)
+  constexpr int APT = MT;      // 16-byte A pieces per thread per step: BM * 4 / 256
+  __shared__ __align__(16) _Float16 as[2][BM * LS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int l32 = lane & 31, kh = lane >> 5;
+  const int m0 = blockIdx.y * BM;
+  const int cg0 = (blockIdx.x * 2 + wn) * 32 * NB;
+
+  GemmLoads<FMT, MT, NB> ld;
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    const int r = min(cg0 + 32 * j + l32, g.N - 1);  // clamped: loads stay unconditional
+    const size_t base = (size_t)(r / kTile) * g.C * kTile + r % kTile;
+    ld.wp[j] = g.w + base;
+    ld.sp[j] = FMT == WF_Q4 ? g.s + base : g.s;
+  }
+  int adst[APT];
+#pragma unroll
+  for (int u = 0; u < APT; u++) {
+    const int p = tid + 256 * u, r = p >> 2, q = p & 3;
+    ld.asrc[u] = g.A + (size_t)min(m0 + r, g.M - 1) * g.lda + q * 8;
+    adst[u] = r * LS + q * 8;
+  }
+
+  float16_t acc[MT][NB];
+#pragma unroll
+  for (int i = 0; i < MT; i++)
+#pragma unroll
+    for (int j = 0; j < NB; j++) acc[i][j] = (float16_t){};
+
+  const int steps = g.K / 32;
+  ld.load(0, kh);
+  for (int c = 0; c < steps; c++) {
+    _Float16* buf = as[c & 1];
+#pragma unroll
+    for (int u = 0; u < APT; u++) *reinterpret_cast<uint4*>(buf + adst[u]) = ld.areg[u];
+    half8_t b[NB][2];
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      if (FMT == WF_Q4) {
+        const _Float16 s = __builtin_bit_cast(_Float16, ld.sreg[j]);
+        const half2_t s2 = {s, s};
+        b[j][0] = dequant8(kh ? ld.wreg[j][0].y : ld.wreg[j][0].x, s2);
+        b[j][1] = dequant8(kh ? ld.wreg[j][0].w : ld.wreg[j][0].z, s2);
+      } else {
+        b[j][0] = as_half8(ld.wreg[j][0]);
+        b[j][1] = as_half8(ld.wreg[j][GemmLoads<FMT, MT, NB>::NW - 1]);
+      }
+    }
+    ld.load(min(c + 1, steps - 1), kh);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < MT; i++) {
+      const _Float16* ar = buf + (wm * 32 * MT + 32 * i + l32) * LS + 8 * kh;
+      const half8_t a1 = *reinterpret_cast<const half8_t*>(ar);
+      const half8_t a2 = *reinterpret_cast<const half8_t*>(ar + 16);
+#pragma unroll
+      for (int j = 0; j < NB; j++) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b[j][0], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, b[j][1], acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+
+  const int rbase = m0 + wm * 32 * MT + 4 * kh;
+  if (EPI == GEMM_SWIGLU) {
+    const int oi = (cg0 / kTile) * 32 + l32;  // canonical gate index of this lane's column
+    if (oi >= g.n_out) return;
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int row = rbase + 32 * i + 8 * (v >> 2) + (v & 3);
+        if (row < g.M) {
+          const float gt = acc[i][0][v], up = acc[i][NB - 1][v];
+          const _Float16 hv = (_Float16)(gt / (1.f + __expf(-gt)) * up);
+          g.Ch[(size_t)row * g.ldc + oi] = __builtin_bit_cast(uint16_t, hv);
+        }
+      }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    const int col = cg0 + 32 * j + l32;
+    if (col >= g.N) continue;
+    const float bias = (EPI == GEMM_STORE && g.bias) ? g.bias[col] : 0.f;
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int row = rbase + 32 * i + 8 * (v >> 2) + (v & 3);
+        if (row < g.M) {
+          float* dst = g.Cf + (size_t)row * g.ldc + col;
+          if (EPI == GEMM_STORE)
+            *dst = acc[i][j][v] + bias;
+          else
+            *dst += acc[i][j][v];
+        }
+      }
+  }
+}
+
+bool launch_gemm(int fmt, int epi, const GemmArgs& g, hipStream_t st) {
+  if (g.K % 32 != 0 || g.lda % 8 != 0 || g.M <= 0 || g.N <= 0) return false;
+  const int mt = g.M > 64 ? 2 : 1;
+  const int nb = (epi == GEMM_SWIGLU || g.N > 64) ? 2 : 1;
+  if (epi == GEMM_SWIGLU && g.N % kTile != 0) return false;
+  const dim3 grid((g.N + 64 * nb - 1) / (64 * nb), (g.M + 64 * mt - 1) / (64 * mt));
+#define GEMM_CASE(F, MTV, NBV, E)                                                         \
+  if (fmt == F && mt == MTV && nb == NBV && epi == E) {                                   \
+    hipLaunchKernelGGL((gemm_kernel<F, MTV, NBV, E>), grid, dim3(256), 0, st, g);         \
+    return true;                                                                          \
+  }
+#define GEMM_EPIS(F, MTV, NBV) \
+  GEMM_CASE(F, MTV, NBV, GEMM_STORE) GEMM_CASE(F, MTV, NBV, GEMM_ADD) GEMM_CASE(F, MTV, NBV, GEMM_SWIGLU)
+  GEMM_EPIS(WF_Q4, 1, 1) GEMM_EPIS(WF_Q4, 1, 2) GEMM_EPIS(WF_Q4, 2, 1) GEMM_EPIS(WF_Q4, 2, 2)
+  GEMM_EPIS(WF_F16, 1, 1) GEMM_EPIS(WF_F16, 1, 2) GEMM_EPIS(WF_F16, 2, 1) GEMM_EPIS(WF_F16, 2, 2)
+#undef GEMM_EPIS
+#undef GEMM_CASE
+  return false;
+}
+
+// ------------------------------------------------------------ row kernels --
+
+// X[m] = embedding row of tokens[m] in fp32 (DecoderWeights.ts:355-383 stages
+// the same rows for the replayed decode graph)
+__global__ void embed_rows_kernel(const int* tokens, const void* emb, int f32, int H, float* X) {
+  const int m = blockIdx.x;
+  const size_t row = (size_t)tokens[m] * H;
+  for (int k = threadIdx.x; k < H; k += blockDim.x)
+    X[(size_t)m * H + k] = f32 ? static_cast<const float*>(emb)[row + k]
+                               : __half2float(static_cast<const __half*>(emb)[row + k]);
+}
+
+void launch_embed_rows(const int* tokens, int M, const void* emb, int f32, int H, float* X, hipStream_t st) {
+  hipLaunchKernelGGL(embed_rows_kernel, dim3(M), dim3(256), 0, st, tokens, emb, f32, H, X);
+}
+
+// Y[m] = fp16(x * rsqrt(mean(x^2) + eps) * w) per row (TSLRMSNorm.ts:18-81)
+__global__ __launch_bounds__(256) void rms_rows_kernel(const float* X, int H, const float* w, float eps,
+                                                       _Float16* Y) {
+  __shared__ float scratch[4];
+  const int m = blockIdx.x;
+  const float* x = X + (size_t)m * H;
+  float ss = 0.f;
+  for (int k = threadIdx.x; k < H; k += 256) ss = fmaf(x[k], x[k], ss);
+  const float inv = rsqrtf(block_sum_f(ss, scratch) / (float)H + eps);
+  for (int k = threadIdx.x; k < H; k += 256) Y[(size_t)m * H + k] = (_Float16)(x[k] * inv * w[k]);
+}
+
+void launch_rms_rows(const float* X, int M, int H, const float* w, float eps, uint16_t* Y, hipStream_t st) {
+  hipLaunchKernelGGL(rms_rows_kernel, dim3(M), dim3(256), 0, st, X, H, w, eps, reinterpret_cast<_Float16*>(Y));
+}
+
+// Rotate-half RoPE of the q and k heads of row m at position p0 + m
+// (TSLAttention.ts:252-286), q to fp16 rows, k and v appended to the cache.
+__global__ __launch_bounds__(256) void rope_kv_kernel(RopeKvArgs a) {
+  const int m = blockIdx.x, pos = a.p0 + m, D = a.D;
+  const int nq = a.Hq * D, nk = a.Hkv * D, half = a.rd > 0 ? a.rd / 2 : 1;
+  const float* row = a.qkv + (size_t)m * (nq + 2 * nk);
+  for (int i = threadIdx.x; i < nq + 2 * nk; i += 256) {
+    const int hd = i / D, d = i % D;
+    float y = row[i];
+    if (i < nq + nk && d < a.rd) {
+      const int j = d < half ? d : d - half;
+      const int pd = d < half ? d + half : d - half;
+      const float sg = d < half ? -1.f : 1.f;
+      y = row[i] * a.rope_cos[(size_t)pos * half + j] + sg * row[hd * D + pd] * a.rope_sin[(size_t)pos * half + j];
+    }
+    if (i < nq) {
+      a.q[(size_t)m * nq + i] = __builtin_bit_cast(uint16_t, (_Float16)y);
+    } else {
+      const bool isv = i >= nq + nk;
+      const int hk = (i - nq - (isv ? nk : 0)) / D;
+      const size_t dst = ((size_t)hk * a.max_tokens + pos) * D + d;
+      void* cache = isv ? a.vc : a.kc;
+      if (a.kv_f32)
+        static_cast<float*>(cache)[dst] = y;
+      else
+        static_cast<__half*>(cache)[dst] = __float2half(y);
+    }
+  }
+}
+
+void launch_rope_kv(const RopeKvArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(rope_kv_kernel, dim3(a.M), dim3(256), 0, st, a);
+}
+
+// ------------------------------------------------------- flash attention --
+// Causal attention of M query rows over the fp16 cache (TSLAttention.ts:
+// 288-449 for one query).  Block: one kv head and 32 query rows, one wave per
+// query head of the group.  Per tile of 32 keys: K rows and V^T staged in LDS
+// once for the group; S^T = K Q^T (lane = query, registers = keys), an online
+// softmax in registers (the two half-waves of a query exchange one value),
+// then O^T += V^T P^T with P^T taken straight from the S^T registers: the key
+// order of the contraction is permuted to match that register layout.
+template <int DT>
+__global__ __launch_bounds__(512) void prefill_attn_kernel(PrefillAttnArgs a) {
+  constexpr int KS = DT + 8;  // halves per K row in LDS
+  constexpr int VS = 36;      // halves per V^T row (32 keys + 4): 8-byte aligned reads
+  constexpr int NDT = DT / 32;
+  __shared__ __align__(16) _Float16 ks[32 * KS];
+  __shared__ __align__(16) _Float16 vt[DT * VS];
+  const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, kh = lane >> 5;
+  const int nqt = (a.M + 31) / 32;
+  const int qt = nqt - 1 - (int)blockIdx.x;  // longest key ranges first
+  const int hk = blockIdx.y;
+  const int gw = (int)blockIdx.z * (nthr >> 6) + wave;
+  const bool active = gw < a.G;
+  const int h = hk * a.G + min(gw, a.G - 1);
+  const int qr = qt * 32 + l32, qpos = a.p0 + qr;
+  const int qhi = a.p0 + min(qt * 32 + 31, a.M - 1);
+  const int kfirst = a.window > 0 ? max(0, a.p0 + qt * 32 - a.window + 1) : 0;
+  const int qfirst = a.window > 0 ? max(0, qpos - a.window + 1) : 0;
+  const int QW = a.Hq * DT;
+
+  half8_t qb[DT / 16];
+  const _Float16* qrow = reinterpret_cast<const _Float16*>(a.q) + (size_t)min(qr, a.M - 1) * QW + h * DT;
+#pragma unroll
+  for (int j = 0; j < DT / 16; j++) qb[j] = *reinterpret_cast<const half8_t*>(qrow + 16 * j + 8 * kh);
+
+  float16_t o[NDT];
+#pragma unroll
+  for (int i = 0; i < NDT; i++) o[i] = (float16_t){};
+  float mrun = -INFINITY, lrun = 0.f;
+  const _Float16* kb = reinterpret_cast<const _Float16*>(a.kc) + (size_t)hk * a.max_tokens * DT;
+  const _Float16* vb = reinterpret_cast<const _Float16*>(a.vc) + (size_t)hk * a.max_tokens * DT;
+
+  for (int kt0 = kfirst & ~31; kt0 <= qhi; kt0 += 32) {
+    __syncthreads();  // the previous tile's LDS reads are done
+    for (int i = tid; i < 32 * DT / 8; i += nthr) {
+      const int r = i / (DT / 8), c8 = i % (DT / 8);
+      const size_t src = (size_t)min(kt0 + r, qhi) * DT + 8 * c8;  // rows past qhi repeat qhi (masked)
+      const uint4 kv = *reinterpret_cast<const uint4*>(kb + src);
+      const half8_t vv = as_half8(*reinterpret_cast<const uint4*>(vb + src));
+      *reinterpret_cast<uint4*>(ks + r * KS + 8 * c8) = kv;
+#pragma unroll
+      for (int e = 0; e < 8; e++) vt[(8 * c8 + e) * VS + r] = vv[e];
+    }
+    __syncthreads();
+    float16_t s = {};
+#pragma unroll
+    for (int j = 0; j < DT / 16; j++) {
+      const half8_t ak = *reinterpret_cast<const half8_t*>(ks + l32 * KS + 16 * j + 8 * kh);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ak, qb[j], s, 0, 0, 0);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      const int key = kt0 + 8 * (v >> 2) + 4 * kh + (v & 3);
+      s[v] = (key > qpos || key < qfirst) ? -INFINITY : s[v] * a.scale_log2;
+      mx = fmaxf(mx, s[v]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(mrun, mx);
+    const float mu = mn == -INFINITY ? 0.f : mn;
+    const float corr = __builtin_amdgcn_exp2f(mrun - mu);
+    float ps = 0.f;
+    half8_t pb[2];
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      const float p = __builtin_amdgcn_exp2f(s[v] - mu);
+      ps += p;
+      pb[v >> 3][v & 7] = (_Float16)p;
+    }
+    lrun = lrun * corr + ps;
+    mrun = mn;
+#pragma unroll
+    for (int i = 0; i < NDT; i++) {
+      o[i] *= corr;
+      const _Float16* vr = vt + (32 * i + l32) * VS + 4 * kh;
+      const half4_t x0 = *reinterpret_cast<const half4_t*>(vr);
+      const half4_t x1 = *reinterpret_cast<const half4_t*>(vr + 8);
+      const half4_t x2 = *reinterpret_cast<const half4_t*>(vr + 16);
+      const half4_t x3 = *reinterpret_cast<const half4_t*>(vr + 24);
+      const half8_t a1 = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+      const half8_t a2 = {x2[0], x2[1], x2[2], x2[3], x3[0], x3[1], x3[2], x3[3]};
+      o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, pb[0], o[i], 0, 0, 0);
+      o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, pb[1], o[i], 0, 0, 0);
+    }
+  }
+  lrun += __shfl_xor(lrun, 32, 64);
+  if (!active || qr >= a.M) return;
+  const float inv = lrun > 0.f ? 1.f / lrun : 0.f;
+  _Float16* orow = reinterpret_cast<_Float16*>(a.out) + (size_t)qr * QW + h * DT;
+#pragma unroll
+  for (int i = 0; i < NDT; i++)
+#pragma unroll
+    for (int grp = 0; grp < 4; grp++) {
+      const half4_t y = {(_Float16)(o[i][4 * grp] * inv), (_Float16)(o[i][4 * grp + 1] * inv),
+                         (_Float16)(o[i][4 * grp + 2] * inv), (_Float16)(o[i][4 * grp + 3] * inv)};
+      *reinterpret_cast<half4_t*>(orow + 32 * i + 8 * grp + 4 * kh) = y;
+    }
+}
+
+bool launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t st) {
+  if (a.D != 64 && a.D != 128) return false;
+  const int wpb = a.G < 8 ? a.G : 8;
+  const dim3 grid((a.M + 31) / 32, a.Hkv, (a.G + wpb - 1) / wpb);
+  if (a.D == 64)
+    hipLaunchKernelGGL(prefill_attn_kernel<64>, grid, dim3(64 * wpb), 0, st, a);
+  else
+    hipLaunchKernelGGL(prefill_attn_kernel<128>, grid, dim3(64 * wpb), 0, st, a);
+  return true;
+}
+
+// fp32 -> fp16 (round to nearest even)
+__global__ void rows_to_f16_kernel(const float* x, size_t n, _Float16* y) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = (_Float16)x[i];
+}
+
+void launch_rows_to_f16(const float* x, size_t n, uint16_t* y, hipStream_t st) {
+  hipLaunchKernelGGL(rows_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, n,
+                     reinterpret_cast<_Float16*>(y));
+}
+
+}  // namespace tlm

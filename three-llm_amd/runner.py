@@ -2,9 +2,9 @@
 
 Mirrors decoder/DecoderTSLRunner.ts:62-594 (paths relative to
 packages/three-llm/src/): the same method names, argument meaning and
-defaults (maxTokens = min(option, contextLimit), prefillChunkSize 32,
-logitCandidateCount 8), driving the device through the C ABI instead of
-three.js compute nodes.  One decode token is one HIP graph launch (the
+defaults (maxTokens = min(option, contextLimit), prefillChunkSize 32 when
+prompts replay the decode graph, logitCandidateCount 8), driving the device
+through the C ABI instead of three.js compute nodes.  One decode token is one HIP graph launch (the
 reference's single queue submission per token, submission.browser.test.ts:54).
 """
 from __future__ import annotations
@@ -66,12 +66,24 @@ class DecoderHIPRunner:
         self.weights = RunnerWeights(weights, tokenizer or TinyTokenizer(eos=weights.recipe.end_of_text_token_id))
         limit = weights.recipe.context_limit
         self.maxTokens = min(options.get("maxTokens") or limit, limit)
-        self.prefillChunkSize = options.get("prefillChunkSize") or 32
         self.logitCandidateCount = options.get("logitCandidateCount") or 8
         desc, inv = weights.model_desc(self.maxTokens)
         self.model = tlm.Model(self.ctx, desc, inv)
         weights.upload(self.model)
         self.model.finalize()
+        # Batched (MFMA) prefill for chunks of at least prefillBatchRows
+        # positions; the reference always replays the decode graph per position,
+        # in submissions of prefillChunkSize (default 32).  With the batched
+        # path on, a chunk is one batched pass, so the default chunk is 2048.
+        self.prefillBatchRows = int(options.get("prefillBatchRows", 64))
+        self.batchedPrefill = False
+        chunk = options.get("prefillChunkSize")
+        try:
+            self.model.set_prefill(self.prefillBatchRows, max(chunk or 2048, 1))
+            self.batchedPrefill = self.prefillBatchRows > 0
+        except tlm.TlmError:
+            self.model.set_prefill(0, 1)
+        self.prefillChunkSize = chunk or (2048 if self.batchedPrefill else 32)
         self._cacheTokens: Optional[List[int]] = None
         self._cacheLogits: Optional[np.ndarray] = None
 

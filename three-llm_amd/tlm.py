@@ -23,9 +23,10 @@ LOGITS = 1
 EXPORTS = [
     "tlm_abi_version", "tlm_last_error", "tlm_open", "tlm_close", "tlm_sync", "tlm_device_info", "tlm_alloc",
     "tlm_free", "tlm_upload", "tlm_download", "tlm_copy", "tlm_linear_create", "tlm_linear_destroy", "tlm_linear_dequant",
-    "tlm_op_linear", "tlm_op_rmsnorm", "tlm_op_silu_mul", "tlm_op_gated_mlp", "tlm_attn_create", "tlm_attn_destroy",
-    "tlm_op_attention", "tlm_attn_reset", "tlm_attn_read_cache", "tlm_op_logits", "tlm_op_argmax",
-    "tlm_model_create", "tlm_model_destroy", "tlm_model_upload", "tlm_model_finalize", "tlm_compute_token",
+    "tlm_op_linear", "tlm_op_linear_rows", "tlm_op_rmsnorm", "tlm_op_silu_mul", "tlm_op_gated_mlp", "tlm_attn_create", "tlm_attn_destroy",
+    "tlm_op_attention", "tlm_op_attention_rows", "tlm_attn_reset", "tlm_attn_read_cache", "tlm_op_logits", "tlm_op_argmax",
+    "tlm_model_create", "tlm_model_destroy", "tlm_model_upload", "tlm_model_finalize", "tlm_model_set_prefill",
+    "tlm_compute_token",
     "tlm_prefill", "tlm_read_logits", "tlm_read_token", "tlm_decode_greedy", "tlm_reset_cache", "tlm_kv_write",
     "tlm_kv_read", "tlm_kv_fill_normal", "tlm_read_hidden", "tlm_time_decode", "tlm_time_kernel", "tlm_time_head",
     "tlm_model_describe", "tlm_synth_normal", "tlm_synth_tokens", "tlm_quantize_q4", "tlm_f32_to_f16",
@@ -85,12 +86,14 @@ def lib():
             "tlm_linear_destroy": ([VP], None),
             "tlm_linear_dequant": ([VP, VP], ctypes.c_int),
             "tlm_op_linear": ([VP, VP, VP, VP], ctypes.c_int),
+            "tlm_op_linear_rows": ([VP, VP, i32, VP, VP], ctypes.c_int),
             "tlm_op_rmsnorm": ([VP, VP, VP, ctypes.c_int, dbl, ctypes.c_int, VP], ctypes.c_int),
             "tlm_op_silu_mul": ([VP, VP, VP, ctypes.c_int, VP], ctypes.c_int),
             "tlm_op_gated_mlp": ([VP, VP, VP, VP], ctypes.c_int),
             "tlm_attn_create": ([VP, ctypes.POINTER(AttnDesc), ctypes.POINTER(VP)], ctypes.c_int),
             "tlm_attn_destroy": ([VP], None),
             "tlm_op_attention": ([VP, VP, ctypes.c_int, VP], ctypes.c_int),
+            "tlm_op_attention_rows": ([VP, VP, i32, i32, VP], ctypes.c_int),
             "tlm_attn_reset": ([VP], ctypes.c_int),
             "tlm_attn_read_cache": ([VP, ctypes.c_int, VP, VP], ctypes.c_int),
             "tlm_op_logits": ([VP, VP, VP, VP], ctypes.c_int),
@@ -99,6 +102,7 @@ def lib():
             "tlm_model_destroy": ([VP], None),
             "tlm_model_upload": ([VP, ctypes.c_int, ctypes.c_int, VP, sz], ctypes.c_int),
             "tlm_model_finalize": ([VP], ctypes.c_int),
+            "tlm_model_set_prefill": ([VP, i32, i32], ctypes.c_int),
             "tlm_compute_token": ([VP, i32, i32, ctypes.c_int], ctypes.c_int),
             "tlm_prefill": ([VP, VP, i32, i32], ctypes.c_int),
             "tlm_read_logits": ([VP, VP, sz], ctypes.c_int),
@@ -264,6 +268,11 @@ class Linear:
         check(lib().tlm_op_linear(self.ptr, x.ptr, bias.ptr if bias else None, y.ptr))
         return y
 
+    def rows(self, x: Buffer, n_rows: int, y: Buffer, bias: Optional[Buffer] = None) -> Buffer:
+        """Batched rows: x fp16 bits [n_rows][k_in] -> y fp32 [n_rows][n_out] (MFMA GEMM)."""
+        check(lib().tlm_op_linear_rows(self.ptr, x.ptr, int(n_rows), bias.ptr if bias else None, y.ptr))
+        return y
+
     def close(self):
         if self.ptr:
             lib().tlm_linear_destroy(self.ptr)
@@ -287,6 +296,11 @@ class Attention:
 
     def __call__(self, qkv: Buffer, position: int, out: Buffer) -> Buffer:
         check(lib().tlm_op_attention(self.ptr, qkv.ptr, position, out.ptr))
+        return out
+
+    def rows(self, qkv: Buffer, n_rows: int, position0: int, out: Buffer) -> Buffer:
+        """Positions position0.. at once: qkv fp32 [n_rows][(H+2Hkv)D] -> out fp16 bits [n_rows][H D]."""
+        check(lib().tlm_op_attention_rows(self.ptr, qkv.ptr, int(n_rows), int(position0), out.ptr))
         return out
 
     def reset(self):
@@ -350,6 +364,10 @@ class Model:
 
     def finalize(self):
         check(lib().tlm_model_finalize(self.ptr))
+
+    def set_prefill(self, min_rows: int, chunk: int = 2048):
+        """Batched (MFMA) prefill for chunks of at least min_rows positions; 0 replays the decode graph."""
+        check(lib().tlm_model_set_prefill(self.ptr, int(min_rows), int(chunk)))
 
     def compute_token(self, token: int, position: int, logits: bool = True):
         check(lib().tlm_compute_token(self.ptr, int(token), int(position), LOGITS if logits else 0))
