@@ -136,7 +136,8 @@ struct tlm_model {
   // MFMA GEMMs over pf_chunk rows at a time; row buffers for pf_cap rows are
   // allocated on first use
   int pf_min_rows = 64, pf_chunk = 2048, pf_cap = 0;
-  float *pf_x = nullptr, *pf_qkv = nullptr;
+  float *pf_x = nullptr, *pf_part = nullptr;  // residual rows, split-K slices
+  size_t pf_part_n = 0;
   uint16_t *pf_xn = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_h = nullptr;
   hipGraphExec_t g_logits = nullptr, g_prefill = nullptr, g_layers = nullptr;
   hipGraph_t graph_logits = nullptr, graph_prefill = nullptr, graph_layers = nullptr;
@@ -462,6 +463,7 @@ int tlm_op_linear(tlm_linear* L, const float* x, const float* bias, float* y) {
 int tlm_op_linear_rows(tlm_linear* L, const uint16_t* x, int32_t rows, const float* bias, float* y) {
   if (!L || !x || !y || rows <= 0) return fail(TLM_ERR_INVALID, "TLMLinear: invalid argument");
   if (L->pair_half) return fail(TLM_ERR_INVALID, "TLMLinear: paired layout");
+  if (L->K % 32) return fail(TLM_ERR_INVALID, "TLMLinear: batched rows need K %% 32 == 0 (K = %d)", L->K);
   GemmArgs g;
   memset(&g, 0, sizeof g);
   g.A = x;
@@ -477,7 +479,8 @@ int tlm_op_linear_rows(tlm_linear* L, const uint16_t* x, int32_t rows, const flo
   g.ldc = L->N;
   if (L->fmt == TLM_FMT_Q4 && L->smax > 0x6FFF)
     return fail(TLM_ERR_INVALID, "TLMLinear: q4 scale above 8188 overflows the fp16 GEMM operand");
-  if (!launch_gemm(wfmt(L->fmt), GEMM_STORE, g, L->ctx->stream))
+  const GemmShape sh = gemm_shape(GEMM_STORE, rows, L->N, L->K, L->ctx->cus);
+  if (!launch_gemm(wfmt(L->fmt), GEMM_STORE, sh, g, L->ctx->stream))
     return fail(TLM_ERR_INVALID, "TLMLinear: batched rows need K %% 32 == 0 (K = %d)", L->K);
   CHECK_LAUNCH("TLMLinear");
   return TLM_OK;
@@ -688,6 +691,8 @@ int tlm_op_attention_rows(tlm_attn* A, const float* qkv, int32_t rows, int32_t p
   RopeKvArgs r;
   memset(&r, 0, sizeof r);
   r.qkv = qkv;
+  r.n_part = 1;
+  r.pstride = 0;
   r.M = rows;
   r.p0 = position0;
   r.Hq = d.heads;
@@ -945,7 +950,7 @@ void tlm_model_destroy(tlm_model* m) {
   tlm_linear_destroy(m->head);
   attn_free(&m->attn, false);
   void* bufs[] = {m->emb, m->final_norm, m->ctrl, m->tokens_out, m->prompt, m->xa, m->x0, m->xf, m->attn_out,
-                  m->pq, m->po, m->rb, m->logits, m->arg_val, m->arg_idx, m->pf_x, m->pf_qkv, m->pf_xn,
+                  m->pq, m->po, m->rb, m->logits, m->arg_val, m->arg_idx, m->pf_x, m->pf_part, m->pf_xn,
                   m->pf_q, m->pf_att, m->pf_h};
   for (void* p : bufs) hipFree(p);
   delete m;
@@ -1205,19 +1210,28 @@ static const char* prefill_unsupported(const tlm_model* m) {
   return nullptr;
 }
 
-static int prefill_alloc(tlm_model* m, int rows) {
+// Row buffers for `rows` positions and `part` floats of split-K slices.
+static int prefill_alloc(tlm_model* m, int rows, size_t part) {
+  if (m->pf_cap >= rows && m->pf_part_n >= part) return TLM_OK;
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  if (m->pf_part_n < part) {
+    hipFree(m->pf_part);
+    m->pf_part = nullptr;
+    m->pf_part_n = 0;
+    int rc = model_alloc((void**)&m->pf_part, sizeof(float) * part);
+    if (rc) return rc;
+    m->pf_part_n = part;
+  }
   if (m->pf_cap >= rows) return TLM_OK;
   rows = std::max(rows, m->pf_chunk);  // one allocation serves every later chunk
-  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
-  void* bufs[] = {m->pf_x, m->pf_qkv, m->pf_xn, m->pf_q, m->pf_att, m->pf_h};
-  for (void* p : bufs) hipFree(p);
-  m->pf_x = m->pf_qkv = nullptr;
+  void* bufs[] = {m->pf_x, m->pf_xn, m->pf_q, m->pf_att, m->pf_h};
+  for (void* q : bufs) hipFree(q);
+  m->pf_x = nullptr;
   m->pf_xn = m->pf_q = m->pf_att = m->pf_h = nullptr;
   m->pf_cap = 0;
   const size_t R = (size_t)rows, H = m->d.hidden_size, I = m->d.intermediate_size;
   int rc = TLM_OK;
   if (!rc) rc = model_alloc((void**)&m->pf_x, sizeof(float) * R * H);
-  if (!rc) rc = model_alloc((void**)&m->pf_qkv, sizeof(float) * R * m->Nqkv);
   if (!rc) rc = model_alloc((void**)&m->pf_xn, 2 * R * H);
   if (!rc) rc = model_alloc((void**)&m->pf_q, 2 * R * m->QS);
   if (!rc) rc = model_alloc((void**)&m->pf_att, 2 * R * m->QS);
@@ -1240,29 +1254,56 @@ static GemmArgs gemm_args(const tlm_linear* L, const uint16_t* A, int lda, int M
   return g;
 }
 
+static RowsArgs rows_args(float* X, const float* part, int n_part, size_t pstride, int H, const float* w, double eps,
+                          uint16_t* Y) {
+  RowsArgs r;
+  r.X = X;
+  r.part = part;
+  r.n_part = n_part;
+  r.pstride = pstride;
+  r.H = H;
+  r.w = w;
+  r.eps = (float)eps;
+  r.Y = Y;
+  return r;
+}
+
 // Positions [p0, p0 + M) through every layer as row batches; the K and V rows
 // land in the cache, nothing else of the model's decode state changes.
-// tokens: device array of the M token ids.
+// tokens: device array of the M token ids.  Per layer: fold + RMSNorm rows ->
+// QKV GEMM (split-K slices) -> RoPE/cache append (folds the slices) -> flash
+// attention -> O GEMM (slices) -> fold + RMSNorm -> gate|up GEMM with SwiGLU ->
+// down GEMM (slices, folded by the next layer's first kernel).
 static int prefill_rows(tlm_model* m, const int* tokens, int p0, int M) {
-  int rc = prefill_alloc(m, M);
-  if (rc) return rc;
   const tlm_model_desc& d = m->d;
   const int H = d.hidden_size, I = d.intermediate_size, D = d.head_dim;
-  const int lf = wfmt(d.linear_fmt);
+  const int lf = wfmt(d.linear_fmt), cus = m->ctx->cus;
+  const Layer& L0 = m->layers[0];
+  const GemmShape sq = gemm_shape(GEMM_PART, M, m->Nqkv, H, cus);
+  const GemmShape so = gemm_shape(GEMM_PART, M, H, m->QS, cus);
+  const GemmShape sg = gemm_shape(GEMM_SWIGLU, M, L0.gu->T * kTile, H, cus);
+  const GemmShape sd = gemm_shape(GEMM_PART, M, H, I, cus);
+  const size_t part = std::max({(size_t)sq.splits * M * m->Nqkv, (size_t)so.splits * M * H, (size_t)sd.splits * M * H});
+  int rc = prefill_alloc(m, M, part);
+  if (rc) return rc;
   hipStream_t st = m->ctx->stream;
+  const size_t rowsH = (size_t)M * H;
   launch_embed_rows(tokens, M, m->emb, d.embed_fmt == TLM_FMT_F32, H, m->pf_x, st);
   for (int l = 0; l < d.num_layers; l++) {
     const Layer& L = m->layers[l];
     bool ok = true;
-    launch_rms_rows(m->pf_x, M, H, L.attn_norm, (float)d.rms_eps, m->pf_xn, st);
+    launch_rms_rows(rows_args(m->pf_x, m->pf_part, l ? sd.splits : 0, rowsH, H, L.attn_norm, d.rms_eps, m->pf_xn),
+                    M, st);
     GemmArgs g = gemm_args(L.qkv, m->pf_xn, H, M);
-    g.bias = L.bqkv;
-    g.Cf = m->pf_qkv;
+    g.Cf = m->pf_part;
     g.ldc = m->Nqkv;
-    ok = ok && launch_gemm(lf, GEMM_STORE, g, st);
+    ok = ok && launch_gemm(lf, GEMM_PART, sq, g, st);
     RopeKvArgs r;
     memset(&r, 0, sizeof r);
-    r.qkv = m->pf_qkv;
+    r.qkv = m->pf_part;
+    r.n_part = sq.splits;
+    r.pstride = (size_t)M * m->Nqkv;
+    r.bias = L.bqkv;
     r.M = M;
     r.p0 = p0;
     r.Hq = d.num_heads;
@@ -1294,23 +1335,26 @@ static int prefill_rows(tlm_model* m, const int* tokens, int p0, int M) {
     pa.scale_log2 = m->attn.scale * 1.4426950408889634f;
     ok = ok && launch_prefill_attention(pa, st);
     g = gemm_args(L.o, m->pf_att, m->QS, M);
-    g.Cf = m->pf_x;
+    g.Cf = m->pf_part;
     g.ldc = H;
-    ok = ok && launch_gemm(lf, GEMM_ADD, g, st);
-    launch_rms_rows(m->pf_x, M, H, L.ffn_norm, (float)d.rms_eps, m->pf_xn, st);
+    ok = ok && launch_gemm(lf, GEMM_PART, so, g, st);
+    launch_rms_rows(rows_args(m->pf_x, m->pf_part, so.splits, rowsH, H, L.ffn_norm, d.rms_eps, m->pf_xn), M, st);
     g = gemm_args(L.gu, m->pf_xn, H, M);
     g.N = L.gu->T * kTile;
     g.Ch = m->pf_h;
     g.ldc = I;
     g.n_out = I;
-    ok = ok && launch_gemm(lf, GEMM_SWIGLU, g, st);
+    ok = ok && launch_gemm(lf, GEMM_SWIGLU, sg, g, st);
     g = gemm_args(L.down, m->pf_h, I, M);
-    g.Cf = m->pf_x;
+    g.Cf = m->pf_part;
     g.ldc = H;
-    ok = ok && launch_gemm(lf, GEMM_ADD, g, st);
+    ok = ok && launch_gemm(lf, GEMM_PART, sd, g, st);
     if (!ok) return fail(TLM_ERR_STATE, "TLMModel: no batched prefill kernel for layer %d", l);
     CHECK_LAUNCH("TLMModel");
   }
+  // the last layer's MLP output joins the residual rows
+  launch_rms_rows(rows_args(m->pf_x, m->pf_part, sd.splits, rowsH, H, nullptr, d.rms_eps, nullptr), M, st);
+  CHECK_LAUNCH("TLMModel");
   return TLM_OK;
 }
 

@@ -157,9 +157,9 @@ int attn_lpp(int D, bool kv_f32);
 // A chunk of M prompt positions per pass: row-major activations, linears as
 // MFMA GEMMs C[M][N] = A[M][K] * W^T over the tiled weight layout.
 enum GemmEpi {
-  GEMM_STORE = 0,   // Cf[m][n] = acc + bias[n]
-  GEMM_ADD = 1,     // Cf[m][n] += acc (residual stream)
-  GEMM_SWIGLU = 2,  // Ch[m][i] = fp16(silu(gate) * up), paired gate|up weight rows
+  GEMM_STORE = 0,   // Cf[m][n] = acc + bias[n] (no split-K)
+  GEMM_PART = 1,    // Cf[z][m][n] = split z's sum (the consumer adds the slices)
+  GEMM_SWIGLU = 2,  // Ch[m][i] = fp16(silu(gate) * up), paired gate|up weight rows (no split-K)
 };
 struct GemmArgs {
   const uint16_t* A;   // fp16 [M][lda]
@@ -172,6 +172,25 @@ struct GemmArgs {
   uint16_t* Ch;        // GEMM_SWIGLU: fp16 [M][ldc]
   int ldc;
   int n_out;           // GEMM_SWIGLU: intermediate size I (outputs i < n_out)
+  int spc;             // 32-k steps per split (set by launch_gemm)
+};
+// Tile and split-K choice of one GEMM (gemm_shape is the only planner, so the
+// host sizes the slice buffers from the same numbers the launch uses).
+struct GemmShape {
+  int mt, nb, gx, gy, spc, splits;
+};
+// Rows of the residual stream: X[m] += sum of n_part slices part[s][m]
+// (slice stride pstride floats, rows of H), then Y[m] = fp16(rmsnorm(X[m]) w)
+// unless Y is null.
+struct RowsArgs {
+  float* X;
+  const float* part;
+  int n_part;
+  size_t pstride;
+  int H;
+  const float* w;
+  float eps;
+  uint16_t* Y;
 };
 struct PrefillAttnArgs {
   const uint16_t* q;    // fp16 [M][Hq D], RoPE applied
@@ -182,7 +201,10 @@ struct PrefillAttnArgs {
   float scale_log2;     // softmax scale * log2(e)
 };
 struct RopeKvArgs {
-  const float* qkv;     // fp32 [M][Nqkv] (bias included)
+  const float* qkv;     // fp32 [n_part][M][Nqkv] split-K slices (summed here)
+  int n_part;
+  size_t pstride;       // floats between slices
+  const float* bias;    // [Nqkv] or null
   int M, p0, Hq, Hkv, D, rd, max_tokens;
   const float* rope_cos;  // [max_tokens][rd / 2]
   const float* rope_sin;
@@ -191,9 +213,10 @@ struct RopeKvArgs {
   void* vc;
   int kv_f32;
 };
-bool launch_gemm(int fmt, int epi, const GemmArgs& g, hipStream_t st);
+GemmShape gemm_shape(int epi, int M, int N, int K, int cus);
+bool launch_gemm(int fmt, int epi, const GemmShape& sh, const GemmArgs& g, hipStream_t st);
 void launch_embed_rows(const int* tokens, int M, const void* emb, int f32, int H, float* X, hipStream_t st);
-void launch_rms_rows(const float* X, int M, int H, const float* w, float eps, uint16_t* Y, hipStream_t st);
+void launch_rms_rows(const RowsArgs& a, int M, hipStream_t st);
 void launch_rope_kv(const RopeKvArgs& a, hipStream_t st);
 bool launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t st);
 void launch_rows_to_f16(const float* x, size_t n, uint16_t* y, hipStream_t st);

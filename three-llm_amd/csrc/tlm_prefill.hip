@@ -54,25 +54,50 @@ __device__ __forceinline__ float block_sum_f(float v, float* scratch) {
 // Global loads of one 32-k step: the thread's A pieces and the lane's weight
 // chunks (q4: one 16-byte chunk + scale; fp16: the two 8-k chunks of its half).
 template <int FMT, int MT, int NB>
-struct GemmLoads {
-  static constexpr int NW = FMT == WF_Q4 ? 1 : 2;
+struct GemmPtrs {
   const uint16_t* asrc[MT];
   const uint4* wp[NB];
   const uint16_t* sp[NB];
-  uint4 areg[MT], wreg[NB][NW];
-  uint16_t sreg[NB];
-  __device__ __forceinline__ void load(int c, int kh) {
-#pragma unroll
-    for (int u = 0; u < MT; u++) areg[u] = *reinterpret_cast<const uint4*>(asrc[u] + c * 32);
-#pragma unroll
-    for (int j = 0; j < NB; j++) {
-      if (FMT == WF_Q4) {
-        wreg[j][0] = wp[j][(size_t)c * kTile];
-        sreg[j] = sp[j][(size_t)c * kTile];
-      } else {
-#pragma unroll
-        for (int e = 0; e < NW; e++) wreg[j][e] = wp[j][(size_t)(4 * c + 2 * e + kh) * kTile];
+};
+// Registers of one step in flight; members are named, not arrays, so that the
+// compiler keeps every stage of the ring in registers.
+template <int FMT, int MT, int NB>
+struct GemmStage {
+  static_assert(MT <= 2 && NB <= 2, "stage registers are spelled out for MT, NB <= 2");
+  uint4 a0, a1;      // A pieces (a1 when MT == 2)
+  uint4 w0, w1;      // column group 0: q4 chunk, or the two fp16 chunks
+  uint4 v0, v1;      // column group 1 (NB == 2)
+  uint16_t s0, s1;   // q4 scales of the groups
+  __device__ __forceinline__ void load(const GemmPtrs<FMT, MT, NB>& p, int c, int kh) {
+    a0 = *reinterpret_cast<const uint4*>(p.asrc[0] + c * 32);
+    if constexpr (MT > 1) a1 = *reinterpret_cast<const uint4*>(p.asrc[1] + c * 32);
+    if constexpr (FMT == WF_Q4) {
+      w0 = p.wp[0][(size_t)c * kTile];
+      s0 = p.sp[0][(size_t)c * kTile];
+      if constexpr (NB > 1) {
+        v0 = p.wp[1][(size_t)c * kTile];
+        s1 = p.sp[1][(size_t)c * kTile];
       }
+    } else {
+      w0 = p.wp[0][(size_t)(4 * c + kh) * kTile];
+      w1 = p.wp[0][(size_t)(4 * c + 2 + kh) * kTile];
+      if constexpr (NB > 1) {
+        v0 = p.wp[1][(size_t)(4 * c + kh) * kTile];
+        v1 = p.wp[1][(size_t)(4 * c + 2 + kh) * kTile];
+      }
+    }
+  }
+  // B operands of column group j for the two 16-k halves of the step
+  __device__ __forceinline__ void operands(int j, int kh, half8_t& b1, half8_t& b2) const {
+    const uint4& x = j ? v0 : w0;
+    if constexpr (FMT == WF_Q4) {
+      const _Float16 s = __builtin_bit_cast(_Float16, j ? s1 : s0);
+      const half2_t s2 = {s, s};
+      b1 = dequant8(kh ? x.y : x.x, s2);
+      b2 = dequant8(kh ? x.w : x.z, s2);
+    } else {
+      b1 = as_half8(x);
+      b2 = as_half8(j ? v1 : w1);
     }
   }
 };
@@ -82,72 +107,45 @@ struct GemmLoads {
 // x 32 NB columns as MT x NB MFMA tiles of 32 x 32.  Per 32-k step the block's
 // A rows [64 MT][32] go through LDS (double buffered, one barrier per step)
 // and each lane forms its column's B operand in registers: q4 codes
-// dequantised once per step, fp16 rows loaded as they are.  The next step's
-// A and W loads are issued before this step's MFMAs.
+// dequantised once per step, fp16 rows loaded as they are.  Global loads run
+// kPf steps ahead of the MFMAs through a ring of register stages (the loop is
+// unrolled by kPf so every stage is a fixed set of registers).
+// Split-K: blockIdx.z takes steps [z spc, (z + 1) spc); GEMM_PART writes each
+// split's sum to its own slice Cf + z M ldc, the consumer adds the slices.
 // MFMA 32x32x16 f16 lane layouts: A: lane l holds A[l % 32][8 (l / 32) + 0..7];
 // B: B[8 (l / 32) + 0..7][l % 32]; D: register v of lane l holds
 // D[8 (v / 4) + 4 (l / 32) + v % 4][l % 32].
 // Columns are physical weight rows: with NB = 2 a wave's two groups are the
 // two halves of one 64-row tile, which for the paired gate|up layout are the
 // gate rows 32t.. and the matching up rows, so GEMM_SWIGLU finishes in-lane.
-template <int FMT, int MT, int NB, int EPI>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
-  constexpr int BM = 64 * MT;
-  constexpr int LS = 40;       // LDS halves per A row (32 + 8: conflict-free 16-byte reads)
-  constexpr int APT = MT;      // 16-byte A pieces per thread per step: BM * 4 / 256
-  __shared__ __align__(16) _Float16 as[2][BM * LS];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
-  const int l32 = lane & 31, kh = lane >> 5;
-  const int m0 = blockIdx.y * BM;
-  const int cg0 = (blockIdx.x * 2 + wn) * 32 * NB;
+constexpr int kPf = 4;  // steps in flight (the four stages of gemm_kernel)
 
-  GemmLoads<FMT, MT, NB> ld;
-#pragma unroll
-  for (int j = 0; j < NB; j++) {
-    const int r = min(cg0 + 32 * j + l32, g.N - 1);  // clamped: loads stay unconditional
-    const size_t base = (size_t)(r / kTile) * g.C * kTile + r % kTile;
-    ld.wp[j] = g.w + base;
-    ld.sp[j] = FMT == WF_Q4 ? g.s + base : g.s;
-  }
-  int adst[APT];
-#pragma unroll
-  for (int u = 0; u < APT; u++) {
-    const int p = tid + 256 * u, r = p >> 2, q = p & 3;
-    ld.asrc[u] = g.A + (size_t)min(m0 + r, g.M - 1) * g.lda + q * 8;
-    adst[u] = r * LS + q * 8;
-  }
-
+template <int FMT, int MT, int NB>
+struct GemmMain {
+  static constexpr int LS = 40;  // LDS halves per A row (32 + 8: conflict-free 16-byte reads)
   float16_t acc[MT][NB];
-#pragma unroll
-  for (int i = 0; i < MT; i++)
-#pragma unroll
-    for (int j = 0; j < NB; j++) acc[i][j] = (float16_t){};
 
-  const int steps = g.K / 32;
-  ld.load(0, kh);
-  for (int c = 0; c < steps; c++) {
-    _Float16* buf = as[c & 1];
-#pragma unroll
-    for (int u = 0; u < APT; u++) *reinterpret_cast<uint4*>(buf + adst[u]) = ld.areg[u];
+  // one step: stage -> LDS buffer and B registers, refill the stage, barrier, MFMAs
+  // returns the stage refilled with step `next` (values, not references: the
+  // ring then stays in registers)
+  __device__ __forceinline__ GemmStage<FMT, MT, NB> step(GemmStage<FMT, MT, NB> st,
+                                                         const GemmPtrs<FMT, MT, NB>& p, _Float16* buf,
+                                                         const int* adst, int next, bool refill, int arow,
+                                                         int kh) {
+    *reinterpret_cast<uint4*>(buf + adst[0]) = st.a0;
+    if constexpr (MT > 1) *reinterpret_cast<uint4*>(buf + adst[1]) = st.a1;
     half8_t b[NB][2];
 #pragma unroll
-    for (int j = 0; j < NB; j++) {
-      if (FMT == WF_Q4) {
-        const _Float16 s = __builtin_bit_cast(_Float16, ld.sreg[j]);
-        const half2_t s2 = {s, s};
-        b[j][0] = dequant8(kh ? ld.wreg[j][0].y : ld.wreg[j][0].x, s2);
-        b[j][1] = dequant8(kh ? ld.wreg[j][0].w : ld.wreg[j][0].z, s2);
-      } else {
-        b[j][0] = as_half8(ld.wreg[j][0]);
-        b[j][1] = as_half8(ld.wreg[j][GemmLoads<FMT, MT, NB>::NW - 1]);
-      }
-    }
-    ld.load(min(c + 1, steps - 1), kh);
+    for (int j = 0; j < NB; j++) st.operands(j, kh, b[j][0], b[j][1]);
+    // the stage's registers are free once the operands are formed: keep the
+    // refill after them so the loads land in the same registers (otherwise the
+    // loop needs copies that wait for the loads)
+    __builtin_amdgcn_sched_barrier(0);
+    if (refill) st.load(p, next, kh);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < MT; i++) {
-      const _Float16* ar = buf + (wm * 32 * MT + 32 * i + l32) * LS + 8 * kh;
+      const _Float16* ar = buf + (arow + 32 * i) * LS + 8 * kh;
       const half8_t a1 = *reinterpret_cast<const half8_t*>(ar);
       const half8_t a2 = *reinterpret_cast<const half8_t*>(ar + 16);
 #pragma unroll
@@ -156,7 +154,62 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, b[j][1], acc[i][j], 0, 0, 0);
       }
     }
+    return st;
   }
+};
+
+template <int FMT, int MT, int NB, int EPI>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+  using Main = GemmMain<FMT, MT, NB>;
+  constexpr int BM = 64 * MT, LS = Main::LS;
+  __shared__ __align__(16) _Float16 as[2][BM * LS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int l32 = lane & 31, kh = lane >> 5;
+  const int m0 = blockIdx.y * BM;
+  const int cg0 = (blockIdx.x * 2 + wn) * 32 * NB;
+  const int c0 = blockIdx.z * g.spc, n = min(g.spc, g.K / 32 - c0);
+
+  GemmPtrs<FMT, MT, NB> p;
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    const int r = min(cg0 + 32 * j + l32, g.N - 1);  // clamped: loads stay unconditional
+    const size_t base = (size_t)(r / kTile) * g.C * kTile + r % kTile;
+    p.wp[j] = g.w + base;
+    p.sp[j] = FMT == WF_Q4 ? g.s + base : g.s;
+  }
+  int adst[MT];
+#pragma unroll
+  for (int u = 0; u < MT; u++) {
+    const int q = tid + 256 * u, r = q >> 2, piece = q & 3;
+    p.asrc[u] = g.A + (size_t)min(m0 + r, g.M - 1) * g.lda + piece * 8;
+    adst[u] = r * LS + piece * 8;
+  }
+
+  Main mm;
+#pragma unroll
+  for (int i = 0; i < MT; i++)
+#pragma unroll
+    for (int j = 0; j < NB; j++) mm.acc[i][j] = (float16_t){};
+
+  // four named stages (not an array: the ring must stay in registers)
+  GemmStage<FMT, MT, NB> s0, s1, s2, s3;
+  s0.load(p, c0, kh);
+  s1.load(p, c0 + min(1, n - 1), kh);
+  s2.load(p, c0 + min(2, n - 1), kh);
+  s3.load(p, c0 + min(3, n - 1), kh);
+  const int arow = wm * 32 * MT + l32;
+  const int nfull = n - n % kPf;
+  for (int cb = 0; cb < nfull; cb += kPf) {
+    s0 = mm.step(s0, p, as[0], adst, c0 + min(cb + 4, n - 1), true, arow, kh);
+    s1 = mm.step(s1, p, as[1], adst, c0 + min(cb + 5, n - 1), true, arow, kh);
+    s2 = mm.step(s2, p, as[0], adst, c0 + min(cb + 6, n - 1), true, arow, kh);
+    s3 = mm.step(s3, p, as[1], adst, c0 + min(cb + 7, n - 1), true, arow, kh);
+  }
+  // tail: stage u holds step nfull + u
+  if (nfull < n) mm.step(s0, p, as[0], adst, 0, false, arow, kh);
+  if (nfull + 1 < n) mm.step(s1, p, as[1], adst, 0, false, arow, kh);
+  if (nfull + 2 < n) mm.step(s2, p, as[0], adst, 0, false, arow, kh);
 
   const int rbase = m0 + wm * 32 * MT + 4 * kh;
   if (EPI == GEMM_SWIGLU) {
@@ -168,13 +221,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
       for (int v = 0; v < 16; v++) {
         const int row = rbase + 32 * i + 8 * (v >> 2) + (v & 3);
         if (row < g.M) {
-          const float gt = acc[i][0][v], up = acc[i][NB - 1][v];
+          const float gt = mm.acc[i][0][v], up = mm.acc[i][NB - 1][v];
           const _Float16 hv = (_Float16)(gt / (1.f + __expf(-gt)) * up);
           g.Ch[(size_t)row * g.ldc + oi] = __builtin_bit_cast(uint16_t, hv);
         }
       }
     return;
   }
+  float* out = g.Cf + (EPI == GEMM_PART ? (size_t)blockIdx.z * g.M * g.ldc : 0);
 #pragma unroll
   for (int j = 0; j < NB; j++) {
     const int col = cg0 + 32 * j + l32;
@@ -185,30 +239,41 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int v = 0; v < 16; v++) {
         const int row = rbase + 32 * i + 8 * (v >> 2) + (v & 3);
-        if (row < g.M) {
-          float* dst = g.Cf + (size_t)row * g.ldc + col;
-          if (EPI == GEMM_STORE)
-            *dst = acc[i][j][v] + bias;
-          else
-            *dst += acc[i][j][v];
-        }
+        if (row < g.M) out[(size_t)row * g.ldc + col] = mm.acc[i][j][v] + bias;
       }
   }
 }
 
-bool launch_gemm(int fmt, int epi, const GemmArgs& g, hipStream_t st) {
-  if (g.K % 32 != 0 || g.lda % 8 != 0 || g.M <= 0 || g.N <= 0) return false;
-  const int mt = g.M > 64 ? 2 : 1;
-  const int nb = (epi == GEMM_SWIGLU || g.N > 64) ? 2 : 1;
-  if (epi == GEMM_SWIGLU && g.N % kTile != 0) return false;
-  const dim3 grid((g.N + 64 * nb - 1) / (64 * nb), (g.M + 64 * mt - 1) / (64 * mt));
+GemmShape gemm_shape(int epi, int M, int N, int K, int cus) {
+  GemmShape s;
+  s.mt = M > 64 ? 2 : 1;
+  s.nb = (epi == GEMM_SWIGLU || N > 64) ? 2 : 1;
+  s.gx = (N + 64 * s.nb - 1) / (64 * s.nb);
+  s.gy = (M + 64 * s.mt - 1) / (64 * s.mt);
+  const int steps = K >= 32 ? K / 32 : 1;  // K % 32 != 0 is rejected by launch_gemm
+  int splits = 1;
+  if (epi == GEMM_PART)  // fill the chip: about two blocks per CU, at least 8 steps per split
+    while (splits < 16 && s.gx * s.gy * splits < 2 * cus && steps / (2 * splits) >= 8) splits *= 2;
+  s.spc = (steps + splits - 1) / splits;
+  s.splits = (steps + s.spc - 1) / s.spc;
+  return s;
+}
+
+bool launch_gemm(int fmt, int epi, const GemmShape& sh, const GemmArgs& ga, hipStream_t st) {
+  if (ga.K % 32 != 0 || ga.lda % 8 != 0 || ga.M <= 0 || ga.N <= 0) return false;
+  if (epi == GEMM_SWIGLU && (ga.N % kTile != 0 || sh.nb != 2)) return false;
+  if (epi != GEMM_PART && sh.splits != 1) return false;
+  GemmArgs g = ga;
+  g.spc = sh.spc;
+  const dim3 grid(sh.gx, sh.gy, sh.splits);
+  const int mt = sh.mt, nb = sh.nb;
 #define GEMM_CASE(F, MTV, NBV, E)                                                         \
   if (fmt == F && mt == MTV && nb == NBV && epi == E) {                                   \
     hipLaunchKernelGGL((gemm_kernel<F, MTV, NBV, E>), grid, dim3(256), 0, st, g);         \
     return true;                                                                          \
   }
 #define GEMM_EPIS(F, MTV, NBV) \
-  GEMM_CASE(F, MTV, NBV, GEMM_STORE) GEMM_CASE(F, MTV, NBV, GEMM_ADD) GEMM_CASE(F, MTV, NBV, GEMM_SWIGLU)
+  GEMM_CASE(F, MTV, NBV, GEMM_STORE) GEMM_CASE(F, MTV, NBV, GEMM_PART) GEMM_CASE(F, MTV, NBV, GEMM_SWIGLU)
   GEMM_EPIS(WF_Q4, 1, 1) GEMM_EPIS(WF_Q4, 1, 2) GEMM_EPIS(WF_Q4, 2, 1) GEMM_EPIS(WF_Q4, 2, 2)
   GEMM_EPIS(WF_F16, 1, 1) GEMM_EPIS(WF_F16, 1, 2) GEMM_EPIS(WF_F16, 2, 1) GEMM_EPIS(WF_F16, 2, 2)
 #undef GEMM_EPIS
@@ -232,36 +297,64 @@ void launch_embed_rows(const int* tokens, int M, const void* emb, int f32, int H
   hipLaunchKernelGGL(embed_rows_kernel, dim3(M), dim3(256), 0, st, tokens, emb, f32, H, X);
 }
 
-// Y[m] = fp16(x * rsqrt(mean(x^2) + eps) * w) per row (TSLRMSNorm.ts:18-81)
-__global__ __launch_bounds__(256) void rms_rows_kernel(const float* X, int H, const float* w, float eps,
-                                                       _Float16* Y) {
+// Residual fold + RMSNorm per row (TSLRMSNorm.ts:18-81): x = X[m] + sum of
+// the split-K slices part[s][m] (written back to X when there are any), then
+// Y[m] = fp16(x * rsqrt(mean(x^2) + eps) * w) unless Y is null.
+constexpr int kRowsPerThread = 16;  // H <= 4096 with 256 threads
+__global__ __launch_bounds__(256) void rms_rows_kernel(RowsArgs a) {
   __shared__ float scratch[4];
   const int m = blockIdx.x;
-  const float* x = X + (size_t)m * H;
+  float* x = a.X + (size_t)m * a.H;
+  float xs[kRowsPerThread];
   float ss = 0.f;
-  for (int k = threadIdx.x; k < H; k += 256) ss = fmaf(x[k], x[k], ss);
-  const float inv = rsqrtf(block_sum_f(ss, scratch) / (float)H + eps);
-  for (int k = threadIdx.x; k < H; k += 256) Y[(size_t)m * H + k] = (_Float16)(x[k] * inv * w[k]);
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; j++) {
+    const int k = threadIdx.x + 256 * j;
+    float v = 0.f;
+    if (k < a.H) {
+      v = x[k];
+      for (int s = 0; s < a.n_part; s++) v += a.part[s * a.pstride + (size_t)m * a.H + k];
+      if (a.n_part) x[k] = v;
+    }
+    xs[j] = v;
+    ss = fmaf(v, v, ss);
+  }
+  if (!a.Y) return;
+  const float inv = rsqrtf(block_sum_f(ss, scratch) / (float)a.H + a.eps);
+  _Float16* y = reinterpret_cast<_Float16*>(a.Y) + (size_t)m * a.H;
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; j++) {
+    const int k = threadIdx.x + 256 * j;
+    if (k < a.H) y[k] = (_Float16)(xs[j] * inv * a.w[k]);
+  }
 }
 
-void launch_rms_rows(const float* X, int M, int H, const float* w, float eps, uint16_t* Y, hipStream_t st) {
-  hipLaunchKernelGGL(rms_rows_kernel, dim3(M), dim3(256), 0, st, X, H, w, eps, reinterpret_cast<_Float16*>(Y));
+void launch_rms_rows(const RowsArgs& a, int M, hipStream_t st) {
+  hipLaunchKernelGGL(rms_rows_kernel, dim3(M), dim3(256), 0, st, a);
 }
 
 // Rotate-half RoPE of the q and k heads of row m at position p0 + m
-// (TSLAttention.ts:252-286), q to fp16 rows, k and v appended to the cache.
+// (TSLAttention.ts:252-286) on bias + the sum of the split-K slices; q to fp16
+// rows, k and v appended to the cache.
 __global__ __launch_bounds__(256) void rope_kv_kernel(RopeKvArgs a) {
   const int m = blockIdx.x, pos = a.p0 + m, D = a.D;
   const int nq = a.Hq * D, nk = a.Hkv * D, half = a.rd > 0 ? a.rd / 2 : 1;
-  const float* row = a.qkv + (size_t)m * (nq + 2 * nk);
-  for (int i = threadIdx.x; i < nq + 2 * nk; i += 256) {
+  const int width = nq + 2 * nk;
+  const float* row = a.qkv + (size_t)m * width;
+  auto val = [&](int i) {
+    float v = a.bias ? a.bias[i] : 0.f;
+    for (int s = 0; s < a.n_part; s++) v += row[s * a.pstride + i];
+    return v;
+  };
+  for (int i = threadIdx.x; i < width; i += 256) {
     const int hd = i / D, d = i % D;
-    float y = row[i];
+    const float x = val(i);
+    float y = x;
     if (i < nq + nk && d < a.rd) {
       const int j = d < half ? d : d - half;
       const int pd = d < half ? d + half : d - half;
       const float sg = d < half ? -1.f : 1.f;
-      y = row[i] * a.rope_cos[(size_t)pos * half + j] + sg * row[hd * D + pd] * a.rope_sin[(size_t)pos * half + j];
+      y = x * a.rope_cos[(size_t)pos * half + j] + sg * val(hd * D + pd) * a.rope_sin[(size_t)pos * half + j];
     }
     if (i < nq) {
       a.q[(size_t)m * nq + i] = __builtin_bit_cast(uint16_t, (_Float16)y);
