@@ -479,7 +479,7 @@ int tlm_op_linear_rows(tlm_linear* L, const uint16_t* x, int32_t rows, const flo
   g.ldc = L->N;
   if (L->fmt == TLM_FMT_Q4 && L->smax > 0x6FFF)
     return fail(TLM_ERR_INVALID, "TLMLinear: q4 scale above 8188 overflows the fp16 GEMM operand");
-  const GemmShape sh = gemm_shape(GEMM_STORE, rows, L->N, L->K, L->ctx->cus);
+  const GemmShape sh = gemm_shape(wfmt(L->fmt), GEMM_STORE, rows, L->N, L->K, L->ctx->cus);
   if (!launch_gemm(wfmt(L->fmt), GEMM_STORE, sh, g, L->ctx->stream))
     return fail(TLM_ERR_INVALID, "TLMLinear: batched rows need K %% 32 == 0 (K = %d)", L->K);
   CHECK_LAUNCH("TLMLinear");
@@ -1279,10 +1279,10 @@ static int prefill_rows(tlm_model* m, const int* tokens, int p0, int M) {
   const int H = d.hidden_size, I = d.intermediate_size, D = d.head_dim;
   const int lf = wfmt(d.linear_fmt), cus = m->ctx->cus;
   const Layer& L0 = m->layers[0];
-  const GemmShape sq = gemm_shape(GEMM_PART, M, m->Nqkv, H, cus);
-  const GemmShape so = gemm_shape(GEMM_PART, M, H, m->QS, cus);
-  const GemmShape sg = gemm_shape(GEMM_SWIGLU, M, L0.gu->T * kTile, H, cus);
-  const GemmShape sd = gemm_shape(GEMM_PART, M, H, I, cus);
+  const GemmShape sq = gemm_shape(lf, GEMM_PART, M, m->Nqkv, H, cus);
+  const GemmShape so = gemm_shape(lf, GEMM_PART, M, H, m->QS, cus);
+  const GemmShape sg = gemm_shape(lf, GEMM_SWIGLU, M, L0.gu->T * kTile, H, cus);
+  const GemmShape sd = gemm_shape(lf, GEMM_PART, M, H, I, cus);
   const size_t part = std::max({(size_t)sq.splits * M * m->Nqkv, (size_t)so.splits * M * H, (size_t)sd.splits * M * H});
   int rc = prefill_alloc(m, M, part);
   if (rc) return rc;

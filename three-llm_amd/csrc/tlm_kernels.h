@@ -177,6 +177,8 @@ struct GemmArgs {
 // Tile and split-K choice of one GEMM (gemm_shape is the only planner, so the
 // host sizes the slice buffers from the same numbers the launch uses).
 struct GemmShape {
+  int ring;  // 1: the q4 LDS-ring kernel (wn waves over 64 wn columns, 32 mt rows)
+  int wn;
   int mt, nb, gx, gy, spc, splits;
 };
 // Rows of the residual stream: X[m] += sum of n_part slices part[s][m]
@@ -213,7 +215,7 @@ struct RopeKvArgs {
   void* vc;
   int kv_f32;
 };
-GemmShape gemm_shape(int epi, int M, int N, int K, int cus);
+GemmShape gemm_shape(int fmt, int epi, int M, int N, int K, int cus);
 bool launch_gemm(int fmt, int epi, const GemmShape& sh, const GemmArgs& g, hipStream_t st);
 void launch_embed_rows(const int* tokens, int M, const void* emb, int f32, int H, float* X, hipStream_t st);
 void launch_rms_rows(const RowsArgs& a, int M, hipStream_t st);

@@ -7,6 +7,7 @@
 #include "tlm_kernels.h"
 #include <hip/hip_fp16.h>
 #include <math.h>
+#include <stdlib.h>
 
 namespace tlm {
 
@@ -244,16 +245,186 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   }
 }
 
-GemmShape gemm_shape(int epi, int M, int N, int K, int cus) {
+// ------------------------------------------------------- q4 GEMM, LDS ring --
+// The q4 GEMM with its operands streamed by direct global -> LDS loads
+// (global_load_lds: no registers held while the loads are in flight).
+// Block: 4 waves side by side over 256 columns (four 64-row weight tiles); a
+// wave owns all 32 MT rows x its 64 columns (MT x 2 MFMA tiles of 32 x 32).
+// Per 32-k step a stage of the LDS ring holds the block's A rows [32 MT][32]
+// (16-byte pieces at a swizzled slot, see a_slot), the 256 weight chunks and
+// their scales.  kRing stages: a step's loads are issued kRing - 1 steps
+// before its MFMAs; every wave issues the same number of loads per stage
+// (small blocks repeat a copy of identical bytes), so one immediate vmcnt
+// bounds the loads still in flight.  Columns: for the paired gate|up layout
+// a wave's two 32-column groups are the gate rows and the matching up rows.
+constexpr int kRing = 4;
+
+// Slot (16 bytes) of piece q of A row r in a stage: piece q ^ f(r), where
+// f(r) = ((r1 ^ r3), r2) makes the 16-byte reads of 8 consecutive rows (32
+// banks) and of 16 consecutive rows (64 banks) hit distinct banks.
+__device__ __forceinline__ int a_swz(int r) { return (((r >> 1) ^ (r >> 3)) & 1) | (((r >> 2) & 1) << 1); }
+__device__ __forceinline__ int a_slot(int r, int q) { return r * 4 + (q ^ a_swz(r)); }
+
+// lane-wise global -> LDS copies; `lds` is the wave's destination base (a
+// byte address in the workgroup's LDS, the same for every lane), lane l
+// writes lds + l * size.  Issued from asm so the compiler keeps no count of
+// them: the kernel waits for them itself (vmcnt) before its barrier.
+__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma4(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(src)
+               : "memory", "m0");
+}
+
+template <int MT, int WN>
+struct RingLayout {
+  static constexpr int BM = 32 * MT;
+  static constexpr int NA = 2 * MT;             // 1 KiB A copies per stage
+  static constexpr int AW = (NA + WN - 1) / WN; // A copies per wave
+  static constexpr int S_BYTES = WN * 128 > 256 ? WN * 128 : 256;
+  static constexpr int W_OFF = BM * 64, S_OFF = W_OFF + WN * 1024, STAGE = S_OFF + S_BYTES;
+  static constexpr int LPS = AW + 2;            // copies per wave per stage: A, one weight tile, scales
+};
+
+template <int MT, int WN, int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_q4_ring_kernel(GemmArgs g) {
+  using RL = RingLayout<MT, WN>;
+  constexpr int STAGE = RL::STAGE, W_OFF = RL::W_OFF, S_OFF = RL::S_OFF;
+  __shared__ __align__(16) unsigned char lds[kRing * STAGE];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, kh = lane >> 5;
+  const int m0 = blockIdx.y * RL::BM, t0 = blockIdx.x * WN, T = (g.N + kTile - 1) / kTile;
+  const int c0 = blockIdx.z * g.spc, n = min(g.spc, g.K / 32 - c0);
+  const uint32_t lbase = (uint32_t)(uintptr_t)lds;
+
+  // this wave's copies of a stage (step-independent parts)
+  const uint16_t* asrc[RL::AW];
+  uint32_t aoff[RL::AW];
+#pragma unroll
+  for (int u = 0; u < RL::AW; u++) {
+    const int ai = (wave * RL::AW + u) % RL::NA, sl = ai * 64 + lane, r = sl >> 2;
+    asrc[u] = g.A + (size_t)min(m0 + r, g.M - 1) * g.lda + 8 * ((sl & 3) ^ a_swz(r));
+    aoff[u] = ai * 1024;
+  }
+  const uint4* wsrc = g.w + (size_t)min(t0 + wave, T - 1) * g.C * kTile + lane;
+  const int sidx = WN == 4 ? (wave & 1) : 0;  // one scale copy covers two tiles
+  const uint16_t* ssrc = g.s + (size_t)min(t0 + 2 * sidx + (lane >> 5), T - 1) * g.C * kTile + 2 * (lane & 31);
+
+  auto issue = [&](int stage, int c) {
+    const uint32_t sb = lbase + stage * STAGE;
+#pragma unroll
+    for (int u = 0; u < RL::AW; u++) lds_dma16(asrc[u] + c * 32, __builtin_amdgcn_readfirstlane(sb + aoff[u]));
+    lds_dma16(wsrc + (size_t)c * kTile, __builtin_amdgcn_readfirstlane(sb + W_OFF + wave * 1024));
+    lds_dma4(ssrc + (size_t)c * kTile, __builtin_amdgcn_readfirstlane(sb + S_OFF + sidx * 256));
+  };
+
+  float16_t acc[MT][2];
+#pragma unroll
+  for (int i = 0; i < MT; i++) acc[i][0] = acc[i][1] = (float16_t){};
+
+#pragma unroll
+  for (int s = 0; s < kRing - 1; s++) issue(s, c0 + min(s, n - 1));
+  for (int i = 0; i < n; i++) {
+    // this wave's copies of step i are done when at most the kRing - 2 later
+    // stages' copies are in flight; the barrier then covers every wave's
+    // copies, and every wave's reads of the stage refilled below
+    __builtin_amdgcn_s_waitcnt(0x3F70 | ((kRing - 2) * RL::LPS));
+    asm volatile("s_barrier" ::: "memory");
+    issue((i + kRing - 1) % kRing, c0 + min(i + kRing - 1, n - 1));
+    const unsigned char* sb = lds + (i % kRing) * STAGE;
+    half8_t b[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int cc = wave * 64 + 32 * j + l32;
+      // the two dwords this lane's k half uses: (x, z) or (y, w)
+      const uint32_t* wq = reinterpret_cast<const uint32_t*>(sb + W_OFF + cc * 16) + kh;
+      const uint32_t d0 = wq[0], d1 = wq[2];
+      const _Float16 sc = *reinterpret_cast<const _Float16*>(sb + S_OFF + cc * 2);
+      const half2_t s2 = {sc, sc};
+      b[j][0] = dequant8(d0, s2);
+      b[j][1] = dequant8(d1, s2);
+    }
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+      const int r = 32 * t + l32;
+      const half8_t a1 = *reinterpret_cast<const half8_t*>(sb + a_slot(r, kh) * 16);
+      const half8_t a2 = *reinterpret_cast<const half8_t*>(sb + a_slot(r, kh + 2) * 16);
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b[j][0], acc[t][j], 0, 0, 0);
+        acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, b[j][1], acc[t][j], 0, 0, 0);
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0x3F70);  // the clamped trailing copies land before the block exits
+
+  const int cg0 = (t0 + wave) * kTile;
+  const int rbase = m0 + 4 * kh;
+  if (EPI == GEMM_SWIGLU) {
+    const int oi = (t0 + wave) * 32 + l32;
+    if (oi >= g.n_out) return;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int row = rbase + 32 * t + 8 * (v >> 2) + (v & 3);
+        if (row < g.M) {
+          const float gt = acc[t][0][v], up = acc[t][1][v];
+          const _Float16 hv = (_Float16)(gt / (1.f + __expf(-gt)) * up);
+          g.Ch[(size_t)row * g.ldc + oi] = __builtin_bit_cast(uint16_t, hv);
+        }
+      }
+    return;
+  }
+  float* out = g.Cf + (EPI == GEMM_PART ? (size_t)blockIdx.z * g.M * g.ldc : 0);
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int col = cg0 + 32 * j + l32;
+    if (col >= g.N) continue;
+    const float bias = (EPI == GEMM_STORE && g.bias) ? g.bias[col] : 0.f;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int row = rbase + 32 * t + 8 * (v >> 2) + (v & 3);
+        if (row < g.M) out[(size_t)row * g.ldc + col] = acc[t][j][v] + bias;
+      }
+  }
+}
+
+// TLM_GEMM_RING=0 selects the register-prefetch kernel for q4 too (comparisons)
+static const bool g_use_ring = [] {
+  const char* e = getenv("TLM_GEMM_RING");
+  return !(e && e[0] == '0');
+}();
+
+GemmShape gemm_shape(int fmt, int epi, int M, int N, int K, int cus) {
   GemmShape s;
-  s.mt = M > 64 ? 2 : 1;
-  s.nb = (epi == GEMM_SWIGLU || N > 64) ? 2 : 1;
-  s.gx = (N + 64 * s.nb - 1) / (64 * s.nb);
-  s.gy = (M + 64 * s.mt - 1) / (64 * s.mt);
+  s.ring = fmt == WF_Q4 && g_use_ring;
+  s.wn = 1;
   const int steps = K >= 32 ? K / 32 : 1;  // K % 32 != 0 is rejected by launch_gemm
+  if (s.ring) {  // waves side by side over 64 wn columns, 32 mt rows
+    s.mt = M > 64 ? 4 : M > 32 ? 2 : 1;
+    s.nb = 2;
+    s.gy = (M + 32 * s.mt - 1) / (32 * s.mt);
+    // four-wave blocks share the A stage; grids too small to fill the CUs use one-wave blocks
+    s.wn = ((N + 255) / 256) * s.gy >= cus / 2 ? 4 : 1;
+    s.gx = (N + 64 * s.wn - 1) / (64 * s.wn);
+  } else {
+    s.mt = M > 64 ? 2 : 1;
+    s.nb = (epi == GEMM_SWIGLU || N > 64) ? 2 : 1;
+    s.gx = (N + 64 * s.nb - 1) / (64 * s.nb);
+    s.gy = (M + 64 * s.mt - 1) / (64 * s.mt);
+    s.wn = 4;
+  }
   int splits = 1;
-  if (epi == GEMM_PART)  // fill the chip: about two blocks per CU, at least 8 steps per split
-    while (splits < 16 && s.gx * s.gy * splits < 2 * cus && steps / (2 * splits) >= 8) splits *= 2;
+  if (epi == GEMM_PART) {  // split K until the grid holds about 8 waves per CU, at least 4 steps per split
+    const int target = 8 * cus;
+    const int waves = s.gx * s.gy * (s.ring ? s.wn : 4);
+    while (splits < 32 && waves * splits < target && steps / (2 * splits) >= 4) splits *= 2;
+  }
   s.spc = (steps + splits - 1) / splits;
   s.splits = (steps + s.spc - 1) / s.spc;
   return s;
@@ -267,6 +438,19 @@ bool launch_gemm(int fmt, int epi, const GemmShape& sh, const GemmArgs& ga, hipS
   g.spc = sh.spc;
   const dim3 grid(sh.gx, sh.gy, sh.splits);
   const int mt = sh.mt, nb = sh.nb;
+  if (sh.ring) {
+    if (fmt != WF_Q4) return false;
+#define RING_CASE(MTV, WNV, E)                                                                   \
+  if (mt == MTV && sh.wn == WNV && epi == E) {                                                   \
+    hipLaunchKernelGGL((gemm_q4_ring_kernel<MTV, WNV, E>), grid, dim3(64 * WNV), 0, st, g);      \
+    return true;                                                                                 \
+  }
+#define RING_EPIS(MTV, WNV) RING_CASE(MTV, WNV, GEMM_STORE) RING_CASE(MTV, WNV, GEMM_PART) RING_CASE(MTV, WNV, GEMM_SWIGLU)
+    RING_EPIS(1, 1) RING_EPIS(2, 1) RING_EPIS(4, 1) RING_EPIS(1, 4) RING_EPIS(2, 4) RING_EPIS(4, 4)
+#undef RING_EPIS
+#undef RING_CASE
+    return false;
+  }
 #define GEMM_CASE(F, MTV, NBV, E)                                                         \
   if (fmt == F && mt == MTV && nb == NBV && epi == E) {                                   \
     hipLaunchKernelGGL((gemm_kernel<F, MTV, NBV, E>), grid, dim3(256), 0, st, g);         \
@@ -299,33 +483,45 @@ void launch_embed_rows(const int* tokens, int M, const void* emb, int f32, int H
 
 // Residual fold + RMSNorm per row (TSLRMSNorm.ts:18-81): x = X[m] + sum of
 // the split-K slices part[s][m] (written back to X when there are any), then
-// Y[m] = fp16(x * rsqrt(mean(x^2) + eps) * w) unless Y is null.
-constexpr int kRowsPerThread = 16;  // H <= 4096 with 256 threads
+// Y[m] = fp16(x * rsqrt(mean(x^2) + eps) * w) unless Y is null.  H % 4 == 0,
+// H <= 4096: each of the 256 threads holds up to four float4 of the row.
+constexpr int kRowVec = 4;
 __global__ __launch_bounds__(256) void rms_rows_kernel(RowsArgs a) {
   __shared__ float scratch[4];
-  const int m = blockIdx.x;
-  float* x = a.X + (size_t)m * a.H;
-  float xs[kRowsPerThread];
+  const int m = blockIdx.x, H4 = a.H >> 2;
+  float4* x = reinterpret_cast<float4*>(a.X + (size_t)m * a.H);
+  const float4* part = reinterpret_cast<const float4*>(a.part + (size_t)m * a.H);
+  const size_t ps4 = a.pstride >> 2;
+  float4 xs[kRowVec];
   float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < kRowsPerThread; j++) {
+  for (int j = 0; j < kRowVec; j++) {
     const int k = threadIdx.x + 256 * j;
-    float v = 0.f;
-    if (k < a.H) {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (k < H4) {
       v = x[k];
-      for (int s = 0; s < a.n_part; s++) v += a.part[s * a.pstride + (size_t)m * a.H + k];
+#pragma unroll 4
+      for (int s = 0; s < a.n_part; s++) {
+        const float4 p = part[s * ps4 + k];
+        v.x += p.x, v.y += p.y, v.z += p.z, v.w += p.w;
+      }
       if (a.n_part) x[k] = v;
     }
     xs[j] = v;
-    ss = fmaf(v, v, ss);
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
   }
   if (!a.Y) return;
   const float inv = rsqrtf(block_sum_f(ss, scratch) / (float)a.H + a.eps);
-  _Float16* y = reinterpret_cast<_Float16*>(a.Y) + (size_t)m * a.H;
+  half4_t* y = reinterpret_cast<half4_t*>(a.Y + (size_t)m * a.H);
+  const float4* w = reinterpret_cast<const float4*>(a.w);
 #pragma unroll
-  for (int j = 0; j < kRowsPerThread; j++) {
+  for (int j = 0; j < kRowVec; j++) {
     const int k = threadIdx.x + 256 * j;
-    if (k < a.H) y[k] = (_Float16)(xs[j] * inv * a.w[k]);
+    if (k < H4) {
+      const float4 wv = w[k], v = xs[j];
+      y[k] = (half4_t){(_Float16)(v.x * inv * wv.x), (_Float16)(v.y * inv * wv.y), (_Float16)(v.z * inv * wv.z),
+                       (_Float16)(v.w * inv * wv.w)};
+    }
   }
 }
 
@@ -335,39 +531,49 @@ void launch_rms_rows(const RowsArgs& a, int M, hipStream_t st) {
 
 // Rotate-half RoPE of the q and k heads of row m at position p0 + m
 // (TSLAttention.ts:252-286) on bias + the sum of the split-K slices; q to fp16
-// rows, k and v appended to the cache.
+// rows, k and v appended to the cache.  A thread takes a rotation pair
+// (d, d + rd/2) of a head, or one element outside the rotary part.
+__device__ __forceinline__ float fold_slices(const float* row, const float* bias, int n_part, size_t pstride, int i) {
+  float v = bias ? bias[i] : 0.f;
+#pragma unroll 4
+  for (int s = 0; s < n_part; s++) v += row[s * pstride + i];
+  return v;
+}
+
+__device__ __forceinline__ void rope_store(const RopeKvArgs& a, int m, int pos, int i, float y) {
+  const int nq = a.Hq * a.D, nk = a.Hkv * a.D;
+  if (i < nq) {
+    a.q[(size_t)m * nq + i] = __builtin_bit_cast(uint16_t, (_Float16)y);
+    return;
+  }
+  const bool isv = i >= nq + nk;
+  const int j = i - nq - (isv ? nk : 0), hk = j / a.D, d = j % a.D;
+  const size_t dst = ((size_t)hk * a.max_tokens + pos) * a.D + d;
+  void* cache = isv ? a.vc : a.kc;
+  if (a.kv_f32)
+    static_cast<float*>(cache)[dst] = y;
+  else
+    static_cast<__half*>(cache)[dst] = __float2half(y);
+}
+
 __global__ __launch_bounds__(256) void rope_kv_kernel(RopeKvArgs a) {
   const int m = blockIdx.x, pos = a.p0 + m, D = a.D;
-  const int nq = a.Hq * D, nk = a.Hkv * D, half = a.rd > 0 ? a.rd / 2 : 1;
+  const int nq = a.Hq * D, nk = a.Hkv * D, half = a.rd / 2;
   const int width = nq + 2 * nk;
   const float* row = a.qkv + (size_t)m * width;
-  auto val = [&](int i) {
-    float v = a.bias ? a.bias[i] : 0.f;
-    for (int s = 0; s < a.n_part; s++) v += row[s * a.pstride + i];
-    return v;
-  };
   for (int i = threadIdx.x; i < width; i += 256) {
-    const int hd = i / D, d = i % D;
-    const float x = val(i);
-    float y = x;
-    if (i < nq + nk && d < a.rd) {
-      const int j = d < half ? d : d - half;
-      const int pd = d < half ? d + half : d - half;
-      const float sg = d < half ? -1.f : 1.f;
-      y = x * a.rope_cos[(size_t)pos * half + j] + sg * val(hd * D + pd) * a.rope_sin[(size_t)pos * half + j];
+    const int d = i % D;
+    const bool rot = i < nq + nk && d < a.rd;
+    if (rot && d >= half) continue;  // the pair's first thread writes both
+    const float x = fold_slices(row, a.bias, a.n_part, a.pstride, i);
+    if (!rot) {
+      rope_store(a, m, pos, i, x);
+      continue;
     }
-    if (i < nq) {
-      a.q[(size_t)m * nq + i] = __builtin_bit_cast(uint16_t, (_Float16)y);
-    } else {
-      const bool isv = i >= nq + nk;
-      const int hk = (i - nq - (isv ? nk : 0)) / D;
-      const size_t dst = ((size_t)hk * a.max_tokens + pos) * D + d;
-      void* cache = isv ? a.vc : a.kc;
-      if (a.kv_f32)
-        static_cast<float*>(cache)[dst] = y;
-      else
-        static_cast<__half*>(cache)[dst] = __float2half(y);
-    }
+    const float x2 = fold_slices(row, a.bias, a.n_part, a.pstride, i + half);
+    const float c = a.rope_cos[(size_t)pos * half + d], sn = a.rope_sin[(size_t)pos * half + d];
+    rope_store(a, m, pos, i, x * c - x2 * sn);
+    rope_store(a, m, pos, i + half, x2 * c + x * sn);
   }
 }
 
