@@ -269,12 +269,12 @@ __device__ __forceinline__ int a_slot(int r, int q) { return r * 4 + (q ^ a_swz(
 // byte address in the workgroup's LDS, the same for every lane), lane l
 // writes lds + l * size.  Issued from asm so the compiler keeps no count of
 // them: the kernel waits for them itself (vmcnt) before its barrier.
-__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(off), "s"(base)
                : "memory", "m0");
 }
-__device__ __forceinline__ void lds_dma4(const void* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(src)
+__device__ __forceinline__ void lds_dma4(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(off), "s"(base)
                : "memory", "m0");
 }
 
@@ -288,69 +288,59 @@ struct RingLayout {
   static constexpr int LPS = AW + 2;            // copies per wave per stage: A, one weight tile, scales
 };
 
-template <int MT, int WN, int EPI>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_q4_ring_kernel(GemmArgs g) {
+// One block's state: loop-invariant byte offsets of its copies and reads, the
+// accumulators, and the step body with the stage index a template constant
+// (LDS addresses become immediates).  k order inside a 32-k step: MFMA 1
+// takes k = 16 kh + 0..7, MFMA 2 k = 16 kh + 8..15 (kh = lane / 32), so a
+// lane's A pieces are 2 kh, 2 kh + 1 and its weight dwords 2 kh, 2 kh + 1
+// (one 8-byte read).
+template <int MT, int WN>
+struct RingBlock {
   using RL = RingLayout<MT, WN>;
-  constexpr int STAGE = RL::STAGE, W_OFF = RL::W_OFF, S_OFF = RL::S_OFF;
-  __shared__ __align__(16) unsigned char lds[kRing * STAGE];
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int l32 = lane & 31, kh = lane >> 5;
-  const int m0 = blockIdx.y * RL::BM, t0 = blockIdx.x * WN, T = (g.N + kTile - 1) / kTile;
-  const int c0 = blockIdx.z * g.spc, n = min(g.spc, g.K / 32 - c0);
-  const uint32_t lbase = (uint32_t)(uintptr_t)lds;
-
-  // this wave's copies of a stage (step-independent parts)
-  const uint16_t* asrc[RL::AW];
-  uint32_t aoff[RL::AW];
-#pragma unroll
-  for (int u = 0; u < RL::AW; u++) {
-    const int ai = (wave * RL::AW + u) % RL::NA, sl = ai * 64 + lane, r = sl >> 2;
-    asrc[u] = g.A + (size_t)min(m0 + r, g.M - 1) * g.lda + 8 * ((sl & 3) ^ a_swz(r));
-    aoff[u] = ai * 1024;
-  }
-  const uint4* wsrc = g.w + (size_t)min(t0 + wave, T - 1) * g.C * kTile + lane;
-  const int sidx = WN == 4 ? (wave & 1) : 0;  // one scale copy covers two tiles
-  const uint16_t* ssrc = g.s + (size_t)min(t0 + 2 * sidx + (lane >> 5), T - 1) * g.C * kTile + 2 * (lane & 31);
-
-  auto issue = [&](int stage, int c) {
-    const uint32_t sb = lbase + stage * STAGE;
-#pragma unroll
-    for (int u = 0; u < RL::AW; u++) lds_dma16(asrc[u] + c * 32, __builtin_amdgcn_readfirstlane(sb + aoff[u]));
-    lds_dma16(wsrc + (size_t)c * kTile, __builtin_amdgcn_readfirstlane(sb + W_OFF + wave * 1024));
-    lds_dma4(ssrc + (size_t)c * kTile, __builtin_amdgcn_readfirstlane(sb + S_OFF + sidx * 256));
-  };
-
+  const char* abase;  // A + 32 c halves, weight and scale bases advance per step
+  const char* wbase;
+  const char* sbase;
+  int a_lds_stride;   // bytes per 32-k step in each operand
+  uint32_t agoff[RL::AW], alds[RL::AW];  // global byte offsets / LDS offsets of this wave's A copies
+  uint32_t wgoff, sgoff, wlds, slds;
+  uint32_t lbase;
+  int rd_a1[MT], rd_a2[MT];              // LDS read offsets of the A pieces (within a stage)
+  int rd_w[2], rd_s[2];
   float16_t acc[MT][2];
-#pragma unroll
-  for (int i = 0; i < MT; i++) acc[i][0] = acc[i][1] = (float16_t){};
 
+  __device__ __forceinline__ void issue(int stage, int c) {
+    const uint32_t sb = lbase + stage * RL::STAGE;
+    const char* ab = abase + (size_t)c * 64;
+    const char* wb = wbase + (size_t)c * kTile * 16;
+    const char* sbs = sbase + (size_t)c * kTile * 2;
 #pragma unroll
-  for (int s = 0; s < kRing - 1; s++) issue(s, c0 + min(s, n - 1));
-  for (int i = 0; i < n; i++) {
-    // this wave's copies of step i are done when at most the kRing - 2 later
+    for (int u = 0; u < RL::AW; u++) lds_dma16(ab, agoff[u], __builtin_amdgcn_readfirstlane(sb + alds[u]));
+    lds_dma16(wb, wgoff, __builtin_amdgcn_readfirstlane(sb + wlds));
+    lds_dma4(sbs, sgoff, __builtin_amdgcn_readfirstlane(sb + slds));
+  }
+
+  template <int S>
+  __device__ __forceinline__ void step(const unsigned char* lds, int refill_c) {
+    // this wave's copies of the step are done when at most the kRing - 2 later
     // stages' copies are in flight; the barrier then covers every wave's
     // copies, and every wave's reads of the stage refilled below
     __builtin_amdgcn_s_waitcnt(0x3F70 | ((kRing - 2) * RL::LPS));
     asm volatile("s_barrier" ::: "memory");
-    issue((i + kRing - 1) % kRing, c0 + min(i + kRing - 1, n - 1));
-    const unsigned char* sb = lds + (i % kRing) * STAGE;
+    issue((S + kRing - 1) % kRing, refill_c);
+    const unsigned char* sb = lds + S * RL::STAGE;
     half8_t b[2][2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-      const int cc = wave * 64 + 32 * j + l32;
-      // the two dwords this lane's k half uses: (x, z) or (y, w)
-      const uint32_t* wq = reinterpret_cast<const uint32_t*>(sb + W_OFF + cc * 16) + kh;
-      const uint32_t d0 = wq[0], d1 = wq[2];
-      const _Float16 sc = *reinterpret_cast<const _Float16*>(sb + S_OFF + cc * 2);
+      const uint2 wv = *reinterpret_cast<const uint2*>(sb + rd_w[j]);
+      const _Float16 sc = *reinterpret_cast<const _Float16*>(sb + rd_s[j]);
       const half2_t s2 = {sc, sc};
-      b[j][0] = dequant8(d0, s2);
-      b[j][1] = dequant8(d1, s2);
+      b[j][0] = dequant8(wv.x, s2);
+      b[j][1] = dequant8(wv.y, s2);
     }
 #pragma unroll
     for (int t = 0; t < MT; t++) {
-      const int r = 32 * t + l32;
-      const half8_t a1 = *reinterpret_cast<const half8_t*>(sb + a_slot(r, kh) * 16);
-      const half8_t a2 = *reinterpret_cast<const half8_t*>(sb + a_slot(r, kh + 2) * 16);
+      const half8_t a1 = *reinterpret_cast<const half8_t*>(sb + rd_a1[t]);
+      const half8_t a2 = *reinterpret_cast<const half8_t*>(sb + rd_a2[t]);
 #pragma unroll
       for (int j = 0; j < 2; j++) {
         acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b[j][0], acc[t][j], 0, 0, 0);
@@ -358,6 +348,62 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
       }
     }
   }
+};
+
+template <int MT, int WN, int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_q4_ring_kernel(GemmArgs g) {
+  using RL = RingLayout<MT, WN>;
+  __shared__ __align__(16) unsigned char lds[kRing * RL::STAGE];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, kh = lane >> 5;
+  const int m0 = blockIdx.y * RL::BM, t0 = blockIdx.x * WN, T = (g.N + kTile - 1) / kTile;
+  const int c0 = blockIdx.z * g.spc, n = min(g.spc, g.K / 32 - c0);
+
+  RingBlock<MT, WN> rb;
+  rb.lbase = (uint32_t)(uintptr_t)lds;
+  rb.abase = reinterpret_cast<const char*>(g.A) + (size_t)c0 * 64;
+  rb.wbase = reinterpret_cast<const char*>(g.w) + (size_t)c0 * kTile * 16;
+  rb.sbase = reinterpret_cast<const char*>(g.s) + (size_t)c0 * kTile * 2;
+#pragma unroll
+  for (int u = 0; u < RL::AW; u++) {
+    const int ai = (wave * RL::AW + u) % RL::NA, sl = ai * 64 + lane, r = sl >> 2;
+    rb.agoff[u] = (uint32_t)(((size_t)min(m0 + r, g.M - 1) * g.lda + 8 * ((sl & 3) ^ a_swz(r))) * 2);
+    rb.alds[u] = ai * 1024;
+  }
+  rb.wgoff = (uint32_t)(((size_t)min(t0 + wave, T - 1) * g.C * kTile + lane) * 16);
+  const int sidx = WN == 4 ? (wave & 1) : 0;  // one scale copy covers two tiles
+  rb.sgoff = (uint32_t)(((size_t)min(t0 + 2 * sidx + (lane >> 5), T - 1) * g.C * kTile + 2 * (lane & 31)) * 2);
+  rb.wlds = RL::W_OFF + wave * 1024;
+  rb.slds = RL::S_OFF + sidx * 256;
+#pragma unroll
+  for (int t = 0; t < MT; t++) {
+    const int r = 32 * t + l32;
+    rb.rd_a1[t] = a_slot(r, 2 * kh) * 16;
+    rb.rd_a2[t] = a_slot(r, 2 * kh + 1) * 16;
+  }
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int cc = wave * 64 + 32 * j + l32;
+    rb.rd_w[j] = RL::W_OFF + cc * 16 + 8 * kh;
+    rb.rd_s[j] = RL::S_OFF + cc * 2;
+  }
+#pragma unroll
+  for (int i = 0; i < MT; i++) rb.acc[i][0] = rb.acc[i][1] = (float16_t){};
+
+  // steps are relative to c0 from here on
+  rb.issue(0, 0);
+  rb.issue(1, min(1, n - 1));
+  rb.issue(2, min(2, n - 1));
+  int i = 0;
+  for (; i + kRing <= n; i += kRing) {
+    rb.template step<0>(lds, min(i + 3, n - 1));
+    rb.template step<1>(lds, min(i + 4, n - 1));
+    rb.template step<2>(lds, min(i + 5, n - 1));
+    rb.template step<3>(lds, min(i + 6, n - 1));
+  }
+  if (i < n) rb.template step<0>(lds, n - 1);
+  if (i + 1 < n) rb.template step<1>(lds, n - 1);
+  if (i + 2 < n) rb.template step<2>(lds, n - 1);
   __builtin_amdgcn_s_waitcnt(0x3F70);  // the clamped trailing copies land before the block exits
 
   const int cg0 = (t0 + wave) * kTile;
@@ -371,7 +417,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
       for (int v = 0; v < 16; v++) {
         const int row = rbase + 32 * t + 8 * (v >> 2) + (v & 3);
         if (row < g.M) {
-          const float gt = acc[t][0][v], up = acc[t][1][v];
+          const float gt = rb.acc[t][0][v], up = rb.acc[t][1][v];
           const _Float16 hv = (_Float16)(gt / (1.f + __expf(-gt)) * up);
           g.Ch[(size_t)row * g.ldc + oi] = __builtin_bit_cast(uint16_t, hv);
         }
@@ -389,7 +435,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 #pragma unroll
       for (int v = 0; v < 16; v++) {
         const int row = rbase + 32 * t + 8 * (v >> 2) + (v & 3);
-        if (row < g.M) out[(size_t)row * g.ldc + col] = acc[t][j][v] + bias;
+        if (row < g.M) out[(size_t)row * g.ldc + col] = rb.acc[t][j][v] + bias;
       }
   }
 }
@@ -583,30 +629,75 @@ void launch_rope_kv(const RopeKvArgs& a, hipStream_t st) {
 
 // ------------------------------------------------------- flash attention --
 // Causal attention of M query rows over the fp16 cache (TSLAttention.ts:
-// 288-449 for one query).  Block: one kv head and 32 query rows, one wave per
-// query head of the group.  Per tile of 32 keys: K rows and V^T staged in LDS
-// once for the group; S^T = K Q^T (lane = query, registers = keys), an online
-// softmax in registers (the two half-waves of a query exchange one value),
-// then O^T += V^T P^T with P^T taken straight from the S^T registers: the key
-// order of the contraction is permuted to match that register layout.
-template <int DT>
-__global__ __launch_bounds__(512) void prefill_attn_kernel(PrefillAttnArgs a) {
-  constexpr int KS = DT + 8;  // halves per K row in LDS
-  constexpr int VS = 36;      // halves per V^T row (32 keys + 4): 8-byte aligned reads
-  constexpr int NDT = DT / 32;
-  __shared__ __align__(16) _Float16 ks[32 * KS];
-  __shared__ __align__(16) _Float16 vt[DT * VS];
-  const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63, wave = tid >> 6;
+// 288-449 for one query).  Block: one kv head, 32 query rows and up to four
+// query heads of the group (one wave each), times NG key groups: group z
+// takes key tiles z, z + NG, ... and the groups merge their (max, sum, O) at
+// the end, which halves the serial chain of the long (late) query tiles.
+// Per tile of 64 keys: K rows and V^T sit in LDS (double buffered; the next
+// tiles' rows are loaded into registers while this one is computed, one
+// barrier per tile); S^T = K Q^T (lane = query, registers = keys), an online
+// softmax in registers (the two half-waves of a query exchange one value;
+// masks only on tiles that cross the causal diagonal or the window start; O
+// is rescaled only when some row's max moved), then O^T += V^T P^T with P^T
+// taken straight from the S^T registers: the key order of the contraction is
+// permuted to match that register layout.  P is rounded to fp16 toward zero.
+template <int DT, int NG>
+struct AttnTile {
+  static constexpr int KT = 64;            // keys per tile
+  static constexpr int KS = DT + 8;        // halves per K row in LDS
+  static constexpr int VS = KT + 4;        // halves per V^T row: 8-byte aligned, conflict-free reads
+  static constexpr int PIECES = KT * DT / 8;  // 16-byte pieces of K (or V) per tile
+  static constexpr int PPT = PIECES / 256;    // pieces per thread (256 threads per key group)
+  static constexpr int TILE_HALVES = KT * KS + DT * VS;
+};
+
+// K and V pieces of one tile in registers: piece i is row i / (DT / 8), dims
+// 8 (i % (DT / 8)) .. + 7; rows past qhi repeat row qhi (their keys are masked).
+template <int DT, int NG>
+struct AttnStage {
+  using AT = AttnTile<DT, NG>;
+  uint4 kr[AT::PPT], vr[AT::PPT];
+  __device__ __forceinline__ void load(const _Float16* kb, const _Float16* vb, int kt0, int qhi, int t) {
+#pragma unroll
+    for (int u = 0; u < AT::PPT; u++) {
+      const int i = t + 256 * u;
+      const size_t src = (size_t)min(kt0 + i / (DT / 8), qhi) * DT + 8 * (i % (DT / 8));
+      kr[u] = *reinterpret_cast<const uint4*>(kb + src);
+      vr[u] = *reinterpret_cast<const uint4*>(vb + src);
+    }
+  }
+  // K rows as they are, V transposed (V^T[d][key])
+  __device__ __forceinline__ void store(_Float16* tile, int t) const {
+    _Float16* ks = tile;
+    _Float16* vt = tile + AT::KT * AT::KS;
+#pragma unroll
+    for (int u = 0; u < AT::PPT; u++) {
+      const int i = t + 256 * u, r = i / (DT / 8), c8 = i % (DT / 8);
+      *reinterpret_cast<uint4*>(&ks[r * AT::KS + 8 * c8]) = kr[u];
+      const half8_t v = as_half8(vr[u]);
+#pragma unroll
+      for (int e = 0; e < 8; e++) vt[(8 * c8 + e) * AT::VS + r] = v[e];
+    }
+  }
+};
+
+template <int DT, int NG>
+__global__ __launch_bounds__(256 * NG) __attribute__((amdgpu_waves_per_eu(2))) void prefill_attn_kernel(PrefillAttnArgs a) {
+  using AT = AttnTile<DT, NG>;
+  constexpr int KT = AT::KT, KS = AT::KS, VS = AT::VS, NDT = DT / 32;
+  __shared__ __align__(16) _Float16 lds[2 * NG * AT::TILE_HALVES];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int grp = __builtin_amdgcn_readfirstlane(tid >> 8), t256 = tid & 255, wave = t256 >> 6;
   const int l32 = lane & 31, kh = lane >> 5;
   const int nqt = (a.M + 31) / 32;
   const int qt = nqt - 1 - (int)blockIdx.x;  // longest key ranges first
   const int hk = blockIdx.y;
-  const int gw = (int)blockIdx.z * (nthr >> 6) + wave;
+  const int gw = (int)blockIdx.z * 4 + wave;
   const bool active = gw < a.G;
   const int h = hk * a.G + min(gw, a.G - 1);
   const int qr = qt * 32 + l32, qpos = a.p0 + qr;
-  const int qhi = a.p0 + min(qt * 32 + 31, a.M - 1);
-  const int kfirst = a.window > 0 ? max(0, a.p0 + qt * 32 - a.window + 1) : 0;
+  const int qlo = a.p0 + qt * 32, qhi = a.p0 + min(qt * 32 + 31, a.M - 1);
+  const int kfirst = a.window > 0 ? max(0, qlo - a.window + 1) : 0;
   const int qfirst = a.window > 0 ? max(0, qpos - a.window + 1) : 0;
   const int QW = a.Hq * DT;
 
@@ -615,88 +706,138 @@ __global__ __launch_bounds__(512) void prefill_attn_kernel(PrefillAttnArgs a) {
 #pragma unroll
   for (int j = 0; j < DT / 16; j++) qb[j] = *reinterpret_cast<const half8_t*>(qrow + 16 * j + 8 * kh);
 
+  const _Float16* kb = reinterpret_cast<const _Float16*>(a.kc) + (size_t)hk * a.max_tokens * DT;
+  const _Float16* vb = reinterpret_cast<const _Float16*>(a.vc) + (size_t)hk * a.max_tokens * DT;
+  AttnStage<DT, NG> sg;
+
   float16_t o[NDT];
 #pragma unroll
   for (int i = 0; i < NDT; i++) o[i] = (float16_t){};
-  float mrun = -INFINITY, lrun = 0.f;
-  const _Float16* kb = reinterpret_cast<const _Float16*>(a.kc) + (size_t)hk * a.max_tokens * DT;
-  const _Float16* vb = reinterpret_cast<const _Float16*>(a.vc) + (size_t)hk * a.max_tokens * DT;
-
-  for (int kt0 = kfirst & ~31; kt0 <= qhi; kt0 += 32) {
-    __syncthreads();  // the previous tile's LDS reads are done
-    for (int i = tid; i < 32 * DT / 8; i += nthr) {
-      const int r = i / (DT / 8), c8 = i % (DT / 8);
-      const size_t src = (size_t)min(kt0 + r, qhi) * DT + 8 * c8;  // rows past qhi repeat qhi (masked)
-      const uint4 kv = *reinterpret_cast<const uint4*>(kb + src);
-      const half8_t vv = as_half8(*reinterpret_cast<const uint4*>(vb + src));
-      *reinterpret_cast<uint4*>(ks + r * KS + 8 * c8) = kv;
+  float mrun = -INFINITY, lrun = 0.f;  // running max (log2 units) and this half-wave's sum
+  const int kbeg = kfirst & ~(KT - 1);
+  const int ntiles = (qhi - kbeg) / KT + 1;
+  const int nsteps = (ntiles + NG - 1) / NG;
+  _Float16* const mytile = lds + grp * AT::TILE_HALVES;  // buffer b at + b NG TILE_HALVES
+  sg.load(kb, vb, kbeg + grp * KT, qhi, t256);
+  sg.store(mytile, t256);
+  __syncthreads();
+  for (int it = 0; it < nsteps; it++) {
+    const int buf = it & 1, tile = it * NG + grp, kt0 = kbeg + tile * KT;
+    sg.load(kb, vb, kt0 + NG * KT, qhi, t256);  // this group's next tile, in flight during the math
+    if (tile < ntiles) {
+      const _Float16* kbuf = mytile + buf * NG * AT::TILE_HALVES;
+      const _Float16* vbuf = kbuf + KT * KS;
+      float16_t s[2];
 #pragma unroll
-      for (int e = 0; e < 8; e++) vt[(8 * c8 + e) * VS + r] = vv[e];
+      for (int b2 = 0; b2 < 2; b2++) {
+        s[b2] = (float16_t){};
+#pragma unroll
+        for (int j = 0; j < DT / 16; j++) {
+          const half8_t ak = *reinterpret_cast<const half8_t*>(kbuf + (32 * b2 + l32) * KS + 16 * j + 8 * kh);
+          s[b2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ak, qb[j], s[b2], 0, 0, 0);
+        }
+      }
+      if (kt0 + KT - 1 > qlo || (a.window > 0 && kt0 < qhi - a.window + 1)) {
+#pragma unroll
+        for (int b2 = 0; b2 < 2; b2++)
+#pragma unroll
+          for (int v = 0; v < 16; v++) {
+            const int key = kt0 + 32 * b2 + 8 * (v >> 2) + 4 * kh + (v & 3);
+            if (key > qpos || key < qfirst) s[b2][v] = -INFINITY;
+          }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int b2 = 0; b2 < 2; b2++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) mx = fmaxf(mx, s[b2][v]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * a.scale_log2;
+      const float mn = fmaxf(mrun, mx);
+      const float mu = mn == -INFINITY ? 0.f : mn;
+      const float corr = __builtin_amdgcn_exp2f(mrun - mu);
+      float ps = 0.f;
+      uint32_t pk[2][8];
+#pragma unroll
+      for (int b2 = 0; b2 < 2; b2++)
+#pragma unroll
+        for (int v = 0; v < 16; v += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(s[b2][v], a.scale_log2, -mu));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(s[b2][v + 1], a.scale_log2, -mu));
+          ps += p0 + p1;
+          pk[b2][v >> 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p0, p1));
+        }
+      lrun = lrun * corr + ps;
+      mrun = mn;
+      if (__builtin_amdgcn_ballot_w64(corr != 1.f)) {
+#pragma unroll
+        for (int i = 0; i < NDT; i++) o[i] *= corr;
+      }
+#pragma unroll
+      for (int b2 = 0; b2 < 2; b2++) {
+        const half8_t pb0 = __builtin_bit_cast(half8_t, make_uint4(pk[b2][0], pk[b2][1], pk[b2][2], pk[b2][3]));
+        const half8_t pb1 = __builtin_bit_cast(half8_t, make_uint4(pk[b2][4], pk[b2][5], pk[b2][6], pk[b2][7]));
+#pragma unroll
+        for (int i = 0; i < NDT; i++) {
+          const _Float16* vr0 = vbuf + (32 * i + l32) * VS + 32 * b2 + 4 * kh;
+          const half4_t x0 = *reinterpret_cast<const half4_t*>(vr0);
+          const half4_t x1 = *reinterpret_cast<const half4_t*>(vr0 + 8);
+          const half4_t x2 = *reinterpret_cast<const half4_t*>(vr0 + 16);
+          const half4_t x3 = *reinterpret_cast<const half4_t*>(vr0 + 24);
+          const half8_t a1 = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+          const half8_t a2 = {x2[0], x2[1], x2[2], x2[3], x3[0], x3[1], x3[2], x3[3]};
+          o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, pb0, o[i], 0, 0, 0);
+          o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, pb1, o[i], 0, 0, 0);
+        }
+      }
     }
+    sg.store(mytile + (buf ^ 1) * NG * AT::TILE_HALVES, t256);
     __syncthreads();
-    float16_t s = {};
-#pragma unroll
-    for (int j = 0; j < DT / 16; j++) {
-      const half8_t ak = *reinterpret_cast<const half8_t*>(ks + l32 * KS + 16 * j + 8 * kh);
-      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ak, qb[j], s, 0, 0, 0);
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int v = 0; v < 16; v++) {
-      const int key = kt0 + 8 * (v >> 2) + 4 * kh + (v & 3);
-      s[v] = (key > qpos || key < qfirst) ? -INFINITY : s[v] * a.scale_log2;
-      mx = fmaxf(mx, s[v]);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mn = fmaxf(mrun, mx);
-    const float mu = mn == -INFINITY ? 0.f : mn;
-    const float corr = __builtin_amdgcn_exp2f(mrun - mu);
-    float ps = 0.f;
-    half8_t pb[2];
-#pragma unroll
-    for (int v = 0; v < 16; v++) {
-      const float p = __builtin_amdgcn_exp2f(s[v] - mu);
-      ps += p;
-      pb[v >> 3][v & 7] = (_Float16)p;
-    }
-    lrun = lrun * corr + ps;
-    mrun = mn;
-#pragma unroll
-    for (int i = 0; i < NDT; i++) {
-      o[i] *= corr;
-      const _Float16* vr = vt + (32 * i + l32) * VS + 4 * kh;
-      const half4_t x0 = *reinterpret_cast<const half4_t*>(vr);
-      const half4_t x1 = *reinterpret_cast<const half4_t*>(vr + 8);
-      const half4_t x2 = *reinterpret_cast<const half4_t*>(vr + 16);
-      const half4_t x3 = *reinterpret_cast<const half4_t*>(vr + 24);
-      const half8_t a1 = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-      const half8_t a2 = {x2[0], x2[1], x2[2], x2[3], x3[0], x3[1], x3[2], x3[3]};
-      o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, pb[0], o[i], 0, 0, 0);
-      o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, pb[1], o[i], 0, 0, 0);
-    }
   }
   lrun += __shfl_xor(lrun, 32, 64);
+  if (NG > 1) {  // group 1 hands (max, sum, O) to group 0 through LDS (the tiles are free now)
+    float* xch = reinterpret_cast<float*>(lds) + (size_t)(wave * 64 + lane) * (2 + 16 * NDT);
+    if (grp == 1) {
+      xch[0] = mrun;
+      xch[1] = lrun;
+#pragma unroll
+      for (int i = 0; i < NDT; i++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) xch[2 + 16 * i + v] = o[i][v];
+    }
+    __syncthreads();
+    if (grp == 1) return;
+    const float m1 = xch[0], l1 = xch[1];
+    const float mn = fmaxf(mrun, m1);
+    const float mu = mn == -INFINITY ? 0.f : mn;
+    const float c0 = __builtin_amdgcn_exp2f(mrun - mu), c1 = __builtin_amdgcn_exp2f(m1 - mu);
+    lrun = lrun * c0 + l1 * c1;
+#pragma unroll
+    for (int i = 0; i < NDT; i++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) o[i][v] = o[i][v] * c0 + xch[2 + 16 * i + v] * c1;
+  }
   if (!active || qr >= a.M) return;
   const float inv = lrun > 0.f ? 1.f / lrun : 0.f;
   _Float16* orow = reinterpret_cast<_Float16*>(a.out) + (size_t)qr * QW + h * DT;
 #pragma unroll
   for (int i = 0; i < NDT; i++)
 #pragma unroll
-    for (int grp = 0; grp < 4; grp++) {
-      const half4_t y = {(_Float16)(o[i][4 * grp] * inv), (_Float16)(o[i][4 * grp + 1] * inv),
-                         (_Float16)(o[i][4 * grp + 2] * inv), (_Float16)(o[i][4 * grp + 3] * inv)};
-      *reinterpret_cast<half4_t*>(orow + 32 * i + 8 * grp + 4 * kh) = y;
+    for (int g4 = 0; g4 < 4; g4++) {
+      const half4_t y = {(_Float16)(o[i][4 * g4] * inv), (_Float16)(o[i][4 * g4 + 1] * inv),
+                         (_Float16)(o[i][4 * g4 + 2] * inv), (_Float16)(o[i][4 * g4 + 3] * inv)};
+      *reinterpret_cast<half4_t*>(orow + 32 * i + 8 * g4 + 4 * kh) = y;
     }
 }
 
 bool launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t st) {
-  if (a.D != 64 && a.D != 128) return false;
-  const int wpb = a.G < 8 ? a.G : 8;
-  const dim3 grid((a.M + 31) / 32, a.Hkv, (a.G + wpb - 1) / wpb);
+  // four query heads per block (waves past the group's heads only stage K/V)
+  const dim3 grid((a.M + 31) / 32, a.Hkv, (a.G + 3) / 4);
   if (a.D == 64)
-    hipLaunchKernelGGL(prefill_attn_kernel<64>, grid, dim3(64 * wpb), 0, st, a);
+    hipLaunchKernelGGL((prefill_attn_kernel<64, 2>), grid, dim3(512), 0, st, a);
+  else if (a.D == 128)
+    hipLaunchKernelGGL((prefill_attn_kernel<128, 1>), grid, dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL(prefill_attn_kernel<128>, grid, dim3(64 * wpb), 0, st, a);
+    return false;
   return true;
 }
 
