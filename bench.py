@@ -13,7 +13,11 @@ Prints one JSON line.  Besides tok/s it reports the fraction of the HBM
 roofline (algorithmic bytes per token over 8 TB/s), the LM head kernel's
 roofline (the dominant kernel: 57% of the bytes) and a CPU baseline: the
 oracle's single-threaded restatement of the reference CPU path timed on a
-bounded sample of the same workload.
+bounded sample of the same workload.  Prefill: the prompt's 127 positions as
+one batched pass (MFMA GEMMs + flash attention; `prefill_tok_s`) and replaying
+the decode graph per position as the reference does (`prefill_replay_tok_s`);
+`prefill_chunk` is one 2048-position chunk on the Llama-3.2-1B shape with its
+FLOP/s against the dense fp16 MFMA peak.
 """
 from __future__ import annotations
 
@@ -100,6 +104,52 @@ def cpu_baseline(hw, prompt, budget_s: float):
     return n / dt, n, dt
 
 
+MFMA_PEAK_F16 = 2.5e15  # dense fp16 MFMA FLOP/s, MI355X
+
+
+def prefill_flops(r, n: int, p0: int = 0) -> float:
+    """Useful FLOPs of one prefill chunk of n positions starting at p0: the
+    linears (2 M N K each) and causal attention (QK^T and PV over the keys
+    [0, pos] of each position); masked-out products are not counted."""
+    H, I, L = r.hidden_size, r.inner_size, r.layer_count
+    nqkv = r.q_size + 2 * r.kv_size
+    lin = 2.0 * n * L * (H * nqkv + r.q_size * H + 2 * I * H + I * H)
+    keys = sum(p + 1 for p in range(p0, p0 + n)) if not r.sliding_window else sum(
+        min(p + 1, r.sliding_window) for p in range(p0, p0 + n))
+    att = 4.0 * r.head_dim * r.head_count * keys * L
+    return lin + att
+
+
+def prefill_chunk_bench(W, R, ctx, workload: str, n: int) -> dict:
+    """One prefill chunk of n random ids on a full-size model (the MFMA GEMM
+    path): median of 3 timed chunks after one warm-up, FLOP/s and the
+    fraction of the dense fp16 MFMA peak."""
+    wl = W.WORKLOADS[workload]
+    hw = W.synthetic(wl)
+    hw.keep = True
+    runner = R.DecoderHIPRunner(hw, {"maxTokens": n + 8, "prefillChunkSize": n}, ctx=ctx)
+    ids = [int(t) for t in W.prompt_tokens(W.Workload(wl.name, wl.config, wl.storage, n, 0, n))]
+    times = []
+    for rep in range(4):
+        runner.resetCache()
+        ctx.sync()
+        t0 = time.perf_counter()
+        runner.prefillTokens(ids, 0, n)
+        ctx.sync()
+        if rep:
+            times.append(time.perf_counter() - t0)
+    dt = sorted(times)[1]
+    flops = prefill_flops(hw.recipe, n)
+    out = {"workload": wl.name, "tokens": n, "batched": runner.batchedPrefill, "ms": round(dt * 1e3, 3),
+           "tok_s": round(n / dt, 1), "tflops": round(flops / dt / 1e12, 1),
+           "mfma_frac": round(flops / dt / MFMA_PEAK_F16, 4), "flops_per_chunk": flops,
+           "peak": "2.5 PFLOP/s dense fp16 MFMA"}
+    log(f"[bench] prefill chunk {wl.name} x {n}: {dt * 1e3:.2f} ms = {n / dt:.0f} tok/s, "
+        f"{flops / dt / 1e12:.0f} TFLOP/s = {100 * flops / dt / MFMA_PEAK_F16:.1f}% of the fp16 MFMA peak")
+    runner.close()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -108,6 +158,10 @@ def main():
     ap.add_argument("--workload", default="qwen2.5-0.5b")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work (0 disables)")
     ap.add_argument("--kernel-iters", type=int, default=50)
+    ap.add_argument("--prefill-workload", default="llama-3.2-1b",
+                    help="model of the prefill-chunk measurement (the MFMA GEMM path)")
+    ap.add_argument("--prefill-chunk", type=int, default=2048,
+                    help="positions of the prefill-chunk measurement (0 skips it)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device-to-device copy of this many MiB, 5 times (the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings), then exit")
@@ -145,14 +199,37 @@ def main():
     start = wl.kv_prefill
     if wl.kv_prefill:
         runner.model.kv_fill_normal(0xC0FFEE, wl.kv_prefill)
-    # prompt prefill (reference semantics: the decode graph replayed per token)
+    # prompt prefill: positions [start, start + n) without logits, batched
+    # (MFMA GEMMs + flash attention) and, for comparison, the reference's
+    # semantics (the decode graph replayed once per position)
     prefill_n = len(prompt) - 1
-    ctx.sync()
-    tp = time.perf_counter()
+    prefill_s = replay_s = None
     if prefill_n > 0:
-        runner.prefillTokens([0] * start + prompt, start, start + prefill_n)
-    ctx.sync()
-    prefill_s = time.perf_counter() - tp
+        toks_all = [0] * start + prompt
+        runner.prefillTokens(toks_all, start, start + prefill_n)  # warm-up (row buffers, code objects)
+        m = runner.model
+        m.set_prefill(0, runner.prefillChunkSize)
+        m.reset_cache()
+        if wl.kv_prefill:
+            m.kv_fill_normal(0xC0FFEE, wl.kv_prefill)
+        ctx.sync()
+        tp = time.perf_counter()
+        runner.prefillTokens(toks_all, start, start + prefill_n)
+        ctx.sync()
+        replay_s = time.perf_counter() - tp
+        if runner.batchedPrefill:
+            m.set_prefill(runner.prefillBatchRows, runner.prefillChunkSize)
+        times = []
+        for _ in range(3):
+            m.reset_cache()
+            if wl.kv_prefill:
+                m.kv_fill_normal(0xC0FFEE, wl.kv_prefill)
+            ctx.sync()
+            tp = time.perf_counter()
+            runner.prefillTokens(toks_all, start, start + prefill_n)
+            ctx.sync()
+            times.append(time.perf_counter() - tp)
+        prefill_s = sorted(times)[1]
     last, pos0 = prompt[-1], start + prefill_n
     steps, warmup = args.steps, args.warmup
     if pos0 + max(steps, warmup) > max_tokens:
@@ -193,7 +270,10 @@ def main():
         f"back-to-back launches of layer 0 (us): "
         + ", ".join(f"{k} {v * 1e3:.1f}" for k, v in stage_ms.items()))
     log(f"[bench] host-driven loop (token read back every step): {host_tok_s:.1f} tok/s")
-    log(f"[bench] prefill {prefill_n} tokens in {prefill_s * 1e3:.1f} ms; first tokens {list(tokens[:8])}")
+    if prefill_n > 0:
+        log(f"[bench] prefill {prefill_n} tokens: {prefill_s * 1e3:.2f} ms batched "
+            f"({'MFMA row batches' if runner.batchedPrefill else 'replay'}), {replay_s * 1e3:.2f} ms replaying the "
+            f"decode graph; first tokens {[int(t) for t in tokens[:8]]}")
     cpu = None
     if args.cpu_budget > 0:
         ncpu = os.cpu_count()
@@ -218,7 +298,8 @@ def main():
         "data": "synthetic",
         "hbm_roofline_frac": round(hbm_frac, 4),
         "bytes_per_token": round(mean_bytes),
-        "prefill_tok_s": round(prefill_n / prefill_s, 1) if prefill_n > 0 and prefill_s > 0 else None,
+        "prefill_tok_s": round(prefill_n / prefill_s, 1) if prefill_n > 0 else None,
+        "prefill_replay_tok_s": round(prefill_n / replay_s, 1) if prefill_n > 0 else None,
         "host_loop_tok_s": round(host_tok_s, 1),
         "config": {"workload": wl.name, "prompt": wl.prompt_len, "decode": steps, "batch": 1,
                    "linears": wl.storage.linear + (" g32 fp16 scales" if wl.storage.linear == "q4" else ""),
@@ -230,6 +311,8 @@ def main():
         "cpu_baseline": cpu,
     }
     runner.close()
+    if args.prefill_chunk:
+        result["prefill_chunk"] = prefill_chunk_bench(W, R, ctx, args.prefill_workload, args.prefill_chunk)
     ctx.close()
     print(json.dumps(result), flush=True)
 
