@@ -162,6 +162,8 @@ def main():
                     help="model of the prefill-chunk measurement (the MFMA GEMM path)")
     ap.add_argument("--prefill-chunk", type=int, default=2048,
                     help="positions of the prefill-chunk measurement (0 skips it)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the prefill-chunk measurement (for profiling); prints its JSON object")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device-to-device copy of this many MiB, 5 times (the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings), then exit")
@@ -184,6 +186,12 @@ def main():
         src.free()
         dst.free()
         ctx.close()
+        return
+    if args.prefill_only:
+        ctx = tlm.Context(0)
+        out = prefill_chunk_bench(W, R, ctx, args.prefill_workload, args.prefill_chunk or 2048)
+        ctx.close()
+        print(json.dumps(out), flush=True)
         return
     wl = W.WORKLOADS[args.workload]
     t0 = time.perf_counter()
