@@ -270,14 +270,24 @@ def main():
         runner.computeToken(int(tok), pos0 + i, True)
         tok = runner.sampleToken(1, {"temperature": 0})
     host_tok_s = n_host / (time.perf_counter() - th)
+    # the same loop sampling top-8 (temperature 0.8): device candidates, host draw
+    import random as _random
+    rnd = _random.Random(7)
+    ctx.sync()
+    th = time.perf_counter()
+    for i in range(n_host):
+        runner.computeToken(int(tok), pos0 + i, True)
+        tok = runner.sampleToken(8, {"temperature": 0.8, "random": rnd.random})
+    host_topk_tok_s = n_host / (time.perf_counter() - th)
     stage_ms = {name: runner.model.time_kernel(k, args.kernel_iters)
-                for name, k in (("qkv", 4), ("attention", 1), ("o", 5), ("mlp", 2))}
+                for name, k in (("qkv", 4), ("attention", 1), ("o", 5), ("mlp", 2), ("top8", 6))}
     log(f"[bench] decode {toks:.1f} tok/s ({ms_step * 1e3:.1f} us/token wall, {ev_ms * 1e3 / steps:.1f} us/token "
         f"events), {mean_bytes / 1e6:.2f} MB/token -> {hbm_frac * 100:.1f}% of HBM roofline")
     log(f"[bench] LM head {lm_ms * 1e3:.1f} us/launch in decode steps = {lm_bw / 1e9:.0f} GB/s; stage times, "
         f"back-to-back launches of layer 0 (us): "
         + ", ".join(f"{k} {v * 1e3:.1f}" for k, v in stage_ms.items()))
-    log(f"[bench] host-driven loop (token read back every step): {host_tok_s:.1f} tok/s")
+    log(f"[bench] host-driven loop (token read back every step): {host_tok_s:.1f} tok/s greedy, "
+        f"{host_topk_tok_s:.1f} tok/s sampling top-8 candidates")
     if prefill_n > 0:
         log(f"[bench] prefill {prefill_n} tokens: {prefill_s * 1e3:.2f} ms batched "
             f"({'MFMA row batches' if runner.batchedPrefill else 'replay'}), {replay_s * 1e3:.2f} ms replaying the "
@@ -309,6 +319,8 @@ def main():
         "prefill_tok_s": round(prefill_n / prefill_s, 1) if prefill_n > 0 else None,
         "prefill_replay_tok_s": round(prefill_n / replay_s, 1) if prefill_n > 0 else None,
         "host_loop_tok_s": round(host_tok_s, 1),
+        "host_loop_top8_tok_s": round(host_topk_tok_s, 1),
+        "top8_candidates_us": round(stage_ms["top8"] * 1e3, 2),
         "config": {"workload": wl.name, "prompt": wl.prompt_len, "decode": steps, "batch": 1,
                    "linears": wl.storage.linear + (" g32 fp16 scales" if wl.storage.linear == "q4" else ""),
                    "head": "fp16 tied" if hw.recipe.tied_embeddings else wl.storage.head, "kv": wl.storage.kv,

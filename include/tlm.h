@@ -139,6 +139,13 @@ int tlm_attn_read_cache(tlm_attn* attn, int count, float* k_out, float* v_out);
  * logits = head x; token = argmax, ties to the lower id.  logits may be NULL. */
 int tlm_op_logits(tlm_linear* head, const float* x, float* logits, int32_t* token);
 int tlm_op_argmax(tlm_ctx* ctx, const float* logits, int n, int32_t* token);
+/* TSLLogitSampler candidate levels (tsl/TSLLogits.ts:276-330): the k best
+ * (token, score) of logits[0, n) in the greedy order (higher score, ties to
+ * the lower id), scores after the softcap cap * tanh(x / cap) when softcap > 0
+ * (:185-191).  Entries at or below LOWEST_FLOAT (-inf, NaN included) never
+ * take part; missing slots are (0, LOWEST_FLOAT).  1 <= k <= 16; device
+ * tokens[k], scores[k].  Enqueue only. */
+int tlm_op_topk(tlm_ctx* ctx, const float* logits, int n, int k, double softcap, int32_t* tokens, float* scores);
 
 /* ------------------------------------------------------------------- model */
 typedef struct tlm_model_desc {
@@ -218,6 +225,11 @@ int tlm_kv_read(tlm_model* model, int layer, int pos0, int count, void* k, void*
 /* Fills positions [0, count) of every layer with N(0,1) values from a
  * counter-based generator on the device (long-context benchmarks). */
 int tlm_kv_fill_normal(tlm_model* model, uint64_t seed, int count);
+/* readCandidates (TSLLogits.ts:336-349) over the model's last logits
+ * (a token computed with TLM_LOGITS): k <= 16 (token, score) pairs to host
+ * memory, best first; waits for the stream.  sampleTopKCandidates
+ * (runtime/math.ts:527-547) then draws from them on the host. */
+int tlm_read_candidates(tlm_model* model, int k, double softcap, int32_t* tokens, float* scores);
 /* Final hidden state (after the final norm) of the last token with logits. */
 int tlm_read_hidden(tlm_model* model, float* out, size_t n);
 
@@ -225,7 +237,8 @@ int tlm_read_hidden(tlm_model* model, float* out, size_t n);
  * decode of n tokens after `warmup` untimed ones, from `position`; ms total.
  * tlm_time_kernel: average ms of one launch of kernel `which` (0 = LM head,
  * 1 = attention of layer 0, 2 = fused gate|up/SwiGLU/down MLP of layer 0,
- * 4 = QKV of layer 0, 5 = O of layer 0) over iters back-to-back launches;
+ * 4 = QKV of layer 0, 5 = O of layer 0, 6 = top-8 candidates over the logits)
+ * over iters back-to-back launches;
  * afterwards the residual accumulators are cleared (the next token starts
  * from the cache and ctrl state as left). */
 int tlm_time_decode(tlm_model* model, int32_t token, int32_t position, int warmup, int n, double* ms);

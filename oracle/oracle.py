@@ -59,6 +59,8 @@ def lib():
                                     F32P, F32P]
         L.orc_argmax.restype = ctypes.c_int
         L.orc_argmax.argtypes = [F32P, ctypes.c_int]
+        L.orc_topk_candidates.argtypes = [F32P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_double,
+                                          ctypes.POINTER(ctypes.c_int), F32P]
         L.orc_q4_quantize.argtypes = [F32P, ctypes.c_int, ctypes.c_int, U8P, U16P]
         L.orc_q4_dequant.argtypes = [U8P, U16P, ctypes.c_int, ctypes.c_int, F32P]
         L.orc_model_new.restype = ctypes.c_void_p
@@ -183,6 +185,16 @@ def attention(qkv, heads, kv_heads, head_dim, position, k_cache, v_cache, inv_fr
 def argmax(logits) -> int:
     logits, lp = _f32(logits)
     return lib().orc_argmax(lp, len(logits))
+
+
+def topk_candidates(logits, k, chunk=8192, softcap=0.0):
+    """TSLLogitSampler candidates: [(token, score)] * k, best first."""
+    lg, lp = _f32(logits)
+    t = np.zeros(k, np.int32)
+    v = np.zeros(k, np.float32)
+    lib().orc_topk_candidates(lp, len(lg), int(chunk), int(k), float(softcap or 0.0),
+                              t.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), v.ctypes.data_as(F32P))
+    return [(int(a), float(b)) for a, b in zip(t, v)]
 
 
 def q4_quantize(w):

@@ -26,6 +26,10 @@
  *   orc_forward_token                HF fixture logits + final hidden, fp32 and
  *                                    fp16-storage variants (19 positions x 5 cases).
  *   orc_argmax                       tie/first-max KATs of tsl.browser.test.ts:82-103.
+ *   orc_topk_candidates              KATs of tsl.browser.test.ts:82-120 (chunked
+ *                                    candidates, softcap); brute force (sort by
+ *                                    score desc, id asc) with ties, -inf and NaN;
+ *                                    the result does not depend on the chunk size.
  *   orc_q4_quantize, orc_q4_dequant  build-defined format (no reference counterpart):
  *                                    exhaustive codes x scale set, round-trip bound.
  */
@@ -307,6 +311,62 @@ int orc_argmax(const float* logits, int n) {
       best_value = logits[i];
     }
   return best;
+}
+
+/* TSLLogitSampler candidate levels, TSLLogits.ts:245-330.  Per chunk of
+ * `chunk` logits and rank r < k: the best (score, id) not already taken in
+ * this chunk, starting from (id 0, LOWEST_FLOAT) and taking strictly higher
+ * scores or equal scores with a lower id (:248-266).  Then per rank r: the
+ * best chunk candidate of rank <= r not already taken globally (:268-300).
+ * Scores pass through cap * tanh(x / cap) first when softcap > 0 (:185-191),
+ * in float as the shader does. */
+void orc_topk_candidates(const float* logits, int n, int chunk, int k, double softcap, int* tokens,
+                         float* scores) {
+  const float lowest = -3.4028234663852886e38f;
+  const int nchunks = (n + chunk - 1) / chunk;
+  int* ct = (int*)malloc(sizeof(int) * (size_t)nchunks * k);
+  float* cs = (float*)malloc(sizeof(float) * (size_t)nchunks * k);
+  for (int c = 0; c < nchunks; c++) {
+    const int off = c * chunk, size = n - off < chunk ? n - off : chunk;
+    for (int r = 0; r < k; r++) {
+      int best = 0;
+      float best_score = lowest;
+      for (int i = 0; i < size; i++) {
+        const int id = off + i;
+        float score = logits[id];
+        if (softcap > 0) score = (float)softcap * tanhf(score / (float)softcap);
+        int selected = 0;
+        for (int p = 0; p < r; p++)
+          if (ct[c * k + p] == id) selected = 1;
+        if (!selected && (score > best_score || (score == best_score && id < best))) {
+          best = id;
+          best_score = score;
+        }
+      }
+      ct[c * k + r] = best;
+      cs[c * k + r] = best_score;
+    }
+  }
+  for (int r = 0; r < k; r++) {
+    int best = 0;
+    float best_score = lowest;
+    for (int c = 0; c < nchunks; c++)
+      for (int q = 0; q <= r; q++) {
+        const int id = ct[c * k + q];
+        const float score = cs[c * k + q];
+        int selected = 0;
+        for (int p = 0; p < r; p++)
+          if (tokens[p] == id) selected = 1;
+        if (!selected && (score > best_score || (score == best_score && id < best))) {
+          best = id;
+          best_score = score;
+        }
+      }
+    tokens[r] = best;
+    scores[r] = best_score;
+  }
+  free(ct);
+  free(cs);
 }
 
 /* ------------------------------------------------------------------- q4 ---

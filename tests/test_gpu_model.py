@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 
 from bridge import close, oracle_model, top2_gap
+from oracle import oracle as orc
 import three_llm_amd.runner as R
 import three_llm_amd.tlm as tlm
 import three_llm_amd.weights as W
@@ -201,4 +202,32 @@ def test_kv_cache_round_trip_and_reset(ctx):
         runner.computeToken(10 ** 6, 0, True)
     with pytest.raises(tlm.TlmError):
         runner.computeToken(1, 64, True)
+    runner.close()
+
+
+def test_device_top_k_sampling_matches_full_logit_sampling(ctx):
+    """readCandidates equals the oracle's candidate levels over the device
+    logits, and generate() with device top-k sampling (TSLLogitSampler) gives
+    the same tokens as sampling from the full logits on the host
+    (sampleTopK, math.ts:549-593) with the same random draws."""
+    import random as _random
+    wl = W.WORKLOADS["tiny"]
+    hw = W.synthetic(wl)
+    hw.keep = True
+    runner = R.DecoderHIPRunner(hw, {"maxTokens": 128}, ctx=ctx)
+    prompt = [int(t) for t in W.prompt_tokens(wl)]
+    for i, t in enumerate(prompt):
+        runner.computeToken(t, i, i == len(prompt) - 1)
+    logits = runner.readLogits()
+    for k in (1, 5, 8):
+        assert runner.readCandidates(k) == orc.topk_candidates(logits, k)
+    streams = []
+    for gpu in (True, False):
+        runner.resetCache()
+        rnd = _random.Random(1234)
+        res = runner.generate("", {"inputTokens": prompt, "temperature": 0.9, "topK": 5, "maxNewTokens": 24,
+                                   "gpuSampling": gpu, "random": rnd.random})
+        streams.append(res["generatedTokens"])
+    print("sampled:", streams[0])
+    assert streams[0] == streams[1] and len(streams[0]) == 24
     runner.close()

@@ -221,6 +221,38 @@ def test_argmax_known_answers(ctx):
     assert tlm.argmax(ctx, ctx.array(big), len(big), tok).read(np.int32)[0] == 777
 
 
+def test_topk_known_answers(ctx):
+    # tsl.browser.test.ts:82-120
+    lg = f32([1, 7, 7, -2, 8, 3, 6])
+    assert tlm.topk(ctx, ctx.array(lg), 7, 3) == [(4, 8.0), (1, 7.0), (2, 7.0)]
+    assert tlm.topk(ctx, ctx.array(lg), 7, 1) == [(4, 8.0)]
+    c = tlm.topk(ctx, ctx.array(f32([10, 2, -1])), 3, 2, softcap=1.0)
+    assert c[0][0] == 0 and c[0][1] <= 1 and c[1][0] == 1
+    lowest = float(np.float32(-3.4028234663852886e38))
+    assert tlm.topk(ctx, ctx.array(f32([np.nan, -np.inf, 2.0])), 3, 3) == [(2, 2.0), (0, lowest), (0, lowest)]
+
+
+@pytest.mark.parametrize("n,k", [(151936, 8), (128256, 16), (4096, 1), (300000, 16), (2049, 5), (10, 16)])
+def test_topk_matches_oracle(ctx, n, k):
+    """GPU candidates (one or two block levels) equal the oracle's restatement
+    of the reference's chunked candidate levels, ids and scores exactly, with
+    ties, -inf, NaN and LOWEST_FLOAT planted; softcap scores within 2 ulp."""
+    rng = np.random.default_rng(n + k)
+    x = f32(np.round(rng.standard_normal(n) * 4, 1))  # rounded: many ties
+    hot = rng.integers(0, n, size=min(n, 40))
+    x[hot] = 9.5  # a tie at the top across the whole vector
+    x[rng.integers(0, n, size=max(1, n // 1000))] = np.nan
+    x[rng.integers(0, n, size=max(1, n // 1000))] = -np.inf
+    buf = ctx.array(x)
+    got = tlm.topk(ctx, buf, n, k)
+    ref = orc.topk_candidates(x, k)
+    assert got == ref
+    got = tlm.topk(ctx, buf, n, k, softcap=30.0)
+    ref = orc.topk_candidates(x, k, softcap=30.0)
+    assert [t for t, _ in got] == [t for t, _ in ref]
+    close([v for _, v in got], [v for _, v in ref], 0, 2.5e-7)
+
+
 @pytest.mark.parametrize("V,H", [(151936, 896), (4096, 256), (1000, 64), (7, 8)])
 def test_logits_head_matches_oracle(ctx, V, H):
     rng = np.random.default_rng(V)

@@ -120,6 +120,48 @@ def test_argmax_first_max_and_ties():
     assert orc.argmax([1, 2, 3]) == 2 and orc.argmax([1, 4, 3]) == 1
 
 
+LOWEST = float(np.float32(-3.4028234663852886e38))
+
+
+def _brute_topk(logits, k, softcap=0.0):
+    """Sort by (score desc, id asc) over the entries above LOWEST_FLOAT; pad
+    with (0, LOWEST_FLOAT)."""
+    x = np.asarray(logits, np.float32)
+    if softcap:
+        x = (np.float32(softcap) * np.tanh(x / np.float32(softcap), dtype=np.float32)).astype(np.float32)
+    ids = np.arange(len(x))
+    valid = x > np.float32(LOWEST)  # NaN compares false
+    order = sorted(ids[valid], key=lambda i: (-float(x[i]), int(i)))[:k]
+    out = [(int(i), float(x[i])) for i in order]
+    return out + [(0, LOWEST)] * (k - len(out))
+
+
+def test_topk_candidates_known_answers():
+    # tsl.browser.test.ts:82-103: chunks [1,7,7,-2] ++ [8,3,6], candidateCount 3
+    assert orc.topk_candidates([1, 7, 7, -2, 8, 3, 6], 3, chunk=4) == [(4, 8.0), (1, 7.0), (2, 7.0)]
+    assert orc.topk_candidates([1, 7, 7, -2, 8, 3, 6], 1, chunk=4) == [(4, 8.0)]
+    # tsl.browser.test.ts:105-120: softcap 1 applied before ranking
+    c = orc.topk_candidates([10, 2, -1], 2, softcap=1.0)
+    assert c[0][0] == 0 and c[0][1] <= 1 and c[1][0] == 1
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_topk_candidates_brute_force_and_chunk_invariance(seed):
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(1, 3000))
+    x = rng.integers(-20, 20, size=n).astype(np.float32)  # many ties
+    for special in (np.inf, -np.inf, np.nan, LOWEST, -LOWEST):
+        x[rng.integers(0, n, size=max(1, n // 50))] = special
+    for k in (1, 3, 8, 16):
+        ref = _brute_topk(x, k)
+        for chunk in (1, 7, 64, 8192):
+            got = orc.topk_candidates(x, k, chunk=chunk)
+            assert [t for t, _ in got] == [t for t, _ in ref], (k, chunk)
+            assert np.array_equal(np.float32([v for _, v in got]), np.float32([v for _, v in ref]))
+    # fewer valid entries than k: the remaining slots are (0, LOWEST_FLOAT)
+    assert orc.topk_candidates([np.nan, -np.inf, 2.0], 3) == [(2, 2.0), (0, LOWEST), (0, LOWEST)]
+
+
 # --------------------------------------------------------------------- RoPE --
 
 def _scaling(case):

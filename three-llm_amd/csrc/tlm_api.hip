@@ -52,7 +52,11 @@ struct tlm_ctx {
   // scratch for op-level argmax
   float* arg_val = nullptr;
   int* arg_idx = nullptr;
+  // top-k levels: two levels of kTopkWork (score, id) pairs
+  float* topk_v = nullptr;
+  int* topk_i = nullptr;
 };
+constexpr size_t kTopkWork = 32768;
 
 struct GemvPlan {
   int waves = 4, cps = 1, splits = 1, gx = 1;
@@ -129,6 +133,8 @@ struct tlm_model {
   float* logits = nullptr;
   float* arg_val = nullptr;
   int* arg_idx = nullptr;
+  float* cand_v = nullptr;  // top-k candidates of the last logits (kTopkMax)
+  int* cand_i = nullptr;
   // attention (shared by the layers; they run one after another)
   tlm_attn attn;
   GemvPlan lm_plan;
@@ -334,6 +340,8 @@ int tlm_open(int device, tlm_ctx** out) {
   hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipMalloc(&c->arg_val, 4096 * sizeof(float));
   if (e == hipSuccess) e = hipMalloc(&c->arg_idx, 4096 * sizeof(int));
+  if (e == hipSuccess) e = hipMalloc(&c->topk_v, 2 * kTopkWork * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&c->topk_i, 2 * kTopkWork * sizeof(int));
   if (e != hipSuccess) {
     tlm_close(c);
     return fail(TLM_ERR_HIP, "TLMContext: setup failed: %s", hipGetErrorString(e));
@@ -347,6 +355,8 @@ void tlm_close(tlm_ctx* ctx) {
   if (ctx->stream) hipStreamSynchronize(ctx->stream);
   hipFree(ctx->arg_val);
   hipFree(ctx->arg_idx);
+  hipFree(ctx->topk_v);
+  hipFree(ctx->topk_i);
   if (ctx->stream) hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -815,6 +825,17 @@ int tlm_op_argmax(tlm_ctx* ctx, const float* logits, int n, int32_t* token) {
   return TLM_OK;
 }
 
+int tlm_op_topk(tlm_ctx* ctx, const float* logits, int n, int k, double softcap, int32_t* tokens, float* scores) {
+  if (!ctx || !logits || !tokens || !scores || n <= 0) return fail(TLM_ERR_INVALID, "TLMLogitSampler: invalid argument");
+  if (k < 1 || k > kTopkMax)
+    return fail(TLM_ERR_INVALID, "TLMLogitSampler: candidate count %d outside [1, %d]", k, kTopkMax);
+  if (!launch_topk(logits, n, k, (float)(softcap > 0 ? softcap : 0), ctx->topk_v, ctx->topk_i, kTopkWork, scores,
+                   tokens, ctx->stream))
+    return fail(TLM_ERR_INVALID, "TLMLogitSampler: %d logits exceed the candidate workspace", n);
+  CHECK_LAUNCH("TLMLogitSampler");
+  return TLM_OK;
+}
+
 // -------------------------------------------------------------------- model --
 
 static int model_alloc(void** p, size_t bytes) {
@@ -916,6 +937,8 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
   M_TRY(model_alloc((void**)&m->logits, sizeof(float) * d->vocab_size));
   M_TRY(model_alloc((void**)&m->arg_val, sizeof(float) * 4096));
   M_TRY(model_alloc((void**)&m->arg_idx, sizeof(int) * 4096));
+  M_TRY(model_alloc((void**)&m->cand_v, sizeof(float) * kTopkMax));
+  M_TRY(model_alloc((void**)&m->cand_i, sizeof(int) * kTopkMax));
 #undef M_TRY
   if (rc) {
     std::string msg = g_error;
@@ -950,7 +973,7 @@ void tlm_model_destroy(tlm_model* m) {
   tlm_linear_destroy(m->head);
   attn_free(&m->attn, false);
   void* bufs[] = {m->emb, m->final_norm, m->ctrl, m->tokens_out, m->prompt, m->xa, m->x0, m->xf, m->attn_out,
-                  m->pq, m->po, m->rb, m->logits, m->arg_val, m->arg_idx, m->pf_x, m->pf_part, m->pf_xn,
+                  m->pq, m->po, m->rb, m->logits, m->arg_val, m->arg_idx, m->cand_v, m->cand_i, m->pf_x, m->pf_part, m->pf_xn,
                   m->pf_q, m->pf_att, m->pf_h};
   for (void* p : bufs) hipFree(p);
   delete m;
@@ -1406,6 +1429,16 @@ int tlm_read_logits(tlm_model* m, float* out, size_t n) {
   return TLM_OK;
 }
 
+int tlm_read_candidates(tlm_model* m, int k, double softcap, int32_t* tokens, float* scores) {
+  if (!m || !tokens || !scores) return fail(TLM_ERR_INVALID, "TLMModel: null argument");
+  int rc = tlm_op_topk(m->ctx, m->logits, m->d.vocab_size, k, softcap, m->cand_i, m->cand_v);
+  if (rc) return rc;
+  HIP_TRY(hipMemcpyAsync(tokens, m->cand_i, sizeof(int32_t) * k, hipMemcpyDeviceToHost, m->ctx->stream));
+  HIP_TRY(hipMemcpyAsync(scores, m->cand_v, sizeof(float) * k, hipMemcpyDeviceToHost, m->ctx->stream));
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  return TLM_OK;
+}
+
 int tlm_read_hidden(tlm_model* m, float* out, size_t n) {
   if (!m || !out || n > (size_t)m->d.hidden_size) return fail(TLM_ERR_INVALID, "TLMModel: invalid hidden read");
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
@@ -1568,7 +1601,7 @@ int tlm_time_head(tlm_model* m, int32_t token, int32_t position, int n, double* 
 }
 
 int tlm_time_kernel(tlm_model* m, int which, int iters, double* avg_ms) {
-  if (!m || !avg_ms || iters <= 0 || which < 0 || which > 5 || which == 3)
+  if (!m || !avg_ms || iters <= 0 || which < 0 || which > 6 || which == 3)
     return fail(TLM_ERR_INVALID, "TLMModel: invalid kernel timing argument");
   int rc = tlm_model_finalize(m);
   if (rc) return rc;
@@ -1576,7 +1609,12 @@ int tlm_time_kernel(tlm_model* m, int which, int iters, double* avg_ms) {
   hipEvent_t e0, e1;
   HIP_TRY(hipEventCreate(&e0));
   HIP_TRY(hipEventCreate(&e1));
-  auto one = [&]() { return which == 0 ? enqueue_head(m, st, false) : enqueue_layer(m, 0, st, which); };
+  auto one = [&]() {
+    if (which == 6)  // top-8 candidates over the logits
+      return launch_topk(m->logits, m->d.vocab_size, 8, 0.f, m->ctx->topk_v, m->ctx->topk_i, kTopkWork, m->cand_v,
+                         m->cand_i, st);
+    return which == 0 ? enqueue_head(m, st, false) : enqueue_layer(m, 0, st, which);
+  };
   if (!one()) return fail(TLM_ERR_STATE, "TLMModel: no kernel variant for stage %d", which);  // warm
   CHECK_LAUNCH("TLMModel");
   HIP_TRY(hipStreamSynchronize(st));

@@ -152,6 +152,11 @@ void launch_kv_fill(void* kc, void* vc, bool f32, size_t heads_stride, int Hkv, 
                     uint64_t seed, hipStream_t st);
 size_t attn_smem_bytes(int gmax, int D, bool kv_f32);
 int attn_lpp(int D, bool kv_f32);
+// top-k candidates (k <= kTopkMax) of an fp32 vector in the greedy order; the
+// workspace holds two levels of wcap (score, id) pairs each
+constexpr int kTopkMax = 16;
+bool launch_topk(const float* logits, int n, int k, float softcap, float* wv, int* wi, size_t wcap, float* out_v,
+                 int* out_i, hipStream_t st);
 
 // ------------------------------------------------------------ batched prefill --
 // A chunk of M prompt positions per pass: row-major activations, linears as

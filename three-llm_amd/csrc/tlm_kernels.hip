@@ -1227,6 +1227,139 @@ void launch_argmax(const float* logits, int n, float* pval, int* pidx, int* toke
   launch_argmax_merge(pval, pidx, blocks, token, nullptr, 0, 0, EmbStage{}, st);
 }
 
+// ---------------------------------------------------------------- top-k --
+// Top-k candidates of TSLLogitSampler (TSLLogits.ts:276-330): the k best
+// (score, id) in the greedy order (higher score, ties to the lower id),
+// scores after the optional softcap cap * tanh(x / cap) (TSLLogits.ts:185-191).
+// An entry takes part only if its score is above LOWEST_FLOAT (so -inf and NaN
+// never do); slots past the last such entry are (id 0, LOWEST_FLOAT), as the
+// reference's selection loops leave them.
+// One block selects from up to kTopkSlice entries held in registers (8 per
+// lane) as 64-bit order keys: every wave finds its k best by k passes (pass r
+// takes the largest key below pass r-1's), then one wave merges the four
+// lists the same way.  Deterministic; levels of blocks until one remains.
+constexpr int kTopkPer = 8;
+constexpr int kTopkSlice = 256 * kTopkPer;
+
+// 64-bit order key of (score, id): the score mapped to an unsigned integer
+// with the same order (-0 counts as +0, so equal scores stay equal) in the
+// high word, the inverted id in the low word: a larger key is better in the
+// greedy order.  0 marks "no candidate".
+__device__ __forceinline__ unsigned long long topk_key(float v, int id) {
+  const uint32_t u = __float_as_uint(v + 0.f);
+  const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)ord << 32) | (uint32_t)(~(uint32_t)id);
+}
+__device__ __forceinline__ float topk_score(unsigned long long key) {
+  const uint32_t ord = (uint32_t)(key >> 32);
+  return __uint_as_float((ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord);
+}
+template <int CTRL>
+__device__ __forceinline__ void max_u64_step(uint32_t& lo, uint32_t& hi) {
+  const uint32_t olo = (uint32_t)dpp<CTRL>((int)lo), ohi = (uint32_t)dpp<CTRL>((int)hi);
+  if (ohi > hi || (ohi == hi && olo > lo)) {
+    lo = olo;
+    hi = ohi;
+  }
+}
+// Largest key of the wave, in every lane: DPP steps within rows of 16, then
+// the four rows' results through readlane.
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long x) {
+  uint32_t lo = (uint32_t)x, hi = (uint32_t)(x >> 32);
+  max_u64_step<kDppXor1>(lo, hi);
+  max_u64_step<kDppXor2>(lo, hi);
+  max_u64_step<kDppHalfMirror>(lo, hi);
+  max_u64_step<kDppMirror>(lo, hi);
+  unsigned long long best = 0;
+#pragma unroll
+  for (int r = 0; r < 64; r += 16) {
+    const unsigned long long v = ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)hi, r) << 32) |
+                                 (uint32_t)__builtin_amdgcn_readlane((int)lo, r);
+    best = v > best ? v : best;
+  }
+  return best;
+}
+
+// IDS: the entries are (vals[e], ids[e]) (a merge level) instead of (vals[e], e).
+template <bool IDS>
+__global__ __launch_bounds__(256) void topk_select_kernel(const float* __restrict__ vals, const int* __restrict__ ids,
+                                                          int n, int k, float softcap, float* out_v, int* out_i) {
+  __shared__ unsigned long long wk[4][kTopkMax];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const size_t base = (size_t)blockIdx.x * kTopkSlice + wave * 64 * kTopkPer;
+  // every load issued before the first use (clamped indices: no branches)
+  float x[kTopkPer];
+  int xi[kTopkPer];
+#pragma unroll
+  for (int u = 0; u < kTopkPer; u++) x[u] = vals[min(base + lane + 64 * u, (size_t)n - 1)];
+#pragma unroll
+  for (int u = 0; u < kTopkPer; u++)
+    xi[u] = IDS ? ids[min(base + lane + 64 * u, (size_t)n - 1)] : (int)(base + lane + 64 * u);
+  if (softcap > 0.f) {
+#pragma unroll
+    for (int u = 0; u < kTopkPer; u++) x[u] = softcap * tanhf(x[u] / softcap);
+  }
+  unsigned long long key[kTopkPer];
+#pragma unroll
+  for (int u = 0; u < kTopkPer; u++) {
+    const bool ok = base + lane + 64 * u < (size_t)n && x[u] > kLowest;  // LOWEST, -inf, NaN: never a candidate
+    key[u] = ok ? topk_key(x[u], xi[u]) : 0ull;
+  }
+  // each wave: its k best in k passes, pass r taking the best key below pass r-1's
+  unsigned long long prev = ~0ull;
+  for (int r = 0; r < k; r++) {
+    unsigned long long best = 0;
+#pragma unroll
+    for (int u = 0; u < kTopkPer; u++) {
+      const unsigned long long c = key[u] < prev ? key[u] : 0ull;
+      best = c > best ? c : best;
+    }
+    best = wave_max_u64(best);
+    if (lane == 0) wk[wave][r] = best;
+    prev = best;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  // wave 0 merges the 4 lists (4 k <= 64 keys, one per lane)
+  const unsigned long long mine = lane < 4 * k ? wk[lane / k][lane % k] : 0ull;
+  prev = ~0ull;
+  for (int r = 0; r < k; r++) {
+    const unsigned long long best = wave_max_u64(mine < prev ? mine : 0ull);
+    if (lane == 0) {
+      out_v[(size_t)blockIdx.x * k + r] = best ? topk_score(best) : kLowest;
+      out_i[(size_t)blockIdx.x * k + r] = best ? (int)~(uint32_t)best : 0;
+    }
+    prev = best ? best : 0ull;
+  }
+}
+
+bool launch_topk(const float* logits, int n, int k, float softcap, float* wv, int* wi, size_t wcap, float* out_v,
+                 int* out_i, hipStream_t st) {
+  if (n <= 0 || k <= 0 || k > kTopkMax) return false;
+  int blocks = (n + kTopkSlice - 1) / kTopkSlice;
+  if ((size_t)blocks * k > wcap) return false;
+  const float* v = logits;
+  const int* ids = nullptr;
+  float cap = softcap;
+  float* bufv[2] = {wv, wv + wcap};
+  int* bufi[2] = {wi, wi + wcap};
+  for (int level = 0;; level++) {
+    const bool last = blocks == 1;
+    float* ov = last ? out_v : bufv[level & 1];
+    int* oi = last ? out_i : bufi[level & 1];
+    if (ids)
+      hipLaunchKernelGGL(topk_select_kernel<true>, dim3(blocks), dim3(256), 0, st, v, ids, n, k, cap, ov, oi);
+    else
+      hipLaunchKernelGGL(topk_select_kernel<false>, dim3(blocks), dim3(256), 0, st, v, ids, n, k, cap, ov, oi);
+    if (last) return true;
+    v = ov;
+    ids = oi;
+    cap = 0.f;
+    n = blocks * k;
+    blocks = (n + kTopkSlice - 1) / kTopkSlice;
+  }
+}
+
 __global__ void set_ctrl_kernel(int* ctrl, int token, int pos, int step, int base, int len, EmbStage es) {
   if (threadIdx.x == 0) {
     ctrl[C_TOKEN] = token;

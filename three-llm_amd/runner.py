@@ -66,7 +66,7 @@ class DecoderHIPRunner:
         self.weights = RunnerWeights(weights, tokenizer or TinyTokenizer(eos=weights.recipe.end_of_text_token_id))
         limit = weights.recipe.context_limit
         self.maxTokens = min(options.get("maxTokens") or limit, limit)
-        self.logitCandidateCount = options.get("logitCandidateCount") or 8
+        self.logitCandidateCount = min(options.get("logitCandidateCount") or 8, 16)  # device top-k holds <= 16
         desc, inv = weights.model_desc(self.maxTokens)
         self.model = tlm.Model(self.ctx, desc, inv)
         weights.upload(self.model)
@@ -107,19 +107,22 @@ class DecoderHIPRunner:
         return self.model.read_logits()
 
     def sampleToken(self, candidateCount: int, options: Optional[dict] = None) -> int:
-        """TSLLogitSampler.sampleToken (TSLLogits.ts:379-383): greedy reads the
-        device argmax (4 bytes); top-k samples from the k best candidates."""
+        """TSLLogitSampler.sampleToken (TSLLogits.ts:351-355): greedy reads the
+        device argmax (4 bytes); top-k takes the k best candidates from the
+        device (readCandidates, :336-349) and draws with sampleTopKCandidates."""
         options = options or {}
         if candidateCount <= 1 or options.get("temperature", 0.8) <= 0:
             return self.model.read_token()
-        logits = self.model.read_logits()
         k = min(max(1, candidateCount), self.logitCandidateCount)
-        order = np.argsort(-logits.astype(np.float64), kind="stable")[:k]
-        candidates = [(int(i), float(logits[i])) for i in order]
+        candidates = self.readCandidates(k)
         kw = {"temperature": options.get("temperature", 0.8)}
         if options.get("random") is not None:
             kw["random"] = options["random"]
         return gen.sample_top_k_candidates(candidates, **kw)
+
+    def readCandidates(self, count: int):
+        """TSLLogitSampler.readCandidates: [(token, score)], best first."""
+        return self.model.read_candidates(min(max(1, count), self.logitCandidateCount))
 
     def resetCache(self):
         """DecoderTSLRunner.resetCache (:541-546)."""

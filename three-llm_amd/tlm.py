@@ -25,6 +25,7 @@ EXPORTS = [
     "tlm_free", "tlm_upload", "tlm_download", "tlm_copy", "tlm_linear_create", "tlm_linear_destroy", "tlm_linear_dequant",
     "tlm_op_linear", "tlm_op_linear_rows", "tlm_op_rmsnorm", "tlm_op_silu_mul", "tlm_op_gated_mlp", "tlm_attn_create", "tlm_attn_destroy",
     "tlm_op_attention", "tlm_op_attention_rows", "tlm_attn_reset", "tlm_attn_read_cache", "tlm_op_logits", "tlm_op_argmax",
+    "tlm_op_topk", "tlm_read_candidates",
     "tlm_model_create", "tlm_model_destroy", "tlm_model_upload", "tlm_model_finalize", "tlm_model_set_prefill",
     "tlm_compute_token",
     "tlm_prefill", "tlm_read_logits", "tlm_read_token", "tlm_decode_greedy", "tlm_reset_cache", "tlm_kv_write",
@@ -98,6 +99,8 @@ def lib():
             "tlm_attn_read_cache": ([VP, ctypes.c_int, VP, VP], ctypes.c_int),
             "tlm_op_logits": ([VP, VP, VP, VP], ctypes.c_int),
             "tlm_op_argmax": ([VP, VP, ctypes.c_int, VP], ctypes.c_int),
+            "tlm_op_topk": ([VP, VP, ctypes.c_int, ctypes.c_int, dbl, VP, VP], ctypes.c_int),
+            "tlm_read_candidates": ([VP, ctypes.c_int, dbl, VP, VP], ctypes.c_int),
             "tlm_model_create": ([VP, ctypes.POINTER(ModelDesc), ctypes.POINTER(VP)], ctypes.c_int),
             "tlm_model_destroy": ([VP], None),
             "tlm_model_upload": ([VP, ctypes.c_int, ctypes.c_int, VP, sz], ctypes.c_int),
@@ -344,6 +347,16 @@ def argmax(ctx: Context, logits_buf: Buffer, n: int, token: Buffer) -> Buffer:
     return token
 
 
+def topk(ctx: Context, logits_buf: Buffer, n: int, k: int, softcap: float = 0.0):
+    """TSLLogitSampler candidates: [(token, score)] * k, best first (blocks on the read)."""
+    tok, sc = ctx.buffer(4 * k), ctx.buffer(4 * k)
+    check(lib().tlm_op_topk(ctx.ptr, logits_buf.ptr, n, k, float(softcap), tok.ptr, sc.ptr))
+    t, v = tok.read(np.int32), sc.read(np.float32)
+    tok.free()
+    sc.free()
+    return [(int(a), float(b)) for a, b in zip(t, v)]
+
+
 # ------------------------------------------------------------------ model --
 
 class Model:
@@ -380,6 +393,13 @@ class Model:
         out = np.empty(self.desc.vocab_size if n is None else n, np.float32)
         check(lib().tlm_read_logits(self.ptr, _ptr(out), out.size))
         return out
+
+    def read_candidates(self, k: int, softcap: float = 0.0):
+        """readCandidates: the k best (token, score) of the last logits, best first."""
+        t = np.zeros(k, np.int32)
+        v = np.zeros(k, np.float32)
+        check(lib().tlm_read_candidates(self.ptr, int(k), float(softcap), _ptr(t), _ptr(v)))
+        return [(int(a), float(b)) for a, b in zip(t, v)]
 
     def read_hidden(self) -> np.ndarray:
         out = np.empty(self.desc.hidden_size, np.float32)
