@@ -87,6 +87,16 @@ class DecoderHIPRunner:
         self._cacheTokens: Optional[List[int]] = None
         self._cacheLogits: Optional[np.ndarray] = None
 
+    @classmethod
+    def from_checkpoint(cls, path: str, options: Optional[dict] = None, ctx: Optional[tlm.Context] = None,
+                        storage=None, tokenizer=None) -> "DecoderHIPRunner":
+        """createTSLRunner(url) for a local Hugging Face directory (config.json +
+        safetensors shards; factory.ts:29-43, HFModelBundle.ts:106-135): linears
+        packed to q4 g32 at upload unless `storage` says otherwise."""
+        from . import checkpoint
+        hw, _ = checkpoint.load_checkpoint(path, storage)
+        return cls(hw, options, ctx=ctx, tokenizer=tokenizer)
+
     # ---- GenerateAsyncControls (generate.ts:31-49) ----
     def computeToken(self, tokenId: int, position: int, computeLogits: bool = True, sampleCandidateCount: int = 0):
         """DecoderTSLRunner.computeToken (:487-502): enqueue, do not wait."""
