@@ -212,3 +212,21 @@ def test_bf16_checkpoint_packed_to_q4_on_gpu(tmp_path):
     close(runner.readLogits(), om.forward(prompt[-1], len(prompt) - 1), 2e-2, 1e-2)
     runner.close()
     om.close()
+    # with a tokenizer beside the weights: text in, text out (generate.ts:210-305)
+    tk = pytest.importorskip("tokenizers")
+    from tokenizers import Tokenizer, models, pre_tokenizers, trainers
+    hf = Tokenizer(models.BPE())
+    hf.pre_tokenizer = pre_tokenizers.ByteLevel(add_prefix_space=False, use_regex=True)
+    hf.train_from_iterator(["Once upon a time there was a little robot named Bolt. " * 20],
+                           trainers.BpeTrainer(vocab_size=400, special_tokens=["<|endoftext|>"],
+                                               initial_alphabet=pre_tokenizers.ByteLevel.alphabet(),
+                                               show_progress=False))
+    hf.model.save(str(tmp_path))
+    runner = R.DecoderHIPRunner.from_checkpoint(str(tmp_path), {"maxTokens": 256})
+    prompt_text = "Once upon a time there was a little robot"
+    ids = runner.weights.tokenizer.encode(prompt_text)
+    assert ids == hf.encode(prompt_text).ids
+    res = runner.generate(prompt_text, {"temperature": 0, "maxNewTokens": 12})
+    assert res["tokens"][:len(ids)] == ids and res["promptTokens"] == len(ids)
+    assert len(res["generatedTokens"]) == 12 and res["text"].startswith(prompt_text)
+    runner.close()

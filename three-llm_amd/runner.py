@@ -91,10 +91,15 @@ class DecoderHIPRunner:
     def from_checkpoint(cls, path: str, options: Optional[dict] = None, ctx: Optional[tlm.Context] = None,
                         storage=None, tokenizer=None) -> "DecoderHIPRunner":
         """createTSLRunner(url) for a local Hugging Face directory (config.json +
-        safetensors shards; factory.ts:29-43, HFModelBundle.ts:106-135): linears
-        packed to q4 g32 at upload unless `storage` says otherwise."""
-        from . import checkpoint
-        hw, _ = checkpoint.load_checkpoint(path, storage)
+        safetensors shards, and the tokenizer when vocab.json / tokenizer.json
+        is there; factory.ts:29-43, HFModelBundle.ts:106-135): linears packed
+        to q4 g32 at upload unless `storage` says otherwise."""
+        import os
+        from . import checkpoint, tokenizer as tk
+        hw, config = checkpoint.load_checkpoint(path, storage)
+        if tokenizer is None and any(os.path.isfile(os.path.join(path, f))
+                                     for f in ("vocab.json", "tokenizer.json")):
+            tokenizer = tk.load_tokenizer(path, config, list(hw.recipe.stop_token_ids))
         return cls(hw, options, ctx=ctx, tokenizer=tokenizer)
 
     # ---- GenerateAsyncControls (generate.ts:31-49) ----
