@@ -183,6 +183,7 @@ struct GemmArgs {
 // host sizes the slice buffers from the same numbers the launch uses).
 struct GemmShape {
   int ring;  // 1: the q4 LDS-ring kernel (wn waves over 64 wn columns, 32 mt rows)
+  int kw;    // 1 (with ring): four waves split K on one 64-column tile
   int wn;
   int mt, nb, gx, gy, spc, splits;
 };

@@ -258,6 +258,17 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 // bounds the loads still in flight.  Columns: for the paired gate|up layout
 // a wave's two 32-column groups are the gate rows and the matching up rows.
 constexpr int kRing = 4;
+// Ring depth: four-wave blocks take a step every ~16 MFMA slots of each of
+// their waves; a one-wave block (small grids) is alone on its CU, finishes a
+// step sooner and needs more steps in flight to cover the memory latency
+// (the in-flight copies stay below vmcnt's limit of 63).
+template <int WN>
+constexpr int ring_depth() { return WN == 1 ? 6 : kRing; }
+
+// s_waitcnt immediate that waits until at most n vector-memory operations are
+// outstanding (n < 64) and leaves the other counters alone: vmcnt bits 3:0 in
+// simm16 bits 3:0 and bits 5:4 in simm16 bits 15:14 (gfx9 encoding).
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) & 3) << 14 | 0x70 | 0xF00; }
 
 // Slot (16 bytes) of piece q of A row r in a stage: piece q ^ f(r), where
 // f(r) = ((r1 ^ r3), r2) makes the 16-byte reads of 8 consecutive rows (32
@@ -286,6 +297,8 @@ struct RingLayout {
   static constexpr int S_BYTES = WN * 128 > 256 ? WN * 128 : 256;
   static constexpr int W_OFF = BM * 64, S_OFF = W_OFF + WN * 1024, STAGE = S_OFF + S_BYTES;
   static constexpr int LPS = AW + 2;            // copies per wave per stage: A, one weight tile, scales
+  static constexpr int NR = ring_depth<WN>();
+  static_assert((NR - 1) * LPS <= 63, "copies in flight within vmcnt's range");
 };
 
 // One block's state: loop-invariant byte offsets of its copies and reads, the
@@ -321,12 +334,13 @@ struct RingBlock {
 
   template <int S>
   __device__ __forceinline__ void step(const unsigned char* lds, int refill_c) {
-    // this wave's copies of the step are done when at most the kRing - 2 later
+    // this wave's copies of the step are done when at most the NR - 2 later
     // stages' copies are in flight; the barrier then covers every wave's
     // copies, and every wave's reads of the stage refilled below
-    __builtin_amdgcn_s_waitcnt(0x3F70 | ((kRing - 2) * RL::LPS));
+    constexpr int NR = RL::NR;
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm((NR - 2) * RL::LPS));
     asm volatile("s_barrier" ::: "memory");
-    issue((S + kRing - 1) % kRing, refill_c);
+    issue((S + NR - 1) % NR, refill_c);
     const unsigned char* sb = lds + S * RL::STAGE;
     half8_t b[2][2];
 #pragma unroll
@@ -350,10 +364,31 @@ struct RingBlock {
   }
 };
 
+// Steps S..E-1 of one pass over the ring, each with its stage a constant:
+// full() refills each stage with the step NR - 1 ahead, tail() runs the steps
+// left after the last full pass (their stages already hold them).
+template <int MT, int WN, int S, int E>
+struct RingSteps {
+  static __device__ __forceinline__ void full(RingBlock<MT, WN>& rb, const unsigned char* lds, int i, int n) {
+    rb.template step<S>(lds, min(i + S + RingLayout<MT, WN>::NR - 1, n - 1));
+    RingSteps<MT, WN, S + 1, E>::full(rb, lds, i, n);
+  }
+  static __device__ __forceinline__ void tail(RingBlock<MT, WN>& rb, const unsigned char* lds, int i, int n) {
+    if (i + S < n) rb.template step<S>(lds, n - 1);
+    RingSteps<MT, WN, S + 1, E>::tail(rb, lds, i, n);
+  }
+};
+template <int MT, int WN, int E>
+struct RingSteps<MT, WN, E, E> {
+  static __device__ __forceinline__ void full(RingBlock<MT, WN>&, const unsigned char*, int, int) {}
+  static __device__ __forceinline__ void tail(RingBlock<MT, WN>&, const unsigned char*, int, int) {}
+};
+
 template <int MT, int WN, int EPI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_q4_ring_kernel(GemmArgs g) {
   using RL = RingLayout<MT, WN>;
-  __shared__ __align__(16) unsigned char lds[kRing * RL::STAGE];
+  constexpr int NR = RL::NR;
+  __shared__ __align__(16) unsigned char lds[NR * RL::STAGE];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, kh = lane >> 5;
   const int m0 = blockIdx.y * RL::BM, t0 = blockIdx.x * WN, T = (g.N + kTile - 1) / kTile;
@@ -391,20 +426,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   for (int i = 0; i < MT; i++) rb.acc[i][0] = rb.acc[i][1] = (float16_t){};
 
   // steps are relative to c0 from here on
-  rb.issue(0, 0);
-  rb.issue(1, min(1, n - 1));
-  rb.issue(2, min(2, n - 1));
+#pragma unroll
+  for (int st = 0; st < NR - 1; st++) rb.issue(st, min(st, n - 1));
   int i = 0;
-  for (; i + kRing <= n; i += kRing) {
-    rb.template step<0>(lds, min(i + 3, n - 1));
-    rb.template step<1>(lds, min(i + 4, n - 1));
-    rb.template step<2>(lds, min(i + 5, n - 1));
-    rb.template step<3>(lds, min(i + 6, n - 1));
-  }
-  if (i < n) rb.template step<0>(lds, n - 1);
-  if (i + 1 < n) rb.template step<1>(lds, n - 1);
-  if (i + 2 < n) rb.template step<2>(lds, n - 1);
-  __builtin_amdgcn_s_waitcnt(0x3F70);  // the clamped trailing copies land before the block exits
+  for (; i + NR <= n; i += NR) RingSteps<MT, WN, 0, NR>::full(rb, lds, i, n);
+  RingSteps<MT, WN, 0, NR - 1>::tail(rb, lds, i, n);
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // the clamped trailing copies land before the block exits
 
   const int cg0 = (t0 + wave) * kTile;
   const int rbase = m0 + 4 * kh;
@@ -440,9 +467,207 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   }
 }
 
+// ------------------------------------------------ q4 GEMM, waves split K --
+// For grids too small to fill the CUs (short prompts): a block's 4 waves take
+// the same 64 columns and 32 MT rows and split the block's K range in four.
+// Each wave streams its own operands through a private LDS ring (global ->
+// LDS copies as above, no block barrier in the loop); at the end waves 1..3
+// hand their accumulators to wave 0 through LDS, which adds them in wave
+// order (deterministic) and runs the epilogue.  Same epilogues as above.
+__device__ __forceinline__ float f4_at(const float4& v, int e) {
+  return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+}
+
+template <int MT>
+struct KwLayout {
+  static constexpr int NR = 4;                           // ring stages per wave
+  static constexpr int NA = 2 * MT;                      // 1 KiB A copies per stage
+  static constexpr int W_OFF = MT * 2048, S_OFF = W_OFF + 1024, STAGE = S_OFF + 256;
+  static constexpr int WAVE_BYTES = NR * STAGE;          // one wave's ring
+  static constexpr int LPS = NA + 2;                     // copies per stage
+  static constexpr int ACC_FLOATS = MT * 2 * 16 * 64;    // one wave's accumulators
+  static_assert(4 * ACC_FLOATS * 4 <= 4 * WAVE_BYTES, "accumulator handoff fits in the rings");
+  static_assert((NR - 1) * LPS <= 63, "copies in flight within vmcnt's range");
+};
+
+template <int MT>
+struct KwWave {
+  using KL = KwLayout<MT>;
+  const char* abase;
+  const char* wbase;
+  const char* sbase;
+  uint32_t agoff[KL::NA];
+  uint32_t wgoff, sgoff, lbase;
+  int rd_a1[MT], rd_a2[MT], rd_w[2], rd_s[2];
+  float16_t acc[MT][2];
+
+  __device__ __forceinline__ void issue(int stage, int c) {
+    const uint32_t sb = lbase + stage * KL::STAGE;
+    const char* ab = abase + (size_t)c * 64;
+#pragma unroll
+    for (int u = 0; u < KL::NA; u++) lds_dma16(ab, agoff[u], __builtin_amdgcn_readfirstlane(sb + u * 1024));
+    lds_dma16(wbase + (size_t)c * kTile * 16, wgoff, __builtin_amdgcn_readfirstlane(sb + KL::W_OFF));
+    lds_dma4(sbase + (size_t)c * kTile * 2, sgoff, __builtin_amdgcn_readfirstlane(sb + KL::S_OFF));
+  }
+
+  template <int S>
+  __device__ __forceinline__ void step(const unsigned char* mine, int refill_c) {
+    // this wave's copies of the step have landed when at most NR - 2 later
+    // stages are in flight; the stage refilled below was last read by this
+    // wave in its previous step
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm((KL::NR - 2) * KL::LPS));
+    asm volatile("" ::: "memory");
+    issue((S + KL::NR - 1) % KL::NR, refill_c);
+    const unsigned char* sb = mine + S * KL::STAGE;
+    half8_t b[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const uint2 wv = *reinterpret_cast<const uint2*>(sb + rd_w[j]);
+      const _Float16 sc = *reinterpret_cast<const _Float16*>(sb + rd_s[j]);
+      const half2_t s2 = {sc, sc};
+      b[j][0] = dequant8(wv.x, s2);
+      b[j][1] = dequant8(wv.y, s2);
+    }
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+      const half8_t a1 = *reinterpret_cast<const half8_t*>(sb + rd_a1[t]);
+      const half8_t a2 = *reinterpret_cast<const half8_t*>(sb + rd_a2[t]);
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b[j][0], acc[t][j], 0, 0, 0);
+        acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, b[j][1], acc[t][j], 0, 0, 0);
+      }
+    }
+  }
+};
+
+template <int MT, int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_q4_kw_kernel(GemmArgs g) {
+  using KL = KwLayout<MT>;
+  __shared__ __align__(16) unsigned char lds[4 * KL::WAVE_BYTES];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l32 = lane & 31, kh = lane >> 5;
+  const int m0 = blockIdx.y * 32 * MT, t0 = blockIdx.x, T = (g.N + kTile - 1) / kTile;
+  const int cb = blockIdx.z * g.spc, nb = min(g.spc, g.K / 32 - cb);
+  const int q = (nb + 3) / 4, c0 = cb + wave * q, n = max(0, min(q, nb - wave * q));
+  const unsigned char* mine = lds + wave * KL::WAVE_BYTES;
+
+  KwWave<MT> kw;
+  kw.lbase = (uint32_t)(uintptr_t)mine;
+  kw.abase = reinterpret_cast<const char*>(g.A) + (size_t)c0 * 64;
+  kw.wbase = reinterpret_cast<const char*>(g.w) + (size_t)c0 * kTile * 16;
+  kw.sbase = reinterpret_cast<const char*>(g.s) + (size_t)c0 * kTile * 2;
+#pragma unroll
+  for (int u = 0; u < KL::NA; u++) {
+    const int sl = u * 64 + lane, r = sl >> 2;
+    kw.agoff[u] = (uint32_t)(((size_t)min(m0 + r, g.M - 1) * g.lda + 8 * ((sl & 3) ^ a_swz(r))) * 2);
+  }
+  kw.wgoff = (uint32_t)(((size_t)min(t0, T - 1) * g.C * kTile + lane) * 16);
+  kw.sgoff = (uint32_t)(((size_t)min(t0 + (lane >> 5), T - 1) * g.C * kTile + 2 * (lane & 31)) * 2);
+#pragma unroll
+  for (int t = 0; t < MT; t++) {
+    kw.rd_a1[t] = a_slot(32 * t + l32, 2 * kh) * 16;
+    kw.rd_a2[t] = a_slot(32 * t + l32, 2 * kh + 1) * 16;
+  }
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    kw.rd_w[j] = KL::W_OFF + (32 * j + l32) * 16 + 8 * kh;
+    kw.rd_s[j] = KL::S_OFF + (32 * j + l32) * 2;
+  }
+#pragma unroll
+  for (int i = 0; i < MT; i++) kw.acc[i][0] = kw.acc[i][1] = (float16_t){};
+  if (n > 0) {  // steps relative to c0
+    kw.issue(0, 0);
+    kw.issue(1, min(1, n - 1));
+    kw.issue(2, min(2, n - 1));
+    int i = 0;
+    for (; i + 4 <= n; i += 4) {
+      kw.template step<0>(mine, min(i + 3, n - 1));
+      kw.template step<1>(mine, min(i + 4, n - 1));
+      kw.template step<2>(mine, min(i + 5, n - 1));
+      kw.template step<3>(mine, min(i + 6, n - 1));
+    }
+    if (i < n) kw.template step<0>(mine, n - 1);
+    if (i + 1 < n) kw.template step<1>(mine, n - 1);
+    if (i + 2 < n) kw.template step<2>(mine, n - 1);
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // every copy of this wave has landed
+  __syncthreads();                           // every wave is done with its ring
+  // Handoff: every wave puts its accumulators in LDS; wave w then owns
+  // registers 4w..4w+3 of every tile (rows 8w..8w+7 of each 32-row band),
+  // adds the four waves' values in wave order and runs the epilogue for them.
+  float4* xch = reinterpret_cast<float4*>(lds);
+  constexpr int Q = MT * 2 * 4;  // float4 per lane per wave
+#pragma unroll
+  for (int t = 0; t < MT; t++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        xch[(wave * Q + (t * 2 + j) * 4 + q) * 64 + lane] =
+            make_float4(kw.acc[t][j][4 * q], kw.acc[t][j][4 * q + 1], kw.acc[t][j][4 * q + 2], kw.acc[t][j][4 * q + 3]);
+  __syncthreads();
+  float4 r[MT][2];
+#pragma unroll
+  for (int t = 0; t < MT; t++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      float4 v = xch[((t * 2 + j) * 4 + wave) * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < 4; w++) {
+        const float4 u = xch[(w * Q + (t * 2 + j) * 4 + wave) * 64 + lane];
+        v.x += u.x; v.y += u.y; v.z += u.z; v.w += u.w;
+      }
+      r[t][j] = v;
+    }
+
+  const int rbase = m0 + 4 * kh + 8 * wave;
+  if (EPI == GEMM_SWIGLU) {
+    const int oi = t0 * 32 + l32;
+    if (oi >= g.n_out) return;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int row = rbase + 32 * t + e;
+        if (row < g.M) {
+          const float gt = f4_at(r[t][0], e), up = f4_at(r[t][1], e);
+          const _Float16 hv = (_Float16)(gt / (1.f + __expf(-gt)) * up);
+          g.Ch[(size_t)row * g.ldc + oi] = __builtin_bit_cast(uint16_t, hv);
+        }
+      }
+    return;
+  }
+  float* out = g.Cf + (EPI == GEMM_PART ? (size_t)blockIdx.z * g.M * g.ldc : 0);
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int col = t0 * kTile + 32 * j + l32;
+    if (col >= g.N) continue;
+    const float bias = (EPI == GEMM_STORE && g.bias) ? g.bias[col] : 0.f;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int row = rbase + 32 * t + e;
+        if (row < g.M) out[(size_t)row * g.ldc + col] = f4_at(r[t][j], e) + bias;
+      }
+  }
+}
+
 // TLM_GEMM_RING=0 selects the register-prefetch kernel for q4 too (comparisons)
 static const bool g_use_ring = [] {
   const char* e = getenv("TLM_GEMM_RING");
+  return !(e && e[0] == '0');
+}();
+// TLM_GEMM_SPLIT_WAVES=n: split K until the grid holds n waves per CU (default 8)
+static const int g_split_waves = [] {
+  const char* e = getenv("TLM_GEMM_SPLIT_WAVES");
+  const int v = e ? atoi(e) : 0;
+  return v > 0 && v <= 64 ? v : 8;
+}();
+// TLM_GEMM_KW=0 keeps one-wave blocks for small grids (comparisons)
+static const bool g_use_kw = [] {
+  const char* e = getenv("TLM_GEMM_KW");
   return !(e && e[0] == '0');
 }();
 
@@ -450,14 +675,25 @@ GemmShape gemm_shape(int fmt, int epi, int M, int N, int K, int cus) {
   GemmShape s;
   s.ring = fmt == WF_Q4 && g_use_ring;
   s.wn = 1;
+  s.kw = 0;
   const int steps = K >= 32 ? K / 32 : 1;  // K % 32 != 0 is rejected by launch_gemm
-  if (s.ring) {  // waves side by side over 64 wn columns, 32 mt rows
+  int min_steps = 4;                       // 32-k steps per wave, at least
+  int kdiv = 1;                            // waves sharing one block's K range
+  if (s.ring) {
     s.mt = M > 64 ? 4 : M > 32 ? 2 : 1;
     s.nb = 2;
     s.gy = (M + 32 * s.mt - 1) / (32 * s.mt);
-    // four-wave blocks share the A stage; grids too small to fill the CUs use one-wave blocks
-    s.wn = ((N + 255) / 256) * s.gy >= cus / 2 ? 4 : 1;
-    s.gx = (N + 64 * s.wn - 1) / (64 * s.wn);
+    if (((N + 255) / 256) * s.gy >= cus / 2) {  // four waves side by side over 256 columns
+      s.wn = 4;
+      s.gx = (N + 255) / 256;
+    } else if (g_use_kw) {  // too few tiles to fill the CUs: four waves split K on one tile
+      s.kw = 1;
+      s.gx = (N + kTile - 1) / kTile;
+      kdiv = 4;
+      min_steps = 2;
+    } else {
+      s.gx = (N + kTile - 1) / kTile;
+    }
   } else {
     s.mt = M > 64 ? 2 : 1;
     s.nb = (epi == GEMM_SWIGLU || N > 64) ? 2 : 1;
@@ -466,10 +702,10 @@ GemmShape gemm_shape(int fmt, int epi, int M, int N, int K, int cus) {
     s.wn = 4;
   }
   int splits = 1;
-  if (epi == GEMM_PART) {  // split K until the grid holds about 8 waves per CU, at least 4 steps per split
-    const int target = 8 * cus;
-    const int waves = s.gx * s.gy * (s.ring ? s.wn : 4);
-    while (splits < 32 && waves * splits < target && steps / (2 * splits) >= 4) splits *= 2;
+  if (epi == GEMM_PART) {  // split K until the grid holds about 8 waves per CU
+    const int target = g_split_waves * cus;
+    const int waves = s.gx * s.gy * (s.ring ? (s.kw ? 4 : s.wn) : 4);
+    while (splits < 32 && waves * splits < target && steps / (2 * splits * kdiv) >= min_steps) splits *= 2;
   }
   s.spc = (steps + splits - 1) / splits;
   s.splits = (steps + s.spc - 1) / s.spc;
@@ -484,6 +720,19 @@ bool launch_gemm(int fmt, int epi, const GemmShape& sh, const GemmArgs& ga, hipS
   g.spc = sh.spc;
   const dim3 grid(sh.gx, sh.gy, sh.splits);
   const int mt = sh.mt, nb = sh.nb;
+  if (sh.ring && sh.kw) {
+    if (fmt != WF_Q4) return false;
+#define KW_CASE(MTV, E)                                                                          \
+  if (mt == MTV && epi == E) {                                                                   \
+    hipLaunchKernelGGL((gemm_q4_kw_kernel<MTV, E>), grid, dim3(256), 0, st, g);                  \
+    return true;                                                                                 \
+  }
+#define KW_EPIS(MTV) KW_CASE(MTV, GEMM_STORE) KW_CASE(MTV, GEMM_PART) KW_CASE(MTV, GEMM_SWIGLU)
+    KW_EPIS(1) KW_EPIS(2) KW_EPIS(4)
+#undef KW_EPIS
+#undef KW_CASE
+    return false;
+  }
   if (sh.ring) {
     if (fmt != WF_Q4) return false;
 #define RING_CASE(MTV, WNV, E)                                                                   \
@@ -602,29 +851,33 @@ __device__ __forceinline__ void rope_store(const RopeKvArgs& a, int m, int pos, 
     static_cast<__half*>(cache)[dst] = __float2half(y);
 }
 
+// One thread per element of the fused q|k|v row (grid: rows x 256-element
+// chunks), so every load of a thread is issued at once; the first element of
+// a rotated pair writes both.
 __global__ __launch_bounds__(256) void rope_kv_kernel(RopeKvArgs a) {
   const int m = blockIdx.x, pos = a.p0 + m, D = a.D;
   const int nq = a.Hq * D, nk = a.Hkv * D, half = a.rd / 2;
   const int width = nq + 2 * nk;
+  const int i = blockIdx.y * 256 + threadIdx.x;
+  if (i >= width) return;
   const float* row = a.qkv + (size_t)m * width;
-  for (int i = threadIdx.x; i < width; i += 256) {
-    const int d = i % D;
-    const bool rot = i < nq + nk && d < a.rd;
-    if (rot && d >= half) continue;  // the pair's first thread writes both
-    const float x = fold_slices(row, a.bias, a.n_part, a.pstride, i);
-    if (!rot) {
-      rope_store(a, m, pos, i, x);
-      continue;
-    }
-    const float x2 = fold_slices(row, a.bias, a.n_part, a.pstride, i + half);
-    const float c = a.rope_cos[(size_t)pos * half + d], sn = a.rope_sin[(size_t)pos * half + d];
-    rope_store(a, m, pos, i, x * c - x2 * sn);
-    rope_store(a, m, pos, i + half, x2 * c + x * sn);
+  const int d = i % D;
+  const bool rot = i < nq + nk && d < a.rd;
+  if (rot && d >= half) return;  // the pair's first thread writes both
+  const float x = fold_slices(row, a.bias, a.n_part, a.pstride, i);
+  if (!rot) {
+    rope_store(a, m, pos, i, x);
+    return;
   }
+  const float x2 = fold_slices(row, a.bias, a.n_part, a.pstride, i + half);
+  const float c = a.rope_cos[(size_t)pos * half + d], sn = a.rope_sin[(size_t)pos * half + d];
+  rope_store(a, m, pos, i, x * c - x2 * sn);
+  rope_store(a, m, pos, i + half, x2 * c + x * sn);
 }
 
 void launch_rope_kv(const RopeKvArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(rope_kv_kernel, dim3(a.M), dim3(256), 0, st, a);
+  const int width = (a.Hq + 2 * a.Hkv) * a.D;
+  hipLaunchKernelGGL(rope_kv_kernel, dim3(a.M, (width + 255) / 256), dim3(256), 0, st, a);
 }
 
 // ------------------------------------------------------- flash attention --
