@@ -51,6 +51,7 @@ def make_linear(ctx, fmt, w):
     (tlm.FMT_Q4, 1, 1152, 896), (tlm.FMT_Q4, 37, 1152, 896), (tlm.FMT_Q4, 64, 896, 896),
     (tlm.FMT_Q4, 127, 1152, 896), (tlm.FMT_Q4, 200, 896, 4864), (tlm.FMT_Q4, 65, 200, 96),
     (tlm.FMT_Q4, 300, 2048, 2048), (tlm.FMT_Q4, 33, 64, 32),
+    (tlm.FMT_Q4, 300, 44032, 64),  # 172 x 3 blocks of 256 columns, ragged last block
     (tlm.FMT_F16, 70, 256, 64), (tlm.FMT_F16, 5, 37, 32), (tlm.FMT_F16, 130, 512, 256)])
 def test_linear_rows_matches_fp16_operand_product(ctx, fmt, M, N, K):
     """Each row equals bias + W x with x and W rounded to fp16 (the device's

@@ -258,17 +258,21 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 // bounds the loads still in flight.  Columns: for the paired gate|up layout
 // a wave's two 32-column groups are the gate rows and the matching up rows.
 constexpr int kRing = 4;
-// Ring depth: four-wave blocks take a step every ~16 MFMA slots of each of
-// their waves; a one-wave block (small grids) is alone on its CU, finishes a
-// step sooner and needs more steps in flight to cover the memory latency
+// Ring depth (even: the operands of consecutive steps alternate between two
+// register sets): four-wave blocks take a step every ~16 MFMA slots of each
+// of their waves; a one-wave block (small grids) is alone on its CU, finishes
+// a step sooner and needs more steps in flight to cover the memory latency
 // (the in-flight copies stay below vmcnt's limit of 63).
 template <int WN>
 constexpr int ring_depth() { return WN == 1 ? 6 : kRing; }
+static_assert(kRing % 2 == 0, "even ring depth");
 
 // s_waitcnt immediate that waits until at most n vector-memory operations are
 // outstanding (n < 64) and leaves the other counters alone: vmcnt bits 3:0 in
 // simm16 bits 3:0 and bits 5:4 in simm16 bits 15:14 (gfx9 encoding).
 constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) & 3) << 14 | 0x70 | 0xF00; }
+// the same with lgkmcnt(0): this wave's LDS reads are complete as well
+constexpr int waitcnt_vm_lgkm0(int n) { return (n & 15) | ((n >> 4) & 3) << 14 | 0x70; }
 
 // Slot (16 bytes) of piece q of A row r in a stage: piece q ^ f(r), where
 // f(r) = ((r1 ^ r3), r2) makes the 16-byte reads of 8 consecutive rows (32
@@ -332,60 +336,119 @@ struct RingBlock {
     lds_dma4(sbs, sgoff, __builtin_amdgcn_readfirstlane(sb + slds));
   }
 
-  template <int S>
-  __device__ __forceinline__ void step(const unsigned char* lds, int refill_c) {
-    // this wave's copies of the step are done when at most the NR - 2 later
-    // stages' copies are in flight; the barrier then covers every wave's
-    // copies, and every wave's reads of the stage refilled below
-    constexpr int NR = RL::NR;
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm((NR - 2) * RL::LPS));
-    asm volatile("s_barrier" ::: "memory");
-    issue((S + NR - 1) % NR, refill_c);
-    const unsigned char* sb = lds + S * RL::STAGE;
+  // One step's MFMA operands: the A pieces as read from LDS and the weights
+  // of the lane's two 32-column groups dequantised to fp16.
+  struct Ops {
+    half8_t a1[MT], a2[MT];
     half8_t b[2][2];
+  };
+
+  template <int S>
+  __device__ __forceinline__ void read_w(const unsigned char* lds, uint2 (&w)[2], _Float16 (&sc)[2]) const {
+    const unsigned char* sb = lds + S * RL::STAGE;
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-      const uint2 wv = *reinterpret_cast<const uint2*>(sb + rd_w[j]);
-      const _Float16 sc = *reinterpret_cast<const _Float16*>(sb + rd_s[j]);
-      const half2_t s2 = {sc, sc};
-      b[j][0] = dequant8(wv.x, s2);
-      b[j][1] = dequant8(wv.y, s2);
+      w[j] = *reinterpret_cast<const uint2*>(sb + rd_w[j]);
+      sc[j] = *reinterpret_cast<const _Float16*>(sb + rd_s[j]);
     }
+  }
+  template <int S>
+  __device__ __forceinline__ void read_a(const unsigned char* lds, Ops& o) const {
+    const unsigned char* sb = lds + S * RL::STAGE;
 #pragma unroll
     for (int t = 0; t < MT; t++) {
-      const half8_t a1 = *reinterpret_cast<const half8_t*>(sb + rd_a1[t]);
-      const half8_t a2 = *reinterpret_cast<const half8_t*>(sb + rd_a2[t]);
+      o.a1[t] = *reinterpret_cast<const half8_t*>(sb + rd_a1[t]);
+      o.a2[t] = *reinterpret_cast<const half8_t*>(sb + rd_a2[t]);
+    }
+  }
+  static __device__ __forceinline__ void dequant(const uint2 (&w)[2], const _Float16 (&sc)[2], Ops& o) {
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const half2_t s2 = {sc[j], sc[j]};
+      o.b[j][0] = dequant8(w[j].x, s2);
+      o.b[j][1] = dequant8(w[j].y, s2);
+    }
+  }
+  template <int S>
+  __device__ __forceinline__ void read(const unsigned char* lds, Ops& o) const {
+    uint2 w[2];
+    _Float16 sc[2];
+    read_w<S>(lds, w, sc);
+    read_a<S>(lds, o);
+    dequant(w, sc, o);
+  }
+
+  // Step i in stage S; `cur` holds its operands, read and dequantised during
+  // step i - 1.  Wait until this wave's copies of step i + 1 have landed (at
+  // most NR - 3 later stages in flight) and its LDS reads are complete; after
+  // the barrier every wave's copies of step i + 1 have landed and every
+  // wave's reads of stage i - 1 (made in step i - 2) are complete.  Then read
+  // step i + 1, refill stage i - 1 with step i + NR - 1, and run step i's
+  // MFMAs with the dequantisation of step i + 1 in their shadow (both waves
+  // of a SIMD pass the barrier together, so VALU work left outside the MFMAs
+  // would serialise with them).
+  template <int S>
+  __device__ __forceinline__ void step(const unsigned char* lds, int refill_c, const Ops& cur, Ops& nxt) {
+    constexpr int NR = RL::NR;
+    __builtin_amdgcn_sched_barrier(0);  // the previous step's MFMAs stay before this barrier
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0((NR - 3) * RL::LPS));
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);  // keep each step's MFMAs after its own barrier
+    uint2 w[2];
+    _Float16 sc[2];
+    read_w<(S + 1) % NR>(lds, w, sc);
+    read_a<(S + 1) % NR>(lds, nxt);
+    issue((S + NR - 1) % NR, refill_c);
+    __builtin_amdgcn_sched_barrier(0);  // the reads and copies go out before the MFMAs
+#pragma unroll
+    for (int t = 0; t < MT; t++)
 #pragma unroll
       for (int j = 0; j < 2; j++) {
-        acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b[j][0], acc[t][j], 0, 0, 0);
-        acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, b[j][1], acc[t][j], 0, 0, 0);
+        acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.a1[t], cur.b[j][0], acc[t][j], 0, 0, 0);
+        acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.a2[t], cur.b[j][1], acc[t][j], 0, 0, 0);
       }
-    }
+    dequant(w, sc, nxt);
+    // order: a few MFMAs while the weight reads land, then one MFMA per
+    // slice of the dequantisation
+    __builtin_amdgcn_sched_group_barrier(0x008, MT, 0);
+#define RING_MV __builtin_amdgcn_sched_group_barrier(0x002, 8, 0); __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    RING_MV RING_MV RING_MV RING_MV RING_MV RING_MV RING_MV RING_MV RING_MV RING_MV
+#undef RING_MV
   }
 };
 
 // Steps S..E-1 of one pass over the ring, each with its stage a constant:
 // full() refills each stage with the step NR - 1 ahead, tail() runs the steps
-// left after the last full pass (their stages already hold them).
+// left after the last full pass (their stages already hold them).  Even steps
+// take their operands from o0 and read the next step's into o1, odd steps
+// the other way round.
 template <int MT, int WN, int S, int E>
 struct RingSteps {
-  static __device__ __forceinline__ void full(RingBlock<MT, WN>& rb, const unsigned char* lds, int i, int n) {
-    rb.template step<S>(lds, min(i + S + RingLayout<MT, WN>::NR - 1, n - 1));
-    RingSteps<MT, WN, S + 1, E>::full(rb, lds, i, n);
+  using RB = RingBlock<MT, WN>;
+  using Ops = typename RB::Ops;
+  static __device__ __forceinline__ void full(RB& rb, const unsigned char* lds, int i, int n, Ops& o0, Ops& o1) {
+    const int c = min(i + S + RingLayout<MT, WN>::NR - 1, n - 1);
+    if constexpr (S % 2 == 0) rb.template step<S>(lds, c, o0, o1);
+    else rb.template step<S>(lds, c, o1, o0);
+    RingSteps<MT, WN, S + 1, E>::full(rb, lds, i, n, o0, o1);
   }
-  static __device__ __forceinline__ void tail(RingBlock<MT, WN>& rb, const unsigned char* lds, int i, int n) {
-    if (i + S < n) rb.template step<S>(lds, n - 1);
-    RingSteps<MT, WN, S + 1, E>::tail(rb, lds, i, n);
+  static __device__ __forceinline__ void tail(RB& rb, const unsigned char* lds, int i, int n, Ops& o0, Ops& o1) {
+    if (i + S < n) {
+      if constexpr (S % 2 == 0) rb.template step<S>(lds, n - 1, o0, o1);
+      else rb.template step<S>(lds, n - 1, o1, o0);
+    }
+    RingSteps<MT, WN, S + 1, E>::tail(rb, lds, i, n, o0, o1);
   }
 };
 template <int MT, int WN, int E>
 struct RingSteps<MT, WN, E, E> {
-  static __device__ __forceinline__ void full(RingBlock<MT, WN>&, const unsigned char*, int, int) {}
-  static __device__ __forceinline__ void tail(RingBlock<MT, WN>&, const unsigned char*, int, int) {}
+  using Ops = typename RingBlock<MT, WN>::Ops;
+  static __device__ __forceinline__ void full(RingBlock<MT, WN>&, const unsigned char*, int, int, Ops&, Ops&) {}
+  static __device__ __forceinline__ void tail(RingBlock<MT, WN>&, const unsigned char*, int, int, Ops&, Ops&) {}
 };
 
 template <int MT, int WN, int EPI>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_q4_ring_kernel(GemmArgs g) {
+__global__ __launch_bounds__(64 * WN) __attribute__((amdgpu_waves_per_eu(2))) void gemm_q4_ring_kernel(GemmArgs g) {
   using RL = RingLayout<MT, WN>;
   constexpr int NR = RL::NR;
   __shared__ __align__(16) unsigned char lds[NR * RL::STAGE];
@@ -406,7 +469,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     rb.alds[u] = ai * 1024;
   }
   rb.wgoff = (uint32_t)(((size_t)min(t0 + wave, T - 1) * g.C * kTile + lane) * 16);
-  const int sidx = WN == 4 ? (wave & 1) : 0;  // one scale copy covers two tiles
+  const int sidx = WN >= 4 ? wave % (WN / 2) : 0;  // one scale copy covers two tiles
   rb.sgoff = (uint32_t)(((size_t)min(t0 + 2 * sidx + (lane >> 5), T - 1) * g.C * kTile + 2 * (lane & 31)) * 2);
   rb.wlds = RL::W_OFF + wave * 1024;
   rb.slds = RL::S_OFF + sidx * 256;
@@ -428,9 +491,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   // steps are relative to c0 from here on
 #pragma unroll
   for (int st = 0; st < NR - 1; st++) rb.issue(st, min(st, n - 1));
+  typename RingBlock<MT, WN>::Ops o0, o1;
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm((NR - 2) * RL::LPS));  // step 0 has landed (this wave's copies)
+  asm volatile("s_barrier" ::: "memory");                        // ... and every wave's
+  rb.template read<0>(lds, o0);
   int i = 0;
-  for (; i + NR <= n; i += NR) RingSteps<MT, WN, 0, NR>::full(rb, lds, i, n);
-  RingSteps<MT, WN, 0, NR - 1>::tail(rb, lds, i, n);
+  for (; i + NR <= n; i += NR) RingSteps<MT, WN, 0, NR>::full(rb, lds, i, n, o0, o1);
+  RingSteps<MT, WN, 0, NR - 1>::tail(rb, lds, i, n, o0, o1);
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // the clamped trailing copies land before the block exits
 
   const int cg0 = (t0 + wave) * kTile;
@@ -943,7 +1010,11 @@ __global__ __launch_bounds__(256 * NG) __attribute__((amdgpu_waves_per_eu(2))) v
   const int grp = __builtin_amdgcn_readfirstlane(tid >> 8), t256 = tid & 255, wave = t256 >> 6;
   const int l32 = lane & 31, kh = lane >> 5;
   const int nqt = (a.M + 31) / 32;
-  const int qt = nqt - 1 - (int)blockIdx.x;  // longest key ranges first
+  // Longest key ranges first in the lower half of the (head, group) blocks and
+  // shortest first in the upper half: with two blocks per CU, blocks L and
+  // L + half of the grid share a CU, so a long query tile pairs with a short one.
+  const int yz = blockIdx.z * gridDim.y + blockIdx.y, nyz = gridDim.y * gridDim.z;
+  const int qt = (2 * yz < nyz) ? nqt - 1 - (int)blockIdx.x : (int)blockIdx.x;
   const int hk = blockIdx.y;
   const int gw = (int)blockIdx.z * 4 + wave;
   const bool active = gw < a.G;
@@ -999,12 +1070,14 @@ __global__ __launch_bounds__(256 * NG) __attribute__((amdgpu_waves_per_eu(2))) v
             if (key > qpos || key < qfirst) s[b2][v] = -INFINITY;
           }
       }
-      float mx = -INFINITY;
+      float mv[16];  // max over the 32 scores as a tree, not a chain
 #pragma unroll
-      for (int b2 = 0; b2 < 2; b2++)
+      for (int v = 0; v < 16; v++) mv[v] = fmaxf(s[0][v], s[1][v]);
 #pragma unroll
-        for (int v = 0; v < 16; v++) mx = fmaxf(mx, s[b2][v]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * a.scale_log2;
+      for (int w = 8; w > 0; w >>= 1)
+#pragma unroll
+        for (int v = 0; v < w; v++) mv[v] = fmaxf(mv[v], mv[v + w]);
+      float mx = fmaxf(mv[0], __shfl_xor(mv[0], 32, 64)) * a.scale_log2;
       const float mn = fmaxf(mrun, mx);
       const float mu = mn == -INFINITY ? 0.f : mn;
       const float corr = __builtin_amdgcn_exp2f(mrun - mu);
