@@ -193,3 +193,35 @@ def test_batched_prefill_matches_replay_and_oracle(ctx, name, layers, prompt_len
     print(name, "stream", stream, "max |logits - replay|", float(np.abs(logits - replay_logits).max()))
     om.close()
     runner.close()
+
+
+def test_batched_prefill_2048_rows_matches_replay(ctx):
+    """One chunk of 2048 positions through two Llama-3.2-1B layers: the
+    large-batch shapes of the q4 GEMM (16 row tiles of 128 x 8..64 column
+    blocks of 256, split K for the partial sums) and 64 query tiles of the
+    flash attention.  Checked against the replayed decode graph, an
+    independent path (the oracle would need ~250 GMAC on the host here)."""
+    layers, n = 2, 2048
+    wl = _workload("llama-3.2-1b", layers, n + 1, max_tokens=n + 8)
+    hw = W.synthetic(wl)
+    hw.keep = True
+    runner = R.DecoderHIPRunner(hw, {"maxTokens": wl.max_tokens, "prefillChunkSize": 2048}, ctx=ctx)
+    prompt = [int(t) for t in np.random.default_rng(5).integers(0, wl.config["vocab_size"], n + 1)]
+    m = runner.model
+    m.set_prefill(0, 2048)
+    m.prefill(prompt, 0, n)
+    m.compute_token(prompt[-1], n, True)
+    replay_logits = m.read_logits()
+    replay_kv = _kv(m, layers, n)
+    m.reset_cache()
+    m.set_prefill(64, 2048)
+    runner.prefillTokens(prompt, 0, n)
+    runner.computeToken(prompt[-1], n, True)
+    logits = runner.readLogits()
+    kv = _kv(m, layers, n)
+    for l in range(layers):
+        for got, ref in zip(kv[l], replay_kv[l]):
+            close(got, ref, 2e-2, 1e-2)
+    close(logits, replay_logits, LOGIT_ATOL, LOGIT_RTOL)
+    print("max |logits - replay|", float(np.abs(logits - replay_logits).max()))
+    runner.close()

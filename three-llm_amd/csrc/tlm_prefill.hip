@@ -39,6 +39,12 @@ __device__ __forceinline__ half8_t dequant8(uint32_t w, half2_t s2) {
 
 __device__ __forceinline__ half8_t as_half8(uint4 v) { return __builtin_bit_cast(half8_t, v); }
 
+// silu(g) * u for a result rounded to fp16: the hardware reciprocal (1 ulp)
+// instead of a full-precision division; g -> -inf gives exp = inf, rcp = 0.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g * __builtin_amdgcn_rcpf(1.f + __expf(-g)) * u;
+}
+
 __device__ __forceinline__ float block_sum_f(float v, float* scratch) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -223,7 +229,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
         const int row = rbase + 32 * i + 8 * (v >> 2) + (v & 3);
         if (row < g.M) {
           const float gt = mm.acc[i][0][v], up = mm.acc[i][NB - 1][v];
-          const _Float16 hv = (_Float16)(gt / (1.f + __expf(-gt)) * up);
+          const _Float16 hv = (_Float16)silu_mul(gt, up);
           g.Ch[(size_t)row * g.ldc + oi] = __builtin_bit_cast(uint16_t, hv);
         }
       }
@@ -512,7 +518,7 @@ __global__ __launch_bounds__(64 * WN) __attribute__((amdgpu_waves_per_eu(2))) vo
         const int row = rbase + 32 * t + 8 * (v >> 2) + (v & 3);
         if (row < g.M) {
           const float gt = rb.acc[t][0][v], up = rb.acc[t][1][v];
-          const _Float16 hv = (_Float16)(gt / (1.f + __expf(-gt)) * up);
+          const _Float16 hv = (_Float16)silu_mul(gt, up);
           g.Ch[(size_t)row * g.ldc + oi] = __builtin_bit_cast(uint16_t, hv);
         }
       }
@@ -699,7 +705,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         const int row = rbase + 32 * t + e;
         if (row < g.M) {
           const float gt = f4_at(r[t][0], e), up = f4_at(r[t][1], e);
-          const _Float16 hv = (_Float16)(gt / (1.f + __expf(-gt)) * up);
+          const _Float16 hv = (_Float16)silu_mul(gt, up);
           g.Ch[(size_t)row * g.ldc + oi] = __builtin_bit_cast(uint16_t, hv);
         }
       }
