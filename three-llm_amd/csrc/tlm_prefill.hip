@@ -263,14 +263,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 // (small blocks repeat a copy of identical bytes), so one immediate vmcnt
 // bounds the loads still in flight.  Columns: for the paired gate|up layout
 // a wave's two 32-column groups are the gate rows and the matching up rows.
+// The depth is even: the operands of consecutive steps alternate between two
+// register sets (a 6-stage ring measured slower).
 constexpr int kRing = 4;
-// Ring depth (even: the operands of consecutive steps alternate between two
-// register sets): four-wave blocks take a step every ~16 MFMA slots of each
-// of their waves; a one-wave block (small grids) is alone on its CU, finishes
-// a step sooner and needs more steps in flight to cover the memory latency
-// (the in-flight copies stay below vmcnt's limit of 63).
-template <int WN>
-constexpr int ring_depth() { return WN == 1 ? 6 : kRing; }
 static_assert(kRing % 2 == 0, "even ring depth");
 
 // s_waitcnt immediate that waits until at most n vector-memory operations are
@@ -307,7 +302,7 @@ struct RingLayout {
   static constexpr int S_BYTES = WN * 128 > 256 ? WN * 128 : 256;
   static constexpr int W_OFF = BM * 64, S_OFF = W_OFF + WN * 1024, STAGE = S_OFF + S_BYTES;
   static constexpr int LPS = AW + 2;            // copies per wave per stage: A, one weight tile, scales
-  static constexpr int NR = ring_depth<WN>();
+  static constexpr int NR = kRing;
   static_assert((NR - 1) * LPS <= 63, "copies in flight within vmcnt's range");
 };
 
@@ -738,11 +733,6 @@ static const int g_split_waves = [] {
   const int v = e ? atoi(e) : 0;
   return v > 0 && v <= 64 ? v : 8;
 }();
-// TLM_GEMM_KW=0 keeps one-wave blocks for small grids (comparisons)
-static const bool g_use_kw = [] {
-  const char* e = getenv("TLM_GEMM_KW");
-  return !(e && e[0] == '0');
-}();
 
 GemmShape gemm_shape(int fmt, int epi, int M, int N, int K, int cus) {
   GemmShape s;
@@ -759,13 +749,11 @@ GemmShape gemm_shape(int fmt, int epi, int M, int N, int K, int cus) {
     if (((N + 255) / 256) * s.gy >= cus / 2) {  // four waves side by side over 256 columns
       s.wn = 4;
       s.gx = (N + 255) / 256;
-    } else if (g_use_kw) {  // too few tiles to fill the CUs: four waves split K on one tile
+    } else {  // too few tiles to fill the CUs: four waves split K on one tile
       s.kw = 1;
       s.gx = (N + kTile - 1) / kTile;
       kdiv = 4;
       min_steps = 2;
-    } else {
-      s.gx = (N + kTile - 1) / kTile;
     }
   } else {
     s.mt = M > 64 ? 2 : 1;
@@ -814,7 +802,7 @@ bool launch_gemm(int fmt, int epi, const GemmShape& sh, const GemmArgs& ga, hipS
     return true;                                                                                 \
   }
 #define RING_EPIS(MTV, WNV) RING_CASE(MTV, WNV, GEMM_STORE) RING_CASE(MTV, WNV, GEMM_PART) RING_CASE(MTV, WNV, GEMM_SWIGLU)
-    RING_EPIS(1, 1) RING_EPIS(2, 1) RING_EPIS(4, 1) RING_EPIS(1, 4) RING_EPIS(2, 4) RING_EPIS(4, 4)
+    RING_EPIS(1, 4) RING_EPIS(2, 4) RING_EPIS(4, 4)
 #undef RING_EPIS
 #undef RING_CASE
     return false;
