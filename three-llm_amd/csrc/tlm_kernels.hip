@@ -972,8 +972,15 @@ __global__ __launch_bounds__(64) void head_kernel(AttnArgs a) {
   constexpr bool GEN = DT == 32;  // runtime head_dim <= 32
   constexpr int EPL = DT > 64 ? DT / 64 : 1;  // q/k/v elements per lane (d = lane + 64 e)
   constexpr int KW = DL * ESZ / 4;            // K dwords per lane
-  const int h = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
-  const int D = GEN ? a.D : DT, G = a.G, hk = h / G, g = h % G;
+  // Block -> (query head, chunk): workgroups go to the 8 XCDs round robin
+  // (block b to XCD b % 8), so the G query heads of one (kv head, chunk) pair
+  // take blocks 8 apart on one XCD and its L2 serves their shared K/V rows:
+  // HBM reads each cached row once instead of once per query head.
+  const int G = a.G, b = blockIdx.x, slot = b >> 3;
+  const int pair = (slot / G) * 8 + (b & 7), g = slot % G;
+  if (pair >= a.Hkv * a.nsplit) return;
+  const int hk = pair % a.Hkv, c = pair / a.Hkv, h = hk * G + g, lane = threadIdx.x;
+  const int D = GEN ? a.D : DT;
   const int pos = a.ctrl[C_POS];
   if (pos < 0 || pos >= a.max_tokens) return;
   const ChunkPlan cp = chunk_plan(pos, a.window, a.nsplit, a.chmin);
@@ -1134,7 +1141,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 
 bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, bool combine, hipStream_t st) {
   (void)gmax;
-  const dim3 grid(a.Hq, a.nsplit);
+  // head_kernel's XCD-aware numbering: groups of 8 (kv head, chunk) pairs x G heads
+  const dim3 grid((unsigned)(((a.Hkv * a.nsplit + 7) / 8) * 8 * a.G));
   const size_t smem = attn_smem_bytes(gmax, a.D, kv_f32);
   const int dt = attn_dt(a.D);
   bool ok = true;
