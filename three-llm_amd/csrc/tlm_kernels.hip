@@ -972,6 +972,8 @@ __global__ __launch_bounds__(64) void head_kernel(AttnArgs a) {
   constexpr bool GEN = DT == 32;  // runtime head_dim <= 32
   constexpr int EPL = DT > 64 ? DT / 64 : 1;  // q/k/v elements per lane (d = lane + 64 e)
   constexpr int KW = DL * ESZ / 4;            // K dwords per lane
+  // fp16 cache, head_dim 128: the output dims of a lane are adjacent (P.V)
+  constexpr bool PAIRD = !GEN && ESZ == 2 && DT == 128;
   // Block -> (query head, chunk): workgroups go to the 8 XCDs round robin
   // (block b to XCD b % 8), so the G query heads of one (kv head, chunk) pair
   // take blocks 8 apart on one XCD and its L2 serves their shared K/V rows:
@@ -1106,22 +1108,35 @@ __global__ __launch_bounds__(64) void head_kernel(AttnArgs a) {
     m = mn;
     if (part == 0) p_l[pl] = p;
     __syncthreads();
+    if constexpr (PAIRD) {  // lane owns dims 2 lane, 2 lane + 1: one 4-byte V read per position
+      float a0 = o[0] * corr, a1 = o[1] * corr;
 #pragma unroll
-    for (int e = 0; e < EPL; e++) {
-      const int d = lane + 64 * e;
-      float acc = o[e] * corr;
-      if (d < D) {
-#pragma unroll 8
-        for (int u = 0; u < SUB; u++) acc = fmaf(p_l[u], kv_load<KT>(vt + (size_t)u * D + d), acc);
+      for (int u = 0; u < SUB; u++) {
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(vt + (size_t)u * DT + 2 * lane);
+        const float pu = p_l[u];
+        a0 = fmaf(pu, h2f(w & 0xFFFFu), a0);
+        a1 = fmaf(pu, h2f(w >> 16), a1);
       }
-      o[e] = acc;
+      o[0] = a0;
+      o[1] = a1;
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPL; e++) {
+        const int d = lane + 64 * e;
+        float acc = o[e] * corr;
+        if (d < D) {
+#pragma unroll 8
+          for (int u = 0; u < SUB; u++) acc = fmaf(p_l[u], kv_load<KT>(vt + (size_t)u * D + d), acc);
+        }
+        o[e] = acc;
+      }
     }
     __syncthreads();
   }
   const size_t row = (size_t)h * a.nsplit + c;
 #pragma unroll
   for (int e = 0; e < EPL; e++) {
-    const int d = lane + 64 * e;
+    const int d = PAIRD ? 2 * lane + e : lane + 64 * e;
     if (d < D) a.pacc[row * D + d] = o[e];
   }
   if (lane == 0) {
