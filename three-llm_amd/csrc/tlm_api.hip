@@ -577,11 +577,15 @@ static int attn_init(tlm_ctx* ctx, const tlm_attn_desc* d, tlm_attn* A, bool own
   if (attn_smem_bytes(A->gmax, d->head_dim, d->kv_fmt == TLM_FMT_F32) > 65536)
     return fail(TLM_ERR_INVALID, "TLMAttention: %d heads per kv head x head_dim %d exceed the LDS budget", A->G,
                 d->head_dim);
-  A->chmin = 32;
+  // per wave: at most 256 positions, about two waves per CU and kv head at
+  // the longest window; a block (chunk of at least 32 positions) spreads its
+  // chunk over up to kAttnWaves waves, so a quarter as many chunks
   const int by_tile = (d->max_tokens + 255) / 256;
   const int by_cus = std::max(1, 2 * ctx->cus / d->kv_heads);
-  const int by_min = (d->max_tokens + A->chmin - 1) / A->chmin;
-  A->nsplit = std::max(by_tile, std::min(by_min, by_cus));
+  const int by_min = (d->max_tokens + 31) / 32;
+  const int waves = std::max(by_tile, std::min(by_min, by_cus));
+  A->chmin = 32;
+  A->nsplit = (waves + kAttnWaves - 1) / kAttnWaves;
   const int D = d->head_dim;
   const size_t esz = d->kv_fmt == TLM_FMT_F32 ? 4 : 2;
   std::vector<float> cs, sn;

@@ -8,6 +8,7 @@ namespace tlm {
 constexpr int kTile = 64;      // output rows per tile: one row per lane of a wave64
 constexpr int kMaxChunks = 8;  // most 16-byte chunks a wave keeps in flight per batch
 constexpr int kMaxPart = 8;    // partial vectors a consumer folds in with one round trip
+constexpr int kAttnWaves = 4;  // decode attention: waves per block, each a quarter of the block's chunk
 // Residual stream accumulators: kRep replicas of an int64 fixed-point vector
 // (value * 2^32).  Producers add into replica (block % kRep) with device-scope
 // atomics; integer addition is associative, so the sum is exact and the same

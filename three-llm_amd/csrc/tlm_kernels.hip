@@ -900,12 +900,27 @@ static int attn_dt(int D) { return D <= 32 ? 32 : D; }
 
 int attn_lpp(int D, bool kv_f32) { return head_tiling(attn_dt(D), kv_f32 ? 4 : 2).lpp; }
 
-// LDS of head_kernel: q, the new k and v, their pre-RoPE values, the pass's
-// probabilities and the V tile.
+// LDS of one head_kernel wave (floats): q, the new k and v, their pre-RoPE
+// values, the pass's probabilities and the V tile (4 KiB); a multiple of 4
+// floats so every wave's region stays 16-byte aligned.
+static constexpr __host__ __device__ inline int head_wave_floats(int dt, int esz) {
+  return (6 * dt + head_tiling(dt, esz).sub + 1024 + 3) & ~3;
+}
+
+// LDS of a head_kernel block: kAttnWaves wave regions, then the merge area
+// [kAttnWaves][2 + DT] (max, sum, unnormalised output of each wave).
 size_t attn_smem_bytes(int gmax, int D, bool kv_f32) {
   (void)gmax;
-  const HeadTiling t = head_tiling(attn_dt(D), kv_f32 ? 4 : 2);
-  return sizeof(float) * (6 * (size_t)attn_dt(D) + t.sub) + 4096;
+  const int dt = attn_dt(D), esz = kv_f32 ? 4 : 2;
+  return sizeof(float) * ((size_t)kAttnWaves * head_wave_floats(dt, esz) + (size_t)kAttnWaves * (2 + dt));
+}
+
+// Order a wave's own LDS writes before its later reads (regions private to
+// one wave: no block barrier, whose waves may run different pass counts).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // Global loads of one head_kernel pass, held in registers: this lane's K-row
@@ -951,9 +966,12 @@ struct HeadLoads {
   }
 };
 
-// One wave = one query head x one chunk of positions (split-K over the
+// One block = one query head x one chunk of positions (split-K over the
 // sequence, flash decoding; TSLAttention.ts:306-428 computes the same scores
-// and softmax over the whole window).  The wave
+// and softmax over the whole window).  A chunk of 32 positions or fewer is one
+// wave's; a longer one is split over up to kAttnWaves waves that merge
+// (max, sum, output) in LDS at the end, so at long windows the combine
+// downstream folds kAttnWaves times fewer partials.  Each wave
 //   * forms its q head and the KV head's new k and v from the QKV partial sums
 //     + bias and applies RoPE (rotate-half, TSLAttention.ts:168-250),
 //   * in the chunk holding `pos`, appends k and v to the cache (head g == 0 of
@@ -962,9 +980,9 @@ struct HeadLoads {
 //     softmax with DPP wave reductions, P.V from the V rows staged in LDS,
 //   * writes (max, sum, unnormalised output) for the combine.
 // All global loads of the first pass are unconditional and issued before the
-// first use; a one-wave block needs no barrier beyond wave-level LDS order.
+// first use; until the merge a wave touches only its own LDS region.
 template <typename KT, int DT>
-__global__ __launch_bounds__(64) void head_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64 * kAttnWaves) void head_kernel(AttnArgs a) {
   extern __shared__ float sm[];
   constexpr int ESZ = sizeof(KT);
   constexpr HeadTiling TL = head_tiling(DT, ESZ);
@@ -981,15 +999,23 @@ __global__ __launch_bounds__(64) void head_kernel(AttnArgs a) {
   const int G = a.G, b = blockIdx.x, slot = b >> 3;
   const int pair = (slot / G) * 8 + (b & 7), g = slot % G;
   if (pair >= a.Hkv * a.nsplit) return;
-  const int hk = pair % a.Hkv, c = pair / a.Hkv, h = hk * G + g, lane = threadIdx.x;
+  const int hk = pair % a.Hkv, c = pair / a.Hkv, h = hk * G + g;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int D = GEN ? a.D : DT;
   const int pos = a.ctrl[C_POS];
   if (pos < 0 || pos >= a.max_tokens) return;
   const ChunkPlan cp = chunk_plan(pos, a.window, a.nsplit, a.chmin);
   if (c >= cp.nact) return;
-  const int t0 = cp.first + c * cp.chunk, t1 = min(t0 + cp.chunk, pos + 1);
+  // the block's chunk [b0, b1), split over nwu <= kAttnWaves waves of at least
+  // 32 positions (block-uniform); this wave's part [t0, t1) may be empty
+  const int b0 = cp.first + c * cp.chunk, b1 = min(b0 + cp.chunk, pos + 1);
+  const int nwu = min(kAttnWaves, (b1 - b0 + 31) / 32);
+  if (nwu == 1 && wv != 0) return;  // one wave does the whole chunk, no merge
+  const int sc = (b1 - b0 + nwu - 1) / nwu;
+  const int t0 = min(b0 + wv * sc, b1), t1 = min(t0 + sc, b1);
+  const bool has = t0 < t1;
   const bool own = pos >= t0 && pos < t1;
-  float* q_l = sm;            // [DT]
+  float* q_l = sm + wv * head_wave_floats(DT, ESZ);  // [DT]
   float* kn = q_l + DT;       // [DT] new k (rounded like the cache)
   float* vn = kn + DT;        // [DT]
   float* raw = vn + DT;       // [3][DT] pre-RoPE q, k, v
@@ -1026,7 +1052,7 @@ __global__ __launch_bounds__(64) void head_kernel(AttnArgs a) {
   // first pass: this lane's K slice and its 64 bytes of the V rows
   HeadLoads<KT, KW, GEN, DL> ld;
   const int row_bytes = D * ESZ;
-  ld.issue(kh, vh, t0, t1, pl, part, D, row_bytes, lane);
+  if (has) ld.issue(kh, vh, t0, t1, pl, part, D, row_bytes, lane);
   __builtin_amdgcn_sched_barrier(0);
 
   // finish q/k/v: sums, RoPE through LDS pairs, cache rounding
@@ -1040,7 +1066,7 @@ __global__ __launch_bounds__(64) void head_kernel(AttnArgs a) {
       const int d = lane + 64 * e;
       if (d < D) raw[r * DT + d] = s;
     }
-  __syncthreads();
+  wave_lds_sync();
 #pragma unroll
   for (int e = 0; e < EPL; e++) {
     const int d = lane + 64 * e;
@@ -1063,7 +1089,7 @@ __global__ __launch_bounds__(64) void head_kernel(AttnArgs a) {
     }
   }
   for (int d = D + lane; d < DT; d += 64) q_l[d] = kn[d] = 0.f;  // padded dims (generic path)
-  __syncthreads();
+  wave_lds_sync();
 
   float m = -INFINITY, l = 0.f, o[EPL];
 #pragma unroll
@@ -1089,7 +1115,7 @@ __global__ __launch_bounds__(64) void head_kernel(AttnArgs a) {
 #pragma unroll
       for (int e = 0; e < DL; e++) kf[e] = kn[min(part * DL + e, DT - 1)];
     }
-    __syncthreads();
+    wave_lds_sync();
     if (own && pos >= tb && pos < tb + SUB)
       for (int d = lane; d < D; d += 64) vt[(size_t)(pos - tb) * D + d] = kv_store<KT>(vn[d]);
     // the next pass's loads overlap this pass's math
@@ -1107,7 +1133,7 @@ __global__ __launch_bounds__(64) void head_kernel(AttnArgs a) {
     l = l * corr + wave_sum(part == 0 ? p : 0.f);
     m = mn;
     if (part == 0) p_l[pl] = p;
-    __syncthreads();
+    wave_lds_sync();
     if constexpr (PAIRD) {  // lane owns dims 2 lane, 2 lane + 1: one 4-byte V read per position
       float a0 = o[0] * corr, a1 = o[1] * corr;
 #pragma unroll
@@ -1131,17 +1157,54 @@ __global__ __launch_bounds__(64) void head_kernel(AttnArgs a) {
         o[e] = acc;
       }
     }
-    __syncthreads();
+    wave_lds_sync();
   }
   const size_t row = (size_t)h * a.nsplit + c;
+  if (nwu == 1) {  // wave 0 alone: its result is the chunk's partial
+#pragma unroll
+    for (int e = 0; e < EPL; e++) {
+      const int d = PAIRD ? 2 * lane + e : lane + 64 * e;
+      if (d < D) a.pacc[row * D + d] = o[e];
+    }
+    if (lane == 0) {
+      a.pml[row * 2] = m;
+      a.pml[row * 2 + 1] = l;
+    }
+    return;
+  }
+  // merge the waves' (max, sum, output) in wave order; wave 0 writes the chunk's partial
+  float* mg = sm + kAttnWaves * head_wave_floats(DT, ESZ);  // [kAttnWaves][2 + DT]
+  float* mine = mg + wv * (2 + DT);
 #pragma unroll
   for (int e = 0; e < EPL; e++) {
     const int d = PAIRD ? 2 * lane + e : lane + 64 * e;
-    if (d < D) a.pacc[row * D + d] = o[e];
+    if (d < D) mine[2 + d] = o[e];
   }
   if (lane == 0) {
-    a.pml[row * 2] = m;
-    a.pml[row * 2 + 1] = l;
+    mine[0] = m;
+    mine[1] = l;
+  }
+  __syncthreads();  // every wave of the block reaches this once
+  if (wv != 0) return;
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kAttnWaves; w++) M = fmaxf(M, mg[w * (2 + DT)]);
+  float wsc[kAttnWaves], L = 0.f;
+#pragma unroll
+  for (int w = 0; w < kAttnWaves; w++) {
+    const float mw = mg[w * (2 + DT)];
+    wsc[w] = mw == -INFINITY ? 0.f : __expf(mw - M);
+    L = fmaf(mg[w * (2 + DT) + 1], wsc[w], L);
+  }
+  for (int d = lane; d < D; d += 64) {
+    float od = 0.f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; w++) od = fmaf(mg[w * (2 + DT) + 2 + d], wsc[w], od);
+    a.pacc[row * D + d] = od;
+  }
+  if (lane == 0) {
+    a.pml[row * 2] = M;
+    a.pml[row * 2 + 1] = L;
   }
 }
 
@@ -1162,14 +1225,14 @@ bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, bool combine, hi
   const int dt = attn_dt(a.D);
   bool ok = true;
   if (kv_f32) {
-    if (dt == 32) hipLaunchKernelGGL((head_kernel<float, 32>), grid, dim3(64), smem, st, a);
-    else if (dt == 64) hipLaunchKernelGGL((head_kernel<float, 64>), grid, dim3(64), smem, st, a);
-    else if (dt == 128) hipLaunchKernelGGL((head_kernel<float, 128>), grid, dim3(64), smem, st, a);
+    if (dt == 32) hipLaunchKernelGGL((head_kernel<float, 32>), grid, dim3(64 * kAttnWaves), smem, st, a);
+    else if (dt == 64) hipLaunchKernelGGL((head_kernel<float, 64>), grid, dim3(64 * kAttnWaves), smem, st, a);
+    else if (dt == 128) hipLaunchKernelGGL((head_kernel<float, 128>), grid, dim3(64 * kAttnWaves), smem, st, a);
     else ok = false;
   } else {
-    if (dt == 32) hipLaunchKernelGGL((head_kernel<uint16_t, 32>), grid, dim3(64), smem, st, a);
-    else if (dt == 64) hipLaunchKernelGGL((head_kernel<uint16_t, 64>), grid, dim3(64), smem, st, a);
-    else if (dt == 128) hipLaunchKernelGGL((head_kernel<uint16_t, 128>), grid, dim3(64), smem, st, a);
+    if (dt == 32) hipLaunchKernelGGL((head_kernel<uint16_t, 32>), grid, dim3(64 * kAttnWaves), smem, st, a);
+    else if (dt == 64) hipLaunchKernelGGL((head_kernel<uint16_t, 64>), grid, dim3(64 * kAttnWaves), smem, st, a);
+    else if (dt == 128) hipLaunchKernelGGL((head_kernel<uint16_t, 128>), grid, dim3(64 * kAttnWaves), smem, st, a);
     else ok = false;
   }
   if (ok && combine) hipLaunchKernelGGL(attn_combine_kernel, dim3(a.Hq), dim3(128), 0, st, a);
