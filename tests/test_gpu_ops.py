@@ -193,6 +193,44 @@ def test_attention_long_fp16_cache(ctx, heads, kv, D, theta, steps, window):
     A.close()
 
 
+def test_attention_decode_after_16384_positions(ctx):
+    """The Llama-3.2-3B decode case (24/8 heads, head_dim 128, theta 5e5, fp16
+    cache) at its real window: positions 0..16383 are appended by the batched
+    rows path (8 calls), the cache is read back, and three decode steps at
+    16384.. are checked against the oracle over that same cache.  At this
+    window a block's chunk (~964 positions) is split over four waves that
+    merge in LDS, and the query heads of a kv head share an XCD."""
+    heads, kv, D, theta, n0 = 24, 8, 128, 5e5, 16384
+    rng = np.random.default_rng(16384)
+    inv, af = orc.rope_parameters(D, theta)
+    M = n0 + 8
+    A = tlm.Attention(ctx, heads, kv, D, M, inv, attention_factor=af, kv_fmt=tlm.FMT_F16)
+    width = (heads + 2 * kv) * D
+    rows_out = ctx.buffer(2 * 2048 * heads * D)
+    for p0 in range(0, n0, 2048):
+        A.rows(ctx.array(f32(rng.standard_normal((2048, width)))), 2048, p0, rows_out)
+    k, v = A.read_cache(n0)
+    kc = np.zeros((M, kv * D), np.float32)
+    vc = np.zeros_like(kc)
+    kc[:n0], vc[:n0] = k, v
+    out = ctx.buffer(4 * heads * D)
+    worst = 0.0
+    for pos in range(n0, n0 + 3):
+        qkv = f32(rng.standard_normal(width))
+        qkv[:heads * D] *= 6.0  # peaked softmax: a few positions carry each head, so a lost chunk shows
+        got = A(ctx.array(qkv), pos, out).read()
+        ref = orc.attention(qkv, heads, kv, D, pos, kc, vc, inv, attention_factor=af, kv_f16=True)
+        assert np.abs(ref).max() > 0.5
+        close(got, ref, 2e-3, 2e-3)
+        worst = max(worst, float(np.abs(got - ref).max() / np.abs(ref).max()))
+    k2, v2 = A.read_cache(n0 + 3)
+    close(v2, vc[:n0 + 3], 0, 0)
+    close(k2[n0:], kc[n0:n0 + 3], 1e-3, 1e-3)
+    assert worst < 1e-4, worst
+    print(f"max |attn - oracle| / max |oracle| over 16384+ positions = {worst:.3g}")
+    A.close()
+
+
 def test_device_copy_is_exact(ctx):
     """tlm_copy: byte-exact device-to-device copy; sizes not a multiple of 16 are rejected."""
     rng = np.random.default_rng(7)
