@@ -87,7 +87,9 @@ static int phys_row(const tlm_linear* L, int r) {
 struct tlm_attn {
   tlm_ctx* ctx = nullptr;
   tlm_attn_desc d{};
-  int G = 1, gmax = 1, nsplit = 1, chmin = 32, lpp = 1;
+  // chunks per query head: short windows (one wave each) and long windows
+  // (up to kAttnWaves waves each); pacc / pml hold the larger
+  int G = 1, gmax = 1, nsplit = 1, nsplit_long = 1, chmin = 32, lpp = 1;
   float scale = 1.f;
   void* kc = nullptr;
   void* vc = nullptr;
@@ -145,8 +147,10 @@ struct tlm_model {
   float *pf_x = nullptr, *pf_part = nullptr;  // residual rows, split-K slices
   size_t pf_part_n = 0;
   uint16_t *pf_xn = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_h = nullptr;
-  hipGraphExec_t g_logits = nullptr, g_prefill = nullptr, g_layers = nullptr;
-  hipGraph_t graph_logits = nullptr, graph_prefill = nullptr, graph_layers = nullptr;
+  // per attention mode: [0] short windows, [1] long windows (long_window)
+  hipGraphExec_t g_logits[2] = {}, g_prefill[2] = {}, g_layers[2] = {};
+  hipGraph_t graph_logits[2] = {}, graph_prefill[2] = {}, graph_layers[2] = {};
+  int host_pos = 0;  // position of the last token enqueued (selects the attention mode)
   bool finalized = false;
   bool use_graphs = true;  // TLM_GRAPHS=0 enqueues the same kernels directly (profilers, debugging)
 };
@@ -574,18 +578,18 @@ static int attn_init(tlm_ctx* ctx, const tlm_attn_desc* d, tlm_attn* A, bool own
   A->gmax = A->G <= 1 ? 1 : A->G <= 2 ? 2 : A->G <= 4 ? 4 : A->G <= 8 ? 8 : 16;
   A->scale = (float)(d->attn_scale > 0 ? d->attn_scale : 1.0 / sqrt((double)d->head_dim));
   A->lpp = attn_lpp(d->head_dim, d->kv_fmt == TLM_FMT_F32);
-  if (attn_smem_bytes(A->gmax, d->head_dim, d->kv_fmt == TLM_FMT_F32) > 65536)
+  if (attn_smem_bytes(A->gmax, d->head_dim, d->kv_fmt == TLM_FMT_F32, true) > 65536)
     return fail(TLM_ERR_INVALID, "TLMAttention: %d heads per kv head x head_dim %d exceed the LDS budget", A->G,
                 d->head_dim);
-  // per wave: at most 256 positions, about two waves per CU and kv head at
-  // the longest window; a block (chunk of at least 32 positions) spreads its
-  // chunk over up to kAttnWaves waves, so a quarter as many chunks
+  // per wave: chunks of at least 32 positions, at most 256, about two waves
+  // per CU and kv head at the longest window.  Long windows: a block spreads
+  // its chunk over up to kAttnWaves waves, so a quarter as many chunks.
   const int by_tile = (d->max_tokens + 255) / 256;
   const int by_cus = std::max(1, 2 * ctx->cus / d->kv_heads);
   const int by_min = (d->max_tokens + 31) / 32;
-  const int waves = std::max(by_tile, std::min(by_min, by_cus));
   A->chmin = 32;
-  A->nsplit = (waves + kAttnWaves - 1) / kAttnWaves;
+  A->nsplit = std::max(by_tile, std::min(by_min, by_cus));
+  A->nsplit_long = (A->nsplit + kAttnWaves - 1) / kAttnWaves;
   const int D = d->head_dim;
   const size_t esz = d->kv_fmt == TLM_FMT_F32 ? 4 : 2;
   std::vector<float> cs, sn;
@@ -596,8 +600,9 @@ static int attn_init(tlm_ctx* ctx, const tlm_attn_desc* d, tlm_attn* A, bool own
   HIP_TRY(hipMalloc(&A->rope_sin, sn.size() * sizeof(float)));
   HIP_TRY(hipMemcpy(A->rope_cos, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice));
   HIP_TRY(hipMemcpy(A->rope_sin, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice));
-  HIP_TRY(hipMalloc(&A->pacc, sizeof(float) * (size_t)d->heads * A->nsplit * D));
-  HIP_TRY(hipMalloc(&A->pml, sizeof(float) * (size_t)d->heads * A->nsplit * 2));
+  const size_t nsp = (size_t)std::max(A->nsplit, A->nsplit_long);
+  HIP_TRY(hipMalloc(&A->pacc, sizeof(float) * (size_t)d->heads * nsp * D));
+  HIP_TRY(hipMalloc(&A->pml, sizeof(float) * (size_t)d->heads * nsp * 2));
   const size_t nqkv = (size_t)(d->heads + 2 * d->kv_heads) * D;
   HIP_TRY(hipMalloc(&A->zero_bias, sizeof(float) * nqkv));
   HIP_TRY(hipMemset(A->zero_bias, 0, sizeof(float) * nqkv));
@@ -626,8 +631,14 @@ static void attn_free(tlm_attn* A, bool own_cache) {
   }
 }
 
+// Windows above kLongWindow positions run the long-window attention kernels.
+static bool long_window(const tlm_attn* A, int pos) {
+  const int n = A->d.sliding_window > 0 ? std::min(pos + 1, A->d.sliding_window) : pos + 1;
+  return n > kLongWindow;
+}
+
 static AttnArgs attn_args(const tlm_attn* A, const float* src, int n_src, int stride, const float* bias,
-                          const int* ctrl, void* kc, void* vc, float* out) {
+                          const int* ctrl, void* kc, void* vc, float* out, bool long_win) {
   AttnArgs a;
   memset(&a, 0, sizeof a);
   a.src = src;
@@ -649,7 +660,7 @@ static AttnArgs attn_args(const tlm_attn* A, const float* src, int n_src, int st
   a.rd = A->d.rotary_dim;
   a.max_tokens = A->d.max_tokens;
   a.window = A->d.sliding_window;
-  a.nsplit = A->nsplit;
+  a.nsplit = long_win ? A->nsplit_long : A->nsplit;
   a.chmin = A->chmin;
   a.lpp = A->lpp;
   a.scale = A->scale;
@@ -683,8 +694,9 @@ int tlm_op_attention(tlm_attn* A, const float* qkv, int position, float* out) {
   hipStream_t st = A->ctx->stream;
   launch_set_ctrl(A->ctrl, 0, position, 0, 0, 0, EmbStage{}, st);
   const int total = (A->d.heads + 2 * A->d.kv_heads) * A->d.head_dim;
-  AttnArgs a = attn_args(A, qkv, 1, total, nullptr, A->ctrl, A->kc, A->vc, out);
-  if (!launch_attention(A->d.kv_fmt == TLM_FMT_F32, A->gmax, a, true, st))
+  const bool lw = long_window(A, position);
+  AttnArgs a = attn_args(A, qkv, 1, total, nullptr, A->ctrl, A->kc, A->vc, out, lw);
+  if (!launch_attention(A->d.kv_fmt == TLM_FMT_F32, A->gmax, a, true, lw, st))
     return fail(TLM_ERR_STATE, "TLMAttention: no kernel variant for this shape");
   CHECK_LAUNCH("TLMAttention");
   return TLM_OK;
@@ -957,12 +969,14 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
 void tlm_model_destroy(tlm_model* m) {
   if (!m) return;
   hipStreamSynchronize(m->ctx->stream);
-  if (m->g_logits) hipGraphExecDestroy(m->g_logits);
-  if (m->g_prefill) hipGraphExecDestroy(m->g_prefill);
-  if (m->g_layers) hipGraphExecDestroy(m->g_layers);
-  if (m->graph_layers) hipGraphDestroy(m->graph_layers);
-  if (m->graph_logits) hipGraphDestroy(m->graph_logits);
-  if (m->graph_prefill) hipGraphDestroy(m->graph_prefill);
+  for (int i = 0; i < 2; i++) {
+    if (m->g_logits[i]) hipGraphExecDestroy(m->g_logits[i]);
+    if (m->g_prefill[i]) hipGraphExecDestroy(m->g_prefill[i]);
+    if (m->g_layers[i]) hipGraphExecDestroy(m->g_layers[i]);
+    if (m->graph_layers[i]) hipGraphDestroy(m->graph_layers[i]);
+    if (m->graph_logits[i]) hipGraphDestroy(m->graph_logits[i]);
+    if (m->graph_prefill[i]) hipGraphDestroy(m->graph_prefill[i]);
+  }
   for (auto& L : m->layers) {
     tlm_linear_destroy(L.qkv);
     tlm_linear_destroy(L.o);
@@ -1055,7 +1069,7 @@ static EmbStage emb_stage(const tlm_model* m) {
 }
 
 // Kernels of one layer.  which: -1 all; otherwise a single stage (timing).
-static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which) {
+static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which, bool long_win) {
   bool ok = true;
   const tlm_model_desc& d = m->d;
   const int H = d.hidden_size, I = d.intermediate_size;
@@ -1076,8 +1090,9 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which) {
   }
   // 2. RoPE + KV append + split-K attention
   if (which < 0 || which == 1) {
-    AttnArgs a = attn_args(&m->attn, m->pq, L.qkv->plan.splits, m->Nqkv, L.bqkv, m->ctrl, L.kc, L.vc, m->attn_out);
-    ok &= launch_attention(d.kv_fmt == TLM_FMT_F32, m->attn.gmax, a, false, st);
+    AttnArgs a = attn_args(&m->attn, m->pq, L.qkv->plan.splits, m->Nqkv, L.bqkv, m->ctrl, L.kc, L.vc, m->attn_out,
+                           long_win);
+    ok &= launch_attention(d.kv_fmt == TLM_FMT_F32, m->attn.gmax, a, false, long_win, st);
   }
   // 3. O projection; its prologue combines the attention chunk partials
   if (which < 0 || which == 5) {
@@ -1087,7 +1102,7 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which) {
     a.pacc = m->attn.pacc;
     a.pml = m->attn.pml;
     a.att_D = d.head_dim;
-    a.att_nsplit = m->attn.nsplit;
+    a.att_nsplit = long_win ? m->attn.nsplit_long : m->attn.nsplit;
     a.att_chmin = m->attn.chmin;
     a.att_window = d.sliding_window;
     a.att_max_tokens = d.max_tokens;
@@ -1150,11 +1165,11 @@ static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, hipEvent_t*
 // (LM head timing).
 enum GraphTail { TAIL_PREFILL = 0, TAIL_LOGITS = 1, TAIL_NONE = 2 };
 
-static int capture(tlm_model* m, int tail, hipGraph_t* g, hipGraphExec_t* ge) {
+static int capture(tlm_model* m, int tail, bool long_win, hipGraph_t* g, hipGraphExec_t* ge) {
   hipStream_t st = m->ctx->stream;
   HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
   bool ok = true;
-  for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1);
+  for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1, long_win);
   if (tail == TAIL_LOGITS)
     ok &= enqueue_head(m, st, true);
   else if (tail == TAIL_PREFILL)
@@ -1177,22 +1192,28 @@ int tlm_model_finalize(tlm_model* m) {
     m->finalized = true;
     return TLM_OK;
   }
-  int rc = capture(m, TAIL_LOGITS, &m->graph_logits, &m->g_logits);
-  if (rc == TLM_OK) rc = capture(m, TAIL_PREFILL, &m->graph_prefill, &m->g_prefill);
+  int rc = TLM_OK;
+  for (int lw = 0; lw < 2 && !rc; lw++) {
+    rc = capture(m, TAIL_LOGITS, lw, &m->graph_logits[lw], &m->g_logits[lw]);
+    if (rc == TLM_OK) rc = capture(m, TAIL_PREFILL, lw, &m->graph_prefill[lw], &m->g_prefill[lw]);
+  }
   if (rc) return rc;
   m->finalized = true;
   return TLM_OK;
 }
 
-// One token of the schedule: the captured graph, or the same kernels enqueued directly.
-static int run_token(tlm_model* m, bool logits) {
+// One token of the schedule at position pos: the captured graph of its
+// attention mode, or the same kernels enqueued directly.
+static int run_token(tlm_model* m, bool logits, int pos) {
   hipStream_t st = m->ctx->stream;
+  const bool lw = long_window(&m->attn, pos);
+  m->host_pos = pos;
   if (m->use_graphs) {
-    HIP_TRY(hipGraphLaunch(logits ? m->g_logits : m->g_prefill, st));
+    HIP_TRY(hipGraphLaunch(logits ? m->g_logits[lw] : m->g_prefill[lw], st));
     return TLM_OK;
   }
   bool ok = true;
-  for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1);
+  for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1, lw);
   if (logits)
     ok &= enqueue_head(m, st, true);
   else
@@ -1219,7 +1240,7 @@ int tlm_compute_token(tlm_model* m, int32_t token, int32_t position, int flags) 
   hipStream_t st = m->ctx->stream;
   launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
   CHECK_LAUNCH("TLMModel");
-  return run_token(m, (flags & TLM_LOGITS) != 0);
+  return run_token(m, (flags & TLM_LOGITS) != 0, position);
 }
 
 // Why the batched prefill cannot serve this model (null: it can).
@@ -1418,7 +1439,7 @@ int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end)
     } else {  // the decode graph replayed per position
       launch_set_ctrl(m->ctrl, tokens[p], p, 0, start, end - start, emb_stage(m), st);
       CHECK_LAUNCH("TLMModel");
-      for (int i = 0; i < n && !rc; i++) rc = run_token(m, false);
+      for (int i = 0; i < n && !rc; i++) rc = run_token(m, false, p + i);
     }
     if (rc) return rc;
     p += n;
@@ -1470,7 +1491,7 @@ int tlm_decode_greedy(tlm_model* m, int32_t token, int32_t position, int n, int3
   launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
   CHECK_LAUNCH("TLMModel");
   for (int i = 0; i < n; i++) {
-    rc = run_token(m, true);
+    rc = run_token(m, true, position + i);
     if (rc) return rc;
   }
   HIP_TRY(hipStreamSynchronize(st));
@@ -1544,7 +1565,7 @@ int tlm_time_decode(tlm_model* m, int32_t token, int32_t position, int warmup, i
   hipStream_t st = m->ctx->stream;
   launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
   for (int i = 0; i < warmup; i++) {
-    rc = run_token(m, true);
+    rc = run_token(m, true, position + i);
     if (rc) return rc;
   }
   hipEvent_t e0, e1;
@@ -1553,7 +1574,7 @@ int tlm_time_decode(tlm_model* m, int32_t token, int32_t position, int warmup, i
   HIP_TRY(hipStreamSynchronize(st));
   HIP_TRY(hipEventRecord(e0, st));
   for (int i = 0; i < n; i++) {
-    rc = run_token(m, true);
+    rc = run_token(m, true, position + warmup + i);
     if (rc) return rc;
   }
   HIP_TRY(hipEventRecord(e1, st));
@@ -1574,19 +1595,22 @@ int tlm_time_head(tlm_model* m, int32_t token, int32_t position, int n, double* 
   rc = tlm_model_finalize(m);
   if (rc) return rc;
   hipStream_t st = m->ctx->stream;
-  if (m->use_graphs && !m->g_layers) {
-    rc = capture(m, TAIL_NONE, &m->graph_layers, &m->g_layers);
-    if (rc) return rc;
-  }
+  for (int lw = 0; lw < 2 && m->use_graphs; lw++)
+    if (!m->g_layers[lw]) {
+      rc = capture(m, TAIL_NONE, lw, &m->graph_layers[lw], &m->g_layers[lw]);
+      if (rc) return rc;
+    }
   std::vector<hipEvent_t> ev(2 * (size_t)n, nullptr);
   for (auto& e : ev) HIP_TRY(hipEventCreate(&e));
   launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
   bool ok = true;
   for (int i = 0; i < n && ok; i++) {
+    const bool lw = long_window(&m->attn, position + i);
+    m->host_pos = position + i;
     if (m->use_graphs) {
-      HIP_TRY(hipGraphLaunch(m->g_layers, st));
+      HIP_TRY(hipGraphLaunch(m->g_layers[lw], st));
     } else {
-      for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1);
+      for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1, lw);
     }
     ok &= enqueue_head(m, st, true, &ev[2 * (size_t)i]);
   }
@@ -1617,7 +1641,8 @@ int tlm_time_kernel(tlm_model* m, int which, int iters, double* avg_ms) {
     if (which == 6)  // top-8 candidates over the logits
       return launch_topk(m->logits, m->d.vocab_size, 8, 0.f, m->ctx->topk_v, m->ctx->topk_i, kTopkWork, m->cand_v,
                          m->cand_i, st);
-    return which == 0 ? enqueue_head(m, st, false) : enqueue_layer(m, 0, st, which);
+    return which == 0 ? enqueue_head(m, st, false)
+                      : enqueue_layer(m, 0, st, which, long_window(&m->attn, m->host_pos));
   };
   if (!one()) return fail(TLM_ERR_STATE, "TLMModel: no kernel variant for stage %d", which);  // warm
   CHECK_LAUNCH("TLMModel");
@@ -1653,7 +1678,7 @@ int tlm_model_describe(tlm_model* m, char* out, size_t len) {
            L.gu->N, L.gu->K, L.down->N, L.down->K, L.gu->T, kMlpWaves, m->mlp_nch, m->mlp_ndb);
   std::string s = "qkv[" + p(L.qkv) + "] o[" + p(L.o) + "] mlp[" + mlp + "] head[" +
                   p(m->head) + " grid=" + std::to_string(m->lm_plan.gx) + " waves=" +
-                  std::to_string(m->lm_plan.waves) + "] attn[nsplit=" + std::to_string(m->attn.nsplit) +
+                  std::to_string(m->lm_plan.waves) + "] attn[nsplit=" + std::to_string(m->attn.nsplit) + "/" + std::to_string(m->attn.nsplit_long) +
                   " G=" + std::to_string(m->attn.G) + "]";
   snprintf(out, len, "%s", s.c_str());
   return TLM_OK;

@@ -9,6 +9,7 @@ constexpr int kTile = 64;      // output rows per tile: one row per lane of a wa
 constexpr int kMaxChunks = 8;  // most 16-byte chunks a wave keeps in flight per batch
 constexpr int kMaxPart = 8;    // partial vectors a consumer folds in with one round trip
 constexpr int kAttnWaves = 4;  // decode attention: waves per block, each a quarter of the block's chunk
+constexpr int kLongWindow = 1024; // decode attention: windows above this many positions run the long-window kernels
 // Residual stream accumulators: kRep replicas of an int64 fixed-point vector
 // (value * 2^32).  Producers add into replica (block % kRep) with device-scope
 // atomics; integer addition is associative, so the sum is exact and the same
@@ -134,7 +135,7 @@ constexpr int kMlpWaves = 8;
 // pro: PRO_COPY (input a.in) or PRO_RMSF (the final norm fused in); nch up to 16
 bool launch_lm_head(int fmt, int pro, int waves, int nch, dim3 grid, const GemvArgs& a, hipStream_t st);
 // attention chunk partials; with `combine` also the combine kernel writing a.out
-bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, bool combine, hipStream_t st);
+bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, bool combine, bool long_win, hipStream_t st);
 size_t gemv_smem_bytes(int fmt, int cps, int waves);
 void launch_rmsnorm(const float* x, const float* w, int n, float eps, int offset, float* y, hipStream_t st);
 void launch_silu_mul(const float* g, const float* u, int n, float* out, hipStream_t st);
@@ -151,7 +152,7 @@ void launch_dequant(int fmt, const uint4* w, const uint16_t* s, int N, int T, in
                     hipStream_t st);
 void launch_kv_fill(void* kc, void* vc, bool f32, size_t heads_stride, int Hkv, int max_tokens, int D, int count,
                     uint64_t seed, hipStream_t st);
-size_t attn_smem_bytes(int gmax, int D, bool kv_f32);
+size_t attn_smem_bytes(int gmax, int D, bool kv_f32, bool long_win);
 int attn_lpp(int D, bool kv_f32);
 // top-k candidates (k <= kTopkMax) of an fp32 vector in the greedy order; the
 // workspace holds two levels of wcap (score, id) pairs each

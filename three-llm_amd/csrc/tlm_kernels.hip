@@ -907,12 +907,12 @@ static constexpr __host__ __device__ inline int head_wave_floats(int dt, int esz
   return (6 * dt + head_tiling(dt, esz).sub + 1024 + 3) & ~3;
 }
 
-// LDS of a head_kernel block: kAttnWaves wave regions, then the merge area
-// [kAttnWaves][2 + DT] (max, sum, unnormalised output of each wave).
-size_t attn_smem_bytes(int gmax, int D, bool kv_f32) {
+// LDS of a head_kernel block: one wave region per wave, then (long windows)
+// the merge area [kAttnWaves][2 + DT] (max, sum, unnormalised output of each wave).
+size_t attn_smem_bytes(int gmax, int D, bool kv_f32, bool long_win) {
   (void)gmax;
-  const int dt = attn_dt(D), esz = kv_f32 ? 4 : 2;
-  return sizeof(float) * ((size_t)kAttnWaves * head_wave_floats(dt, esz) + (size_t)kAttnWaves * (2 + dt));
+  const int dt = attn_dt(D), esz = kv_f32 ? 4 : 2, nw = long_win ? kAttnWaves : 1;
+  return sizeof(float) * ((size_t)nw * head_wave_floats(dt, esz) + (long_win ? (size_t)nw * (2 + dt) : 0));
 }
 
 // Order a wave's own LDS writes before its later reads (regions private to
@@ -968,10 +968,13 @@ struct HeadLoads {
 
 // One block = one query head x one chunk of positions (split-K over the
 // sequence, flash decoding; TSLAttention.ts:306-428 computes the same scores
-// and softmax over the whole window).  A chunk of 32 positions or fewer is one
-// wave's; a longer one is split over up to kAttnWaves waves that merge
-// (max, sum, output) in LDS at the end, so at long windows the combine
-// downstream folds kAttnWaves times fewer partials.  Each wave
+// and softmax over the whole window).  Short windows (LONG false): one wave
+// per block, block b = head b % Hq, chunk b / Hq.  Long windows (LONG): a
+// chunk longer than 32 positions is split over up to kAttnWaves waves that
+// merge (max, sum, output) in LDS at the end, so the combine downstream folds
+// kAttnWaves times fewer partials, and the block numbering is XCD-aware
+// (below).  The host captures one graph per mode and picks it per position.
+// Each wave
 //   * forms its q head and the KV head's new k and v from the QKV partial sums
 //     + bias and applies RoPE (rotate-half, TSLAttention.ts:168-250),
 //   * in the chunk holding `pos`, appends k and v to the cache (head g == 0 of
@@ -981,8 +984,8 @@ struct HeadLoads {
 //   * writes (max, sum, unnormalised output) for the combine.
 // All global loads of the first pass are unconditional and issued before the
 // first use; until the merge a wave touches only its own LDS region.
-template <typename KT, int DT>
-__global__ __launch_bounds__(64 * kAttnWaves) void head_kernel(AttnArgs a) {
+template <typename KT, int DT, bool LONG>
+__global__ __launch_bounds__(64 * (LONG ? kAttnWaves : 1)) void head_kernel(AttnArgs a) {
   extern __shared__ float sm[];
   constexpr int ESZ = sizeof(KT);
   constexpr HeadTiling TL = head_tiling(DT, ESZ);
@@ -992,15 +995,28 @@ __global__ __launch_bounds__(64 * kAttnWaves) void head_kernel(AttnArgs a) {
   constexpr int KW = DL * ESZ / 4;            // K dwords per lane
   // fp16 cache, head_dim 128: the output dims of a lane are adjacent (P.V)
   constexpr bool PAIRD = !GEN && ESZ == 2 && DT == 128;
-  // Block -> (query head, chunk): workgroups go to the 8 XCDs round robin
-  // (block b to XCD b % 8), so the G query heads of one (kv head, chunk) pair
-  // take blocks 8 apart on one XCD and its L2 serves their shared K/V rows:
-  // HBM reads each cached row once instead of once per query head.
-  const int G = a.G, b = blockIdx.x, slot = b >> 3;
-  const int pair = (slot / G) * 8 + (b & 7), g = slot % G;
-  if (pair >= a.Hkv * a.nsplit) return;
-  const int hk = pair % a.Hkv, c = pair / a.Hkv, h = hk * G + g;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  constexpr int NW = LONG ? kAttnWaves : 1;
+  const int G = a.G, b = blockIdx.x;
+  int hk, c, h, g;
+  if (LONG) {
+    // Block -> (query head, chunk): workgroups go to the 8 XCDs round robin
+    // (block b to XCD b % 8), so the G query heads of one (kv head, chunk)
+    // pair take blocks 8 apart on one XCD and its L2 serves their shared K/V
+    // rows: HBM reads each cached row once instead of once per query head.
+    const int slot = b >> 3, pair = (slot / G) * 8 + (b & 7);
+    if (pair >= a.Hkv * a.nsplit) return;
+    g = slot % G;
+    hk = pair % a.Hkv;
+    c = pair / a.Hkv;
+    h = hk * G + g;
+  } else {
+    if (b >= a.Hq * a.nsplit) return;
+    h = b % a.Hq;
+    c = b / a.Hq;
+    hk = h / G;
+    g = h % G;
+  }
+  const int lane = threadIdx.x & 63, wv = LONG ? threadIdx.x >> 6 : 0;
   const int D = GEN ? a.D : DT;
   const int pos = a.ctrl[C_POS];
   if (pos < 0 || pos >= a.max_tokens) return;
@@ -1009,11 +1025,10 @@ __global__ __launch_bounds__(64 * kAttnWaves) void head_kernel(AttnArgs a) {
   // the block's chunk [b0, b1), split over nwu <= kAttnWaves waves of at least
   // 32 positions (block-uniform); this wave's part [t0, t1) may be empty
   const int b0 = cp.first + c * cp.chunk, b1 = min(b0 + cp.chunk, pos + 1);
-  const int nwu = min(kAttnWaves, (b1 - b0 + 31) / 32);
+  const int nwu = LONG ? min(NW, (b1 - b0 + 31) / 32) : 1;
   if (nwu == 1 && wv != 0) return;  // one wave does the whole chunk, no merge
   const int sc = (b1 - b0 + nwu - 1) / nwu;
   const int t0 = min(b0 + wv * sc, b1), t1 = min(t0 + sc, b1);
-  const bool has = t0 < t1;
   const bool own = pos >= t0 && pos < t1;
   float* q_l = sm + wv * head_wave_floats(DT, ESZ);  // [DT]
   float* kn = q_l + DT;       // [DT] new k (rounded like the cache)
@@ -1052,7 +1067,9 @@ __global__ __launch_bounds__(64 * kAttnWaves) void head_kernel(AttnArgs a) {
   // first pass: this lane's K slice and its 64 bytes of the V rows
   HeadLoads<KT, KW, GEN, DL> ld;
   const int row_bytes = D * ESZ;
-  if (has) ld.issue(kh, vh, t0, t1, pl, part, D, row_bytes, lane);
+  // unconditional (the compiler then waits for the prologue loads alone): an
+  // empty part is [b1, b1) with b1 >= 1, so its clamped row b1 - 1 is cached
+  ld.issue(kh, vh, t0, t1, pl, part, D, row_bytes, lane);
   __builtin_amdgcn_sched_barrier(0);
 
   // finish q/k/v: sums, RoPE through LDS pairs, cache rounding
@@ -1173,7 +1190,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void head_kernel(AttnArgs a) {
     return;
   }
   // merge the waves' (max, sum, output) in wave order; wave 0 writes the chunk's partial
-  float* mg = sm + kAttnWaves * head_wave_floats(DT, ESZ);  // [kAttnWaves][2 + DT]
+  float* mg = sm + NW * head_wave_floats(DT, ESZ);  // [NW][2 + DT]
   float* mine = mg + wv * (2 + DT);
 #pragma unroll
   for (int e = 0; e < EPL; e++) {
@@ -1188,10 +1205,10 @@ __global__ __launch_bounds__(64 * kAttnWaves) void head_kernel(AttnArgs a) {
   if (wv != 0) return;
   float M = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < kAttnWaves; w++) M = fmaxf(M, mg[w * (2 + DT)]);
-  float wsc[kAttnWaves], L = 0.f;
+  for (int w = 0; w < NW; w++) M = fmaxf(M, mg[w * (2 + DT)]);
+  float wsc[NW], L = 0.f;
 #pragma unroll
-  for (int w = 0; w < kAttnWaves; w++) {
+  for (int w = 0; w < NW; w++) {
     const float mw = mg[w * (2 + DT)];
     wsc[w] = mw == -INFINITY ? 0.f : __expf(mw - M);
     L = fmaf(mg[w * (2 + DT) + 1], wsc[w], L);
@@ -1199,7 +1216,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void head_kernel(AttnArgs a) {
   for (int d = lane; d < D; d += 64) {
     float od = 0.f;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; w++) od = fmaf(mg[w * (2 + DT) + 2 + d], wsc[w], od);
+    for (int w = 0; w < NW; w++) od = fmaf(mg[w * (2 + DT) + 2 + d], wsc[w], od);
     a.pacc[row * D + d] = od;
   }
   if (lane == 0) {
@@ -1217,24 +1234,25 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     a.out[(size_t)row * a.D + d] = attn_combine_elem(a.pacc, a.pml, row, d, a.D, a.nsplit, cp.nact);
 }
 
-bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, bool combine, hipStream_t st) {
-  (void)gmax;
-  // head_kernel's XCD-aware numbering: groups of 8 (kv head, chunk) pairs x G heads
-  const dim3 grid((unsigned)(((a.Hkv * a.nsplit + 7) / 8) * 8 * a.G));
-  const size_t smem = attn_smem_bytes(gmax, a.D, kv_f32);
+bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, bool combine, bool long_win, hipStream_t st) {
+  // long windows: XCD-aware numbering, groups of 8 (kv head, chunk) pairs x G heads
+  const dim3 grid(long_win ? (unsigned)(((a.Hkv * a.nsplit + 7) / 8) * 8 * a.G) : (unsigned)(a.Hq * a.nsplit));
+  const dim3 block(64 * (long_win ? kAttnWaves : 1));
+  const size_t smem = attn_smem_bytes(gmax, a.D, kv_f32, long_win);
   const int dt = attn_dt(a.D);
-  bool ok = true;
-  if (kv_f32) {
-    if (dt == 32) hipLaunchKernelGGL((head_kernel<float, 32>), grid, dim3(64 * kAttnWaves), smem, st, a);
-    else if (dt == 64) hipLaunchKernelGGL((head_kernel<float, 64>), grid, dim3(64 * kAttnWaves), smem, st, a);
-    else if (dt == 128) hipLaunchKernelGGL((head_kernel<float, 128>), grid, dim3(64 * kAttnWaves), smem, st, a);
-    else ok = false;
-  } else {
-    if (dt == 32) hipLaunchKernelGGL((head_kernel<uint16_t, 32>), grid, dim3(64 * kAttnWaves), smem, st, a);
-    else if (dt == 64) hipLaunchKernelGGL((head_kernel<uint16_t, 64>), grid, dim3(64 * kAttnWaves), smem, st, a);
-    else if (dt == 128) hipLaunchKernelGGL((head_kernel<uint16_t, 128>), grid, dim3(64 * kAttnWaves), smem, st, a);
-    else ok = false;
+#define HEAD_CASE(KT, DTV)                                                                        \
+  if (dt == DTV) {                                                                                \
+    if (long_win) hipLaunchKernelGGL((head_kernel<KT, DTV, true>), grid, block, smem, st, a);     \
+    else hipLaunchKernelGGL((head_kernel<KT, DTV, false>), grid, block, smem, st, a);             \
+    ok = true;                                                                                    \
   }
+  bool ok = false;
+  if (kv_f32) {
+    HEAD_CASE(float, 32) HEAD_CASE(float, 64) HEAD_CASE(float, 128)
+  } else {
+    HEAD_CASE(uint16_t, 32) HEAD_CASE(uint16_t, 64) HEAD_CASE(uint16_t, 128)
+  }
+#undef HEAD_CASE
   if (ok && combine) hipLaunchKernelGGL(attn_combine_kernel, dim3(a.Hq), dim3(128), 0, st, a);
   return ok;
 }
