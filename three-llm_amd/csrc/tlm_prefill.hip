@@ -959,11 +959,25 @@ template <int DT, int NG>
 struct AttnTile {
   static constexpr int KT = 64;            // keys per tile
   static constexpr int KS = DT + 8;        // halves per K row in LDS
-  static constexpr int VS = KT + 4;        // halves per V^T row: 8-byte aligned, conflict-free reads
+  // halves per V row: the four rows a half-wave's transposing reads touch fall
+  // on different banks (row strides of 40 and 80 dwords)
+  static constexpr int VS = DT + (DT == 64 ? 16 : 32);
   static constexpr int PIECES = KT * DT / 8;  // 16-byte pieces of K (or V) per tile
   static constexpr int PPT = PIECES / 256;    // pieces per thread (256 threads per key group)
-  static constexpr int TILE_HALVES = KT * KS + DT * VS;
+  static constexpr int TILE_HALVES = KT * KS + KT * VS;
 };
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16 (gfx950): in each group of 16 lanes, lane j names 4
+// halves in[j][0..3] and lane i receives in[4 k + i / 4][i % 4], k = 0..3.
+// With lane j at V[key0 + j / 4][d0 + 4 (j % 4)], lane i receives
+// V[key0 + k][d0 + i]: four consecutive keys of one dim (checked on the
+// device with an index-valued LDS probe).
+__device__ __forceinline__ half4_t lds_read_tr4(const _Float16* p) {
+  const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (short4_t __attribute__((address_space(3)))*)(p));
+  return __builtin_bit_cast(half4_t, v);
+}
 
 // K and V pieces of one tile in registers: piece i is row i / (DT / 8), dims
 // 8 (i % (DT / 8)) .. + 7; rows past qhi repeat row qhi (their keys are masked).
@@ -980,17 +994,15 @@ struct AttnStage {
       vr[u] = *reinterpret_cast<const uint4*>(vb + src);
     }
   }
-  // K rows as they are, V transposed (V^T[d][key])
+  // K and V rows as they are (V is read transposed, lds_read_tr4)
   __device__ __forceinline__ void store(_Float16* tile, int t) const {
     _Float16* ks = tile;
-    _Float16* vt = tile + AT::KT * AT::KS;
+    _Float16* vs = tile + AT::KT * AT::KS;
 #pragma unroll
     for (int u = 0; u < AT::PPT; u++) {
       const int i = t + 256 * u, r = i / (DT / 8), c8 = i % (DT / 8);
       *reinterpret_cast<uint4*>(&ks[r * AT::KS + 8 * c8]) = kr[u];
-      const half8_t v = as_half8(vr[u]);
-#pragma unroll
-      for (int e = 0; e < 8; e++) vt[(8 * c8 + e) * AT::VS + r] = v[e];
+      *reinterpret_cast<uint4*>(&vs[r * AT::VS + 8 * c8]) = vr[u];
     }
   }
 };
@@ -1098,11 +1110,14 @@ __global__ __launch_bounds__(256 * NG) __attribute__((amdgpu_waves_per_eu(2))) v
         const half8_t pb1 = __builtin_bit_cast(half8_t, make_uint4(pk[b2][4], pk[b2][5], pk[b2][6], pk[b2][7]));
 #pragma unroll
         for (int i = 0; i < NDT; i++) {
-          const _Float16* vr0 = vbuf + (32 * i + l32) * VS + 32 * b2 + 4 * kh;
-          const half4_t x0 = *reinterpret_cast<const half4_t*>(vr0);
-          const half4_t x1 = *reinterpret_cast<const half4_t*>(vr0 + 8);
-          const half4_t x2 = *reinterpret_cast<const half4_t*>(vr0 + 16);
-          const half4_t x3 = *reinterpret_cast<const half4_t*>(vr0 + 24);
+          // lane (16 g + j) names V[32 b2 + 4 kh + j / 4 + 8 s][32 i + 16 (g % 2) + 4 (j % 4)]
+          // and receives keys 32 b2 + 4 kh + 8 s + 0..3 of dim 32 i + l32
+          const _Float16* vr0 = vbuf + (32 * b2 + 4 * kh + (lane & 15) / 4) * VS + 32 * i + 16 * ((lane >> 4) & 1) +
+                                4 * (lane & 3);
+          const half4_t x0 = lds_read_tr4(vr0);
+          const half4_t x1 = lds_read_tr4(vr0 + 8 * VS);
+          const half4_t x2 = lds_read_tr4(vr0 + 16 * VS);
+          const half4_t x3 = lds_read_tr4(vr0 + 24 * VS);
           const half8_t a1 = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
           const half8_t a2 = {x2[0], x2[1], x2[2], x2[3], x3[0], x3[1], x3[2], x3[3]};
           o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, pb0, o[i], 0, 0, 0);
