@@ -91,22 +91,24 @@ def test_linear_rows_rejects_unsupported(ctx):
 
 # -------------------------------------------------------------- attention --
 
-@pytest.mark.parametrize("heads,kv,D,theta,before,rows,window", [
-    (14, 2, 64, 1e6, 0, 127, 0),      # Qwen2.5-0.5B heads, one prompt chunk
-    (32, 8, 64, 5e5, 0, 300, 0),      # Llama-3.2-1B heads
-    (24, 8, 128, 5e5, 0, 100, 0),     # Llama-3.2-3B heads (head_dim 128)
-    (14, 2, 64, 1e6, 45, 90, 0),      # continuation after 45 decoded positions
-    (4, 2, 64, 1e4, 20, 200, 50),     # sliding window
-    (8, 1, 128, 1e4, 3, 1, 0),        # one row
+@pytest.mark.parametrize("heads,kv,D,theta,before,rows,window,rd", [
+    (14, 2, 64, 1e6, 0, 127, 0, 64),      # Qwen2.5-0.5B heads, one prompt chunk
+    (32, 8, 64, 5e5, 0, 300, 0, 64),      # Llama-3.2-1B heads
+    (24, 8, 128, 5e5, 0, 100, 0, 128),    # Llama-3.2-3B heads (head_dim 128)
+    (14, 2, 64, 1e6, 45, 90, 0, 64),      # continuation after 45 decoded positions
+    (4, 2, 64, 1e4, 20, 200, 50, 64),     # sliding window
+    (8, 1, 128, 1e4, 3, 1, 0, 128),       # one row
+    (8, 2, 64, 1e4, 10, 71, 0, 32),       # partial rotary: dims 32..63 pass through
 ])
-def test_attention_rows_match_oracle(ctx, heads, kv, D, theta, before, rows, window):
+def test_attention_rows_match_oracle(ctx, heads, kv, D, theta, before, rows, window, rd):
     """Positions [before, before + rows) as one batched call after `before`
     decode-op positions; every row against the oracle's attention with the same
     fp16 cache rounding, and the cache rows it appended."""
     rng = np.random.default_rng(heads * D + rows)
-    inv, af = orc.rope_parameters(D, theta)
+    inv, af = orc.rope_parameters(rd, theta)
     T = before + rows + 8
-    A = tlm.Attention(ctx, heads, kv, D, T, inv, attention_factor=af, sliding_window=window, kv_fmt=tlm.FMT_F16)
+    A = tlm.Attention(ctx, heads, kv, D, T, inv, rotary_dim=rd, attention_factor=af, sliding_window=window,
+                      kv_fmt=tlm.FMT_F16)
     kc = np.zeros((T, kv * D), np.float32)
     vc = np.zeros_like(kc)
     width = (heads + 2 * kv) * D
@@ -114,11 +116,12 @@ def test_attention_rows_match_oracle(ctx, heads, kv, D, theta, before, rows, win
     for pos in range(before):
         qkv = f32(rng.standard_normal(width))
         A(ctx.array(qkv), pos, out1)
-        orc.attention(qkv, heads, kv, D, pos, kc, vc, inv, attention_factor=af, sliding_window=window, kv_f16=True)
+        orc.attention(qkv, heads, kv, D, pos, kc, vc, inv, rotary_dim=rd, attention_factor=af,
+                      sliding_window=window, kv_f16=True)
     qkv = f32(rng.standard_normal((rows, width)))
     got = A.rows(ctx.array(qkv), rows, before, ctx.buffer(2 * rows * heads * D)).read(np.uint16)
     got = got.view(np.float16).astype(np.float32).reshape(rows, heads * D)
-    ref = np.stack([orc.attention(qkv[i], heads, kv, D, before + i, kc, vc, inv, attention_factor=af,
+    ref = np.stack([orc.attention(qkv[i], heads, kv, D, before + i, kc, vc, inv, rotary_dim=rd, attention_factor=af,
                                   sliding_window=window, kv_f16=True) for i in range(rows)])
     # fp16 q, probabilities and output on top of the cache rounding
     close(got, ref, 4e-3, 4e-3)

@@ -763,7 +763,18 @@ GemmShape gemm_shape(int fmt, int epi, int M, int N, int K, int cus) {
     s.wn = 4;
   }
   int splits = 1;
-  if (epi == GEMM_PART) {  // split K until the grid holds about 8 waves per CU
+  if (epi == GEMM_PART && s.ring && !s.kw) {
+    // four-wave ring blocks, two per CU: pick the split count with the least
+    // (rounds of blocks x steps per block) + the split slices' write and read
+    // (M N 8 bytes each at ~6 TB/s, in units of a ~1 us step)
+    const double slice_steps = (double)M * N * 8.0 / 6e6;
+    double best = 1e30;
+    for (int sp = 1; sp <= 32 && steps / sp >= min_steps; sp *= 2) {
+      const int rounds = (s.gx * s.gy * sp + 2 * cus - 1) / (2 * cus);
+      const double cost = (double)rounds * ((steps + sp - 1) / sp) + sp * slice_steps;
+      if (cost < best) best = cost, splits = sp;
+    }
+  } else if (epi == GEMM_PART) {  // split K until the grid holds about 8 waves per CU
     const int target = g_split_waves * cus;
     const int waves = s.gx * s.gy * (s.ring ? (s.kw ? 4 : s.wn) : 4);
     while (splits < 32 && waves * splits < target && steps / (2 * splits * kdiv) >= min_steps) splits *= 2;
@@ -912,33 +923,59 @@ __device__ __forceinline__ void rope_store(const RopeKvArgs& a, int m, int pos, 
     static_cast<__half*>(cache)[dst] = __float2half(y);
 }
 
-// One thread per element of the fused q|k|v row (grid: rows x 256-element
-// chunks), so every load of a thread is issued at once; the first element of
-// a rotated pair writes both.
-__global__ __launch_bounds__(256) void rope_kv_kernel(RopeKvArgs a) {
-  const int m = blockIdx.x, pos = a.p0 + m, D = a.D;
-  const int nq = a.Hq * D, nk = a.Hkv * D, half = a.rd / 2;
-  const int width = nq + 2 * nk;
-  const int i = blockIdx.y * 256 + threadIdx.x;
-  if (i >= width) return;
-  const float* row = a.qkv + (size_t)m * width;
-  const int d = i % D;
-  const bool rot = i < nq + nk && d < a.rd;
-  if (rot && d >= half) return;  // the pair's first thread writes both
-  const float x = fold_slices(row, a.bias, a.n_part, a.pstride, i);
-  if (!rot) {
-    rope_store(a, m, pos, i, x);
-    return;
+// Pair pi of a q|k|v row: head pi / (D / 2), q = pi % (D / 2).  In a rotated
+// head (q or k) q < rd / 2 is the rotate-half pair (d, d + rd / 2) and the
+// rest covers dims rd.. two at a time; a v head takes dims 2 q, 2 q + 1.
+__device__ __forceinline__ void rope_pair(const RopeKvArgs& a, int pi, int& i0, int& i1, bool& rot, int& dr) {
+  const int hd = a.D / 2, h = pi / hd, q = pi - h * hd, half = a.rd / 2;
+  rot = h < a.Hq + a.Hkv && q < half;
+  dr = q;
+  if (rot) {
+    i0 = h * a.D + q;
+    i1 = i0 + half;
+  } else {
+    const int d = h < a.Hq + a.Hkv ? a.rd + 2 * (q - half) : 2 * q;
+    i0 = h * a.D + d;
+    i1 = i0 + 1;
   }
-  const float x2 = fold_slices(row, a.bias, a.n_part, a.pstride, i + half);
-  const float c = a.rope_cos[(size_t)pos * half + d], sn = a.rope_sin[(size_t)pos * half + d];
-  rope_store(a, m, pos, i, x * c - x2 * sn);
-  rope_store(a, m, pos, i + half, x2 * c + x * sn);
+}
+
+// RoPE + cache append of the rows' q|k|v (the split-K slices summed with the
+// bias first; TSLAttention.ts:168-286 for one row).  Thread = one element
+// pair of RKV_ROWS consecutive rows (grid: row groups x 256-pair chunks): no
+// idle threads, and the 2 RKV_ROWS n_part loads of a thread go out at once.
+constexpr int RKV_ROWS = 2;
+__global__ __launch_bounds__(256) void rope_kv_kernel(RopeKvArgs a) {
+  const int D = a.D, width = (a.Hq + 2 * a.Hkv) * D;
+  const int pi = blockIdx.y * 256 + threadIdx.x;
+  if (pi >= width / 2) return;
+  int i0, i1, dr;
+  bool rot;
+  rope_pair(a, pi, i0, i1, rot, dr);
+  const int half = a.rd / 2;
+  float x0[RKV_ROWS], x1[RKV_ROWS], c[RKV_ROWS], sn[RKV_ROWS];
+#pragma unroll
+  for (int r = 0; r < RKV_ROWS; r++) {
+    const int m = min(blockIdx.x * RKV_ROWS + r, a.M - 1), pos = a.p0 + m;
+    const float* row = a.qkv + (size_t)m * width;
+    x0[r] = fold_slices(row, a.bias, a.n_part, a.pstride, i0);
+    x1[r] = fold_slices(row, a.bias, a.n_part, a.pstride, i1);
+    c[r] = rot ? a.rope_cos[(size_t)pos * half + dr] : 1.f;
+    sn[r] = rot ? a.rope_sin[(size_t)pos * half + dr] : 0.f;
+  }
+#pragma unroll
+  for (int r = 0; r < RKV_ROWS; r++) {
+    const int m = blockIdx.x * RKV_ROWS + r;
+    if (m >= a.M) break;
+    const int pos = a.p0 + m;
+    rope_store(a, m, pos, i0, rot ? x0[r] * c[r] - x1[r] * sn[r] : x0[r]);
+    rope_store(a, m, pos, i1, rot ? x1[r] * c[r] + x0[r] * sn[r] : x1[r]);
+  }
 }
 
 void launch_rope_kv(const RopeKvArgs& a, hipStream_t st) {
-  const int width = (a.Hq + 2 * a.Hkv) * a.D;
-  hipLaunchKernelGGL(rope_kv_kernel, dim3(a.M, (width + 255) / 256), dim3(256), 0, st, a);
+  const int pairs = (a.Hq + 2 * a.Hkv) * a.D / 2;
+  hipLaunchKernelGGL(rope_kv_kernel, dim3((a.M + RKV_ROWS - 1) / RKV_ROWS, (pairs + 255) / 256), dim3(256), 0, st, a);
 }
 
 // ------------------------------------------------------- flash attention --
