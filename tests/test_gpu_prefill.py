@@ -52,6 +52,7 @@ def make_linear(ctx, fmt, w):
     (tlm.FMT_Q4, 127, 1152, 896), (tlm.FMT_Q4, 200, 896, 4864), (tlm.FMT_Q4, 65, 200, 96),
     (tlm.FMT_Q4, 300, 2048, 2048), (tlm.FMT_Q4, 33, 64, 32),
     (tlm.FMT_Q4, 300, 44032, 64),  # 172 x 3 blocks of 256 columns, ragged last block
+    (tlm.FMT_Q4, 1100, 4096, 128),  # 9 x 16 blocks of 128 rows x 256 columns, the last 76 rows
     (tlm.FMT_F16, 70, 256, 64), (tlm.FMT_F16, 5, 37, 32), (tlm.FMT_F16, 130, 512, 256)])
 def test_linear_rows_matches_fp16_operand_product(ctx, fmt, M, N, K):
     """Each row equals bias + W x with x and W rounded to fp16 (the device's
