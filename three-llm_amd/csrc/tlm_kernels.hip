@@ -257,17 +257,33 @@ struct GemvPrologue {
 #pragma unroll
       for (int r = 0; r < R; r++) {
         const int f = min(tid + r * nt, K4 - 1);
-        w[r] = *reinterpret_cast<const float4*>(a.norm_w + 4 * f);
-        if (kRmsF) {
+        // a wave holding no element of the row issues no loads (wave-uniform):
+        // each vector load instruction costs the CU's memory pipeline the same
+        // time whether its lanes read one cache line or sixteen
+        const bool held = (tid & ~63) + r * nt < K4;
+        if (held) {
+          w[r] = *reinterpret_cast<const float4*>(a.norm_w + 4 * f);
+          if (kRmsF) {
 #pragma unroll
-          for (int q = 0; q < kRep; q++) {
-            const ulonglong2* src = reinterpret_cast<const ulonglong2*>(a.acc_in + (size_t)q * a.K + 4 * f);
-            fx[kRmsF ? r : 0][q][0] = src[0];
-            fx[kRmsF ? r : 0][q][1] = src[1];
+            for (int q = 0; q < kRep; q++) {
+              const ulonglong2* src = reinterpret_cast<const ulonglong2*>(a.acc_in + (size_t)q * a.K + 4 * f);
+              fx[kRmsF ? r : 0][q][0] = src[0];
+              fx[kRmsF ? r : 0][q][1] = src[1];
+            }
+          } else {
+            x[r] = *reinterpret_cast<const float4*>(a.base + 4 * f);
+            load_parts(a.pin, a.n_pin, a.pin_stride, 4 * f, p[r]);
           }
         } else {
-          x[r] = *reinterpret_cast<const float4*>(a.base + 4 * f);
-          load_parts(a.pin, a.n_pin, a.pin_stride, 4 * f, p[r]);
+          w[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (kRmsF) {
+#pragma unroll
+            for (int q = 0; q < kRep; q++) fx[kRmsF ? r : 0][q][0] = fx[kRmsF ? r : 0][q][1] = make_ulonglong2(0, 0);
+          } else {
+            x[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int j = 0; j < kMaxPart; j++) p[r][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+          }
         }
       }
     } else if (fast) {
@@ -435,7 +451,11 @@ __device__ __forceinline__ float dot_q4(const uint4 d, const float* __restrict__
   float a0 = 0.f, a1 = 0.f;
 #pragma unroll
   for (int j = 0; j < 4; j++) {
-    const uint32_t lo = wv[j] & 0x0F0F0F0Fu, hi = (wv[j] >> 4) & 0x0F0F0F0Fu;
+    uint32_t lo = wv[j] & 0x0F0F0F0Fu, hi = (wv[j] >> 4) & 0x0F0F0F0Fu;
+    // opaque to the optimiser: otherwise it folds the masks into per-nibble
+    // bit-field extracts (v_bfe_u32 + v_cvt_f32_ubyte0) instead of converting
+    // byte k of lo / hi directly (v_cvt_f32_ubyte{0..3}), 24 more VALU per chunk
+    asm("" : "+v"(lo), "+v"(hi));
     const float4 xa = *reinterpret_cast<const float4*>(x + 8 * j);
     const float4 xb = *reinterpret_cast<const float4*>(x + 8 * j + 4);
     a0 = fmaf((float)(lo & 0xFFu), xa.x, a0);
