@@ -495,7 +495,7 @@ int tlm_op_linear_rows(tlm_linear* L, const uint16_t* x, int32_t rows, const flo
     return fail(TLM_ERR_INVALID, "TLMLinear: q4 scale above 8188 overflows the fp16 GEMM operand");
   const GemmShape sh = gemm_shape(wfmt(L->fmt), GEMM_STORE, rows, L->N, L->K, L->ctx->cus);
   if (!launch_gemm(wfmt(L->fmt), GEMM_STORE, sh, g, L->ctx->stream))
-    return fail(TLM_ERR_INVALID, "TLMLinear: batched rows need K %% 32 == 0 (K = %d)", L->K);
+    return fail(TLM_ERR_STATE, "TLMLinear: no batched kernel variant for %d x %d", L->N, L->K);
   CHECK_LAUNCH("TLMLinear");
   return TLM_OK;
 }
@@ -747,11 +747,12 @@ int tlm_op_attention_rows(tlm_attn* A, const float* qkv, int32_t rows, int32_t p
   pa.max_tokens = d.max_tokens;
   pa.window = d.sliding_window;
   pa.scale_log2 = A->scale * 1.4426950408889634f;
-  launch_prefill_attention(pa, st);
+  const bool launched = launch_prefill_attention(pa, st);
   hipError_t e = hipGetLastError();
   if (e == hipSuccess) e = hipStreamSynchronize(st);
   hipFree(q);
   if (e != hipSuccess) return fail(TLM_ERR_HIP, "TLMAttention: batched rows failed: %s", hipGetErrorString(e));
+  if (!launched) return fail(TLM_ERR_STATE, "TLMAttention: no batched attention kernel for this shape");
   return TLM_OK;
 }
 
