@@ -109,6 +109,24 @@ def test_tiny_config_greedy_stream(ctx):
     om.close()
 
 
+def test_decode_reaches_the_last_cache_position(ctx):
+    """Tiny config with a 40-position cache: prompt 16, then greedy decode
+    through position 39 (the last row of the cache) equal to the oracle's
+    stream; position 40 is refused."""
+    wl = W.WORKLOADS["tiny"]
+    hw = W.synthetic(wl)
+    hw.keep = True
+    runner = R.DecoderHIPRunner(hw, {"maxTokens": 40}, ctx=ctx)
+    om = oracle_model(hw, 40, kv_f16=True)
+    prompt = W.prompt_tokens(wl)[:16]
+    dev, ref, gaps = greedy_against_oracle(runner, om, prompt, 25)
+    assert_streams_match(dev, ref, gaps)
+    with pytest.raises(tlm.TlmError):
+        runner.computeToken(int(dev[-1]), 40, True)
+    runner.close()
+    om.close()
+
+
 def _reduced_qwen(layers):
     wl = W.WORKLOADS["qwen2.5-0.5b"]
     cfg = dict(wl.config, num_hidden_layers=layers)

@@ -164,6 +164,27 @@ def test_attention_reference_cases(ctx, case):
     A.close()
 
 
+@pytest.mark.parametrize("kv_fmt", [tlm.FMT_F16, tlm.FMT_F32], ids=["f16", "f32"])
+def test_attention_window_of_one_returns_the_current_value_row(ctx, kv_fmt):
+    """A sliding window of 1 leaves only the current position: the softmax over
+    one score is 1, so every query head's output is its kv head's new V row
+    (rounded like the cache), whatever q and the cached past hold."""
+    heads, kv, D, T = 4, 2, 64, 48
+    inv = orc.rope_parameters(D, 1e4)[0]
+    A = tlm.Attention(ctx, heads, kv, D, T, inv, sliding_window=1, kv_fmt=kv_fmt)
+    out = ctx.buffer(4 * heads * D)
+    rng = np.random.default_rng(11)
+    for pos in range(T):
+        qkv = rng.standard_normal((heads + 2 * kv) * D).astype(np.float32)
+        got = A(ctx.array(qkv), pos, out).read().reshape(heads, D)
+        v = qkv[(heads + kv) * D:].reshape(kv, D)
+        if kv_fmt == tlm.FMT_F16:
+            v = v.astype(np.float16).astype(np.float32)
+        want = np.repeat(v, heads // kv, axis=0)
+        close(got, want, 1e-7, 1e-6)
+    A.close()
+
+
 @pytest.mark.parametrize("heads,kv,D,theta,steps,window", [(14, 2, 64, 1e6, 700, 0), (24, 8, 128, 5e5, 300, 0),
                                                            (32, 8, 64, 5e5, 1100, 0), (4, 2, 64, 1e4, 300, 100)])
 def test_attention_long_fp16_cache(ctx, heads, kv, D, theta, steps, window):
