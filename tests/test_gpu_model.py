@@ -127,6 +127,33 @@ def test_decode_reaches_the_last_cache_position(ctx):
     om.close()
 
 
+def test_long_window_decode_with_more_than_16_chunks(ctx):
+    """One kv head and a 2200-position cache give 69 short-window chunks and
+    18 long-window chunks per query head, more than the 16 the O projection's
+    prologue folds per round trip (its 24-slot form).  Prompt 1100 positions
+    (batched prefill), then logits at positions 1100..1103 (the long-window
+    mode) against the oracle."""
+    cfg = {"model_type": "llama", "hidden_size": 256, "intermediate_size": 512, "num_hidden_layers": 2,
+           "num_attention_heads": 4, "num_key_value_heads": 1, "head_dim": 64, "vocab_size": 2048,
+           "rope_theta": 1e4, "rms_norm_eps": 1e-6, "tie_word_embeddings": True,
+           "max_position_embeddings": 4096, "eos_token_id": -1}
+    wl = W.Workload("long-window-1kv", cfg, W.Storage(linear="q4", head="f16", embed="f16"), 1104, 1, 2200)
+    hw = W.synthetic(wl)
+    hw.keep = True
+    runner = R.DecoderHIPRunner(hw, {"maxTokens": wl.max_tokens}, ctx=ctx)
+    assert "nsplit=69/18" in runner.model.describe()
+    om = oracle_model(hw, wl.max_tokens, kv_f16=True, threads=16)
+    prompt = W.prompt_tokens(wl)
+    runner.prefillTokens([int(x) for x in prompt[:1100]], 0, 1100)
+    for i in range(1100):
+        om.forward(int(prompt[i]), i)
+    for i in range(1100, 1104):
+        runner.computeToken(int(prompt[i]), i, True)
+        close(runner.readLogits(), om.forward(int(prompt[i]), i), LOGIT_ATOL, LOGIT_RTOL)
+    runner.close()
+    om.close()
+
+
 def _reduced_qwen(layers):
     wl = W.WORKLOADS["qwen2.5-0.5b"]
     cfg = dict(wl.config, num_hidden_layers=layers)

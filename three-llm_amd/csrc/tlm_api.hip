@@ -1111,7 +1111,8 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which, bool l
     // (layer 0: the previous token's final norm): clear it for its next use
     a.zero_ptr = m->rb + (size_t)((l + nl - 1) % nl) * rstride;
     a.zero_n = (int)rstride;
-    ok &= launch_linear(L.o, PRO_ATTN, a, st);
+    // more than 16 long-window chunks: the 24-slot combine keeps it to one round trip
+    ok &= launch_linear(L.o, long_win && a.att_nsplit > 16 ? PRO_ATTN3 : PRO_ATTN, a, st);
   }
   // 4. x_mid = x + O partials; RMSNorm; gate|up; SwiGLU; down, accumulated
   //    with x_mid into rb[l]

@@ -29,6 +29,7 @@ enum Prologue {
   PRO_RMS2 = 4,    // PRO_RMS for K up to 8 elements per thread (chosen by launch_gemv)
   PRO_RMSF = 5,    // x = rmsnorm(sum of the kRep fixed-point replicas acc_in) * w
   PRO_RMSF2 = 6,   // PRO_RMSF for K up to 8 elements per thread (chosen by launch_gemv)
+  PRO_ATTN3 = 7,   // PRO_ATTN folding 24 chunk partials per round trip instead of 16 (long windows)
 };
 
 // Split of the attention window [first, pos] into chunks; identical on host and device.

@@ -205,7 +205,11 @@ struct GemvPrologue {
   ulonglong2 fx[kRmsF ? R : 1][kRep][2];  // RMSF: the 4 elements' replicas
   float4 p[2][kMaxPart];  // RMS: partials per float4 (R rows); SWIGLU: [0] gate, [1] up partials
   static constexpr int kSlotLanes = 8;  // ATTN: lanes sharing one float4, splitting its chunk slots
-  static constexpr int kSlotsPerLane = 2;
+  static constexpr bool kAttn = PRO == PRO_ATTN || PRO == PRO_ATTN3;
+  // chunk slots per lane: 16 per float4 and round trip, or 24 for the long-
+  // window combine (17 chunks at 16384 positions would otherwise take a second
+  // dependent round trip; the short windows keep the smaller first load)
+  static constexpr int kSlotsPerLane = PRO == PRO_ATTN3 ? 3 : 2;
   float2 ml[kSlotsPerLane];  // ATTN: (m, l) and accumulators of this lane's chunk slots
   float4 ac[kSlotsPerLane];
   int nact;
@@ -234,7 +238,7 @@ struct GemvPrologue {
     } else if (PRO == PRO_SWIGLU) {
       load_parts(a.pin, a.n_pin, a.pin_stride, kc, p[0]);
       load_parts(a.pin + a.up_off, a.n_pin, a.pin_stride, kc, p[1]);
-    } else if (PRO == PRO_ATTN) {
+    } else if (kAttn) {
       // slots jb + (lane & 7) + 8u of the float4 at f
       const int row = kc / a.att_D, d = kc % a.att_D;
       const float* mlp = a.pml + (size_t)row * a.att_nsplit * 2;
@@ -251,7 +255,7 @@ struct GemvPrologue {
 
   __device__ __forceinline__ void issue(const GemvArgs& a, int k0, int klen_pad) {
     const int tid = threadIdx.x, nt = blockDim.x;
-    fast = (a.K & 3) == 0 && (PRO != PRO_ATTN || (a.att_D & 3) == 0);
+    fast = (a.K & 3) == 0 && (!kAttn || (a.att_D & 3) == 0);
     if (kRms) {
       const int K4 = a.K >> 2;
 #pragma unroll
@@ -289,7 +293,7 @@ struct GemvPrologue {
     } else if (fast) {
       // ATTN: the first chunk slots are read before the position is known
       // (slots past the active count are masked in attn_finish)
-      load_slice4(a, PRO == PRO_ATTN ? tid / kSlotLanes : tid, k0, klen_pad / 4, 0, a.att_nsplit);
+      load_slice4(a, kAttn ? tid / kSlotLanes : tid, k0, klen_pad / 4, 0, a.att_nsplit);
     }
   }
 
@@ -302,7 +306,7 @@ struct GemvPrologue {
       return make_float4(g.x / (1.f + __expf(-g.x)) * u.x, g.y / (1.f + __expf(-g.y)) * u.y,
                          g.z / (1.f + __expf(-g.z)) * u.z, g.w / (1.f + __expf(-g.w)) * u.w);
     }
-    return x[0];  // not reached for PRO_ATTN (attn_finish)
+    return x[0];  // not reached for the attention prologues (attn_finish)
   }
 
   // Flash-decoding combine of the attention chunk partials: eight lanes share
@@ -382,7 +386,7 @@ struct GemvPrologue {
                          float* xm = nullptr) {
     const int tid = threadIdx.x, nt = blockDim.x;
     // the position is read here, after the weight loads are issued
-    if (PRO == PRO_ATTN) nact = chunk_plan(a.ctrl[C_POS], a.att_window, a.att_nsplit, a.att_chmin).nact;
+    if (kAttn) nact = chunk_plan(a.ctrl[C_POS], a.att_window, a.att_nsplit, a.att_chmin).nact;
     if (kRms) {
       // residual stream x = base + sum(pin), then TSLRMSNorm.ts:50-74 over all K
       const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && a.xout != nullptr;
@@ -428,7 +432,7 @@ struct GemvPrologue {
         }
         xl[i] = y;
       }
-    } else if (PRO == PRO_ATTN) {
+    } else if (kAttn) {
       attn_finish(a, xl, xsum, k0, klen_pad);
     } else {
       const int n4 = klen_pad / 4;
@@ -743,6 +747,8 @@ bool launch_gemv(int fmt, int pro, int waves, int nch, dim3 grid, const GemvArgs
   GEMV_W(WF_Q4, PRO_SWIGLU)
   GEMV_W(WF_Q4, PRO_ATTN)
   GEMV_W(WF_F16, PRO_ATTN)
+  GEMV_W(WF_Q4, PRO_ATTN3)
+  GEMV_W(WF_F16, PRO_ATTN3)
   GEMV_W(WF_F16, PRO_COPY)
   GEMV_W(WF_F16, PRO_RMSF)
   GEMV_W(WF_F16, PRO_RMSF2)
