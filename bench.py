@@ -67,11 +67,14 @@ def bytes_per_token(hw, position: int, kv_first: int = 0) -> float:
     return lin + head + emb + norms + (position + 1 - kv_first) * kv_row + kv_row
 
 
-def lm_head_bytes(hw) -> float:
+def lm_head_bytes(hw, cus: int) -> float:
     """Algorithmic bytes of one LM head launch: fp16 head rows, the normed
-    hidden vector, the logits and the per-block argmax partials."""
+    hidden vector, the logits and the per-block argmax partials (one per
+    block: ceil(T / per) blocks of per = ceil(T / (2 cus)) 64-row tiles)."""
     r = hw.recipe
-    blocks = min((r.vocab_size + 63) // 64, 4096)
+    tiles = (r.vocab_size + 63) // 64
+    per = max(-(-tiles // (2 * cus)), -(-tiles // 4096))
+    blocks = -(-tiles // per)
     return r.vocab_size * r.hidden_size * 2.0 + r.hidden_size * 4 + r.vocab_size * 4 + blocks * 8
 
 
@@ -258,7 +261,7 @@ def main():
     # dominant kernel: the LM head, timed inside decode steps over the same
     # positions (a pair of HIP events on the model stream around each launch)
     lm_ms = runner.model.time_head(last, pos0, min(steps, args.kernel_iters))
-    lm_bytes = lm_head_bytes(hw)
+    lm_bytes = lm_head_bytes(hw, ctx.info()[1])
     lm_bw = lm_bytes / (lm_ms * 1e-3)
     # host-driven loop (computeToken + sampleToken per token: one 4-byte
     # device-to-host read and one stream sync per token over PCIe)

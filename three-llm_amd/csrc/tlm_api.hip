@@ -812,11 +812,22 @@ int tlm_attn_read_cache(tlm_attn* A, int count, float* k_out, float* v_out) {
 
 // ------------------------------------------------------------------- logits --
 
+// LM head grid: every block resident at once (two 8-wave blocks per CU) with
+// the same number of 64-row tiles, at most 4096 blocks (the argmax partials).
+// One block per tile ran ~4.6 rounds with a ragged last one (47 us at
+// 151936 x 896 on 256 CUs); five tiles per block (475 blocks) took 44.5 us.
+// Counts that leave some CUs a block more than others were slower (6, 7 and 8
+// tiles per block: 48-58 us).
+static int lm_head_grid(int T, int cus) {
+  const int per = std::max((T + 2 * cus - 1) / (2 * cus), (T + 4095) / 4096);
+  return (T + per - 1) / per;
+}
+
 int tlm_op_logits(tlm_linear* head, const float* x, float* logits, int32_t* token) {
   if (!head || !x || !token) return fail(TLM_ERR_INVALID, "TLMLogits: null argument");
   tlm_ctx* ctx = head->ctx;
   GemvPlan p = plan_gemv(head->T, head->C, ctx->cus, chunk_k(head->fmt), true);
-  p.gx = std::min(head->T, 4096);
+  p.gx = lm_head_grid(head->T, ctx->cus);
   GemvArgs a;
   fill_gemv_args(a, head, nullptr);
   a.cps = p.cps;
@@ -943,7 +954,7 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
     if (mlp_smem_bytes(wfmt(lf), L0.gu->C, H) > 65536)
       rc = fail(TLM_ERR_INVALID, "TLMModel: hidden size %d too large for the fused MLP block", H);
     m->lm_plan = plan_gemv(m->head->T, m->head->C, ctx->cus, chunk_k(m->head->fmt), true);
-    m->lm_plan.gx = std::min(m->head->T, 4096);
+    m->lm_plan.gx = lm_head_grid(m->head->T, ctx->cus);
     {  // every chunk of a wave's row slice in flight at once (up to 16)
       const int per = (m->head->C + m->lm_plan.waves - 1) / m->lm_plan.waves;
       m->lm_plan.nch = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : 16;
