@@ -945,7 +945,7 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
     const Layer& L0 = m->layers[0];
     M_TRY(model_alloc((void**)&m->pq, sizeof(float) * L0.qkv->plan.splits * m->Nqkv));
     M_TRY(model_alloc((void**)&m->po, sizeof(float) * L0.o->plan.splits * H));
-    // fused MLP: 8 waves; gate|up chunks and down (tile, chunk) items per wave
+    // fused MLP: kMlpWaves waves; gate|up chunks and down (tile, chunk) items per wave
     const int per = (L0.gu->C + kMlpWaves - 1) / kMlpWaves;
     m->mlp_nch = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : 8;
     const int items = L0.down->T * (32 / chunk_k(lf));
