@@ -1341,6 +1341,10 @@ static int prefill_rows(tlm_model* m, const int* tokens, int p0, int M) {
   const int lf = wfmt(d.linear_fmt), cus = m->ctx->cus;
   const Layer& L0 = m->layers[0];
   const GemmShape sq = gemm_shape(lf, GEMM_PART, M, m->Nqkv, H, cus);
+  // small chunks (the K-wave QKV GEMM), head_dim 64, full rotary: RoPE and the
+  // cache append run in the QKV GEMM's epilogue (no split-K slices, no rope_kv)
+  const GemmShape sr = gemm_shape(lf, GEMM_ROPE, M, m->Nqkv, H, cus);
+  const bool rope_epi = sr.ring && sr.kw && D == 64 && d.rotary_dim == 64;
   const GemmShape so = gemm_shape(lf, GEMM_PART, M, H, m->QS, cus);
   const GemmShape sg = gemm_shape(lf, GEMM_SWIGLU, M, L0.gu->T * kTile, H, cus);
   const GemmShape sd = gemm_shape(lf, GEMM_PART, M, H, I, cus);
@@ -1356,29 +1360,44 @@ static int prefill_rows(tlm_model* m, const int* tokens, int p0, int M) {
     launch_rms_rows(rows_args(m->pf_x, m->pf_part, l ? sd.splits : 0, rowsH, H, L.attn_norm, d.rms_eps, m->pf_xn),
                     M, st);
     GemmArgs g = gemm_args(L.qkv, m->pf_xn, H, M);
-    g.Cf = m->pf_part;
-    g.ldc = m->Nqkv;
-    ok = ok && launch_gemm(lf, GEMM_PART, sq, g, st);
-    RopeKvArgs r;
-    memset(&r, 0, sizeof r);
-    r.qkv = m->pf_part;
-    r.n_part = sq.splits;
-    r.pstride = (size_t)M * m->Nqkv;
-    r.bias = L.bqkv;
-    r.M = M;
-    r.p0 = p0;
-    r.Hq = d.num_heads;
-    r.Hkv = d.num_kv_heads;
-    r.D = D;
-    r.rd = d.rotary_dim;
-    r.max_tokens = d.max_tokens;
-    r.rope_cos = m->attn.rope_cos;
-    r.rope_sin = m->attn.rope_sin;
-    r.q = m->pf_q;
-    r.kc = L.kc;
-    r.vc = L.vc;
-    r.kv_f32 = 0;
-    launch_rope_kv(r, st);
+    if (rope_epi) {
+      g.bias = L.bqkv;
+      g.Ch = m->pf_q;
+      g.ldc = m->QS;
+      g.rope_cos = m->attn.rope_cos;
+      g.rope_sin = m->attn.rope_sin;
+      g.p0 = p0;
+      g.Hq = d.num_heads;
+      g.Hkv = d.num_kv_heads;
+      g.max_tokens = d.max_tokens;
+      g.kc = static_cast<uint16_t*>(L.kc);
+      g.vc = static_cast<uint16_t*>(L.vc);
+      ok = ok && launch_gemm(lf, GEMM_ROPE, sr, g, st);
+    } else {
+      g.Cf = m->pf_part;
+      g.ldc = m->Nqkv;
+      ok = ok && launch_gemm(lf, GEMM_PART, sq, g, st);
+      RopeKvArgs r;
+      memset(&r, 0, sizeof r);
+      r.qkv = m->pf_part;
+      r.n_part = sq.splits;
+      r.pstride = (size_t)M * m->Nqkv;
+      r.bias = L.bqkv;
+      r.M = M;
+      r.p0 = p0;
+      r.Hq = d.num_heads;
+      r.Hkv = d.num_kv_heads;
+      r.D = D;
+      r.rd = d.rotary_dim;
+      r.max_tokens = d.max_tokens;
+      r.rope_cos = m->attn.rope_cos;
+      r.rope_sin = m->attn.rope_sin;
+      r.q = m->pf_q;
+      r.kc = L.kc;
+      r.vc = L.vc;
+      r.kv_f32 = 0;
+      launch_rope_kv(r, st);
+    }
     PrefillAttnArgs pa;
     memset(&pa, 0, sizeof pa);
     pa.q = m->pf_q;

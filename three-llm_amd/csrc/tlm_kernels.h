@@ -174,6 +174,8 @@ enum GemmEpi {
   GEMM_STORE = 0,   // Cf[m][n] = acc + bias[n] (no split-K)
   GEMM_PART = 1,    // Cf[z][m][n] = split z's sum (the consumer adds the slices)
   GEMM_SWIGLU = 2,  // Ch[m][i] = fp16(silu(gate) * up), paired gate|up weight rows (no split-K)
+  GEMM_ROPE = 3,    // q|k|v rows, head_dim 64, full rotary: + bias, RoPE at position p0 + m; q to
+                    // Ch (fp16 [M][Hq 64]), k and v to the fp16 caches (K-wave kernel, no split-K)
 };
 struct GemmArgs {
   const uint16_t* A;   // fp16 [M][lda]
@@ -187,6 +189,12 @@ struct GemmArgs {
   int ldc;
   int n_out;           // GEMM_SWIGLU: intermediate size I (outputs i < n_out)
   int spc;             // 32-k steps per split (set by launch_gemm)
+  // GEMM_ROPE
+  const float* rope_cos;  // [max_tokens][32], attention factor folded in
+  const float* rope_sin;
+  int p0, Hq, Hkv, max_tokens;
+  uint16_t* kc;        // fp16 [Hkv][max_tokens][64] (this layer)
+  uint16_t* vc;
 };
 // Tile and split-K choice of one GEMM (gemm_shape is the only planner, so the
 // host sizes the slice buffers from the same numbers the launch uses).

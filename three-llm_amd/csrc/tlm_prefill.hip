@@ -690,6 +690,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     }
 
   const int rbase = m0 + 4 * kh + 8 * wave;
+  if (EPI == GEMM_ROPE) {
+    // tile t0 is one head of 64: q heads, then k, then v.  Lane l32 holds dims
+    // d = l32 and d + 32 of its rows, the rotate-half pair of RoPE
+    // (TSLAttention.ts:168-250 for one row; the rope_kv kernel's arithmetic)
+    const int d = l32, kind = t0 < g.Hq ? 0 : t0 < g.Hq + g.Hkv ? 1 : 2;
+    const int hk = kind == 1 ? t0 - g.Hq : t0 - g.Hq - g.Hkv;
+    const float b0 = g.bias ? g.bias[t0 * kTile + d] : 0.f, b1 = g.bias ? g.bias[t0 * kTile + d + 32] : 0.f;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int row = rbase + 32 * t + e;
+        if (row >= g.M) continue;
+        const int pos = g.p0 + row;
+        const float x0 = f4_at(r[t][0], e) + b0, x1 = f4_at(r[t][1], e) + b1;
+        float y0 = x0, y1 = x1;
+        if (kind < 2) {
+          const float c = g.rope_cos[(size_t)pos * 32 + d], sn = g.rope_sin[(size_t)pos * 32 + d];
+          y0 = x0 * c - x1 * sn;
+          y1 = x1 * c + x0 * sn;
+        }
+        if (kind == 0) {
+          uint16_t* qr = g.Ch + (size_t)row * g.ldc + t0 * kTile;
+          qr[d] = __builtin_bit_cast(uint16_t, (_Float16)y0);
+          qr[d + 32] = __builtin_bit_cast(uint16_t, (_Float16)y1);
+        } else {
+          uint16_t* cr = (kind == 1 ? g.kc : g.vc) + ((size_t)hk * g.max_tokens + pos) * kTile;
+          cr[d] = __half_as_ushort(__float2half(y0));
+          cr[d + 32] = __half_as_ushort(__float2half(y1));
+        }
+      }
+    return;
+  }
   if (EPI == GEMM_SWIGLU) {
     const int oi = t0 * 32 + l32;
     if (oi >= g.n_out) return;
@@ -797,6 +830,7 @@ bool launch_gemm(int fmt, int epi, const GemmShape& sh, const GemmArgs& ga, hipS
   if (ga.K % 32 != 0 || ga.lda % 8 != 0 || ga.M <= 0 || ga.N <= 0) return false;
   if (epi == GEMM_SWIGLU && (ga.N % kTile != 0 || sh.nb != 2)) return false;
   if (epi != GEMM_PART && sh.splits != 1) return false;
+  if (epi == GEMM_ROPE && !(sh.ring && sh.kw && ga.N % kTile == 0)) return false;  // the K-wave kernel only
   GemmArgs g = ga;
   g.spc = sh.spc;
   const dim3 grid(sh.gx, sh.gy, sh.splits);
@@ -808,7 +842,7 @@ bool launch_gemm(int fmt, int epi, const GemmShape& sh, const GemmArgs& ga, hipS
     hipLaunchKernelGGL((gemm_q4_kw_kernel<MTV, E>), grid, dim3(256), 0, st, g);                  \
     return true;                                                                                 \
   }
-#define KW_EPIS(MTV) KW_CASE(MTV, GEMM_STORE) KW_CASE(MTV, GEMM_PART) KW_CASE(MTV, GEMM_SWIGLU)
+#define KW_EPIS(MTV) KW_CASE(MTV, GEMM_STORE) KW_CASE(MTV, GEMM_PART) KW_CASE(MTV, GEMM_SWIGLU) KW_CASE(MTV, GEMM_ROPE)
     KW_EPIS(1) KW_EPIS(2) KW_EPIS(4)
 #undef KW_EPIS
 #undef KW_CASE
