@@ -185,16 +185,18 @@ def test_attention_window_of_one_returns_the_current_value_row(ctx, kv_fmt):
     A.close()
 
 
-@pytest.mark.parametrize("heads,kv,D,theta,steps,window", [(14, 2, 64, 1e6, 700, 0), (24, 8, 128, 5e5, 300, 0),
-                                                           (32, 8, 64, 5e5, 1100, 0), (4, 2, 64, 1e4, 300, 100)])
-def test_attention_long_fp16_cache(ctx, heads, kv, D, theta, steps, window):
-    """fp16 cache, split-K over many chunks: every output against the oracle
-    run with the same fp16 cache rounding.  The 1100-step case crosses the
+@pytest.mark.parametrize("heads,kv,D,theta,steps,window,kv_fmt", [
+    (14, 2, 64, 1e6, 700, 0, tlm.FMT_F16), (24, 8, 128, 5e5, 300, 0, tlm.FMT_F16),
+    (32, 8, 64, 5e5, 1100, 0, tlm.FMT_F16), (4, 2, 64, 1e4, 300, 100, tlm.FMT_F16),
+    (24, 8, 128, 5e5, 300, 0, tlm.FMT_F32), (4, 2, 128, 5e5, 1100, 0, tlm.FMT_F32)])
+def test_attention_long_fp16_cache(ctx, heads, kv, D, theta, steps, window, kv_fmt):
+    """fp16 (and fp32) cache, split-K over many chunks: every output against
+    the oracle run with the same cache rounding.  The 1100-step cases cross the
     1024-position window where the long-window kernels take over."""
     rng = np.random.default_rng(heads * D)
     inv, af = orc.rope_parameters(D, theta)
     M = steps + 8
-    A = tlm.Attention(ctx, heads, kv, D, M, inv, attention_factor=af, sliding_window=window, kv_fmt=tlm.FMT_F16)
+    A = tlm.Attention(ctx, heads, kv, D, M, inv, attention_factor=af, sliding_window=window, kv_fmt=kv_fmt)
     kc = np.zeros((M, kv * D), np.float32)
     vc = np.zeros_like(kc)
     out = ctx.buffer(4 * heads * D)
@@ -203,7 +205,7 @@ def test_attention_long_fp16_cache(ctx, heads, kv, D, theta, steps, window):
         qkv = f32(rng.standard_normal((heads + 2 * kv) * D))
         got = A(ctx.array(qkv), pos, out).read()
         ref = orc.attention(qkv, heads, kv, D, pos, kc, vc, inv, attention_factor=af, sliding_window=window,
-                            kv_f16=True)
+                            kv_f16=kv_fmt == tlm.FMT_F16)
         # K/V are rounded to fp16 from RoPE values computed in fp32 (device) or
         # double (oracle); an occasional 1-ulp fp16 difference bounds this.
         close(got, ref, 2e-3, 2e-3)
