@@ -88,6 +88,17 @@ def read_traffic(kernel: str):
     return float(m.group(1)) if m else None
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or 'unknown'."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(hw, prompt, budget_s: float):
     """The oracle (C restatement of the reference CPU path: fp32 storage,
     double accumulation, one thread) over positions 0, 1, ... of the same
@@ -301,6 +312,7 @@ def main():
         rate, n, dt = cpu_baseline(hw, prompt if len(prompt) > 1 else list(W.prompt_tokens(
             W.Workload("s", wl.config, wl.storage, 64, 0, 64))), args.cpu_budget)
         cpu = {"value": round(rate, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+               "cpu": cpu_model(), "host_threads": ncpu,
                "sample": f"oracle forward of the first {n} prompt positions of the same workload "
                          f"({dt:.1f} s, fp32 weights, double accumulation, 1 of {ncpu} host threads)"}
         log(f"[bench] cpu baseline {rate:.3f} tok/s over {n} tokens")
@@ -315,7 +327,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        # arithmetic: fp32 activations and accumulation over q4 g32 weights
+        # (fp16 scales), an fp16 LM head and an fp16 KV cache
+        "dtype": "f32 math; q4 g32 linears, f16 head, f16 kv" if wl.storage.kv == "f16" else
+                 f"f32 math; {wl.storage.linear} linears, {wl.storage.kv} kv",
         "data": "synthetic",
         "hbm_roofline_frac": round(hbm_frac, 4),
         "bytes_per_token": round(mean_bytes),

@@ -7,7 +7,6 @@ from __future__ import annotations
 
 import ctypes
 import os
-import subprocess
 from pathlib import Path
 
 import numpy as np
@@ -22,19 +21,19 @@ U16P = ctypes.POINTER(ctypes.c_uint16)
 EMBED, LM_HEAD, FINAL_NORM, ATTN_NORM, FFN_NORM, WQKV, BQKV, WO, WGATE, WUP, WDOWN = range(11)
 
 
-def build() -> Path:
-    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
-    return LIB_PATH
-
-
 _lib = None
 
 
 def lib():
+    """Loads liboracle.so; raises if it was not built.  It is built by
+    `make -C oracle` (or __graft_entry__.build()) before any GPU work: this
+    module starts no process, since the tests and the bench call it after the
+    GPU is open."""
     global _lib
     if _lib is None:
         if not LIB_PATH.exists():
-            build()
+            raise RuntimeError(f"oracle: {LIB_PATH} is missing; build it with `make -C oracle` "
+                               "before running the tests or the bench")
         L = ctypes.CDLL(str(LIB_PATH))
         L.orc_f16_to_f32.restype = ctypes.c_float
         L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
@@ -70,6 +69,8 @@ def lib():
         L.orc_model_free.argtypes = [ctypes.c_void_p]
         L.orc_model_reset.argtypes = [ctypes.c_void_p]
         L.orc_model_read_cache.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, F32P, F32P]
+        L.orc_model_write_cache.restype = ctypes.c_int
+        L.orc_model_write_cache.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, F32P, F32P]
         L.orc_forward_token.restype = ctypes.c_int
         L.orc_forward_token.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, F32P, F32P]
         L.orc_set_threads.argtypes = [ctypes.c_int]
@@ -246,6 +247,17 @@ class Model:
         v = np.zeros((count, kv), np.float32)
         lib().orc_model_read_cache(self.ptr, layer, count, k.ctypes.data_as(F32P), v.ctypes.data_as(F32P))
         return k, v
+
+    def write_cache(self, layer, pos0, k, v):
+        """Cache rows [pos0, pos0 + count) of one layer, (count, kv_heads, head_dim)
+        or (count, kv_heads * head_dim) fp32 (e.g. a device cache widened)."""
+        kv = self.dims["kv_heads"] * self.dims["head_dim"]
+        k = np.ascontiguousarray(np.asarray(k, np.float32).reshape(-1, kv))
+        v = np.ascontiguousarray(np.asarray(v, np.float32).reshape(-1, kv))
+        assert k.shape == v.shape
+        if lib().orc_model_write_cache(self.ptr, int(layer), int(pos0), k.shape[0], k.ctypes.data_as(F32P),
+                                       v.ctypes.data_as(F32P)) != 0:
+            raise ValueError("oracle: cache rows out of range")
 
     def forward(self, token, position, want_hidden=False):
         logits = np.zeros(self.dims["vocab"], np.float32)

@@ -407,6 +407,8 @@ void orc_q4_quantize(const float* w, int N, int K, uint8_t* packed, uint16_t* sc
 
 void orc_q4_dequant(const uint8_t* packed, const uint16_t* scales, int N, int K, float* out) {
   int G = K / 32;
+  /* rows are independent: threads split them without changing any value */
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1 && (long)N * K > (1L << 20))
   for (int n = 0; n < N; n++)
     for (int k = 0; k < K; k++) {
       uint8_t b = packed[(size_t)n * (K / 2) + k / 2];
@@ -530,6 +532,18 @@ void orc_model_read_cache(const orc_model* m, int layer, int count, float* k, fl
   size_t kv = (size_t)m->kv_heads * m->head_dim;
   memcpy(k, m->kcache + (size_t)layer * m->max_tokens * kv, sizeof(float) * kv * count);
   memcpy(v, m->vcache + (size_t)layer * m->max_tokens * kv, sizeof(float) * kv * count);
+}
+
+/* Write cache rows [pos0, pos0 + count) of one layer ([count][kv_heads*D]
+ * fp32), e.g. rows a device produced, so that the oracle continues from
+ * that cache (positions past the rows it computed itself). */
+int orc_model_write_cache(orc_model* m, int layer, int pos0, int count, const float* k, const float* v) {
+  if (layer < 0 || layer >= m->layers || pos0 < 0 || count < 0 || pos0 + count > m->max_tokens) return -1;
+  size_t kv = (size_t)m->kv_heads * m->head_dim;
+  size_t off = ((size_t)layer * m->max_tokens + pos0) * kv;
+  memcpy(m->kcache + off, k, sizeof(float) * kv * count);
+  memcpy(m->vcache + off, v, sizeof(float) * kv * count);
+  return 0;
 }
 
 /* forwardToken, decoder/DecoderCPURunner.ts:47-138: the sequential

@@ -247,6 +247,15 @@ def test_kv_cache_round_trip_and_reset(ctx):
         runner.computeToken(10 ** 6, 0, True)
     with pytest.raises(tlm.TlmError):
         runner.computeToken(1, 64, True)
+    # host buffers the library would read past, or of the wrong element type
+    with pytest.raises(tlm.TlmError):
+        m.kv_write(1, 3, k.astype(np.float32), v)
+    with pytest.raises(tlm.TlmError):
+        m.kv_write(1, 3, k[:, :1], v[:, :1])
+    with pytest.raises(tlm.TlmError):
+        m.kv_write(1, 3, k, v[:4])
+    with pytest.raises(tlm.TlmError):
+        m.prefill([1, 2, 3], 0, 4)
     runner.close()
 
 

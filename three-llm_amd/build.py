@@ -2,7 +2,8 @@
 
     python three-llm_amd/build.py
 
-hipcc cross-compiles without a GPU.  Packed-FP32 instructions are disabled for
+Each source compiles to an object under three-llm_amd/_build/ (in parallel),
+then the objects link into libtlm.so.  hipcc cross-compiles without a GPU.  Packed-FP32 instructions are disabled for
 all device code (-packed-fp32-ops); the host pass warns that it does not know
 the feature, which is harmless.
 """
@@ -17,6 +18,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libtlm.so"
+OBJ = HERE / "_build"
 SOURCES = ["tlm_api.hip", "tlm_kernels.hip", "tlm_prefill.hip", "tlm_host.cpp"]
 ARCH = os.environ.get("TLM_OFFLOAD_ARCH", "gfx950")
 
@@ -28,22 +30,43 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libtlm.so)")
 
 
+def _flags():
+    return ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
+            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+            "-Wall", "-Wno-unused-result", "-Wno-unused-value", "-Wno-unused-command-line-argument"]
+
+
 def build(verbose: bool = False) -> Path:
+    """Compiles every source to an object in parallel, then links libtlm.so."""
+    OBJ.mkdir(exist_ok=True)
+    procs = []
+    for src in SOURCES:
+        obj = OBJ / (src + ".o")
+        cmd = [hipcc()] + _flags() + ["-c", "-o", str(obj), str(CSRC / src)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((src, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+    failed = False
+    for src, obj, pr in procs:
+        out, _ = pr.communicate()
+        if pr.returncode != 0:
+            sys.stderr.write(out)
+            failed = True
+        elif verbose:
+            warnings = [l for l in out.splitlines()
+                        if "warning:" in l and "packed-fp32-ops" not in l and "target-feature" not in l
+                        and "reserved registers" not in l]
+            if warnings:
+                print("\n".join(warnings))
+    if failed:
+        raise RuntimeError("hipcc failed building libtlm.so")
     out_tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), "-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}",
-           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-           "-Wall", "-Wno-unused-result", "-Wno-unused-value", "-Wno-unused-command-line-argument",
-           "-o", str(out_tmp)] + [str(CSRC / s) for s in SOURCES] + ["-lpthread"]
-    if verbose:
-        print(" ".join(cmd), flush=True)
+    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(out_tmp)] + \
+          [str(OBJ / (s + ".o")) for s in SOURCES] + ["-lpthread"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError("hipcc failed building libtlm.so")
-    warnings = [l for l in (res.stdout + res.stderr).splitlines()
-                if "warning" in l and "packed-fp32-ops" not in l and "target-feature" not in l]
-    if verbose and warnings:
-        print("\n".join(warnings))
+        raise RuntimeError("linking libtlm.so failed")
     os.replace(out_tmp, LIB)
     return LIB
 

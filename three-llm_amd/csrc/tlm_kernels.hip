@@ -15,110 +15,10 @@
 #include <algorithm>
 #include <hip/hip_fp16.h>
 
-#include "tlm_kernels.h"
+#include "tlm_device.h"
 
 namespace tlm {
 
-static constexpr float kLowest = -3.4028234663852886e38f;  // TSLLogits.ts:21 LOWEST_FLOAT
-
-__device__ __forceinline__ float h2f(uint32_t bits) { return __half2float(__ushort_as_half((unsigned short)bits)); }
-
-// Fixed-point residual values (x * 2^32 as a two's-complement int64).
-__device__ __forceinline__ unsigned long long to_fx(float v) {
-  return (unsigned long long)__float2ll_rn(v * kFxScale);
-}
-__device__ __forceinline__ float from_fx(unsigned long long s) { return __ll2float_rn((long long)s) * kFxInv; }
-
-// Cross-lane moves through DPP (data-parallel primitives: a VALU operand
-// modifier, no LDS round trip).  Every reduction below pairs lanes
-// symmetrically, so all lanes of a group end with the same bits.
-constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]: lane ^ 1
-constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]: lane ^ 2
-constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within each 8 lanes
-constexpr int kDppMirror = 0x140;     // lane i <-> 15 - i within each 16 lanes
-
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-template <int CTRL>
-__device__ __forceinline__ int dpp(int v) {
-  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
-}
-__device__ __forceinline__ float readlane(float v, int l) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
-}
-
-// Sum over each aligned group of 8 lanes, in every lane of the group.
-__device__ __forceinline__ float sum8(float v) {
-  v += dpp<kDppXor1>(v);
-  v += dpp<kDppXor2>(v);
-  return v + dpp<kDppHalfMirror>(v);
-}
-
-// Sum / max over the 64 lanes of a wave (wave-uniform result).
-__device__ __forceinline__ float wave_sum(float v) {
-  v = sum8(v);
-  v += dpp<kDppMirror>(v);
-  return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-  v = fmaxf(v, dpp<kDppXor1>(v));
-  v = fmaxf(v, dpp<kDppXor2>(v));
-  v = fmaxf(v, dpp<kDppHalfMirror>(v));
-  v = fmaxf(v, dpp<kDppMirror>(v));
-  return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
-}
-
-// Block-wide sum (blockDim.x a multiple of 64); every thread gets the result.
-// scratch holds one float per wave and must not be in use by another
-// reduction of the same kernel (each kernel calls this once per scratch).
-__device__ float block_sum(float v, float* scratch) {
-  v = wave_sum(v);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  if (lane == 0) scratch[wave] = v;
-  __syncthreads();
-  float r = 0.f;
-  for (int i = 0; i < nw; i++) r += scratch[i];
-  return r;
-}
-
-// Greedy order of TSLLogits.ts:228-229: higher score, ties to the lower id.
-// A strict total order on (score, id) for non-NaN scores; lanes start from
-// (LOWEST, INT_MAX) and only take better candidates, so NaN never enters.
-__device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
-
-template <int CTRL>
-__device__ __forceinline__ void argmax_step(float& v, int& i) {
-  const float ov = dpp<CTRL>(v);
-  const int oi = dpp<CTRL>(i);
-  if (better(ov, oi, v, i)) {
-    v = ov;
-    i = oi;
-  }
-}
-
-// Best (score, id) of the wave, in every lane.
-__device__ void wave_argmax(float& v, int& i) {
-  argmax_step<kDppXor1>(v, i);
-  argmax_step<kDppXor2>(v, i);
-  argmax_step<kDppHalfMirror>(v, i);
-  argmax_step<kDppMirror>(v, i);
-  float bv = readlane(v, 0);
-  int bi = __builtin_amdgcn_readlane(i, 0);
-#pragma unroll
-  for (int r = 16; r < 64; r += 16) {
-    const float rv = readlane(v, r);
-    const int ri = __builtin_amdgcn_readlane(i, r);
-    if (better(rv, ri, bv, bi)) {
-      bv = rv;
-      bi = ri;
-    }
-  }
-  v = bv;
-  i = bi;
-}
 
 // ------------------------------------------------------------------ GEMV --
 
@@ -447,51 +347,6 @@ struct GemvPrologue {
   }
 };
 
-// 32 q4 weights of one row (one 16-byte chunk) against x[0..32).
-// sum_k s*(n_k - 8)*x_k = s*(sum_k n_k x_k - 8*sum_k x_k); n_k in [0,15] via
-// byte-lane conversions (v_cvt_f32_ubyte*).
-__device__ __forceinline__ float dot_q4(const uint4 d, const float* __restrict__ x, float xsum, float s) {
-  const uint32_t wv[4] = {d.x, d.y, d.z, d.w};
-  float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    uint32_t lo = wv[j] & 0x0F0F0F0Fu, hi = (wv[j] >> 4) & 0x0F0F0F0Fu;
-    // opaque to the optimiser: otherwise it folds the masks into per-nibble
-    // bit-field extracts (v_bfe_u32 + v_cvt_f32_ubyte0) instead of converting
-    // byte k of lo / hi directly (v_cvt_f32_ubyte{0..3}), 24 more VALU per chunk
-    asm("" : "+v"(lo), "+v"(hi));
-    const float4 xa = *reinterpret_cast<const float4*>(x + 8 * j);
-    const float4 xb = *reinterpret_cast<const float4*>(x + 8 * j + 4);
-    a0 = fmaf((float)(lo & 0xFFu), xa.x, a0);
-    a1 = fmaf((float)(hi & 0xFFu), xa.y, a1);
-    a0 = fmaf((float)((lo >> 8) & 0xFFu), xa.z, a0);
-    a1 = fmaf((float)((hi >> 8) & 0xFFu), xa.w, a1);
-    a0 = fmaf((float)((lo >> 16) & 0xFFu), xb.x, a0);
-    a1 = fmaf((float)((hi >> 16) & 0xFFu), xb.y, a1);
-    a0 = fmaf((float)(lo >> 24), xb.z, a0);
-    a1 = fmaf((float)(hi >> 24), xb.w, a1);
-  }
-  return s * ((a0 + a1) - 8.f * xsum);
-}
-
-// 8 fp16 weights of one row against x[0..8).
-__device__ __forceinline__ float dot_f16(const uint4 d, const float* __restrict__ x) {
-  const uint32_t wv[4] = {d.x, d.y, d.z, d.w};
-  const float4 xa = *reinterpret_cast<const float4*>(x);
-  const float4 xb = *reinterpret_cast<const float4*>(x + 4);
-  float a0 = 0.f, a1 = 0.f;
-  a0 = fmaf(h2f(wv[0] & 0xFFFFu), xa.x, a0);
-  a1 = fmaf(h2f(wv[0] >> 16), xa.y, a1);
-  a0 = fmaf(h2f(wv[1] & 0xFFFFu), xa.z, a0);
-  a1 = fmaf(h2f(wv[1] >> 16), xa.w, a1);
-  a0 = fmaf(h2f(wv[2] & 0xFFFFu), xb.x, a0);
-  a1 = fmaf(h2f(wv[2] >> 16), xb.y, a1);
-  a0 = fmaf(h2f(wv[3] & 0xFFFFu), xb.z, a0);
-  a1 = fmaf(h2f(wv[3] >> 16), xb.w, a1);
-  return a0 + a1;
-}
-
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // NCH: chunks a wave keeps in flight per batch (>= its chunk count when that
 // fits, so no load is a clamped duplicate).  STREAM: weights read once per
@@ -905,61 +760,6 @@ bool launch_mlp(int fmt, int nch, int ndb, int blocks, const MlpArgs& m, hipStre
 
 // ------------------------------------------------------------- attention --
 
-template <typename KT>
-__device__ __forceinline__ float kv_load(const KT* p);
-template <>
-__device__ __forceinline__ float kv_load<uint16_t>(const uint16_t* p) { return h2f(*p); }
-template <>
-__device__ __forceinline__ float kv_load<float>(const float* p) { return *p; }
-template <typename KT>
-__device__ __forceinline__ KT kv_store(float v);
-template <>
-__device__ __forceinline__ uint16_t kv_store<uint16_t>(float v) { return __half_as_ushort(__float2half_rn(v)); }
-template <>
-__device__ __forceinline__ float kv_store<float>(float v) { return v; }
-
-// Tiling of head_kernel: LPP lanes per cached position, so each lane holds 64
-// bytes of a K row; SUB = 64 / LPP positions per pass; the V rows of a pass
-// (always 4 KiB) are staged in LDS with 64 bytes per lane.
-struct HeadTiling {
-  int lpp, sub, dl;
-};
-static constexpr __host__ __device__ inline HeadTiling head_tiling(int dt, int esz) {
-  HeadTiling t{};
-  t.lpp = dt * esz <= 64 ? 1 : dt * esz / 64;
-  t.sub = 64 / t.lpp;
-  t.dl = dt / t.lpp;  // K elements per lane
-  return t;
-}
-
-// Compiled head dimension: 64 and 128 exactly; 32 covers any even head_dim
-// <= 32 through runtime bounds (element-wise, clamped loads).
-static int attn_dt(int D) { return D <= 32 ? 32 : D; }
-
-int attn_lpp(int D, bool kv_f32) { return head_tiling(attn_dt(D), kv_f32 ? 4 : 2).lpp; }
-
-// LDS of one head_kernel wave (floats): q, the new k and v, their pre-RoPE
-// values, the pass's probabilities and the V tile (4 KiB); a multiple of 4
-// floats so every wave's region stays 16-byte aligned.
-static constexpr __host__ __device__ inline int head_wave_floats(int dt, int esz) {
-  return (6 * dt + head_tiling(dt, esz).sub + 1024 + 3) & ~3;
-}
-
-// LDS of a head_kernel block: one wave region per wave, then (long windows)
-// the merge area [kAttnWaves][2 + DT] (max, sum, unnormalised output of each wave).
-size_t attn_smem_bytes(int gmax, int D, bool kv_f32, bool long_win) {
-  (void)gmax;
-  const int dt = attn_dt(D), esz = kv_f32 ? 4 : 2, nw = long_win ? kAttnWaves : 1;
-  return sizeof(float) * ((size_t)nw * head_wave_floats(dt, esz) + (long_win ? (size_t)nw * (2 + dt) : 0));
-}
-
-// Order a wave's own LDS writes before its later reads (regions private to
-// one wave: no block barrier, whose waves may run different pass counts).
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // Global loads of one head_kernel pass, held in registers: this lane's K-row
 // slice (DL elements) and its 64 bytes of the pass's V rows.  Unconditional:

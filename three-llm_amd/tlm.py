@@ -18,6 +18,8 @@ FMT_F16, FMT_Q4, FMT_F32 = 1, 2, 3
 (T_EMBED, T_LM_HEAD, T_LM_HEAD_SCALES, T_FINAL_NORM, T_ATTN_NORM, T_FFN_NORM, T_WQKV, T_WQKV_SCALES, T_BQKV, T_WO,
  T_WO_SCALES, T_WGATE, T_WGATE_SCALES, T_WUP, T_WUP_SCALES, T_WDOWN, T_WDOWN_SCALES) = range(17)
 LOGITS = 1
+# error codes of include/tlm.h
+TLM_ERR_INVALID, TLM_ERR_HIP, TLM_ERR_OOM, TLM_ERR_STATE, TLM_ERR_RANGE = -1, -2, -3, -4, -5
 
 # exported symbols (checked by the CPU test suite against include/tlm.h)
 EXPORTS = [
@@ -386,7 +388,11 @@ class Model:
         check(lib().tlm_compute_token(self.ptr, int(token), int(position), LOGITS if logits else 0))
 
     def prefill(self, tokens, start: int, end: int):
-        t = np.ascontiguousarray(tokens, np.int32)
+        t = np.ascontiguousarray(tokens, np.int32).reshape(-1)
+        # the library reads tokens[start, end): a shorter array would be read past its end
+        if not 0 <= int(start) <= int(end) <= t.size:
+            raise TlmError(TLM_ERR_RANGE, f"TLMModel: prefill range [{start}, {end}) outside the "
+                                          f"{t.size} tokens given")
         check(lib().tlm_prefill(self.ptr, _ptr(t), int(start), int(end)))
 
     def read_logits(self, n: Optional[int] = None) -> np.ndarray:
@@ -420,6 +426,17 @@ class Model:
         check(lib().tlm_reset_cache(self.ptr))
 
     def kv_write(self, layer: int, pos0: int, k: np.ndarray, v: np.ndarray):
+        """k, v: (count, kv_heads, head_dim) in the cache's element type (uint16 fp16
+        bits, or float32 for an fp32 cache); the library copies count rows of each."""
+        dt = np.float32 if self.desc.kv_fmt == FMT_F32 else np.uint16
+        k, v = np.asarray(k), np.asarray(v)
+        for name, a in (("k", k), ("v", v)):
+            if a.ndim != 3 or a.shape[1:] != (self.desc.num_kv_heads, self.desc.head_dim) or a.dtype != dt:
+                raise TlmError(TLM_ERR_INVALID, f"TLMModel: kv_write {name} must be (count, "
+                                                f"{self.desc.num_kv_heads}, {self.desc.head_dim}) {np.dtype(dt).name}, "
+                                                f"got {a.shape} {a.dtype}")
+        if k.shape[0] != v.shape[0]:
+            raise TlmError(TLM_ERR_INVALID, f"TLMModel: kv_write k has {k.shape[0]} rows, v {v.shape[0]}")
         check(lib().tlm_kv_write(self.ptr, layer, pos0, k.shape[0], _ptr(np.ascontiguousarray(k)),
                                  _ptr(np.ascontiguousarray(v))))
 
