@@ -248,6 +248,17 @@ int tlm_time_kernel(tlm_model* model, int which, int iters, double* avg_ms);
  * the LM head launch inside a real step (its weights cold in the caches, as in
  * decode).  Leaves the cache and ctrl state advanced like tlm_decode_greedy. */
 int tlm_time_head(tlm_model* model, int32_t token, int32_t position, int n, double* avg_ms);
+/* tlm_trace_decode: n greedy decode steps from (token, position) through the
+ * persistent schedule, launched directly with its timeline on; `out` receives
+ * the last step's timeline: for every (block, wave), layer l < L and stage
+ * (0 qkv, 1 attention, 2 O, 3 gate|up, 4 down), 4 wall-clock stamps (100 MHz:
+ * weights issued, input ready, computed, published; 0 where the wave had no
+ * such work); layer slot L, stage 0 holds the kernel's start and end.
+ * n_out must be blocks * 16 * (L + 1) * 5 * 4 (see tlm_model_describe for the
+ * block count).  TLM_ERR_STATE when the model has no
+ * persistent schedule or a position needs the long-window kernels.  Tracing
+ * has no counterpart in the reference (the browser has no device clock). */
+int tlm_trace_decode(tlm_model* model, int32_t token, int32_t position, int n, uint64_t* out, size_t n_out);
 /* Launch layout chosen for the model (for reports): per-stage grid sizes. */
 int tlm_model_describe(tlm_model* model, char* out, size_t len);
 

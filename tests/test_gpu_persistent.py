@@ -1,0 +1,114 @@
+"""The persistent per-token schedule (one kernel per decode token: every CU
+runs fixed stage items of every layer and hands sequence-tagged partial sums
+to the next stage through device memory) against the graph of per-stage
+kernels and against the oracle.  The reference runs one submission per token
+(DecoderTSLRunner.ts:487-502); both schedules give the same logits.
+
+Tolerances: persistent vs per-stage kernels max-abs 2e-3 / rel 1e-3 (the
+same math with other fp32 summation orders of the K-split partials); both
+against the oracle max-abs 2e-2 / rel 1e-2, greedy tokens equal unless the
+oracle's top-2 gap is under 2e-2.
+"""
+import os
+import re
+
+import numpy as np
+import pytest
+
+from bridge import close, oracle_model, top2_gap
+import three_llm_amd.runner as R
+import three_llm_amd.tlm as tlm
+import three_llm_amd.weights as W
+
+pytestmark = pytest.mark.gpu
+LOGIT_ATOL, LOGIT_RTOL = 2e-2, 1e-2
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = tlm.Context(0)
+    yield c
+    c.close()
+
+
+def _workload(name, layers, max_tokens):
+    wl = W.WORKLOADS[name]
+    cfg = dict(wl.config, num_hidden_layers=layers)
+    return W.Workload(wl.name, cfg, wl.storage, wl.prompt_len, 8, max_tokens, qkv_bias=wl.qkv_bias)
+
+
+def _runner(hw, ctx, max_tokens, persistent):
+    old = os.environ.get("TLM_PERSISTENT")
+    os.environ["TLM_PERSISTENT"] = "1" if persistent else "0"
+    try:
+        return R.DecoderHIPRunner(hw, {"maxTokens": max_tokens, "prefillBatchRows": 0}, ctx=ctx)
+    finally:
+        if old is None:
+            del os.environ["TLM_PERSISTENT"]
+        else:
+            os.environ["TLM_PERSISTENT"] = old
+
+
+@pytest.mark.parametrize("name,layers", [("tiny", 2), ("qwen2.5-0.5b", 4), ("llama-3.2-1b", 2)])
+def test_persistent_equals_stage_kernels_and_oracle(ctx, name, layers):
+    wl = _workload(name, layers, 256)
+    hw = W.synthetic(wl)
+    hw.keep = True
+    ps = _runner(hw, ctx, 256, True)
+    ref = _runner(hw, ctx, 256, False)
+    assert "persistent[off]" in ref.model.describe()
+    desc = ps.model.describe()
+    assert re.search(r"persistent\[\d+ blocks", desc), desc
+    om = oracle_model(hw, 256, kv_f16=True, threads=16)
+    prompt = [int(t) for t in W.prompt_tokens(wl)][:10]
+    for i, t in enumerate(prompt):
+        ps.computeToken(t, i, True)
+        ref.computeToken(t, i, True)
+        got = ps.readLogits()
+        close(got, ref.readLogits(), 2e-3, 1e-3)
+        close(got, om.forward(t, i), LOGIT_ATOL, LOGIT_RTOL)
+    L = wl.config["num_hidden_layers"]
+    for l in range(L):  # the appended cache rows agree too
+        for a, b in zip(ps.model.kv_read(l, 0, len(prompt)), ref.model.kv_read(l, 0, len(prompt))):
+            close(a.view(np.float16).astype(np.float32), b.view(np.float16).astype(np.float32), 2e-3, 1e-3)
+    # the device-driven greedy loop (one persistent kernel + head per token)
+    tok = ps.sampleToken(1, {"temperature": 0})
+    assert tok == ref.sampleToken(1, {"temperature": 0})
+    dev = list(ps.decodeGreedy(tok, len(prompt), 6))
+    t = tok
+    for step, d in enumerate(dev):
+        r = om.forward(t, len(prompt) + step)
+        if d != int(np.argmax(r)):
+            assert top2_gap(r) < LOGIT_ATOL
+            break
+        t = d
+    ps.close()
+    ref.close()
+    om.close()
+
+
+def test_trace_orders_every_stage(ctx):
+    """tlm_trace_decode: per block and layer, each item's stamps run issue <=
+    ready <= computed <= published, and a stage is ready only after every
+    item of the stage before it has published (the handoff is a dependency)."""
+    wl = _workload("qwen2.5-0.5b", 3, 256)
+    hw = W.synthetic(wl)
+    ps = _runner(hw, ctx, 256, True)
+    nb = int(re.search(r"persistent\[(\d+) blocks", ps.model.describe()).group(1))
+    tr = ps.model.trace_decode(5, 20, 3, nb).astype(np.int64)[:, 0]  # wave 0: [block][layer][stage][event]
+    L = 3
+    used = [np.where(tr[:, 0, st, 0] > 0)[0] for st in range(5)]
+    assert all(len(u) > 0 for u in used)
+    for st in range(5):
+        ev = tr[used[st], :L, st, :]
+        assert (ev > 0).all()
+        assert (np.diff(ev, axis=-1) >= 0).all()
+    for l in range(L):
+        for st in range(1, 5):
+            prev_pub = tr[used[st - 1], l, st - 1, 3].min()
+            assert tr[used[st], l, st, 1].min() >= prev_pub
+        if l > 0:
+            assert tr[used[0], l, 0, 1].min() >= tr[used[4], l - 1, 4, 3].min()
+    with pytest.raises(tlm.TlmError):
+        ps.model.trace_decode(5, 20, 3, nb + 1)
+    ps.close()

@@ -150,6 +150,19 @@ struct tlm_model {
   // per attention mode: [0] short windows, [1] long windows (long_window)
   hipGraphExec_t g_logits[2] = {}, g_prefill[2] = {}, g_layers[2] = {};
   hipGraph_t graph_logits[2] = {}, graph_prefill[2] = {}, graph_layers[2] = {};
+  // persistent schedule (windows up to kLongWindow positions): one kernel per
+  // token for every layer; ps_on when the model's shape has a compiled variant
+  PsShape ps{};
+  bool ps_on = false;
+  int ps_blocks = 0;
+  size_t ps_smem = 0;
+  PsLayer* ps_layers = nullptr;  // device [L]
+  int* ps_roles = nullptr;       // device [blocks][2][2]
+  PsArgs* ps_args_dev = nullptr;  // the kernel's arguments (device memory)
+  unsigned long long *ps_pub_x = nullptr, *ps_pub_qkv = nullptr, *ps_pub_o = nullptr, *ps_pub_xm = nullptr,
+                     *ps_pub_h = nullptr;
+  hipGraphExec_t g_ps_logits = nullptr, g_ps_prefill = nullptr;
+  hipGraph_t graph_ps_logits = nullptr, graph_ps_prefill = nullptr;
   int host_pos = 0;  // position of the last token enqueued (selects the attention mode)
   bool finalized = false;
   bool use_graphs = true;  // TLM_GRAPHS=0 enqueues the same kernels directly (profilers, debugging)
@@ -876,6 +889,115 @@ static int model_alloc(void** p, size_t bytes) {
 
 void tlm_model_destroy(tlm_model* m);
 
+static PsArgs ps_args(const tlm_model* m) {
+  const tlm_model_desc& d = m->d;
+  const Layer& L0 = m->layers[0];
+  PsArgs a;
+  memset(&a, 0, sizeof a);
+  a.layers = m->ps_layers;
+  a.roles = m->ps_roles;
+  a.L = d.num_layers;
+  a.H = d.hidden_size;
+  a.I = d.intermediate_size;
+  a.Hq = d.num_heads;
+  a.Hkv = d.num_kv_heads;
+  a.D = d.head_dim;
+  a.G = d.num_heads / d.num_kv_heads;
+  a.rd = d.rotary_dim;
+  a.max_tokens = d.max_tokens;
+  a.window = d.sliding_window;
+  a.Nqkv = m->Nqkv;
+  a.QS = m->QS;
+  a.Cx = L0.qkv->C;
+  a.Co = L0.o->C;
+  a.Cd = L0.down->C;
+  a.To = L0.o->T;
+  a.Tgu = L0.gu->T;
+  a.Tq = L0.qkv->T;
+  a.mw = m->ps.mw;
+  a.kq = m->ps.kq;
+  a.cq = (a.Cx + a.kq - 1) / a.kq;
+  a.ko = m->ps.ko;
+  a.co = (a.Co + a.ko - 1) / a.ko;
+  a.ks = m->ps.ks;
+  a.cs = (a.Cd + a.ks - 1) / a.ks;
+  a.eps = (float)d.rms_eps;
+  a.scale = m->attn.scale;
+  a.ctrl = m->ctrl;
+  a.emb = m->emb;
+  a.emb_f32 = d.embed_fmt == TLM_FMT_F32 ? 1 : 0;
+  a.rope_cos = m->attn.rope_cos;
+  a.rope_sin = m->attn.rope_sin;
+  a.pub_x = m->ps_pub_x;
+  a.pub_qkv = m->ps_pub_qkv;
+  a.pub_o = m->ps_pub_o;
+  a.pub_xm = m->ps_pub_xm;
+  a.pub_h = m->ps_pub_h;
+  return a;
+}
+
+// The persistent schedule of a model whose shape has a compiled variant
+// (TLM_PERSISTENT=0 turns it off): the device table of layer pointers, the
+// handoff buffers (zeroed: token number 0 never matches) and ctrl[C_SEQ] = 1.
+static int ps_setup(tlm_model* m) {
+  const tlm_model_desc& d = m->d;
+  const char* env = getenv("TLM_PERSISTENT");
+  if (env && env[0] == '0') return TLM_OK;
+  const int H = d.hidden_size, L = d.num_layers;
+  const Layer& L0 = m->layers[0];
+  m->ps = ps_shape(wfmt(d.linear_fmt), d.kv_fmt == TLM_FMT_F32 ? 1 : 0, H, d.intermediate_size, d.head_dim,
+                   d.num_heads, d.num_kv_heads, m->ctx->cus);
+  if (!m->ps.dt) return TLM_OK;
+  m->ps_blocks = m->ctx->cus;
+  std::vector<int> roles((size_t)2 * kPsRoles * m->ps_blocks);
+  if (!ps_roles(m->ps, m->ps_blocks, H, d.num_heads, d.num_kv_heads, L0.gu->T, roles.data())) {
+    m->ps = PsShape{};
+    return TLM_OK;
+  }
+  m->ps_smem = ps_smem_bytes(m->ps, H, m->QS);
+  if (!ps_prepare(m->ps, m->ps_smem)) {
+    m->ps = PsShape{};
+    return TLM_OK;
+  }
+  std::vector<PsLayer> tab(L);
+  for (int l = 0; l < L; l++) {
+    const Layer& Ly = m->layers[l];
+    PsLayer& t = tab[l];
+    t.wqkv = Ly.qkv->w;
+    t.sqkv = Ly.qkv->s;
+    t.bqkv = Ly.bqkv ? Ly.bqkv : m->attn.zero_bias;
+    t.attn_norm = Ly.attn_norm;
+    t.wo = Ly.o->w;
+    t.so = Ly.o->s;
+    t.wgu = Ly.gu->w;
+    t.sgu = Ly.gu->s;
+    t.ffn_norm = Ly.ffn_norm;
+    t.wd = Ly.down->w;
+    t.sd = Ly.down->s;
+    t.kc = Ly.kc;
+    t.vc = Ly.vc;
+  }
+  const size_t w8 = sizeof(unsigned long long);
+  int rc = model_alloc((void**)&m->ps_layers, sizeof(PsLayer) * L);
+  if (!rc) rc = model_alloc((void**)&m->ps_roles, sizeof(int) * roles.size());
+  if (!rc) rc = model_alloc((void**)&m->ps_pub_x, w8 * L * kPsMaxKs * H);
+  if (!rc) rc = model_alloc((void**)&m->ps_pub_qkv, w8 * L * m->ps.kq * m->Nqkv);
+  if (!rc) rc = model_alloc((void**)&m->ps_pub_o, w8 * L * m->QS);
+  if (!rc) rc = model_alloc((void**)&m->ps_pub_xm, w8 * L * m->ps.ko * H);
+  if (!rc) rc = model_alloc((void**)&m->ps_pub_h, w8 * L * L0.gu->T * 32);
+  if (rc) return rc;
+  HIP_TRY(hipMemcpy(m->ps_layers, tab.data(), sizeof(PsLayer) * L, hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy(m->ps_roles, roles.data(), sizeof(int) * roles.size(), hipMemcpyHostToDevice));
+  const int seq = 1;  // the buffers are zero: token number 0 never matches
+  HIP_TRY(hipMemcpy(m->ctrl + C_SEQ, &seq, sizeof(int), hipMemcpyHostToDevice));
+  m->ps_on = true;
+  rc = model_alloc((void**)&m->ps_args_dev, sizeof(PsArgs));
+  if (rc) return rc;
+  const PsArgs a = ps_args(m);
+  HIP_TRY(hipMemcpy(m->ps_args_dev, &a, sizeof a, hipMemcpyHostToDevice));
+  return TLM_OK;
+}
+
 int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
   if (!ctx || !d || !out) return fail(TLM_ERR_INVALID, "TLMModel: null argument");
   if (d->hidden_size <= 0 || d->intermediate_size <= 0 || d->num_layers <= 0 || d->vocab_size <= 0 ||
@@ -967,6 +1089,7 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
   M_TRY(model_alloc((void**)&m->arg_idx, sizeof(int) * 4096));
   M_TRY(model_alloc((void**)&m->cand_v, sizeof(float) * kTopkMax));
   M_TRY(model_alloc((void**)&m->cand_i, sizeof(int) * kTopkMax));
+  if (rc == TLM_OK) rc = ps_setup(m);
 #undef M_TRY
   if (rc) {
     std::string msg = g_error;
@@ -981,6 +1104,10 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
 void tlm_model_destroy(tlm_model* m) {
   if (!m) return;
   hipStreamSynchronize(m->ctx->stream);
+  if (m->g_ps_logits) hipGraphExecDestroy(m->g_ps_logits);
+  if (m->g_ps_prefill) hipGraphExecDestroy(m->g_ps_prefill);
+  if (m->graph_ps_logits) hipGraphDestroy(m->graph_ps_logits);
+  if (m->graph_ps_prefill) hipGraphDestroy(m->graph_ps_prefill);
   for (int i = 0; i < 2; i++) {
     if (m->g_logits[i]) hipGraphExecDestroy(m->g_logits[i]);
     if (m->g_prefill[i]) hipGraphExecDestroy(m->g_prefill[i]);
@@ -1004,7 +1131,8 @@ void tlm_model_destroy(tlm_model* m) {
   attn_free(&m->attn, false);
   void* bufs[] = {m->emb, m->final_norm, m->ctrl, m->tokens_out, m->prompt, m->xa, m->x0, m->xf, m->attn_out,
                   m->pq, m->po, m->rb, m->logits, m->arg_val, m->arg_idx, m->cand_v, m->cand_i, m->pf_x, m->pf_part, m->pf_xn,
-                  m->pf_q, m->pf_att, m->pf_h};
+                  m->pf_q, m->pf_att, m->pf_h, m->ps_layers, m->ps_roles, m->ps_pub_x, m->ps_pub_qkv,
+                  m->ps_pub_o, m->ps_pub_xm, m->ps_pub_h, m->ps_args_dev};
   for (void* p : bufs) hipFree(p);
   delete m;
 }
@@ -1153,12 +1281,17 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which, bool l
 // last layer's residual accumulator; block 0 stores the result for
 // readHidden) and the first argmax pass fused in, then the argmax merge.
 // `ev` (optional) brackets the LM head kernel with two events.
-static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, hipEvent_t* ev = nullptr) {
+static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, hipEvent_t* ev = nullptr, bool ps = false) {
   const tlm_model_desc& d = m->d;
   GemvArgs a;
   fill_gemv_args(a, m->head, nullptr);
   a.cps = m->lm_plan.cps;
   a.acc_in = m->rb + (size_t)(d.num_layers - 1) * kRep * d.hidden_size;
+  if (ps) {  // the persistent schedule's last residual: the published down partials
+    static_assert(kPsMaxKs == kRep, "the LM head prologue folds kRep partials");
+    a.acc_in = m->ps_pub_x + (size_t)(d.num_layers - 1) * kPsMaxKs * d.hidden_size;
+    a.ps_words = 1;
+  }
   a.norm_w = m->final_norm;
   a.eps = (float)d.rms_eps;
   a.xnorm = m->xf;
@@ -1170,7 +1303,16 @@ static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, hipEvent_t*
     return false;
   if (ev) hipEventRecord(ev[1], st);
   launch_argmax_merge(m->arg_val, m->arg_idx, m->lm_plan.gx, m->ctrl, advance ? m->tokens_out : nullptr,
-                      advance ? 1 : 0, d.max_tokens, emb_stage(m), st);
+                      advance ? 1 : 0, d.max_tokens, emb_stage(m), st, ps ? 1 : 0);
+  return true;
+}
+
+// One token of the persistent schedule, then its tail: the LM head and the
+// argmax merge, or the prefill advance.
+static bool enqueue_ps(tlm_model* m, hipStream_t st, int tail) {
+  if (!launch_ps_token(m->ps, m->ps_blocks, m->ps_smem, m->ps_args_dev, st)) return false;
+  if (tail == 1) return enqueue_head(m, st, true, nullptr, true);
+  launch_prefill_advance(m->ctrl, m->prompt, emb_stage(m), st, 1);
   return true;
 }
 
@@ -1195,6 +1337,18 @@ static int capture(tlm_model* m, int tail, bool long_win, hipGraph_t* g, hipGrap
   return TLM_OK;
 }
 
+static int capture_ps(tlm_model* m, int tail, hipGraph_t* g, hipGraphExec_t* ge) {
+  hipStream_t st = m->ctx->stream;
+  HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  const bool ok = enqueue_ps(m, st, tail);
+  hipError_t le = hipGetLastError();
+  HIP_TRY(hipStreamEndCapture(st, g));
+  if (le != hipSuccess) return fail(TLM_ERR_HIP, "TLMModel: launch during capture failed: %s", hipGetErrorString(le));
+  if (!ok) return fail(TLM_ERR_STATE, "TLMModel: no persistent kernel variant for this model");
+  HIP_TRY(hipGraphInstantiate(ge, *g, nullptr, nullptr, 0));
+  return TLM_OK;
+}
+
 int tlm_model_finalize(tlm_model* m) {
   if (!m) return fail(TLM_ERR_INVALID, "TLMModel: null model");
   if (m->finalized) return TLM_OK;
@@ -1210,6 +1364,10 @@ int tlm_model_finalize(tlm_model* m) {
     rc = capture(m, TAIL_LOGITS, lw, &m->graph_logits[lw], &m->g_logits[lw]);
     if (rc == TLM_OK) rc = capture(m, TAIL_PREFILL, lw, &m->graph_prefill[lw], &m->g_prefill[lw]);
   }
+  if (rc == TLM_OK && m->ps_on) {
+    rc = capture_ps(m, 1, &m->graph_ps_logits, &m->g_ps_logits);
+    if (rc == TLM_OK) rc = capture_ps(m, 0, &m->graph_ps_prefill, &m->g_ps_prefill);
+  }
   if (rc) return rc;
   m->finalized = true;
   return TLM_OK;
@@ -1221,6 +1379,15 @@ static int run_token(tlm_model* m, bool logits, int pos) {
   hipStream_t st = m->ctx->stream;
   const bool lw = long_window(&m->attn, pos);
   m->host_pos = pos;
+  if (m->ps_on && !lw) {  // the persistent schedule
+    if (m->use_graphs) {
+      HIP_TRY(hipGraphLaunch(logits ? m->g_ps_logits : m->g_ps_prefill, st));
+      return TLM_OK;
+    }
+    if (!enqueue_ps(m, st, logits ? 1 : 0)) return fail(TLM_ERR_STATE, "TLMModel: no persistent kernel variant");
+    CHECK_LAUNCH("TLMModel");
+    return TLM_OK;
+  }
   if (m->use_graphs) {
     HIP_TRY(hipGraphLaunch(logits ? m->g_logits[lw] : m->g_prefill[lw], st));
     return TLM_OK;
@@ -1479,9 +1646,24 @@ int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end)
   return TLM_OK;
 }
 
+// After a sync: a time-out of one of the persistent schedule's waits (every
+// wait is bounded; a late block sets ctrl[C_ERR] and leaves) makes the read fail.
+static int ps_check(tlm_model* m, const int* ctrl_host = nullptr) {
+  if (!m->ps_on) return TLM_OK;
+  int err = 0;
+  if (ctrl_host) err = ctrl_host[C_ERR];
+  else HIP_TRY(hipMemcpy(&err, m->ctrl + C_ERR, sizeof(int), hipMemcpyDeviceToHost));
+  if (!err) return TLM_OK;
+  const int zero = 0;
+  HIP_TRY(hipMemcpy(m->ctrl + C_ERR, &zero, sizeof(int), hipMemcpyHostToDevice));
+  return fail(TLM_ERR_HIP, "TLMModel: a wait of the persistent decode schedule timed out; the tokens computed "
+                           "since the last read are invalid");
+}
+
 int tlm_read_logits(tlm_model* m, float* out, size_t n) {
   if (!m || !out || n > (size_t)m->d.vocab_size) return fail(TLM_ERR_INVALID, "TLMModel: invalid logits read");
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  if (int rc = ps_check(m)) return rc;
   HIP_TRY(hipMemcpy(out, m->logits, sizeof(float) * n, hipMemcpyDeviceToHost));
   return TLM_OK;
 }
@@ -1493,12 +1675,13 @@ int tlm_read_candidates(tlm_model* m, int k, double softcap, int32_t* tokens, fl
   HIP_TRY(hipMemcpyAsync(tokens, m->cand_i, sizeof(int32_t) * k, hipMemcpyDeviceToHost, m->ctx->stream));
   HIP_TRY(hipMemcpyAsync(scores, m->cand_v, sizeof(float) * k, hipMemcpyDeviceToHost, m->ctx->stream));
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
-  return TLM_OK;
+  return ps_check(m);
 }
 
 int tlm_read_hidden(tlm_model* m, float* out, size_t n) {
   if (!m || !out || n > (size_t)m->d.hidden_size) return fail(TLM_ERR_INVALID, "TLMModel: invalid hidden read");
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  if (int rc = ps_check(m)) return rc;
   HIP_TRY(hipMemcpy(out, m->xf, sizeof(float) * n, hipMemcpyDeviceToHost));
   return TLM_OK;
 }
@@ -1506,7 +1689,10 @@ int tlm_read_hidden(tlm_model* m, float* out, size_t n) {
 int tlm_read_token(tlm_model* m, int32_t* token) {
   if (!m || !token) return fail(TLM_ERR_INVALID, "TLMModel: null argument");
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
-  HIP_TRY(hipMemcpy(token, m->ctrl + C_TOKEN, sizeof(int32_t), hipMemcpyDeviceToHost));
+  int ctrl[8];
+  HIP_TRY(hipMemcpy(ctrl, m->ctrl, sizeof ctrl, hipMemcpyDeviceToHost));
+  if (int rc = ps_check(m, ctrl)) return rc;
+  *token = ctrl[C_TOKEN];
   return TLM_OK;
 }
 
@@ -1527,6 +1713,7 @@ int tlm_decode_greedy(tlm_model* m, int32_t token, int32_t position, int n, int3
     if (rc) return rc;
   }
   HIP_TRY(hipStreamSynchronize(st));
+  if (int rc = ps_check(m)) return rc;
   if (n > 0) HIP_TRY(hipMemcpy(out, m->tokens_out, sizeof(int32_t) * n, hipMemcpyDeviceToHost));
   return TLM_OK;
 }
@@ -1696,6 +1883,44 @@ int tlm_time_kernel(tlm_model* m, int which, int iters, double* avg_ms) {
   return TLM_OK;
 }
 
+int tlm_trace_decode(tlm_model* m, int32_t token, int32_t position, int n, uint64_t* out, size_t n_out) {
+  if (!m || !out || n <= 0) return fail(TLM_ERR_INVALID, "TLMModel: invalid trace argument");
+  int rc = check_token(m, token, position);
+  if (rc) return rc;
+  if ((long)position + n > m->d.max_tokens) return fail(TLM_ERR_RANGE, "TLMModel: traced decode passes max_tokens");
+  if (!m->ps_on) return fail(TLM_ERR_STATE, "TLMModel: this model has no persistent schedule");
+  if (long_window(&m->attn, position + n - 1))
+    return fail(TLM_ERR_STATE, "TLMModel: position %d needs the long-window kernels", position + n - 1);
+  const size_t need = (size_t)m->ps_blocks * kPsWaves * (m->d.num_layers + 1) * PS_STAGES * kPsEvents;
+  if (n_out != need) return fail(TLM_ERR_INVALID, "TLMModel: trace buffer holds %zu stamps, need %zu", n_out, need);
+  rc = tlm_model_finalize(m);
+  if (rc) return rc;
+  unsigned long long* tr = nullptr;
+  PsArgs* ad = nullptr;
+  HIP_TRY(hipMalloc(&tr, need * sizeof(unsigned long long)));
+  if (hipMalloc(&ad, sizeof(PsArgs)) != hipSuccess) {
+    hipFree(tr);
+    return fail(TLM_ERR_OOM, "TLMModel: trace arguments");
+  }
+  PsArgs a = ps_args(m);
+  a.trace = tr;
+  hipStream_t st = m->ctx->stream;
+  bool ok = hipMemcpy(ad, &a, sizeof a, hipMemcpyHostToDevice) == hipSuccess;
+  launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
+  for (int i = 0; i < n && ok; i++) {
+    ok &= hipMemsetAsync(tr, 0, need * sizeof(unsigned long long), st) == hipSuccess;
+    ok &= launch_ps_token(m->ps, m->ps_blocks, m->ps_smem, ad, st);
+    ok &= enqueue_head(m, st, true, nullptr, true);
+  }
+  hipError_t e = hipStreamSynchronize(st);
+  if (ok && e == hipSuccess) e = hipMemcpy(out, tr, need * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+  hipFree(tr);
+  hipFree(ad);
+  if (!ok) return fail(TLM_ERR_STATE, "TLMModel: traced launch failed");
+  if (e != hipSuccess) return fail(TLM_ERR_HIP, "TLMModel: %s", hipGetErrorString(e));
+  return ps_check(m);
+}
+
 int tlm_model_describe(tlm_model* m, char* out, size_t len) {
   if (!m || !out) return fail(TLM_ERR_INVALID, "TLMModel: null argument");
   const Layer& L = m->layers[0];
@@ -1712,6 +1937,18 @@ int tlm_model_describe(tlm_model* m, char* out, size_t len) {
                   p(m->head) + " grid=" + std::to_string(m->lm_plan.gx) + " waves=" +
                   std::to_string(m->lm_plan.waves) + "] attn[nsplit=" + std::to_string(m->attn.nsplit) + "/" + std::to_string(m->attn.nsplit_long) +
                   " G=" + std::to_string(m->attn.G) + "]";
+  if (m->ps_on) {
+    const PsArgs a = ps_args(m);
+    const int To = a.To, nq = (a.Hq + 2 * a.Hkv) * a.kq, ng = (a.Tgu + a.mw - 1) / a.mw;
+    const int items = nq + a.Hq + To * a.ko + ng + To * a.ks;
+    char b[320];
+    snprintf(b, sizeof b, " persistent[%d blocks, %d items: %d qkv (%d splits), %d att, %d o (%d splits), %d gate|up "
+             "(32x%d), %d down (%d splits); %zu B LDS; variant nx=%d no=%d nd=%d]", m->ps_blocks, items, nq, a.kq,
+             a.Hq, To * a.ko, a.ko, ng, a.mw, To * a.ks, a.ks, m->ps_smem, m->ps.nx, m->ps.no, m->ps.nd);
+    s += b;
+  } else {
+    s += " persistent[off]";
+  }
   snprintf(out, len, "%s", s.c_str());
   return TLM_OK;
 }

@@ -10,6 +10,20 @@
 
 namespace tlm {
 
+// A pointer known to address global memory (address space 1): loads and
+// stores through it are global_* instructions.  Pointers read from memory
+// (argument tables) are otherwise generic, and flat instructions count in
+// lgkmcnt too, so every LDS wait would also wait for them.
+#define TLM_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ const TLM_GLOBAL T* gl(const T* p) {
+  return (const TLM_GLOBAL T*)p;
+}
+template <typename T>
+__device__ __forceinline__ TLM_GLOBAL T* glw(T* p) {
+  return (TLM_GLOBAL T*)p;
+}
+
 constexpr float kLowest = -3.4028234663852886e38f;  // TSLLogits.ts:21 LOWEST_FLOAT
 
 __device__ __forceinline__ float h2f(uint32_t bits) { return __half2float(__ushort_as_half((unsigned short)bits)); }
@@ -156,6 +170,23 @@ __device__ __forceinline__ float dot_f16(const uint4 d, const float* __restrict_
 }
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Global-memory vector loads (through the native vector types: HIP's vector
+// classes cannot bind an address-space-1 reference).
+__device__ __forceinline__ uint4 ldg_u4(const uint4* p) {
+  const u32x4 v = *gl(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ldg_u2(const void* p) {
+  const u32x2 v = *gl(reinterpret_cast<const u32x2*>(p));
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ float4 ldg_f4(const float* p) {
+  const f32x4 v = *gl(reinterpret_cast<const f32x4*>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
 
 template <typename KT>
 __device__ __forceinline__ float kv_load(const KT* p);
@@ -188,7 +219,6 @@ constexpr __host__ __device__ inline HeadTiling head_tiling(int dt, int esz) {
 // <= 32 through runtime bounds (element-wise, clamped loads).
 inline int attn_dt(int D) { return D <= 32 ? 32 : D; }
 
-int attn_lpp(int D, bool kv_f32) { return head_tiling(attn_dt(D), kv_f32 ? 4 : 2).lpp; }
 
 // LDS of one head_kernel wave (floats): q, the new k and v, their pre-RoPE
 // values, the pass's probabilities and the V tile (4 KiB); a multiple of 4
@@ -197,13 +227,6 @@ constexpr __host__ __device__ inline int head_wave_floats(int dt, int esz) {
   return (6 * dt + head_tiling(dt, esz).sub + 1024 + 3) & ~3;
 }
 
-// LDS of a head_kernel block: one wave region per wave, then (long windows)
-// the merge area [kAttnWaves][2 + DT] (max, sum, unnormalised output of each wave).
-size_t attn_smem_bytes(int gmax, int D, bool kv_f32, bool long_win) {
-  (void)gmax;
-  const int dt = attn_dt(D), esz = kv_f32 ? 4 : 2, nw = long_win ? kAttnWaves : 1;
-  return sizeof(float) * ((size_t)nw * head_wave_floats(dt, esz) + (long_win ? (size_t)nw * (2 + dt) : 0));
-}
 
 // Order a wave's own LDS writes before its later reads (regions private to
 // one wave: no block barrier, whose waves may run different pass counts).
@@ -212,5 +235,50 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
+
+// Global loads of one head_kernel pass, held in registers: this lane's K-row
+// slice (DL elements) and its 64 bytes of the pass's V rows.  Unconditional:
+// rows are clamped to t1 - 1.
+template <typename KT, int KW, bool GEN, int DL>
+struct HeadLoads {
+  static constexpr int ESZ = sizeof(KT);
+  uint32_t kw[KW];
+  uint4 vs[4];
+  __device__ __forceinline__ void issue(const KT* kh, const KT* vh, int tb, int t1, int pl, int part, int D,
+                                        int row_bytes, int lane) {
+    const int t = min(tb + pl, t1 - 1);
+    if (!GEN) {
+      const TLM_GLOBAL u32x4* kr = gl(reinterpret_cast<const u32x4*>(kh + (size_t)t * D + part * DL));
+#pragma unroll
+      for (int j = 0; j < KW / 4; j++) {
+        const u32x4 v = kr[j];
+        kw[4 * j] = v.x;
+        kw[4 * j + 1] = v.y;
+        kw[4 * j + 2] = v.z;
+        kw[4 * j + 3] = v.w;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int off = (j * 64 + lane) * 16;  // byte offset in the [SUB][D] tile
+        const int r = min(tb + off / row_bytes, t1 - 1);
+        const u32x4 v = *gl(reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(vh + (size_t)r * D) +
+                                                          off % row_bytes));
+        vs[j] = make_uint4(v.x, v.y, v.z, v.w);
+      }
+    } else {
+      const KT* kr = kh + (size_t)t * D;
+#pragma unroll
+      for (int e = 0; e < DL; e++) {
+        const int k = min(part * DL + e, D - 1);
+        const uint32_t v = ESZ == 2 ? (uint32_t)((const uint16_t*)kr)[k] : ((const uint32_t*)kr)[k];
+        if (ESZ == 2) {
+          if (e & 1) kw[e >> 1] |= v << 16; else kw[e >> 1] = v;
+        } else {
+          kw[e] = v;
+        }
+      }
+    }
+  }
+};
 
 }  // namespace tlm

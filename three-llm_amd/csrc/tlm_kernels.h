@@ -47,8 +47,10 @@ __host__ __device__ inline ChunkPlan chunk_plan(int pos, int window, int nsplit,
 }
 
 // ctrl block (device int32[8]): per-token state read by every kernel so that one
-// captured graph serves every position.
-enum Ctrl { C_TOKEN = 0, C_POS = 1, C_STEP = 2, C_BASE = 3, C_LEN = 4 };
+// captured graph serves every position.  C_SEQ numbers the tokens of the
+// persistent schedule (the tag of its published words, never 0); C_ERR
+// collects its wait time-outs.
+enum Ctrl { C_TOKEN = 0, C_POS = 1, C_STEP = 2, C_BASE = 3, C_LEN = 4, C_SEQ = 5, C_ERR = 7 };
 
 // Embedding row staging: the kernels that choose the next token (set_ctrl,
 // prefill_advance, argmax_merge) also write its embedding row, in fixed point,
@@ -93,6 +95,9 @@ struct GemvArgs {
   int* tokens_out;     // greedy stream (indexed by ctrl[C_STEP]), may be null
   int advance;         // 1: last block advances ctrl (token <- argmax, pos++, step++)
   int max_steps;
+  // PRO_RMSF input of the persistent schedule: acc_in holds kRep partials of
+  // published words (fp32 value in bits 0..31), summed as floats
+  int ps_words;
 };
 
 // Fused gate|up -> SwiGLU -> down of one 32-index slice of the intermediate
@@ -149,11 +154,12 @@ void launch_silu_mul(const float* g, const float* u, int n, float* out, hipStrea
 void launch_reduce(const float* part, int n_part, int stride, const float* bias, int n, float* y, hipStream_t st);
 void launch_argmax(const float* logits, int n, float* pval, int* pidx, int* token, int blocks, hipStream_t st);
 // second pass of the greedy sampler; `ctrl` receives the token at ctrl[C_TOKEN]
+// ps: the token came from the persistent schedule; advance its token number (C_SEQ)
 void launch_argmax_merge(const float* pval, const int* pidx, int n, int* ctrl, int* tokens_out, int advance,
-                         int max_steps, const EmbStage& es, hipStream_t st);
+                         int max_steps, const EmbStage& es, hipStream_t st, int ps = 0);
 void launch_set_ctrl(int* ctrl, int token, int pos, int step, int base, int len, const EmbStage& es,
                      hipStream_t st);
-void launch_prefill_advance(int* ctrl, const int* prompt, const EmbStage& es, hipStream_t st);
+void launch_prefill_advance(int* ctrl, const int* prompt, const EmbStage& es, hipStream_t st, int ps = 0);
 void launch_copy(uint4* dst, const uint4* src, size_t n16, hipStream_t st);
 void launch_dequant(int fmt, const uint4* w, const uint16_t* s, int N, int T, int C, int K, float* out,
                     hipStream_t st);
@@ -166,6 +172,91 @@ int attn_lpp(int D, bool kv_f32);
 constexpr int kTopkMax = 16;
 bool launch_topk(const float* logits, int n, int k, float softcap, float* wv, int* wi, size_t wcap, float* out_v,
                  int* out_i, hipStream_t st);
+
+// --------------------------------------------- persistent per-token schedule --
+// One launch computes every layer of one token on one 1024-thread block per
+// CU.  A layer is five stages; every block holds at most kPsRoles (stage, item)
+// roles, fixed for the launch, so it issues a role's weights as soon as its
+// previous role is published, then waits.  The stages run one after another,
+// so a block's later role costs no time.  Linears are split along K over
+// several items (more CUs per stage); their consumers add the partial sums:
+//   QKV   (item = head x one of kq K-splits: Hq q, Hkv k, Hkv v heads)  RMSNorm
+//         of the residual, the head's D rows of q|k|v partial sums, RoPE (linear,
+//         so applied per partial), bias in split 0
+//   ATT   (item = query head)  sums the q|k|v partials, appends the rounded k
+//         and v to the cache, attention over the window split over the 16
+//         waves and merged in LDS
+//   O     (item = 64-row tile of H x one of ko K-splits)  partial x_mid rows
+//         (split 0 adds the residual rows)
+//   GU    (item = mw paired 32-index gate|up tiles)  RMSNorm of x_mid, gate|up,
+//         SwiGLU
+//   DOWN  (item = 64-row tile x one of ks K-splits)  partial rows of the down
+//         projection (split 0 adds x_mid): the residual is the sum of the ks
+//         partials
+// Producers publish 8-byte words (fp32 value, token number ctrl[C_SEQ]) with
+// device-scope stores (past the per-XCD L2); a consumer polls its words until
+// they all carry the current token number.  No atomics, no clearing between
+// tokens.  Every wait is bounded (kPsTimeoutTicks); a time-out sets ctrl[C_ERR].
+constexpr int kPsWaves = 16;
+constexpr int kPsMaxKs = 4;        // K-splits of a linear (partials its consumers add)
+constexpr int kPsRoles = 3;        // (stage, item) roles per block
+constexpr long long kPsTimeoutTicks = 10000000;  // 100 ms of the 100 MHz wall clock
+enum PsStage { PS_QKV = 0, PS_ATT = 1, PS_O = 2, PS_GU = 3, PS_DOWN = 4, PS_STAGES = 5 };
+struct PsLayer {
+  const uint4* wqkv;
+  const uint16_t* sqkv;
+  const float* bqkv;      // [Nqkv] (zeros without a bias)
+  const float* attn_norm;
+  const uint4* wo;
+  const uint16_t* so;
+  const uint4* wgu;       // paired gate|up tiles
+  const uint16_t* sgu;
+  const float* ffn_norm;
+  const uint4* wd;
+  const uint16_t* sd;
+  void* kc;               // [Hkv][max_tokens][D]
+  void* vc;
+};
+struct PsArgs {
+  const PsLayer* layers;  // [L]
+  const int* roles;       // [blocks][kPsRoles][2]: (stage, item) pairs in stage order; stage -1: none
+  int L, H, I, Hq, Hkv, D, G, rd, max_tokens, window;
+  int Nqkv, QS;
+  int Cx, Co, Cd;         // chunks per row: H-input linears (qkv, gate|up), O (K = QS), down (K = I)
+  int To, Tgu, Tq;        // 64-row tiles: H outputs (O, down), gate|up (paired), qkv
+  int mw;                 // gate|up tiles per GU item
+  int kq, cq, ko, co, ks, cs;  // K-splits and chunks per split: qkv, O, down
+  float eps, scale;
+  int* ctrl;
+  const void* emb;        // [V][H] fp16 or fp32 (layer 0's residual)
+  int emb_f32;
+  const float* rope_cos;  // [max_tokens][max(rd / 2, 1)]
+  const float* rope_sin;
+  // published words (fp32 value, token number), per layer
+  unsigned long long* pub_x;    // [L][kPsMaxKs][H] down partials (splits >= ks stay zero)
+  unsigned long long* pub_qkv;  // [L][kq][Nqkv] partial q, k (RoPE applied), v
+  unsigned long long* pub_o;    // [L][QS] attention output
+  unsigned long long* pub_xm;   // [L][ko][H] partial x_mid
+  unsigned long long* pub_h;    // [L][Tgu * 32] silu(gate) * up (zero past I)
+  // optional timeline: per (block, wave), per layer and stage, kPsEvents
+  // wall-clock stamps (100 MHz) taken by the wave's first lane; stage slot
+  // PS_STAGES of layer L holds the kernel's start and end
+  unsigned long long* trace;
+};
+constexpr int kPsEvents = 4;  // weights issued, input ready, computed, published
+// Template choice of the persistent kernel for a model (dt == 0: none).
+struct PsShape {
+  int fmt, kv_f32, dt, nx, no, nd, mw, kq, ko, ks;
+};
+PsShape ps_shape(int fmt, int kv_f32, int H, int I, int D, int Hq, int Hkv, int cus);
+size_t ps_smem_bytes(const PsShape& sh, int H, int QS);
+// Block roles of a shape: [blocks][kPsRoles][2] (stage, item), stage -1 = none;
+// false when the items need more than kPsRoles roles per block.
+bool ps_roles(const PsShape& sh, int blocks, int H, int Hq, int Hkv, int Tgu, int* roles);
+// once per model, outside stream capture: allows the kernel smem bytes of LDS
+bool ps_prepare(const PsShape& sh, size_t smem);
+// a_dev: the arguments in device memory (kernel reads them with scalar loads)
+bool launch_ps_token(const PsShape& sh, int blocks, size_t smem, const PsArgs* a_dev, hipStream_t st);
 
 // ------------------------------------------------------------ batched prefill --
 // A chunk of M prompt positions per pass: row-major activations, linears as

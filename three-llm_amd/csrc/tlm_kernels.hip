@@ -71,9 +71,6 @@ __device__ float attn_combine_elem(const float* pacc, const float* pml, int row,
   return O / L;
 }
 
-// Elements handled per thread in one round trip by the attention gather.
-constexpr int kEpt = 4;
-
 // Stores 4 prologue outputs at slice offset i (a multiple of 4) and, for q4,
 // adds them into the group sums sum_k x_k of the 32-element groups: the 8
 // lanes covering a group reduce with shuffles.  Every lane of the wave must
@@ -268,6 +265,17 @@ struct GemvPrologue {
   // Residual row float4 r: base + partials, or the sum of the fixed-point replicas.
   __device__ __forceinline__ float4 residual4(const GemvArgs& a, int r) {
     if (kRmsF) {
+      if (a.ps_words) {  // published words: the fp32 value in the low half, partials summed in order
+        float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int q = 0; q < kRep; q++) {
+          y.x += __uint_as_float((unsigned)fx[kRmsF ? r : 0][q][0].x);
+          y.y += __uint_as_float((unsigned)fx[kRmsF ? r : 0][q][0].y);
+          y.z += __uint_as_float((unsigned)fx[kRmsF ? r : 0][q][1].x);
+          y.w += __uint_as_float((unsigned)fx[kRmsF ? r : 0][q][1].y);
+        }
+        return y;
+      }
       unsigned long long s0 = 0, s1 = 0, s2 = 0, s3 = 0;
 #pragma unroll
       for (int q = 0; q < kRep; q++) {
@@ -528,9 +536,16 @@ __device__ __forceinline__ void stage_embedding(const EmbStage& es, int token) {
                             : h2f(((const uint16_t*)es.emb)[(size_t)token * es.H + i]));
 }
 
+// The persistent schedule's token number advances once its token is done
+// (never 0: zeroed words never match).
+__device__ __forceinline__ void ps_next_token(int* ctrl) {
+  const unsigned seq = (unsigned)ctrl[C_SEQ] + 1u;
+  ctrl[C_SEQ] = (int)(seq ? seq : 1u);
+}
+
 __global__ __launch_bounds__(1024) void argmax_merge_kernel(const float* pval, const int* pidx, int n, int* ctrl,
                                                             int* tokens_out, int advance, int max_steps,
-                                                            EmbStage es) {
+                                                            EmbStage es, int ps) {
   __shared__ float sv[16];
   __shared__ int si[16];
   __shared__ int tok_s;
@@ -565,6 +580,7 @@ __global__ __launch_bounds__(1024) void argmax_merge_kernel(const float* pval, c
       ctrl[C_POS] += 1;
       ctrl[C_STEP] += 1;
     }
+    if (ps) ps_next_token(ctrl);
     tok_s = token;
   }
   __syncthreads();
@@ -572,9 +588,9 @@ __global__ __launch_bounds__(1024) void argmax_merge_kernel(const float* pval, c
 }
 
 void launch_argmax_merge(const float* pval, const int* pidx, int n, int* ctrl, int* tokens_out, int advance,
-                         int max_steps, const EmbStage& es, hipStream_t st) {
+                         int max_steps, const EmbStage& es, hipStream_t st, int ps) {
   hipLaunchKernelGGL(argmax_merge_kernel, dim3(1), dim3(1024), 0, st, pval, pidx, n, ctrl, tokens_out, advance,
-                     max_steps, es);
+                     max_steps, es, ps);
 }
 
 size_t gemv_smem_bytes(int fmt, int cps, int waves) {
@@ -760,49 +776,16 @@ bool launch_mlp(int fmt, int nch, int ndb, int blocks, const MlpArgs& m, hipStre
 
 // ------------------------------------------------------------- attention --
 
+int attn_lpp(int D, bool kv_f32) { return head_tiling(attn_dt(D), kv_f32 ? 4 : 2).lpp; }
 
-// Global loads of one head_kernel pass, held in registers: this lane's K-row
-// slice (DL elements) and its 64 bytes of the pass's V rows.  Unconditional:
-// rows are clamped to t1 - 1.
-template <typename KT, int KW, bool GEN, int DL>
-struct HeadLoads {
-  static constexpr int ESZ = sizeof(KT);
-  uint32_t kw[KW];
-  uint4 vs[4];
-  __device__ __forceinline__ void issue(const KT* kh, const KT* vh, int tb, int t1, int pl, int part, int D,
-                                        int row_bytes, int lane) {
-    const int t = min(tb + pl, t1 - 1);
-    if (!GEN) {
-      const uint4* kr = reinterpret_cast<const uint4*>(kh + (size_t)t * D + part * DL);
-#pragma unroll
-      for (int j = 0; j < KW / 4; j++) {
-        const uint4 v = kr[j];
-        kw[4 * j] = v.x;
-        kw[4 * j + 1] = v.y;
-        kw[4 * j + 2] = v.z;
-        kw[4 * j + 3] = v.w;
-      }
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int off = (j * 64 + lane) * 16;  // byte offset in the [SUB][D] tile
-        const int r = min(tb + off / row_bytes, t1 - 1);
-        vs[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(vh + (size_t)r * D) + off % row_bytes);
-      }
-    } else {
-      const KT* kr = kh + (size_t)t * D;
-#pragma unroll
-      for (int e = 0; e < DL; e++) {
-        const int k = min(part * DL + e, D - 1);
-        const uint32_t v = ESZ == 2 ? (uint32_t)((const uint16_t*)kr)[k] : ((const uint32_t*)kr)[k];
-        if (ESZ == 2) {
-          if (e & 1) kw[e >> 1] |= v << 16; else kw[e >> 1] = v;
-        } else {
-          kw[e] = v;
-        }
-      }
-    }
-  }
-};
+// LDS of a head_kernel block: one wave region per wave, then (long windows)
+// the merge area [kAttnWaves][2 + DT] (max, sum, unnormalised output of each wave).
+size_t attn_smem_bytes(int gmax, int D, bool kv_f32, bool long_win) {
+  (void)gmax;
+  const int dt = attn_dt(D), esz = kv_f32 ? 4 : 2, nw = long_win ? kAttnWaves : 1;
+  return sizeof(float) * ((size_t)nw * head_wave_floats(dt, esz) + (long_win ? (size_t)nw * (2 + dt) : 0));
+}
+
 
 // One block = one query head x one chunk of positions (split-K over the
 // sequence, flash decoding; TSLAttention.ts:306-428 computes the same scores
@@ -1320,7 +1303,7 @@ void launch_set_ctrl(int* ctrl, int token, int pos, int step, int base, int len,
 
 // prefillChunkComputeNodes' advance node (DecoderTSLRunner.ts:216-225): next
 // position, next prompt token.
-__global__ void prefill_advance_kernel(int* ctrl, const int* prompt, EmbStage es) {
+__global__ void prefill_advance_kernel(int* ctrl, const int* prompt, EmbStage es, int ps) {
   const int pos = ctrl[C_POS] + 1;
   const int i = pos - ctrl[C_BASE];
   const bool next = i >= 0 && i < ctrl[C_LEN];
@@ -1329,12 +1312,13 @@ __global__ void prefill_advance_kernel(int* ctrl, const int* prompt, EmbStage es
   if (threadIdx.x == 0) {
     ctrl[C_POS] = pos;
     if (next) ctrl[C_TOKEN] = token;
+    if (ps) ps_next_token(ctrl);
   }
   if (next) stage_embedding(es, token);
 }
 
-void launch_prefill_advance(int* ctrl, const int* prompt, const EmbStage& es, hipStream_t st) {
-  hipLaunchKernelGGL(prefill_advance_kernel, dim3(1), dim3(256), 0, st, ctrl, prompt, es);
+void launch_prefill_advance(int* ctrl, const int* prompt, const EmbStage& es, hipStream_t st, int ps) {
+  hipLaunchKernelGGL(prefill_advance_kernel, dim3(1), dim3(256), 0, st, ctrl, prompt, es, ps);
 }
 
 // Streaming copy, 16 bytes per lane per iteration.

@@ -32,6 +32,7 @@ EXPORTS = [
     "tlm_compute_token",
     "tlm_prefill", "tlm_read_logits", "tlm_read_token", "tlm_decode_greedy", "tlm_reset_cache", "tlm_kv_write",
     "tlm_kv_read", "tlm_kv_fill_normal", "tlm_read_hidden", "tlm_time_decode", "tlm_time_kernel", "tlm_time_head",
+    "tlm_trace_decode",
     "tlm_model_describe", "tlm_synth_normal", "tlm_synth_tokens", "tlm_quantize_q4", "tlm_f32_to_f16",
 ]
 
@@ -122,6 +123,7 @@ def lib():
             "tlm_time_kernel": ([VP, ctypes.c_int, ctypes.c_int, ctypes.POINTER(dbl)], ctypes.c_int),
             "tlm_time_head": ([VP, i32, i32, ctypes.c_int, ctypes.POINTER(dbl)], ctypes.c_int),
             "tlm_model_describe": ([VP, ctypes.c_char_p, sz], ctypes.c_int),
+            "tlm_trace_decode": ([VP, i32, i32, ctypes.c_int, VP, sz], ctypes.c_int),
             "tlm_synth_normal": ([u64, u64, sz, ctypes.c_float, VP], ctypes.c_int),
             "tlm_synth_tokens": ([u64, u64, sz, i32, VP], ctypes.c_int),
             "tlm_quantize_q4": ([VP, ctypes.c_int, ctypes.c_int, VP, VP], ctypes.c_int),
@@ -461,6 +463,15 @@ class Model:
         ms = ctypes.c_double()
         check(lib().tlm_time_head(self.ptr, int(token), int(position), n, ctypes.byref(ms)))
         return ms.value
+
+    def trace_decode(self, token: int, position: int, n: int, blocks: int) -> np.ndarray:
+        """Timeline of the last of n persistent-schedule decode steps:
+        uint64 [blocks][16 waves][layers + 1][5 stages][4 events] wall-clock
+        stamps (100 MHz)."""
+        L = self.desc.num_layers
+        out = np.zeros((blocks, 16, L + 1, 5, 4), np.uint64)
+        check(lib().tlm_trace_decode(self.ptr, int(token), int(position), int(n), _ptr(out), out.size))
+        return out
 
     def time_kernel(self, which: int, iters: int) -> float:
         ms = ctypes.c_double()
