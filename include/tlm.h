@@ -130,6 +130,16 @@ int tlm_op_attention(tlm_attn* attn, const float* qkv, int position, float* out)
  * [max(0, pos - W + 1), pos] on MFMA; out: fp16 bits device [rows][heads * head_dim].
  * Needs an fp16 cache and head_dim 64 or 128.  Waits for the stream. */
 int tlm_op_attention_rows(tlm_attn* attn, const float* qkv, int32_t rows, int32_t position0, uint16_t* out);
+/* Allocation-free tlm_op_attention_rows.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops).  The same kernels and results; the rotated
+ * fp16 queries are staged in a fixed 4 MiB device array of the library (one
+ * per device, held until the process ends) instead of a buffer allocated per
+ * call, so rows * heads * head_dim * 2 may not exceed 4 MiB (TLM_ERR_RANGE
+ * otherwise).  Enqueue only: no allocation, free or wait.  Every call on one
+ * device shares that array, so calls that overlap on one device (other
+ * streams or contexts) race. */
+int tlm_op_attention_rows_noalloc(tlm_attn* attn, const float* qkv, int32_t rows, int32_t position0, uint16_t* out);
 int tlm_attn_reset(tlm_attn* attn);
 /* Cache rows [0, count) as fp32 [count][kv_heads*head_dim] (host). */
 int tlm_attn_read_cache(tlm_attn* attn, int count, float* k_out, float* v_out);

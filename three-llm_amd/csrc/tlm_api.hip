@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -42,6 +43,36 @@ static int fail(int code, const char* fmt, ...) {
     if (e_ != hipSuccess) return fail(TLM_ERR_HIP, "%s: launch failed: %s", component, hipGetErrorString(e_)); \
   } while (0)
 
+// ------------------------------------------------- allocation-free scratch --
+// tlm_op_attention_rows_noalloc stages the batched attention's rotated fp16
+// queries here instead of in a hipMalloc'd buffer.  Each device that loads the
+// library holds its own copy until the process ends.  In host code the name
+// `scratch` is only a stand-in for the device array: kernels and copies get
+// the device address that hipGetSymbolAddress returns (once per device, at
+// tlm_open, with that device current).  Every call on a device shares that
+// device's copy, so calls that overlap on one device race.
+constexpr size_t kScratchBytes = (size_t)4 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+constexpr int kScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch[kScratchDevices] = {};
+
+static int scratch_address(int device, void** out) {  // device current
+  if (device < 0 || device >= kScratchDevices)
+    return fail(TLM_ERR_INVALID, "TLMContext: device %d beyond the %d the scratch table holds", device,
+                kScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(TLM_ERR_HIP, "TLMContext: scratch address on device %d: %s", device, hipGetErrorString(e));
+    g_scratch[device] = p;
+  }
+  *out = g_scratch[device];
+  return TLM_OK;
+}
+
 // ---------------------------------------------------------------- objects --
 
 struct tlm_ctx {
@@ -55,6 +86,7 @@ struct tlm_ctx {
   // top-k levels: two levels of kTopkWork (score, id) pairs
   float* topk_v = nullptr;
   int* topk_i = nullptr;
+  void* scratch = nullptr;  // this device's copy of `scratch` (device address)
 };
 constexpr size_t kTopkWork = 32768;
 
@@ -362,6 +394,11 @@ int tlm_open(int device, tlm_ctx** out) {
   if (e != hipSuccess) {
     tlm_close(c);
     return fail(TLM_ERR_HIP, "TLMContext: setup failed: %s", hipGetErrorString(e));
+  }
+  const int rc = scratch_address(device, &c->scratch);
+  if (rc) {
+    tlm_close(c);
+    return rc;
   }
   *out = c;
   return TLM_OK;
@@ -715,7 +752,11 @@ int tlm_op_attention(tlm_attn* A, const float* qkv, int position, float* out) {
   return TLM_OK;
 }
 
-int tlm_op_attention_rows(tlm_attn* A, const float* qkv, int32_t rows, int32_t position0, uint16_t* out) {
+// RoPE + cache append of `rows` positions from position0, then their causal
+// attention, enqueued on the context's stream; q: fp16 staging of the rotated
+// queries, [rows][heads * head_dim].
+static int check_attention_rows(const tlm_attn* A, const float* qkv, int32_t rows, int32_t position0,
+                                const uint16_t* out) {
   if (!A || !qkv || !out || rows <= 0) return fail(TLM_ERR_INVALID, "TLMAttention: invalid argument");
   const tlm_attn_desc& d = A->d;
   if (position0 < 0 || position0 + rows > d.max_tokens)
@@ -723,10 +764,13 @@ int tlm_op_attention_rows(tlm_attn* A, const float* qkv, int32_t rows, int32_t p
                 d.max_tokens);
   if (d.kv_fmt == TLM_FMT_F32 || (d.head_dim != 64 && d.head_dim != 128))
     return fail(TLM_ERR_INVALID, "TLMAttention: batched rows need an fp16 cache and head_dim 64 or 128");
+  return TLM_OK;
+}
+
+static bool enqueue_attention_rows(tlm_attn* A, const float* qkv, int32_t rows, int32_t position0, uint16_t* out,
+                                   uint16_t* q) {
+  const tlm_attn_desc& d = A->d;
   hipStream_t st = A->ctx->stream;
-  uint16_t* q = nullptr;
-  const size_t qn = (size_t)rows * d.heads * d.head_dim;
-  HIP_TRY(hipMalloc(&q, 2 * qn));
   RopeKvArgs r;
   memset(&r, 0, sizeof r);
   r.qkv = qkv;
@@ -760,12 +804,35 @@ int tlm_op_attention_rows(tlm_attn* A, const float* qkv, int32_t rows, int32_t p
   pa.max_tokens = d.max_tokens;
   pa.window = d.sliding_window;
   pa.scale_log2 = A->scale * 1.4426950408889634f;
-  const bool launched = launch_prefill_attention(pa, st);
+  return launch_prefill_attention(pa, st);
+}
+
+int tlm_op_attention_rows(tlm_attn* A, const float* qkv, int32_t rows, int32_t position0, uint16_t* out) {
+  int rc = check_attention_rows(A, qkv, rows, position0, out);
+  if (rc) return rc;
+  uint16_t* q = nullptr;
+  HIP_TRY(hipMalloc(&q, sizeof(uint16_t) * (size_t)rows * A->d.heads * A->d.head_dim));
+  const bool launched = enqueue_attention_rows(A, qkv, rows, position0, out, q);
   hipError_t e = hipGetLastError();
-  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e == hipSuccess) e = hipStreamSynchronize(A->ctx->stream);
   hipFree(q);
   if (e != hipSuccess) return fail(TLM_ERR_HIP, "TLMAttention: batched rows failed: %s", hipGetErrorString(e));
   if (!launched) return fail(TLM_ERR_STATE, "TLMAttention: no batched attention kernel for this shape");
+  return TLM_OK;
+}
+
+int tlm_op_attention_rows_noalloc(tlm_attn* A, const float* qkv, int32_t rows, int32_t position0, uint16_t* out) {
+  int rc = check_attention_rows(A, qkv, rows, position0, out);
+  if (rc) return rc;
+  const size_t need = sizeof(uint16_t) * (size_t)rows * A->d.heads * A->d.head_dim;
+  if (need > kScratchBytes)
+    return fail(TLM_ERR_RANGE, "TLMAttention: %d rows need %zu bytes of query staging; the allocation-free "
+                "entry point holds %zu (at most %zu rows of this shape)", rows, need, kScratchBytes,
+                kScratchBytes / (sizeof(uint16_t) * A->d.heads * A->d.head_dim));
+  if (!A->ctx->scratch) return fail(TLM_ERR_STATE, "TLMAttention: the context has no scratch address");
+  if (!enqueue_attention_rows(A, qkv, rows, position0, out, static_cast<uint16_t*>(A->ctx->scratch)))
+    return fail(TLM_ERR_STATE, "TLMAttention: no batched attention kernel for this shape");
+  CHECK_LAUNCH("TLMAttention");
   return TLM_OK;
 }
 

@@ -26,7 +26,7 @@ EXPORTS = [
     "tlm_abi_version", "tlm_last_error", "tlm_open", "tlm_close", "tlm_sync", "tlm_device_info", "tlm_alloc",
     "tlm_free", "tlm_upload", "tlm_download", "tlm_copy", "tlm_linear_create", "tlm_linear_destroy", "tlm_linear_dequant",
     "tlm_op_linear", "tlm_op_linear_rows", "tlm_op_rmsnorm", "tlm_op_silu_mul", "tlm_op_gated_mlp", "tlm_attn_create", "tlm_attn_destroy",
-    "tlm_op_attention", "tlm_op_attention_rows", "tlm_attn_reset", "tlm_attn_read_cache", "tlm_op_logits", "tlm_op_argmax",
+    "tlm_op_attention", "tlm_op_attention_rows", "tlm_op_attention_rows_noalloc", "tlm_attn_reset", "tlm_attn_read_cache", "tlm_op_logits", "tlm_op_argmax",
     "tlm_op_topk", "tlm_read_candidates",
     "tlm_model_create", "tlm_model_destroy", "tlm_model_upload", "tlm_model_finalize", "tlm_model_set_prefill",
     "tlm_compute_token",
@@ -98,6 +98,7 @@ def lib():
             "tlm_attn_destroy": ([VP], None),
             "tlm_op_attention": ([VP, VP, ctypes.c_int, VP], ctypes.c_int),
             "tlm_op_attention_rows": ([VP, VP, i32, i32, VP], ctypes.c_int),
+            "tlm_op_attention_rows_noalloc": ([VP, VP, i32, i32, VP], ctypes.c_int),
             "tlm_attn_reset": ([VP], ctypes.c_int),
             "tlm_attn_read_cache": ([VP, ctypes.c_int, VP, VP], ctypes.c_int),
             "tlm_op_logits": ([VP, VP, VP, VP], ctypes.c_int),
@@ -308,6 +309,12 @@ class Attention:
     def rows(self, qkv: Buffer, n_rows: int, position0: int, out: Buffer) -> Buffer:
         """Positions position0.. at once: qkv fp32 [n_rows][(H+2Hkv)D] -> out fp16 bits [n_rows][H D]."""
         check(lib().tlm_op_attention_rows(self.ptr, qkv.ptr, int(n_rows), int(position0), out.ptr))
+        return out
+
+    def rows_noalloc(self, qkv: Buffer, n_rows: int, position0: int, out: Buffer) -> Buffer:
+        """rows() through the allocation-free entry point (enqueue only; the
+        query staging is the library's fixed 4 MiB device array)."""
+        check(lib().tlm_op_attention_rows_noalloc(self.ptr, qkv.ptr, int(n_rows), int(position0), out.ptr))
         return out
 
     def reset(self):
