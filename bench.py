@@ -2,16 +2,17 @@
 
     python bench.py [--steps K] [--warmup W] [--workload qwen2.5-0.5b]
 
-A step is one decode token at batch 1: one HIP graph launch covering every
-layer, the LM head and the greedy argmax, with the token fed back on the
-device.  The default workload is the Qwen2.5-0.5B-shaped decoder (24 layers,
+A step is one decode token at batch 1: one HIP graph launch (the persistent
+layer kernel, the LM head and the greedy argmax), with the token fed back on
+the device.  The default workload is the Qwen2.5-0.5B-shaped decoder (24 layers,
 hidden 896, q4 g32 linears, fp16 tied head): a 128-token random prompt, then
 K = 256 greedy decode steps timed (positions 127..382), after W untimed
 warm-up steps over the same positions.  Weights are synthetic N(0, 0.02).
 
 Prints one JSON line.  Besides tok/s it reports the fraction of the HBM
-roofline (algorithmic bytes per token over 8 TB/s), the LM head kernel's
-roofline (the dominant kernel: 57% of the bytes) and a CPU baseline: the
+roofline (algorithmic bytes per token over 8 TB/s), the roofline of the
+step's dominant kernel (the layer part: about 90% of the step's time), the
+LM head's (57% of the bytes) as an extra field, and a CPU baseline: the
 oracle's single-threaded restatement of the reference CPU path timed on a
 bounded sample of the same workload.  Prefill: the prompt's 127 positions as
 one batched pass (MFMA GEMMs + flash attention; `prefill_tok_s`) and replaying
@@ -65,6 +66,17 @@ def bytes_per_token(hw, position: int, kv_first: int = 0) -> float:
     esz = 4 if hw.storage.kv == "f32" else 2
     kv_row = L * 2 * r.kv_head_count * r.head_dim * esz
     return lin + head + emb + norms + (position + 1 - kv_first) * kv_row + kv_row
+
+
+def layer_bytes(hw, position: int) -> float:
+    """Algorithmic bytes of the layer part of the token at `position` (the
+    persistent kernel): every layer's weights, norms and biases, the embedding
+    row, the KV rows [0, position] read and the row at position written; the
+    per-token bytes without the LM head and the final norm."""
+    r = hw.recipe
+    head = r.vocab_size * r.hidden_size * (2.0 if r.tied_embeddings else
+                                           {"q4": 0.5 + 2.0 / 32, "f16": 2.0, "f32": 4.0}[hw.storage.head])
+    return bytes_per_token(hw, position, 0) - head - r.hidden_size * 4
 
 
 def lm_head_bytes(hw, cus: int) -> float:
@@ -269,9 +281,16 @@ def main():
     ms_step = wall * 1e3 / steps
     mean_bytes = sum(bytes_per_token(hw, pos0 + i, 0) for i in range(steps)) / steps
     hbm_frac = mean_bytes * toks / HBM_PEAK
-    # dominant kernel: the LM head, timed inside decode steps over the same
-    # positions (a pair of HIP events on the model stream around each launch)
-    lm_ms = runner.model.time_head(last, pos0, min(steps, args.kernel_iters))
+    # the dominant kernel of the step: the layer part (the persistent kernel,
+    # one launch per token; the layer graph where the window is long), timed
+    # inside decode steps over the same positions (a pair of HIP events on the
+    # model stream around each launch); then the LM head the same way
+    n_k = min(steps, args.kernel_iters)
+    persistent = "persistent[off]" not in runner.model.describe() and not wl.kv_prefill
+    lay_ms = runner.model.time_layers(last, pos0, n_k)
+    lay_bytes = sum(layer_bytes(hw, pos0 + i) for i in range(n_k)) / n_k
+    lay_bw = lay_bytes / (lay_ms * 1e-3)
+    lm_ms = runner.model.time_head(last, pos0, n_k)
     lm_bytes = lm_head_bytes(hw, ctx.info()[1])
     lm_bw = lm_bytes / (lm_ms * 1e-3)
     # host-driven loop (computeToken + sampleToken per token: one 4-byte
@@ -297,6 +316,8 @@ def main():
                 for name, k in (("qkv", 4), ("attention", 1), ("o", 5), ("mlp", 2), ("top8", 6))}
     log(f"[bench] decode {toks:.1f} tok/s ({ms_step * 1e3:.1f} us/token wall, {ev_ms * 1e3 / steps:.1f} us/token "
         f"events), {mean_bytes / 1e6:.2f} MB/token -> {hbm_frac * 100:.1f}% of HBM roofline")
+    log(f"[bench] layer part ({'persistent kernel' if persistent else 'layer graph'}) {lay_ms * 1e3:.1f} us/token "
+        f"= {lay_bw / 1e9:.0f} GB/s of {lay_bytes / 1e6:.2f} MB")
     log(f"[bench] LM head {lm_ms * 1e3:.1f} us/launch in decode steps = {lm_bw / 1e9:.0f} GB/s; stage times, "
         f"back-to-back launches of layer 0 (us): "
         + ", ".join(f"{k} {v * 1e3:.1f}" for k, v in stage_ms.items()))
@@ -343,9 +364,16 @@ def main():
                    "linears": wl.storage.linear + (" g32 fp16 scales" if wl.storage.linear == "q4" else ""),
                    "head": "fp16 tied" if hw.recipe.tied_embeddings else wl.storage.head, "kv": wl.storage.kv,
                    "kv_prefill": wl.kv_prefill, "device": dev_name},
-        "roofline": {"bound": "hbm", "kernel": "lm_head_kernel", "achieved": round(lm_bw / 1e9, 1),
-                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(lm_bw / HBM_PEAK, 4),
-                     "traffic": read_traffic("lm_head"), "avg_launch_us": round(lm_ms * 1e3, 2)},
+        "roofline": {"bound": "hbm", "kernel": "ps_token_kernel" if persistent else "layer graph (per-stage kernels)",
+                     "achieved": round(lay_bw / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": round(lay_bw / HBM_PEAK, 4),
+                     "traffic": read_traffic("ps_token") if persistent else None,
+                     "avg_launch_us": round(lay_ms * 1e3, 2), "algorithmic_bytes": round(lay_bytes),
+                     "step_share": round(lay_ms / ms_step, 3)},
+        "lm_head": {"bound": "hbm", "kernel": "lm_head_kernel", "achieved": round(lm_bw / 1e9, 1),
+                    "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(lm_bw / HBM_PEAK, 4),
+                    "traffic": read_traffic("lm_head"), "avg_launch_us": round(lm_ms * 1e3, 2),
+                    "algorithmic_bytes": round(lm_bytes), "step_share": round(lm_ms / ms_step, 3)},
         "cpu_baseline": cpu,
     }
     runner.close()

@@ -253,11 +253,15 @@ int tlm_read_hidden(tlm_model* model, float* out, size_t n);
  * from the cache and ctrl state as left). */
 int tlm_time_decode(tlm_model* model, int32_t token, int32_t position, int warmup, int n, double* ms);
 int tlm_time_kernel(tlm_model* model, int which, int iters, double* avg_ms);
-/* tlm_time_head: n greedy decode steps from (token, position), each the layer
- * graph then the LM head bracketed by its own pair of events; average ms of
- * the LM head launch inside a real step (its weights cold in the caches, as in
- * decode).  Leaves the cache and ctrl state advanced like tlm_decode_greedy. */
+/* tlm_time_head / tlm_time_layers: n greedy decode steps from (token,
+ * position), each the layer part (the persistent kernel, or the layer graph in
+ * the long-window case) then the LM head, each part bracketed by its own pair
+ * of events on the model stream; average ms of the LM head launch, or of the
+ * layer part, inside a real step (weights cold in the caches, as in decode).
+ * Leaves the cache and ctrl state advanced like tlm_decode_greedy.  No
+ * reference counterpart (measurement). */
 int tlm_time_head(tlm_model* model, int32_t token, int32_t position, int n, double* avg_ms);
+int tlm_time_layers(tlm_model* model, int32_t token, int32_t position, int n, double* avg_ms);
 /* tlm_trace_decode: n greedy decode steps from (token, position) through the
  * persistent schedule, launched directly with its timeline on; `out` receives
  * the last step's timeline: for every (block, wave), layer l < L and stage

@@ -1873,8 +1873,12 @@ int tlm_time_decode(tlm_model* m, int32_t token, int32_t position, int warmup, i
   return TLM_OK;
 }
 
-int tlm_time_head(tlm_model* m, int32_t token, int32_t position, int n, double* avg_ms) {
-  if (!m || !avg_ms || n <= 0) return fail(TLM_ERR_INVALID, "TLMModel: invalid timing argument");
+// n decode steps from (token, position) with HIP events on the model stream
+// around the layer part (the persistent kernel, or the layer graph / per-stage
+// kernels) and around the LM head of each step; averages in ms.
+static int time_step_parts(tlm_model* m, int32_t token, int32_t position, int n, double* layers_ms,
+                           double* head_ms) {
+  if (!m || n <= 0) return fail(TLM_ERR_INVALID, "TLMModel: invalid timing argument");
   int rc = check_token(m, token, position);
   if (rc) return rc;
   if ((long)position + n > m->d.max_tokens) return fail(TLM_ERR_RANGE, "TLMModel: timed decode passes max_tokens");
@@ -1886,32 +1890,50 @@ int tlm_time_head(tlm_model* m, int32_t token, int32_t position, int n, double* 
       rc = capture(m, TAIL_NONE, lw, &m->graph_layers[lw], &m->g_layers[lw]);
       if (rc) return rc;
     }
-  std::vector<hipEvent_t> ev(2 * (size_t)n, nullptr);
+  std::vector<hipEvent_t> ev(4 * (size_t)n, nullptr);
   for (auto& e : ev) HIP_TRY(hipEventCreate(&e));
   launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
   bool ok = true;
   for (int i = 0; i < n && ok; i++) {
     const bool lw = long_window(&m->attn, position + i);
+    const bool ps = m->ps_on && !lw;
     m->host_pos = position + i;
-    if (m->use_graphs) {
+    hipEventRecord(ev[4 * (size_t)i], st);
+    if (ps) {
+      ok &= launch_ps_token(m->ps, m->ps_blocks, m->ps_smem, m->ps_args_dev, st);
+    } else if (m->use_graphs) {
       HIP_TRY(hipGraphLaunch(m->g_layers[lw], st));
     } else {
       for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1, lw);
     }
-    ok &= enqueue_head(m, st, true, &ev[2 * (size_t)i]);
+    hipEventRecord(ev[4 * (size_t)i + 1], st);
+    ok &= enqueue_head(m, st, true, &ev[4 * (size_t)i + 2], ps);
   }
   if (!ok) return fail(TLM_ERR_STATE, "TLMModel: no kernel variant for a stage of this model");
   CHECK_LAUNCH("TLMModel");
   HIP_TRY(hipStreamSynchronize(st));
-  double total = 0.0;
+  double tl = 0.0, th = 0.0;
   for (int i = 0; i < n; i++) {
-    float f = 0.f;
-    HIP_TRY(hipEventElapsedTime(&f, ev[2 * i], ev[2 * i + 1]));
-    total += f;
+    float f = 0.f, g = 0.f;
+    HIP_TRY(hipEventElapsedTime(&f, ev[4 * i], ev[4 * i + 1]));
+    HIP_TRY(hipEventElapsedTime(&g, ev[4 * i + 2], ev[4 * i + 3]));
+    tl += f;
+    th += g;
   }
   for (auto& e : ev) hipEventDestroy(e);
-  *avg_ms = total / n;
-  return TLM_OK;
+  if (layers_ms) *layers_ms = tl / n;
+  if (head_ms) *head_ms = th / n;
+  return ps_check(m);
+}
+
+int tlm_time_head(tlm_model* m, int32_t token, int32_t position, int n, double* avg_ms) {
+  if (!avg_ms) return fail(TLM_ERR_INVALID, "TLMModel: invalid timing argument");
+  return time_step_parts(m, token, position, n, nullptr, avg_ms);
+}
+
+int tlm_time_layers(tlm_model* m, int32_t token, int32_t position, int n, double* avg_ms) {
+  if (!avg_ms) return fail(TLM_ERR_INVALID, "TLMModel: invalid timing argument");
+  return time_step_parts(m, token, position, n, avg_ms, nullptr);
 }
 
 int tlm_time_kernel(tlm_model* m, int which, int iters, double* avg_ms) {

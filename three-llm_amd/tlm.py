@@ -32,7 +32,7 @@ EXPORTS = [
     "tlm_compute_token",
     "tlm_prefill", "tlm_read_logits", "tlm_read_token", "tlm_decode_greedy", "tlm_reset_cache", "tlm_kv_write",
     "tlm_kv_read", "tlm_kv_fill_normal", "tlm_read_hidden", "tlm_time_decode", "tlm_time_kernel", "tlm_time_head",
-    "tlm_trace_decode",
+    "tlm_time_layers", "tlm_trace_decode",
     "tlm_model_describe", "tlm_synth_normal", "tlm_synth_tokens", "tlm_quantize_q4", "tlm_f32_to_f16",
 ]
 
@@ -123,6 +123,7 @@ def lib():
             "tlm_time_decode": ([VP, i32, i32, ctypes.c_int, ctypes.c_int, ctypes.POINTER(dbl)], ctypes.c_int),
             "tlm_time_kernel": ([VP, ctypes.c_int, ctypes.c_int, ctypes.POINTER(dbl)], ctypes.c_int),
             "tlm_time_head": ([VP, i32, i32, ctypes.c_int, ctypes.POINTER(dbl)], ctypes.c_int),
+            "tlm_time_layers": ([VP, i32, i32, ctypes.c_int, ctypes.POINTER(dbl)], ctypes.c_int),
             "tlm_model_describe": ([VP, ctypes.c_char_p, sz], ctypes.c_int),
             "tlm_trace_decode": ([VP, i32, i32, ctypes.c_int, VP, sz], ctypes.c_int),
             "tlm_synth_normal": ([u64, u64, sz, ctypes.c_float, VP], ctypes.c_int),
@@ -469,6 +470,13 @@ class Model:
         """Average ms of the LM head kernel inside n real decode steps."""
         ms = ctypes.c_double()
         check(lib().tlm_time_head(self.ptr, int(token), int(position), n, ctypes.byref(ms)))
+        return ms.value
+
+    def time_layers(self, token: int, position: int, n: int) -> float:
+        """Average ms of the layer part (the persistent kernel, or the layer
+        graph) inside n real decode steps."""
+        ms = ctypes.c_double()
+        check(lib().tlm_time_layers(self.ptr, int(token), int(position), n, ctypes.byref(ms)))
         return ms.value
 
     def trace_decode(self, token: int, position: int, n: int, blocks: int) -> np.ndarray:
