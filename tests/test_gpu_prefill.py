@@ -229,3 +229,33 @@ def test_batched_prefill_2048_rows_matches_replay(ctx):
     close(logits, replay_logits, LOGIT_ATOL, LOGIT_RTOL)
     print("max |logits - replay|", float(np.abs(logits - replay_logits).max()))
     runner.close()
+
+
+@pytest.mark.parametrize("name,layers,prompt_len", [
+    ("qwen2.5-0.5b", 24, 128),   # 127 rows: the K-wave GEMMs (each wave streams its K range through an LDS ring)
+    ("llama-3.2-1b", 16, 301),   # 300 rows
+])
+def test_batched_prefill_is_repeatable(ctx, name, layers, prompt_len):
+    """The same chunk prefilled five times on one model gives bit-identical
+    cache rows in every layer.  (A refill of a GEMM's LDS ring stage that did
+    not wait for the wave's last reads of that stage once made rows of random
+    layers differ between runs.)"""
+    wl = _workload(name, layers, prompt_len)
+    hw = W.synthetic(wl)
+    runner = R.DecoderHIPRunner(hw, {"maxTokens": prompt_len + 8}, ctx=ctx)
+    assert runner.batchedPrefill
+    prompt = [int(t) for t in W.prompt_tokens(wl)]
+    n = len(prompt) - 1
+    first = None
+    for rep in range(5):
+        runner.resetCache()
+        runner.prefillTokens(prompt, 0, n)
+        rows = [np.concatenate([a.reshape(n, -1) for a in runner.model.kv_read(l, 0, n)], axis=1)
+                for l in range(layers)]
+        if first is None:
+            first = rows
+            continue
+        for l in range(layers):
+            diff = np.where((rows[l] != first[l]).reshape(n, -1).any(axis=1))[0]
+            assert len(diff) == 0, f"run {rep}: layer {l} rows {diff[:8]} differ from run 0"
+    runner.close()

@@ -582,8 +582,10 @@ struct KwWave {
   __device__ __forceinline__ void step(const unsigned char* mine, int refill_c) {
     // this wave's copies of the step have landed when at most NR - 2 later
     // stages are in flight; the stage refilled below was last read by this
-    // wave in its previous step
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm((KL::NR - 2) * KL::LPS));
+    // wave in its previous step, and those LDS reads must be complete before
+    // the copies may overwrite it: the scheduler leaves the last of them
+    // (an A operand) in flight past this point, so wait for lgkmcnt(0) too
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0((KL::NR - 2) * KL::LPS));
     asm volatile("" ::: "memory");
     issue((S + KL::NR - 1) % KL::NR, refill_c);
     const unsigned char* sb = mine + S * KL::STAGE;
