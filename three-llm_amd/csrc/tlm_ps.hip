@@ -59,244 +59,266 @@ __device__ __forceinline__ void ps_stamp(const PsArgs& a, int l, int stage, int 
 
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
-// Block-wide gather of n published words into LDS: word i is read from
-// addr(i) and its value stored at dst[i].  Word i belongs to wave
-// (i / 64) % 16, lane i % 64, so the 16 waves poll disjoint slices and no word
-// is requested twice; a wave keeps all its (at most NW) loads in flight and
-// spins until its whole slice carries seq, then the block meets at one
-// barrier.  Detecting the data and loading it is one round trip.
-// Block-uniform; false on time-out.
-template <int NW, typename F>
-__device__ bool ps_gather(int n, unsigned seq, F addr, float* dst, int* wflags) {
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  int nu = 0;  // this wave's loads (wave-uniform)
+// ------------------------------------------------------- wave-level inputs --
+// A linear stage's wave owns input chunks cbase + wave + 16 u (u < NU) and
+// reads just their CK elements: no block barrier before its dot products.
+// Element k of the input is the sum of np published partial vectors, word
+// addr(p, k) for partial p.  Lane l reads element e = l % CK of each chunk
+// for partials p = l / CK + j (64 / CK), j < PPL, and the lanes of one
+// element add their sums, so every lane with l % CK == e ends with x[u] =
+// element e of chunk u.  Chunks at or past cend read as zero.  Polls until
+// every word carries seq; false on time-out (wave-uniform).
+template <int CK, int NU, typename F>
+__device__ __forceinline__ bool wl_gather(int cbase, int cend, int np, unsigned seq, F addr, int wave,
+                                          float (&x)[NU]) {
+  constexpr int S = 64 / CK;                          // lanes per element
+  constexpr int PPL = (kPsMaxKs + S - 1) / S;         // partials per lane
+  const int lane = threadIdx.x & 63, e = lane % CK, slot = lane / CK;
+  PsSpin spin;
+  for (;;) {
+    u64 w[NU][PPL];
 #pragma unroll
-  for (int u = 0; u < NW; u++)
-    if (u * 1024 + wave * 64 < n) nu = u + 1;
-  bool ok = true;
-  if (nu > 0) {
-    PsSpin spin;
-    for (;;) {
-      u64 w[NW];
+    for (int u = 0; u < NU; u++)
 #pragma unroll
-      for (int u = 0; u < NW; u++)
-        if (u < nu) w[u] = ld_dev(addr(min(u * 1024 + wave * 64 + lane, n - 1)));
-      bool got = true;
-#pragma unroll
-      for (int u = 0; u < NW; u++) {
-        const int i = u * 1024 + wave * 64 + lane;
-        if (u < nu && i < n) {
-          got &= word_is(w[u], seq);
-          dst[i] = word_value(w[u]);
-        }
+      for (int j = 0; j < PPL; j++) {
+        const int c = cbase + wave + 16 * u, p = slot + j * S;
+        w[u][j] = c < cend && p < np ? ld_dev(addr(p, c * CK + e)) : word(0.f, seq);
       }
-      if (__all(got)) break;
-      if (spin.tick() && spin.late()) {
-        ok = false;
-        break;
+    bool got = true;
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+      float v = 0.f;
+#pragma unroll
+      for (int j = 0; j < PPL; j++) {
+        got &= word_is(w[u][j], seq);
+        v += word_value(w[u][j]);
       }
+      x[u] = v;
     }
+    if (__all(got)) break;
+    if (spin.tick() && spin.late()) return false;
   }
-  if (lane == 0) wflags[wave] = ok ? 1 : 0;
-  __syncthreads();
-  bool all = true;
 #pragma unroll
-  for (int w = 0; w < kPsWaves; w++) all &= wflags[w] != 0;
-  return all;
-}
-
-// v = thread t's elements 4t..4t+3 (t < H / 4, zeros elsewhere) of the sum of
-// ks LDS rows of H floats (partials of one vector).
-__device__ __forceinline__ float4 ps_row4(const float* x, int H, int ks) {
-  const int tid = threadIdx.x;
-  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (tid < (H >> 2)) {
-    float4 y[kPsMaxKs];  // all rows requested before the first add
-#pragma unroll
-    for (int s = 0; s < kPsMaxKs; s++) y[s] = *reinterpret_cast<const float4*>(x + (size_t)min(s, ks - 1) * H + 4 * tid);
-#pragma unroll
-    for (int s = 0; s < kPsMaxKs; s++)
-      if (s < ks) v = make_float4(v.x + y[s].x, v.y + y[s].y, v.z + y[s].z, v.w + y[s].w);
+  for (int u = 0; u < NU; u++) {
+    if (CK <= 8) x[u] += __shfl_xor(x[u], 8, 64);
+    if (CK <= 16) x[u] += __shfl_xor(x[u], 16, 64);
+    x[u] += __shfl_xor(x[u], 32, 64);
   }
-  return v;
+  return true;
 }
 
-// Sum over the n <= kPsMaxKs LDS values x[0], x[stride], ..., all requested
-// before the first add.
-__device__ __forceinline__ float ps_sum_rows(const float* x, int stride, int n) {
-  float y[kPsMaxKs];
+// The same chunks from the token's embedding row (layer 0's residual).
+template <int CK, int NU>
+__device__ __forceinline__ void wl_embedding(const PsArgs& a, int token, int cend, int wave, float (&x)[NU]) {
+  const int e = (threadIdx.x & 63) % CK;
 #pragma unroll
-  for (int s = 0; s < kPsMaxKs; s++) y[s] = x[min(s, n - 1) * stride];
-  float v = 0.f;
-#pragma unroll
-  for (int s = 0; s < kPsMaxKs; s++)
-    if (s < n) v += y[s];
-  return v;
-}
-
-// Sum over the block's 16 waves (every thread gets it); scratch: 16 floats,
-// 16-byte aligned.
-__device__ __forceinline__ float ps_block_sum(float v, float* scratch) {
-  v = wave_sum(v);
-  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
-  __syncthreads();
-  const float4* s4 = reinterpret_cast<const float4*>(scratch);
-  const float4 a = s4[0], b = s4[1], c = s4[2], d = s4[3];
-  return (((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w))) +
-         (((c.x + c.y) + (c.z + c.w)) + ((d.x + d.y) + (d.z + d.w)));
-}
-
-// xn = v * rsqrt(mean(x^2) + eps) * w (thread t owns elements 4t..4t+3 of the
-// H-element row; H % 64 == 0, H <= 4096); q4: xsum[g] = sum of the 32-element
-// group g of xn.  Ends with a block barrier.
-template <int FMT>
-__device__ __forceinline__ void ps_norm(float4 v, float4 w, int H, float eps, float* xn, float* xsum, float* scratch) {
-  const int tid = threadIdx.x;
-  const bool mine = tid < (H >> 2);
-  float ss = v.x * v.x;
-  ss = fmaf(v.y, v.y, ss);
-  ss = fmaf(v.z, v.z, ss);
-  ss = fmaf(v.w, v.w, ss);
-  const float inv = rsqrtf(ps_block_sum(ss, scratch) / (float)H + eps);
-  const float4 y = make_float4(v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w);
-  if (mine) *reinterpret_cast<float4*>(xn + 4 * tid) = y;
-  if (FMT == WF_Q4) {
-    const float g = sum8(mine ? (y.x + y.y) + (y.z + y.w) : 0.f);
-    if (mine && (tid & 7) == 0) xsum[tid >> 3] = g;
+  for (int u = 0; u < NU; u++) {
+    const int c = wave + 16 * u;
+    const size_t k = (size_t)token * a.H + (size_t)min(c, cend - 1) * CK + e;
+    const float v = a.emb_f32 ? gl(reinterpret_cast<const float*>(a.emb))[k]
+                              : h2f(gl(reinterpret_cast<const uint16_t*>(a.emb))[k]);
+    x[u] = c < cend ? v : 0.f;
   }
-  __syncthreads();
 }
 
-// q4: xsum[g] = sum of the 32-element group g of the n LDS values x (n a
-// multiple of 32).  Every lane of the block calls it.
+// Residual rows of a row-tile item, lane = row: the sum of np published
+// partials at addr(p) (lane's row), polled (wave-level).
+template <typename F>
+__device__ __forceinline__ bool wl_rows(int np, unsigned seq, F addr, float& xr) {
+  PsSpin spin;
+  for (;;) {
+    u64 w[kPsMaxKs];
+#pragma unroll
+    for (int p = 0; p < kPsMaxKs; p++) w[p] = p < np ? ld_dev(addr(p)) : word(0.f, seq);
+    bool got = true;
+    float v = 0.f;
+#pragma unroll
+    for (int p = 0; p < kPsMaxKs; p++) {
+      got &= word_is(w[p], seq);
+      v += word_value(w[p]);
+    }
+    xr = v;
+    if (__all(got)) return true;
+    if (spin.tick() && spin.late()) return false;
+  }
+}
+
+// Stage the wave's chunk inputs for its dot products: xw[u][e] = x[u] * nw
+// (nw: the element's norm weight, 1 without a norm) in the wave's LDS slots;
+// xs[u] = the chunk's sum of those (q4 group sums); ss = the sum of squares
+// of the raw x over the wave's chunks.  Ends with the wave's LDS writes
+// visible to its lanes.
+template <int CK, int NU>
+__device__ __forceinline__ void wl_stage(const float (&x)[NU], const float (&nw)[NU], float* xw, float (&xs)[NU],
+                                         float& ss) {
+  const int lane = threadIdx.x & 63;
+  const bool mine = lane < CK;
+  float q = 0.f;
+#pragma unroll
+  for (int u = 0; u < NU; u++) {
+    const float y = x[u] * nw[u];
+    if (mine) xw[u * CK + lane] = y;
+    q = fmaf(mine ? x[u] : 0.f, x[u], q);
+    xs[u] = CK == 32 ? wave_sum(mine ? y : 0.f) : 0.f;
+  }
+  ss = wave_sum(q);
+  wave_lds_sync();
+}
+
+// One 16-byte chunk of a weight row against its CK staged inputs.
 template <int FMT>
-__device__ __forceinline__ void ps_groups(const float* x, float* xsum, int n) {
-  if (FMT != WF_Q4) return;
-  const int tid = threadIdx.x;
-  const bool mine = tid < (n >> 2);
-  float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (mine) y = *reinterpret_cast<const float4*>(x + 4 * tid);
-  const float g = sum8((y.x + y.y) + (y.z + y.w));
-  if (mine && (tid & 7) == 0) xsum[tid >> 3] = g;
+__device__ __forceinline__ float chunk_dot(uint4 d, uint16_t s, const float* x, float xs) {
+  if (FMT == WF_Q4) return dot_q4(d, x, xs, h2f(s));
+  return dot_f16(d, x);
 }
 
-__device__ __forceinline__ float4 ld_f4(const float* p, int H) {
-  const int tid = threadIdx.x;
-  if (tid >= (H >> 2)) return make_float4(0.f, 0.f, 0.f, 0.f);
-  return ldg_f4(p + 4 * tid);
-}
-
-// One 16-byte chunk of a weight row against the matching slice of x.
-template <int FMT>
-__device__ __forceinline__ float chunk_dot(uint4 d, uint16_t s, const float* x, const float* xsum, int c) {
-  if (FMT == WF_Q4) return dot_q4(d, x + 32 * c, xsum[c], h2f(s));
-  return dot_f16(d, x + 8 * c);
-}
-
-// Weights of NT consecutive 64-row tiles (t0.., clamped to T - 1), chunks
-// c0 + wave + 16 u (u < NU) of a row of C chunks, for an input slice of n
-// chunks from c0: a wave's share of a row-tile GEMV.  Loads are
-// unconditional (indices clamped) and masked in dot().
+// Weights of NT consecutive 64-row tiles (t0.., clamped to T - 1): chunk
+// cbase + wave + 16 u (u < NU) of each row of C chunks when it lies in
+// [clo, chi) (the item's K range), else masked.  Loads are unconditional
+// (indices clamped into the range).
 template <int FMT, int NU, int NT>
 struct PsRows {
   uint4 d[NT][NU];
   uint16_t s[NT][NU];
-  __device__ __forceinline__ void load(const uint4* w, const uint16_t* sc, int C, int T, int t0, int c0, int n,
-                                       int wave) {
+  __device__ __forceinline__ void load(const uint4* w, const uint16_t* sc, int C, int T, int t0, int cbase, int clo,
+                                       int chi, int wave) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int t = 0; t < NT; t++)
 #pragma unroll
       for (int u = 0; u < NU; u++) {
-        const size_t at = ((size_t)min(t0 + t, T - 1) * C + c0 + min(wave + 16 * u, n - 1)) * kTile + lane;
+        const int c = min(max(cbase + wave + 16 * u, clo), chi - 1);
+        const size_t at = ((size_t)min(t0 + t, T - 1) * C + c) * kTile + lane;
         d[t][u] = ldg_u4(w + at);
         if (FMT == WF_Q4) s[t][u] = gl(sc)[at];
       }
   }
-  // x: the slice's input (x[0] = element c0 * chunk); xsum: its group sums
-  __device__ __forceinline__ float dot(int t, const float* x, const float* xsum, int n, int wave) const {
+  __device__ __forceinline__ float dot(int t, const float* xw, const float (&xs)[NU], int cbase, int clo, int chi,
+                                       int wave) const {
+    constexpr int CK = FMT == WF_Q4 ? 32 : 8;
     float acc = 0.f;
 #pragma unroll
-    for (int u = 0; u < NU; u++)
-      if (wave + 16 * u < n) acc += chunk_dot<FMT>(d[t][u], s[t][u], x, xsum, wave + 16 * u);
+    for (int u = 0; u < NU; u++) {
+      const int c = cbase + wave + 16 * u;
+      if (c >= clo && c < chi) acc += chunk_dot<FMT>(d[t][u], s[t][u], xw + u * CK, xs[u]);
+    }
     return acc;
   }
 };
 
+// Block-uniform AND of the waves' flags (wf: 16 ints of LDS); a block barrier.
+__device__ __forceinline__ bool ps_all(bool ok, int* wf) {
+  if ((threadIdx.x & 63) == 0) wf[threadIdx.x >> 6] = ok ? 1 : 0;
+  __syncthreads();
+  const int4* f4 = reinterpret_cast<const int4*>(wf);
+  const int4 a = f4[0], b = f4[1], c = f4[2], d = f4[3];
+  return (a.x & a.y & a.z & a.w & b.x & b.y & b.z & b.w & c.x & c.y & c.z & c.w & d.x & d.y & d.z & d.w) != 0;
+}
+
+// Sum of the 16 waves' LDS values v[0], v[stride], ... (all requested first).
+__device__ __forceinline__ float ps_sum16(const float* v, int stride) {
+  float r[kPsWaves];
+#pragma unroll
+  for (int w = 0; w < kPsWaves; w++) r[w] = v[w * stride];
+  float s = 0.f;
+#pragma unroll
+  for (int w = 0; w < kPsWaves; w++) s += r[w];
+  return s;
+}
+
+// Norm weights of this lane's element of the wave's chunks (1 past cend).
+template <int CK, int NU>
+__device__ __forceinline__ void wl_norm_weights(const float* nw, int cend, int wave, float (&w)[NU]) {
+  const int e = (threadIdx.x & 63) % CK;
+#pragma unroll
+  for (int u = 0; u < NU; u++) {
+    const int c = wave + 16 * u;
+    w[u] = c < cend ? gl(nw)[c * CK + e] : 1.f;
+  }
+}
+
+// LDS of a linear stage: per-wave input slots, then the wave partials.
+struct PsLinLds {
+  float* xw;   // [16][NU][CK] this wave's staged inputs
+  float* red;  // [16][R][64] per-wave partial outputs
+  float* ssw;  // [16] per-wave sums of squares
+  int* wf;     // [16] per-wave flags
+  float* out;  // [2][64] the item's outputs (QKV RoPE partner reads)
+};
+template <int CK, int NU, int R>
+__device__ __forceinline__ PsLinLds ps_lin_lds(float* sm) {
+  PsLinLds s;
+  s.red = sm;
+  s.ssw = s.red + kPsWaves * R * 64;
+  s.wf = reinterpret_cast<int*>(s.ssw + kPsWaves);
+  s.out = reinterpret_cast<float*>(s.wf + kPsWaves);
+  s.xw = s.out + 128 + wave_id() * NU * CK;
+  return s;
+}
+constexpr int ps_lin_floats(int ck, int nu, int r) { return kPsWaves * r * 64 + 2 * kPsWaves + 128 + kPsWaves * nu * ck; }
+
 // ---------------------------------------------------------------- QKV head --
 // Item i: head i / kq (rows of q head h, k head h - Hq or v head h - Hq - Hkv)
-// over the input chunks of split i % kq.  Publishes the partial sums with RoPE
-// applied (a rotation is linear) and the bias in split 0.
+// over the input chunks of split j = i % kq.  Each wave reads its chunks of
+// the whole residual (the norm needs all of it) and dots those in the split;
+// the norm's scale multiplies the summed dot products (a rotation and a
+// scale are linear).  Publishes the partial sums with RoPE applied and the
+// bias in split 0.
 template <int FMT, typename KT, int DT, int NX>
 __device__ __forceinline__ bool ps_qkv(const PsArgs& a, int l, int i, int pos, int token, unsigned seq, float* sm) {
   constexpr int NT = DT / 64;
   constexpr int CK = FMT == WF_Q4 ? 32 : 8;
-  constexpr int NW = (kPsMaxKs * 16 * NX * CK + 1023) / 1024;  // gathered words per lane: ks partials of H
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int H = a.H;
-  float* red = sm;                        // [16][NT][64]
-  float* xn = red + kPsWaves * NT * 64;   // [H]
-  float* xsum = xn + H;                   // [H / 32, rounded to 4]
-  float* out = xsum + ((H / 32 + 3) & ~3);  // [DT]
-  float* scratch = out + DT;              // [16]
-  int* wflags = reinterpret_cast<int*>(scratch + 16);  // [16]
-  float* xb = scratch + 32;               // [ks][H] the residual's published partials
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const PsLinLds s = ps_lin_lds<CK, NX, NT>(sm);
   const TLM_GLOBAL PsLayer& Ly = gl(a.layers)[l];
   const int hd = i / a.kq, j = i % a.kq;
   const int r0 = hd * DT;
   const int kind = hd < a.Hq ? 0 : hd < a.Hq + a.Hkv ? 1 : 2;
-  const int c0 = j * a.cq, cn = min(a.cq, a.Cx - c0);  // this split's input chunks
+  const int c0 = j * a.cq, c1 = min(c0 + a.cq, a.Cx);  // this split's input chunks
   PsRows<FMT, NX, NT> wr;
-  wr.load(Ly.wqkv, Ly.sqkv, a.Cx, a.Tq, r0 / kTile, c0, cn, wave);
-  const float bias = tid < DT && j == 0 ? gl(Ly.bqkv)[r0 + tid] : 0.f;
-  const float4 nw = ld_f4(Ly.attn_norm, H);
-  // rotate-half RoPE of element d = tid with its partner (TSLAttention.ts:168-250)
-  const int half = a.rd > 0 ? a.rd / 2 : 1;
-  float rc = 1.f, rs = 0.f, sg = 0.f;
-  int pd = 0;
-  if (tid < DT && kind < 2 && tid < a.rd) {
-    const int jj = tid < half ? tid : tid - half;
-    rc = gl(a.rope_cos)[(size_t)pos * half + jj];
-    rs = gl(a.rope_sin)[(size_t)pos * half + jj];
-    pd = tid < half ? tid + half : tid - half;
-    sg = tid < half ? -1.f : 1.f;
-  }
+  wr.load(Ly.wqkv, Ly.sqkv, a.Cx, a.Tq, r0 / kTile, 0, c0, c1, wave);
+  float nw[NX];
+  wl_norm_weights<CK, NX>(Ly.attn_norm, a.Cx, wave, nw);
+  float bias[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) bias[t] = j == 0 && wave == 0 ? gl(Ly.bqkv)[r0 + 64 * t + lane] : 0.f;
   if (wave == 0) ps_stamp(a, l, PS_QKV, 0);
-  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (l == 0) {  // the token's embedding row (DecoderWeights.ts:355-383)
-    if (tid < (H >> 2)) {
-      if (a.emb_f32) {
-        v = ldg_f4(reinterpret_cast<const float*>(a.emb) + (size_t)token * H + 4 * tid);
-      } else {
-        const uint2 e = ldg_u2(reinterpret_cast<const uint16_t*>(a.emb) + (size_t)token * H + 4 * tid);
-        v = make_float4(h2f(e.x & 0xFFFFu), h2f(e.x >> 16), h2f(e.y & 0xFFFFu), h2f(e.y >> 16));
-      }
-    }
+  float x[NX];
+  bool ok = true;
+  if (l == 0) {
+    wl_embedding<CK, NX>(a, token, a.Cx, wave, x);
   } else {
-    const u64* px = a.pub_x + (size_t)(l - 1) * kPsMaxKs * H;
-    if (!ps_gather<NW>(a.ks * H, seq, [&](int k) { return px + k; }, xb, wflags)) return false;
-    v = ps_row4(xb, H, a.ks);
+    const u64* px = a.pub_x + (size_t)(l - 1) * kPsMaxKs * a.H;
+    ok = wl_gather<CK, NX>(0, a.Cx, a.ks, seq, [&](int p, int k) { return px + (size_t)p * a.H + k; }, wave, x);
   }
   if (wave == 0) ps_stamp(a, l, PS_QKV, 1);
-  ps_norm<FMT>(v, nw, H, a.eps, xn, xsum, scratch);
+  float xs[NX], ss = 0.f;
+  wl_stage<CK, NX>(x, nw, s.xw, xs, ss);
 #pragma unroll
-  for (int t = 0; t < NT; t++)
-    red[(wave * NT + t) * 64 + lane] = wr.dot(t, xn + c0 * CK, xsum + (FMT == WF_Q4 ? c0 : 0), cn, wave);
-  __syncthreads();
-  if (tid < DT) {
-    float s = bias;
+  for (int t = 0; t < NT; t++) s.red[(wave * NT + t) * 64 + lane] = wr.dot(t, s.xw, xs, 0, c0, c1, wave);
+  if (lane == 0) s.ssw[wave] = ss;
+  if (!ps_all(ok, s.wf)) return false;
+  if (wave == 0) {
+    ps_stamp(a, l, PS_QKV, 2);
+    const float inv = rsqrtf(ps_sum16(s.ssw, 1) / (float)a.H + a.eps);
 #pragma unroll
-    for (int w = 0; w < kPsWaves; w++) s += red[(w * NT + (tid >> 6)) * 64 + (tid & 63)];
-    out[tid] = s;
+    for (int t = 0; t < NT; t++) s.out[64 * t + lane] = bias[t] + inv * ps_sum16(s.red + t * 64 + lane, NT * 64);
+    wave_lds_sync();
+    // rotate-half RoPE of element d with its partner (TSLAttention.ts:168-250)
+    const int half = a.rd > 0 ? a.rd / 2 : 1;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const int d = 64 * t + lane;
+      float val = s.out[d];
+      if (kind < 2 && d < a.rd) {
+        const int jj = d < half ? d : d - half;
+        const float rc = gl(a.rope_cos)[(size_t)pos * half + jj], rs = gl(a.rope_sin)[(size_t)pos * half + jj];
+        val = val * rc + (d < half ? -s.out[d + half] : s.out[d - half]) * rs;
+      }
+      st_dev(a.pub_qkv + ((size_t)l * a.kq + j) * a.Nqkv + r0 + d, word(val, seq));
+    }
+    ps_stamp(a, l, PS_QKV, 3);
   }
-  __syncthreads();
-  if (wave == 0) ps_stamp(a, l, PS_QKV, 2);
-  if (tid < DT) {
-    float val = out[tid];
-    if (kind < 2 && tid < a.rd) val = out[tid] * rc + sg * out[pd] * rs;
-    st_dev(a.pub_qkv + ((size_t)l * a.kq + j) * a.Nqkv + r0 + tid, word(val, seq));
-  }
-  if (wave == 0) ps_stamp(a, l, PS_QKV, 3);
   return true;
 }
 
@@ -305,15 +327,17 @@ __device__ __forceinline__ bool ps_qkv(const PsArgs& a, int l, int i, int pos, i
 // and its V tile (4 KiB).
 template <typename KT, int DT>
 constexpr int ps_wave_floats() {
-  return (head_tiling(DT, sizeof(KT)).sub + 1024 + 3) & ~3;  // p_l, then a pass of V rows
+  return (3 * DT + head_tiling(DT, sizeof(KT)).sub + 1024 + 3) & ~3;
 }
 
 // Item h: query head h over the window [first, pos].  Wave w takes the
-// contiguous positions [first + w per, + per) (per: a multiple of 32); its
-// first pass of cached K/V rows is requested before q is polled.  The row at
-// pos comes from the published k and v (this token's cache write is not
-// ordered before these reads).  The 16 waves merge (max, sum, output) in LDS
-// in wave order.
+// contiguous positions [first + w per, + per) (per: a multiple of the pass
+// length); its first pass of cached K/V rows is requested before it polls
+// q (and, in the wave whose range holds pos, the new k and v): the sums of
+// the kq published partials, read by every active wave itself.  The row at
+// pos comes from those k and v (this token's cache write is not ordered
+// before the cache reads).  The 16 waves merge (max, sum, output) in LDS in
+// wave order.
 template <typename KT, int DT>
 __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first, int pos, unsigned seq, float* sm) {
   constexpr int ESZ = sizeof(KT);
@@ -327,56 +351,81 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
   const TLM_GLOBAL PsLayer& Ly = gl(a.layers)[l];
   const int hk = h / a.G;
   const int n = pos - first + 1;
-  const int per = max(32, ((n + kPsWaves - 1) / kPsWaves + 31) & ~31);
+  const int per = max(SUB, ((n + kPsWaves - 1) / kPsWaves + SUB - 1) / SUB * SUB);
   const int t0 = min(first + wave * per, pos + 1), t1 = min(t0 + per, pos + 1);
   const bool active = t0 < t1;
   const bool own = active && pos < t1;  // this wave's range holds pos
-  float* p_l = sm + wave * WF;
+  float* q_l = sm + wave * WF;
+  float* kn = q_l + DT;
+  float* vn = kn + DT;
+  float* p_l = vn + DT;
   KT* vt = reinterpret_cast<KT*>(p_l + SUB);
   float* mg = sm + kPsWaves * WF;  // [16][2 + DT] per-wave (max, sum, output)
   int* good = reinterpret_cast<int*>(mg + kPsWaves * (2 + DT));  // [16]
-  float* gat = reinterpret_cast<float*>(good + kPsWaves);  // [kq][3][DT] published partials of q, k, v
-  float* q_l = gat + kPsMaxKs * 3 * DT;  // [3][DT] their sums: q, then k and v rounded like the cache
-  float* kn = q_l + DT;
-  float* vn = kn + DT;
-  int* wflags = reinterpret_cast<int*>(vn + DT);  // [16]
   const KT* kh = reinterpret_cast<const KT*>(Ly.kc) + (size_t)hk * a.max_tokens * DT;
   const KT* vh = reinterpret_cast<const KT*>(Ly.vc) + (size_t)hk * a.max_tokens * DT;
   const int pl = lane / LPP, part = lane % LPP;
   HeadLoads<KT, KW, false, DL> ld;
   const int tc0 = active ? t0 : first, tc1 = active ? t1 : first + 1;  // in-range rows for idle waves
   ld.issue(kh, vh, tc0, tc1, pl, part, DT, DT * ESZ, lane);
-  ps_stamp(a, l, PS_ATT, 0);
+  if (wave == 0) ps_stamp(a, l, PS_ATT, 0);
   float m = -INFINITY, lsum = 0.f, o[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; e++) o[e] = 0.f;
-  // q of head h and this position's k and v: the sums of the kq partials
-  const u64* pq = a.pub_qkv + (size_t)l * a.kq * a.Nqkv;
-  constexpr int NWG = (kPsMaxKs * 3 * DT + 1023) / 1024;
-  const bool ok = ps_gather<NWG>(a.kq * 3 * DT, seq,
-                                 [&](int k) {
-                                   const int j = k / (3 * DT), r = k - j * 3 * DT, c = r / DT, d = r - c * DT;
-                                   const int off = c == 0 ? h * DT : a.QS + (c - 1) * a.Hkv * DT + hk * DT;
-                                   return pq + (size_t)j * a.Nqkv + off + d;
-                                 },
-                                 gat, wflags);
-  if (ok && tid < 3 * DT) {
-    float sum = ps_sum_rows(gat + tid, 3 * DT, a.kq);
-    if (tid >= DT) {  // k and v: rounded like the cache
-      const KT r = kv_store<KT>(sum);
-      sum = kv_load<KT>(&r);
-      // the first query head of the group appends this position's k and v
-      // (TSLAttention.ts:252-286); every head of the group rounds the same sums
-      if (h % a.G == 0) {
-        KT* cache = reinterpret_cast<KT*>(tid < 2 * DT ? Ly.kc : Ly.vc);
-        glw(cache)[((size_t)hk * a.max_tokens + pos) * DT + (tid < 2 * DT ? tid - DT : tid - 2 * DT)] = r;
+  bool ok = true;
+  if (active) {
+    const u64* pq = a.pub_qkv + (size_t)l * a.kq * a.Nqkv;
+    PsSpin spin;
+    for (;;) {  // lane d: element d (+ 64 e) of q and, in the own wave, of k and v
+      float sq[EPL], sk[EPL], sv[EPL];
+      bool got = true;
+#pragma unroll
+      for (int e = 0; e < EPL; e++) {
+        u64 wq[kPsMaxKs], wk[kPsMaxKs], wv[kPsMaxKs];
+        const int d = lane + 64 * e;
+#pragma unroll
+        for (int j = 0; j < kPsMaxKs; j++) {
+          const u64* pj = pq + (size_t)j * a.Nqkv;
+          const bool in = j < a.kq;
+          wq[j] = in ? ld_dev(pj + h * DT + d) : word(0.f, seq);
+          wk[j] = in && own ? ld_dev(pj + a.QS + hk * DT + d) : word(0.f, seq);
+          wv[j] = in && own ? ld_dev(pj + a.QS + a.Hkv * DT + hk * DT + d) : word(0.f, seq);
+        }
+        sq[e] = sk[e] = sv[e] = 0.f;
+#pragma unroll
+        for (int j = 0; j < kPsMaxKs; j++) {
+          got &= word_is(wq[j], seq) & word_is(wk[j], seq) & word_is(wv[j], seq);
+          sq[e] += word_value(wq[j]);
+          sk[e] += word_value(wk[j]);
+          sv[e] += word_value(wv[j]);
+        }
+      }
+      if (__all(got)) {
+#pragma unroll
+        for (int e = 0; e < EPL; e++) {
+          const int d = lane + 64 * e;
+          q_l[d] = sq[e];
+          if (own) {  // k and v rounded like the cache
+            const KT kr = kv_store<KT>(sk[e]), vr = kv_store<KT>(sv[e]);
+            kn[d] = kv_load<KT>(&kr);
+            vn[d] = kv_load<KT>(&vr);
+            // the first query head of the group appends this position's k and
+            // v (TSLAttention.ts:252-286); every head of the group rounds the
+            // same sums
+            if (h % a.G == 0) {
+              glw(reinterpret_cast<KT*>(Ly.kc))[((size_t)hk * a.max_tokens + pos) * DT + d] = kr;
+              glw(reinterpret_cast<KT*>(Ly.vc))[((size_t)hk * a.max_tokens + pos) * DT + d] = vr;
+            }
+          }
+        }
+        break;
+      }
+      if (spin.tick() && spin.late()) {
+        ok = false;
+        break;
       }
     }
-    q_l[tid] = sum;
-  }
-  __syncthreads();
-  if (active) {
-    ps_stamp(a, l, PS_ATT, 1);
+    if (wave == 0) ps_stamp(a, l, PS_ATT, 1);
     if (ok) {
       wave_lds_sync();
       const float* qp = q_l + part * DL;  // this lane's q slice (LDS broadcast reads)
@@ -456,25 +505,26 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
   if (lane == 0) {
     mine[0] = m;
     mine[1] = lsum;
-    good[wave] = ok ? 1 : 0;
   }
-  __syncthreads();
-  bool all_good = true;
-#pragma unroll
-  for (int w = 0; w < kPsWaves; w++) all_good &= good[w] != 0;
-  if (!all_good) return false;  // block-uniform
+  if (!ps_all(ok, good)) return false;  // block-uniform
   if (wave == 0) ps_stamp(a, l, PS_ATT, 2);
   if (tid < DT) {
+    float mw[kPsWaves], lw[kPsWaves], ow[kPsWaves];
+#pragma unroll
+    for (int w = 0; w < kPsWaves; w++) {
+      mw[w] = mg[w * (2 + DT)];
+      lw[w] = mg[w * (2 + DT) + 1];
+      ow[w] = mg[w * (2 + DT) + 2 + tid];
+    }
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kPsWaves; w++) M = fmaxf(M, mg[w * (2 + DT)]);
+    for (int w = 0; w < kPsWaves; w++) M = fmaxf(M, mw[w]);
     float L = 0.f, od = 0.f;
 #pragma unroll
     for (int w = 0; w < kPsWaves; w++) {
-      const float mw = mg[w * (2 + DT)];
-      const float sc = mw == -INFINITY ? 0.f : __expf(mw - M);
-      L = fmaf(mg[w * (2 + DT) + 1], sc, L);
-      od = fmaf(mg[w * (2 + DT) + 2 + tid], sc, od);
+      const float sc = mw[w] == -INFINITY ? 0.f : __expf(mw[w] - M);
+      L = fmaf(lw[w], sc, L);
+      od = fmaf(ow[w], sc, od);
     }
     st_dev(a.pub_o + (size_t)l * a.QS + h * DT + tid, word(od / L, seq));
   }
@@ -484,93 +534,86 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
 
 // -------------------------------------------------------------- O row tile --
 // Item i: rows 64 t .. 64 t + 63 (t = i % To) of the O projection over the
-// attention-output chunks of split j = i / To; split 0 adds the residual rows:
-// the partials of x_mid.
+// attention-output chunks of split j = i / To; split 0 adds the residual
+// rows (the sum of the down partials, or layer 0's embedding row): the
+// partials of x_mid.
 template <int FMT, int NO>
 __device__ __forceinline__ bool ps_o(const PsArgs& a, int l, int i, int token, unsigned seq, float* sm) {
   constexpr int CK = FMT == WF_Q4 ? 32 : 8;
-  constexpr int NW = (16 * NO * CK + kPsMaxKs * 64 + 1023) / 1024;  // gathered words per lane
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int H = a.H, QS = a.QS;
-  float* red = sm;                                 // [16][64]
-  float* xo = red + kPsWaves * 64;                 // [QS] attention output, then [ks][64] residual rows
-  float* xos = xo + QS + kPsMaxKs * 64;            // [QS / 32, rounded to 4]
-  int* wflags = reinterpret_cast<int*>(xos + ((QS / 32 + 3) & ~3));  // [16]
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int H = a.H;
+  const PsLinLds s = ps_lin_lds<CK, NO, 1>(sm);
   const TLM_GLOBAL PsLayer& Ly = gl(a.layers)[l];
   const int t = i % a.To, j = i / a.To;
-  const int c0 = j * a.co, cn = min(a.co, a.Co - c0), kn = cn * CK;  // this split's input chunks
+  const int c0 = j * a.co, c1 = min(c0 + a.co, a.Co);  // this split's input chunks
   PsRows<FMT, NO, 1> wr;
-  wr.load(Ly.wo, Ly.so, a.Co, a.To, t, c0, cn, wave);
-  const int row = t * kTile + tid;  // threads tid < 64: the residual rows
-  const bool rt = tid < kTile && row < H;
-  float xr = 0.f;
-  if (l == 0 && rt && j == 0)
-    xr = a.emb_f32 ? gl(reinterpret_cast<const float*>(a.emb))[(size_t)token * H + row]
-                   : h2f(gl(reinterpret_cast<const uint16_t*>(a.emb))[(size_t)token * H + row]);
+  wr.load(Ly.wo, Ly.so, a.Co, a.To, t, c0, c0, c1, wave);
+  const int row = t * kTile + lane;
   if (wave == 0) ps_stamp(a, l, PS_O, 0);
-  const u64* po = a.pub_o + (size_t)l * QS + c0 * CK;
-  const u64* px = a.pub_x + (size_t)(l > 0 ? l - 1 : 0) * kPsMaxKs * H + t * kTile;
-  const int nx = l > 0 && j == 0 ? a.ks * kTile : 0;
-  if (!ps_gather<NW>(kn + nx, seq,
-                     [&](int k) { return k < kn ? po + k : px + (size_t)((k - kn) >> 6) * H + ((k - kn) & 63); },
-                     xo, wflags))
-    return false;
-  if (wave == 0) ps_stamp(a, l, PS_O, 1);
-  ps_groups<FMT>(xo, xos, kn);
-  if (l > 0 && j == 0 && tid < kTile) xr = ps_sum_rows(xo + kn + tid, kTile, a.ks);
-  __syncthreads();
-  red[wave * 64 + lane] = wr.dot(0, xo, xos, cn, wave);
-  __syncthreads();
-  if (wave == 0) ps_stamp(a, l, PS_O, 2);
-  if (rt) {
-    float s = 0.f;
+  float x[NO], one[NO];
 #pragma unroll
-    for (int w = 0; w < kPsWaves; w++) s += red[w * 64 + tid];
-    st_dev(a.pub_xm + ((size_t)l * a.ko + j) * H + row, word(xr + s, seq));  // TSLAdd.ts:10-33
+  for (int u = 0; u < NO; u++) one[u] = 1.f;
+  const u64* po = a.pub_o + (size_t)l * a.QS;
+  bool ok = wl_gather<CK, NO>(c0, c1, 1, seq, [&](int, int k) { return po + k; }, wave, x);
+  float xr = 0.f;
+  if (wave == 0 && j == 0) {
+    if (l == 0) {
+      const size_t k = (size_t)token * H + min(row, H - 1);
+      xr = a.emb_f32 ? gl(reinterpret_cast<const float*>(a.emb))[k]
+                     : h2f(gl(reinterpret_cast<const uint16_t*>(a.emb))[k]);
+    } else {
+      const u64* px = a.pub_x + (size_t)(l - 1) * kPsMaxKs * H + min(row, H - 1);
+      ok &= wl_rows(a.ks, seq, [&](int p) { return px + (size_t)p * H; }, xr);
+    }
   }
-  if (wave == 0) ps_stamp(a, l, PS_O, 3);
+  if (wave == 0) ps_stamp(a, l, PS_O, 1);
+  float xs[NO], ss;
+  wl_stage<CK, NO>(x, one, s.xw, xs, ss);
+  s.red[wave * 64 + lane] = wr.dot(0, s.xw, xs, c0, c0, c1, wave);
+  if (!ps_all(ok, s.wf)) return false;
+  if (wave == 0) {
+    ps_stamp(a, l, PS_O, 2);
+    const float v = xr + ps_sum16(s.red + lane, 64);
+    if (row < H) st_dev(a.pub_xm + ((size_t)l * a.ko + j) * H + row, word(v, seq));  // TSLAdd.ts:10-33
+    ps_stamp(a, l, PS_O, 3);
+  }
   return true;
 }
 
 // ------------------------------------------------------------ gate|up tiles --
 // Item g: paired tiles g mw .. g mw + mw - 1 (tile t: gate rows 32 t.. in lanes
 // 0..31, the matching up rows in lanes 32..63); publishes h = silu(g) * u for
-// intermediate indices 32 t .. 32 t + 31.
+// intermediate indices 32 t .. 32 t + 31.  The input is x_mid (the sum of the
+// ko O partials), normed: the norm's scale multiplies the dot products.
 template <int FMT, int NX, int MW>
 __device__ __forceinline__ bool ps_gu(const PsArgs& a, int l, int g, unsigned seq, float* sm) {
   constexpr int CK = FMT == WF_Q4 ? 32 : 8;
-  constexpr int NW = (kPsMaxKs * 16 * NX * CK + 1023) / 1024;  // gathered words per lane: ko partials of H
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int H = a.H;
-  float* red = sm;                          // [16][MW][64]
-  float* xn = red + kPsWaves * MW * 64;     // [H]
-  float* xsum = xn + H;                     // [H / 32, rounded to 4]
-  float* scratch = xsum + ((H / 32 + 3) & ~3);  // [16]
-  int* wflags = reinterpret_cast<int*>(scratch + 16);  // [16]
-  float* xb = scratch + 32;                 // [ko][H] x_mid partials
+  const PsLinLds s = ps_lin_lds<CK, NX, MW>(sm);
   const TLM_GLOBAL PsLayer& Ly = gl(a.layers)[l];
   PsRows<FMT, NX, MW> wr;
-  wr.load(Ly.wgu, Ly.sgu, a.Cx, a.Tgu, g * MW, 0, a.Cx, wave);
-  const float4 nw = ld_f4(Ly.ffn_norm, H);
+  wr.load(Ly.wgu, Ly.sgu, a.Cx, a.Tgu, g * MW, 0, 0, a.Cx, wave);
+  float nw[NX];
+  wl_norm_weights<CK, NX>(Ly.ffn_norm, a.Cx, wave, nw);
   if (wave == 0) ps_stamp(a, l, PS_GU, 0);
   const u64* pm = a.pub_xm + (size_t)l * a.ko * H;
-  if (!ps_gather<NW>(a.ko * H, seq, [&](int k) { return pm + k; }, xb, wflags)) return false;
-  const float4 v = ps_row4(xb, H, a.ko);
+  float x[NX];
+  const bool ok = wl_gather<CK, NX>(0, a.Cx, a.ko, seq, [&](int p, int k) { return pm + (size_t)p * H + k; }, wave, x);
   if (wave == 0) ps_stamp(a, l, PS_GU, 1);
-  ps_norm<FMT>(v, nw, H, a.eps, xn, xsum, scratch);
+  float xs[NX], ss;
+  wl_stage<CK, NX>(x, nw, s.xw, xs, ss);
 #pragma unroll
-  for (int s = 0; s < MW; s++)
-    red[(wave * MW + s) * 64 + lane] = g * MW + s < a.Tgu ? wr.dot(s, xn, xsum, a.Cx, wave) : 0.f;
-  __syncthreads();
+  for (int u = 0; u < MW; u++)
+    s.red[(wave * MW + u) * 64 + lane] = g * MW + u < a.Tgu ? wr.dot(u, s.xw, xs, 0, 0, a.Cx, wave) : 0.f;
+  if (lane == 0) s.ssw[wave] = ss;
+  if (!ps_all(ok, s.wf)) return false;
   if (wave == 0) ps_stamp(a, l, PS_GU, 2);
-  if (wave < MW && g * MW + wave < a.Tgu) {  // wave s finishes tile g mw + s
-    float gs = 0.f, us = 0.f;
-#pragma unroll
-    for (int w = 0; w < kPsWaves; w++) {
-      gs += red[(w * MW + wave) * 64 + (lane & 31)];
-      us += red[(w * MW + wave) * 64 + (lane | 32)];
-    }
-    const float hv = gs / (1.f + __expf(-gs)) * us;  // TSLSiLUMul.ts:15-29
+  if (wave < MW && g * MW + wave < a.Tgu) {  // wave u finishes tile g mw + u
+    const float inv = rsqrtf(ps_sum16(s.ssw, 1) / (float)H + a.eps);
+    const float v = inv * ps_sum16(s.red + wave * 64 + lane, MW * 64);
+    const float us = __shfl_xor(v, 32, 64);      // lanes < 32: gate; their up rows sit in lanes + 32
+    const float hv = v / (1.f + __expf(-v)) * us;  // TSLSiLUMul.ts:15-29
     if (lane < 32) st_dev(a.pub_h + (size_t)l * a.Tgu * 32 + (g * MW + wave) * 32 + lane, word(hv, seq));
   }
   if (wave == 0) ps_stamp(a, l, PS_GU, 3);
@@ -581,46 +624,38 @@ __device__ __forceinline__ bool ps_gu(const PsArgs& a, int l, int g, unsigned se
 // Item (t, s): rows 64 t .. 64 t + 63 of the down projection over the input
 // chunks [s cs, (s + 1) cs); split 0 adds x_mid (the MLP residual).
 template <int FMT, int ND>
-__device__ __forceinline__ bool ps_down(const PsArgs& a, int l, int t, int s, unsigned seq, float* sm) {
+__device__ __forceinline__ bool ps_down(const PsArgs& a, int l, int t, int sp, unsigned seq, float* sm) {
   constexpr int CK = FMT == WF_Q4 ? 32 : 8;
-  constexpr int NW = (16 * ND * CK + kPsMaxKs * 64 + 1023) / 1024;  // gathered words per lane
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int H = a.H;
-  const int c0 = s * a.cs, cn = min(a.cs, a.Cd - c0);
-  const int kn = cn * CK;  // input elements of the split
-  float* red = sm;                          // [16][64]
-  float* hs = red + kPsWaves * 64;          // [cs CK] the split's h, then [ko][64] x_mid rows (split 0)
-  float* hss = hs + a.cs * CK + kPsMaxKs * 64;  // [cs CK / 32, rounded to 4]
-  int* wflags = reinterpret_cast<int*>(hss + ((a.cs * CK / 32 + 3) & ~3));  // [16]
+  const PsLinLds s = ps_lin_lds<CK, ND, 1>(sm);
   const TLM_GLOBAL PsLayer& Ly = gl(a.layers)[l];
+  const int c0 = sp * a.cs, c1 = min(c0 + a.cs, a.Cd);
   PsRows<FMT, ND, 1> wr;
-  wr.load(Ly.wd, Ly.sd, a.Cd, a.To, t, c0, cn, wave);
+  wr.load(Ly.wd, Ly.sd, a.Cd, a.To, t, c0, c0, c1, wave);
+  const int row = t * kTile + lane;
   if (wave == 0) ps_stamp(a, l, PS_DOWN, 0);
-  const u64* ph = a.pub_h + (size_t)l * a.Tgu * 32 + (size_t)c0 * CK;
-  const u64* pm = a.pub_xm + (size_t)l * a.ko * H + t * kTile;
-  const int row = t * kTile + tid;
-  const bool rt = tid < kTile && row < H;
-  const int nm = s == 0 ? a.ko * kTile : 0;
-  if (!ps_gather<NW>(kn + nm, seq,
-                     [&](int k) { return k < kn ? ph + k : pm + (size_t)((k - kn) >> 6) * H + ((k - kn) & 63); }, hs,
-                     wflags))
-    return false;
-  if (wave == 0) ps_stamp(a, l, PS_DOWN, 1);
-  ps_groups<FMT>(hs, hss, kn);
-  float xm = 0.f;
-  if (s == 0 && tid < kTile) xm = ps_sum_rows(hs + kn + tid, kTile, a.ko);
-  __syncthreads();
-  red[wave * 64 + lane] = wr.dot(0, hs, hss, cn, wave);
-  __syncthreads();
-  if (wave == 0) ps_stamp(a, l, PS_DOWN, 2);
-  if (rt) {
-    const float v = s == 0 ? xm : 0.f;  // split 0 carries x_mid (TSLAdd.ts:10-33)
-    float d = 0.f;
+  const u64* ph = a.pub_h + (size_t)l * a.Tgu * 32;
+  float x[ND], one[ND];
 #pragma unroll
-    for (int w = 0; w < kPsWaves; w++) d += red[w * 64 + tid];
-    st_dev(a.pub_x + ((size_t)l * kPsMaxKs + s) * H + row, word(v + d, seq));
+  for (int u = 0; u < ND; u++) one[u] = 1.f;
+  bool ok = wl_gather<CK, ND>(c0, c1, 1, seq, [&](int, int k) { return ph + k; }, wave, x);
+  float xm = 0.f;
+  if (wave == 0 && sp == 0) {
+    const u64* pm = a.pub_xm + (size_t)l * a.ko * H + min(row, H - 1);
+    ok &= wl_rows(a.ko, seq, [&](int p) { return pm + (size_t)p * H; }, xm);
   }
-  if (wave == 0) ps_stamp(a, l, PS_DOWN, 3);
+  if (wave == 0) ps_stamp(a, l, PS_DOWN, 1);
+  float xs[ND], ss;
+  wl_stage<CK, ND>(x, one, s.xw, xs, ss);
+  s.red[wave * 64 + lane] = wr.dot(0, s.xw, xs, c0, c0, c1, wave);
+  if (!ps_all(ok, s.wf)) return false;
+  if (wave == 0) {
+    ps_stamp(a, l, PS_DOWN, 2);
+    const float v = xm + ps_sum16(s.red + lane, 64);  // split 0 carries x_mid (TSLAdd.ts:10-33)
+    if (row < H) st_dev(a.pub_x + ((size_t)l * kPsMaxKs + sp) * H + row, word(v, seq));
+    ps_stamp(a, l, PS_DOWN, 3);
+  }
   return true;
 }
 
@@ -770,17 +805,16 @@ bool ps_roles(const PsShape& sh, int blocks, int H, int Hq, int Hkv, int Tgu, in
 }
 
 size_t ps_smem_bytes(const PsShape& sh, int H, int QS) {
+  (void)H;
+  (void)QS;
   const int CK = sh.fmt == WF_Q4 ? 32 : 8;
   const size_t esz = sh.kv_f32 ? 4 : 2;
   const int sub = head_tiling(sh.dt, (int)esz).sub;
-  auto r4 = [](size_t n) { return (n + 3) & ~(size_t)3; };
-  const size_t att = (size_t)kPsWaves * ((sub + 1024 + 3) & ~3) + kPsWaves * (2 + sh.dt) + kPsWaves +
-                     (size_t)(kPsMaxKs + 1) * 3 * sh.dt + kPsWaves;
-  const size_t qkv = (size_t)kPsWaves * (sh.dt / 64) * 64 + H + r4(H / 32) + sh.dt + 32 + (size_t)kPsMaxKs * H;
-  const size_t o = (size_t)kPsWaves * 64 + QS + kPsMaxKs * 64 + r4(QS / 32) + kPsWaves;
-  const size_t gu = (size_t)kPsWaves * sh.mw * 64 + H + r4(H / 32) + 32 + (size_t)kPsMaxKs * H;
-  const size_t cs = (size_t)sh.nd * 16 * CK;  // a down split's input elements, at most
-  const size_t down = (size_t)kPsWaves * 64 + cs + kPsMaxKs * 64 + r4(cs / 32) + kPsWaves;
+  const size_t att = (size_t)kPsWaves * ((3 * sh.dt + sub + 1024 + 3) & ~3) + kPsWaves * (2 + sh.dt) + kPsWaves;
+  const size_t qkv = ps_lin_floats(CK, sh.nx, sh.dt / 64);
+  const size_t o = ps_lin_floats(CK, sh.no, 1);
+  const size_t gu = ps_lin_floats(CK, sh.nx, sh.mw);
+  const size_t down = ps_lin_floats(CK, sh.nd, 1);
   return sizeof(float) * std::max({att, qkv, o, gu, down});
 }
 
