@@ -365,11 +365,15 @@ static bool launch_linear(const tlm_linear* L, int pro, const GemvArgs& a, hipSt
 
 // ------------------------------------------------------------------ context --
 
+// The host-side helpers of tlm_host.cpp report through the same message.
+int tlm_host_fail(int code, const char* msg) { return fail(code, "%s", msg); }
+
 extern "C" {
 
 int tlm_abi_version(void) { return TLM_ABI_VERSION; }
 
 const char* tlm_last_error(void) { return g_error.c_str(); }
+
 
 int tlm_open(int device, tlm_ctx** out) {
   if (!out) return fail(TLM_ERR_INVALID, "TLMContext: null output");

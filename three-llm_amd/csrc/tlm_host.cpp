@@ -84,10 +84,12 @@ float f16_bits_to_f32(uint16_t h) {
 
 }  // namespace
 
+int tlm_host_fail(int code, const char* msg);  // tlm_api.hip: sets tlm_last_error()
+
 extern "C" {
 
 int tlm_synth_normal(uint64_t seed, uint64_t stream, size_t n, float stddev, float* out) {
-  if (!out && n) return TLM_ERR_INVALID;
+  if (!out && n) return tlm_host_fail(TLM_ERR_INVALID, "TLMSynth: null output");
   const uint64_t key = stream_key(seed, stream);
   const size_t pairs = (n + 1) / 2;
   parallel_for(pairs, [&](size_t b, size_t e) {
@@ -104,7 +106,7 @@ int tlm_synth_normal(uint64_t seed, uint64_t stream, size_t n, float stddev, flo
 }
 
 int tlm_synth_tokens(uint64_t seed, uint64_t stream, size_t n, int32_t vocab, int32_t* out) {
-  if (vocab <= 0 || (!out && n)) return TLM_ERR_INVALID;
+  if (vocab <= 0 || (!out && n)) return tlm_host_fail(TLM_ERR_INVALID, "TLMSynth: vocabulary must be positive and the output non-null");
   const uint64_t key = stream_key(seed, stream);
   for (size_t i = 0; i < n; i++) out[i] = (int32_t)(splitmix64(key + i) % (uint64_t)vocab);
   return TLM_OK;
@@ -114,7 +116,8 @@ int tlm_synth_tokens(uint64_t seed, uint64_t stream, size_t n, int32_t vocab, in
 // (largest finite fp16 at most), q = clamp(rint(w / f32(s)), -8, 7), q = 0 when
 // s == 0, nibble q + 8 with even k in the low nibble.
 int tlm_quantize_q4(const float* w, int n_out, int k_in, uint8_t* packed, uint16_t* scales) {
-  if (!w || !packed || !scales || n_out <= 0 || k_in <= 0 || k_in % 32 != 0) return TLM_ERR_INVALID;
+  if (!w || !packed || !scales || n_out <= 0 || k_in <= 0 || k_in % 32 != 0)
+    return tlm_host_fail(TLM_ERR_INVALID, "TLMQuantize: q4 needs non-null buffers, n_out > 0 and k_in a positive multiple of 32");
   const int G = k_in / 32;
   parallel_for((size_t)n_out * G, [&](size_t b, size_t e) {
     for (size_t idx = b; idx < e; idx++) {
@@ -142,7 +145,7 @@ int tlm_quantize_q4(const float* w, int n_out, int k_in, uint8_t* packed, uint16
 }
 
 int tlm_f32_to_f16(const float* in, size_t n, uint16_t* out) {
-  if ((!in || !out) && n) return TLM_ERR_INVALID;
+  if ((!in || !out) && n) return tlm_host_fail(TLM_ERR_INVALID, "TLMQuantize: null buffer");
   parallel_for(n, [&](size_t b, size_t e) {
     for (size_t i = b; i < e; i++) out[i] = f32_to_f16_bits(in[i]);
   });
