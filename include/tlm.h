@@ -216,7 +216,10 @@ int tlm_prefill(tlm_model* model, const int32_t* tokens, int32_t start, int32_t 
  * that, as the reference always does (DecoderTSLRunner.ts:472-480).
  * min_rows <= 0 turns the batched path off; TLM_ERR_INVALID names why a model
  * cannot use it (fp32 cache, head_dim other than 64/128, sizes not multiples
- * of 32, a q4 scale above 8188). */
+ * of 32, a q4 scale above 8188).  The row batches keep activations in fp16:
+ * when one rounds to inf or is NaN, a device flag trips and tlm_prefill
+ * replays that chunk on the fp32 decode graph (it waits for the stream after
+ * each batched chunk to read the flag; tlm_model_describe counts such chunks). */
 int tlm_model_set_prefill(tlm_model* model, int32_t min_rows, int32_t chunk);
 /* readLogits (DecoderTSLRunner.ts:532-535): waits, copies n <= vocab floats. */
 int tlm_read_logits(tlm_model* model, float* out, size_t n);

@@ -259,3 +259,42 @@ def test_batched_prefill_is_repeatable(ctx, name, layers, prompt_len):
             diff = np.where((rows[l] != first[l]).reshape(n, -1).any(axis=1))[0]
             assert len(diff) == 0, f"run {rep}: layer {l} rows {diff[:8]} differ from run 0"
     runner.close()
+
+
+def test_fp16_overflow_in_a_batched_chunk_replays_it_on_the_decode_path(ctx):
+    """Layer 0's gate and up weights scaled to N(0, 10): the SwiGLU output of
+    the batched chunk passes 65504, the row kernels' overflow flag trips and
+    tlm_prefill replays the chunk on the fp32 decode graph, so the cache rows
+    and the next logits equal the pure replay's bit for bit and stay finite.
+    Unscaled weights never trip it."""
+    wl = _workload("qwen2.5-0.5b", 2, 100)
+    hw = W.synthetic(wl)
+    src = hw._source
+    hw._source = lambda kind, layer: src(kind, layer) * (500.0 if kind in (W.WGATE, W.WUP) and layer == 0 else 1.0)
+    hw.keep = True
+    prompt = [int(t) for t in W.prompt_tokens(wl)]
+    n = len(prompt) - 1
+    runs = []
+    for min_rows in (64, 0):  # batched (falls back), then the reference's replay only
+        runner = R.DecoderHIPRunner(hw, {"maxTokens": n + 8}, ctx=ctx)
+        m = runner.model
+        m.set_prefill(min_rows, 2048)
+        runner.prefillTokens(prompt, 0, n)
+        runner.computeToken(prompt[-1], n, True)
+        logits = runner.readLogits()
+        kv = [np.concatenate([a.reshape(n, -1) for a in m.kv_read(l, 0, n)], axis=1) for l in range(2)]
+        runs.append((logits, kv, m.describe()))
+        runner.close()
+    (lb, kvb, db), (lr, kvr, dr) = runs
+    assert "1 replayed after fp16 overflow" in db, db
+    assert "0 replayed after fp16 overflow" in dr
+    assert np.isfinite(lb).all()
+    assert np.array_equal(lb, lr)
+    for a, b in zip(kvb, kvr):
+        assert np.array_equal(a, b)
+    # the same model with unscaled weights: the batched chunk stands
+    plain = W.synthetic(wl)
+    runner = R.DecoderHIPRunner(plain, {"maxTokens": n + 8}, ctx=ctx)
+    runner.prefillTokens(prompt, 0, n)
+    assert "0 replayed after fp16 overflow" in runner.model.describe()
+    runner.close()

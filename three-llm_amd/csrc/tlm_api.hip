@@ -177,6 +177,8 @@ struct tlm_model {
   // allocated on first use
   int pf_min_rows = 64, pf_chunk = 2048, pf_cap = 0;
   float *pf_x = nullptr, *pf_part = nullptr;  // residual rows, split-K slices
+  int* pf_ovf = nullptr;   // device flag: a batched chunk rounded a non-finite fp16 activation
+  int pf_replayed = 0;     // batched chunks replayed on the decode graph after such a flag
   size_t pf_part_n = 0;
   uint16_t *pf_xn = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_h = nullptr;
   // per attention mode: [0] short windows, [1] long windows (long_window)
@@ -1202,7 +1204,7 @@ void tlm_model_destroy(tlm_model* m) {
   attn_free(&m->attn, false);
   void* bufs[] = {m->emb, m->final_norm, m->ctrl, m->tokens_out, m->prompt, m->xa, m->x0, m->xf, m->attn_out,
                   m->pq, m->po, m->rb, m->logits, m->arg_val, m->arg_idx, m->cand_v, m->cand_i, m->pf_x, m->pf_part, m->pf_xn,
-                  m->pf_q, m->pf_att, m->pf_h, m->ps_layers, m->ps_roles, m->ps_pub_x, m->ps_pub_qkv,
+                  m->pf_q, m->pf_att, m->pf_h, m->pf_ovf, m->ps_layers, m->ps_roles, m->ps_pub_x, m->ps_pub_qkv,
                   m->ps_pub_o, m->ps_pub_xm, m->ps_pub_h, m->ps_args_dev};
   for (void* p : bufs) hipFree(p);
   delete m;
@@ -1511,6 +1513,10 @@ static const char* prefill_unsupported(const tlm_model* m) {
 
 // Row buffers for `rows` positions and `part` floats of split-K slices.
 static int prefill_alloc(tlm_model* m, int rows, size_t part) {
+  if (!m->pf_ovf) {
+    int rc = model_alloc((void**)&m->pf_ovf, sizeof(int));
+    if (rc) return rc;
+  }
   if (m->pf_cap >= rows && m->pf_part_n >= part) return TLM_OK;
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
   if (m->pf_part_n < part) {
@@ -1554,8 +1560,9 @@ static GemmArgs gemm_args(const tlm_linear* L, const uint16_t* A, int lda, int M
 }
 
 static RowsArgs rows_args(float* X, const float* part, int n_part, size_t pstride, int H, const float* w, double eps,
-                          uint16_t* Y) {
+                          uint16_t* Y, int* ovf) {
   RowsArgs r;
+  r.ovf = ovf;
   r.X = X;
   r.part = part;
   r.n_part = n_part;
@@ -1595,9 +1602,10 @@ static int prefill_rows(tlm_model* m, const int* tokens, int p0, int M) {
   for (int l = 0; l < d.num_layers; l++) {
     const Layer& L = m->layers[l];
     bool ok = true;
-    launch_rms_rows(rows_args(m->pf_x, m->pf_part, l ? sd.splits : 0, rowsH, H, L.attn_norm, d.rms_eps, m->pf_xn),
+    launch_rms_rows(rows_args(m->pf_x, m->pf_part, l ? sd.splits : 0, rowsH, H, L.attn_norm, d.rms_eps, m->pf_xn, m->pf_ovf),
                     M, st);
     GemmArgs g = gemm_args(L.qkv, m->pf_xn, H, M);
+    g.ovf = m->pf_ovf;
     if (rope_epi) {
       g.bias = L.bqkv;
       g.Ch = m->pf_q;
@@ -1634,6 +1642,7 @@ static int prefill_rows(tlm_model* m, const int* tokens, int p0, int M) {
       r.kc = L.kc;
       r.vc = L.vc;
       r.kv_f32 = 0;
+      r.ovf = m->pf_ovf;
       launch_rope_kv(r, st);
     }
     PrefillAttnArgs pa;
@@ -1656,8 +1665,9 @@ static int prefill_rows(tlm_model* m, const int* tokens, int p0, int M) {
     g.Cf = m->pf_part;
     g.ldc = H;
     ok = ok && launch_gemm(lf, GEMM_PART, so, g, st);
-    launch_rms_rows(rows_args(m->pf_x, m->pf_part, so.splits, rowsH, H, L.ffn_norm, d.rms_eps, m->pf_xn), M, st);
+    launch_rms_rows(rows_args(m->pf_x, m->pf_part, so.splits, rowsH, H, L.ffn_norm, d.rms_eps, m->pf_xn, m->pf_ovf), M, st);
     g = gemm_args(L.gu, m->pf_xn, H, M);
+    g.ovf = m->pf_ovf;
     g.N = L.gu->T * kTile;
     g.Ch = m->pf_h;
     g.ldc = I;
@@ -1671,7 +1681,7 @@ static int prefill_rows(tlm_model* m, const int* tokens, int p0, int M) {
     CHECK_LAUNCH("TLMModel");
   }
   // the last layer's MLP output joins the residual rows
-  launch_rms_rows(rows_args(m->pf_x, m->pf_part, sd.splits, rowsH, H, nullptr, d.rms_eps, nullptr), M, st);
+  launch_rms_rows(rows_args(m->pf_x, m->pf_part, sd.splits, rowsH, H, nullptr, d.rms_eps, nullptr, nullptr), M, st);
   CHECK_LAUNCH("TLMModel");
   return TLM_OK;
 }
@@ -1704,9 +1714,23 @@ int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end)
   const bool batched = m->pf_min_rows > 0 && !prefill_unsupported(m);
   for (int p = start; p < end;) {
     const int n = std::min(end - p, batched ? m->pf_chunk : end - p);
-    if (batched && n >= m->pf_min_rows) {
+    bool replay = !(batched && n >= m->pf_min_rows);
+    if (!replay) {
       rc = prefill_rows(m, m->prompt + (p - start), p, n);
-    } else {  // the decode graph replayed per position
+      if (rc) return rc;
+      // an fp16 activation of the chunk overflowed (or was NaN): the chunk's
+      // cache rows are rewritten by the fp32 decode path
+      int ovf = 0;
+      HIP_TRY(hipMemcpyAsync(&ovf, m->pf_ovf, sizeof(int), hipMemcpyDeviceToHost, st));
+      HIP_TRY(hipStreamSynchronize(st));
+      if (ovf) {
+        const int zero = 0;
+        HIP_TRY(hipMemcpy(m->pf_ovf, &zero, sizeof(int), hipMemcpyHostToDevice));
+        m->pf_replayed++;
+        replay = true;
+      }
+    }
+    if (replay) {  // the decode graph replayed per position
       launch_set_ctrl(m->ctrl, tokens[p], p, 0, start, end - start, emb_stage(m), st);
       CHECK_LAUNCH("TLMModel");
       for (int i = 0; i < n && !rc; i++) rc = run_token(m, false, p + i);
@@ -2042,6 +2066,8 @@ int tlm_model_describe(tlm_model* m, char* out, size_t len) {
   } else {
     s += " persistent[off]";
   }
+  s += " prefill[batched from " + std::to_string(m->pf_min_rows) + " rows, chunk " + std::to_string(m->pf_chunk) +
+       ", " + std::to_string(m->pf_replayed) + " replayed after fp16 overflow]";
   snprintf(out, len, "%s", s.c_str());
   return TLM_OK;
 }

@@ -286,6 +286,7 @@ struct GemmArgs {
   int p0, Hq, Hkv, max_tokens;
   uint16_t* kc;        // fp16 [Hkv][max_tokens][64] (this layer)
   uint16_t* vc;
+  int* ovf;            // set to 1 when an fp16 output (h, q, k, v) is not finite; may be null
 };
 // Tile and split-K choice of one GEMM (gemm_shape is the only planner, so the
 // host sizes the slice buffers from the same numbers the launch uses).
@@ -307,6 +308,7 @@ struct RowsArgs {
   const float* w;
   float eps;
   uint16_t* Y;
+  int* ovf;             // set to 1 when a normed fp16 value is not finite; may be null
 };
 struct PrefillAttnArgs {
   const uint16_t* q;    // fp16 [M][Hq D], RoPE applied
@@ -328,6 +330,7 @@ struct RopeKvArgs {
   void* kc;             // [Hkv][max_tokens][D]
   void* vc;
   int kv_f32;
+  int* ovf;             // set to 1 when an fp16 q, k or v is not finite; may be null
 };
 GemmShape gemm_shape(int fmt, int epi, int M, int N, int K, int cus);
 bool launch_gemm(int fmt, int epi, const GemmShape& sh, const GemmArgs& g, hipStream_t st);

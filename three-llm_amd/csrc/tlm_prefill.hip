@@ -11,6 +11,14 @@
 
 namespace tlm {
 
+// fp16 rounding of a prefill activation with the overflow report: values at
+// or beyond 65520 in magnitude (they round to inf) and NaN set *ovf, and the
+// host then replays the chunk on the fp32 decode path.
+__device__ __forceinline__ _Float16 f16_guard(int* ovf, float v) {
+  if (ovf && !(fabsf(v) < 65520.f)) __hip_atomic_fetch_or(ovf, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return (_Float16)v;
+}
+
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
@@ -229,7 +237,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
         const int row = rbase + 32 * i + 8 * (v >> 2) + (v & 3);
         if (row < g.M) {
           const float gt = mm.acc[i][0][v], up = mm.acc[i][NB - 1][v];
-          const _Float16 hv = (_Float16)silu_mul(gt, up);
+          const _Float16 hv = f16_guard(g.ovf, silu_mul(gt, up));
           g.Ch[(size_t)row * g.ldc + oi] = __builtin_bit_cast(uint16_t, hv);
         }
       }
@@ -513,7 +521,7 @@ __global__ __launch_bounds__(64 * WN) __attribute__((amdgpu_waves_per_eu(2))) vo
         const int row = rbase + 32 * t + 8 * (v >> 2) + (v & 3);
         if (row < g.M) {
           const float gt = rb.acc[t][0][v], up = rb.acc[t][1][v];
-          const _Float16 hv = (_Float16)silu_mul(gt, up);
+          const _Float16 hv = f16_guard(g.ovf, silu_mul(gt, up));
           g.Ch[(size_t)row * g.ldc + oi] = __builtin_bit_cast(uint16_t, hv);
         }
       }
@@ -715,12 +723,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         }
         if (kind == 0) {
           uint16_t* qr = g.Ch + (size_t)row * g.ldc + t0 * kTile;
-          qr[d] = __builtin_bit_cast(uint16_t, (_Float16)y0);
-          qr[d + 32] = __builtin_bit_cast(uint16_t, (_Float16)y1);
+          qr[d] = __builtin_bit_cast(uint16_t, f16_guard(g.ovf, y0));
+          qr[d + 32] = __builtin_bit_cast(uint16_t, f16_guard(g.ovf, y1));
         } else {
           uint16_t* cr = (kind == 1 ? g.kc : g.vc) + ((size_t)hk * g.max_tokens + pos) * kTile;
-          cr[d] = __half_as_ushort(__float2half(y0));
-          cr[d + 32] = __half_as_ushort(__float2half(y1));
+          cr[d] = __builtin_bit_cast(uint16_t, f16_guard(g.ovf, y0));
+          cr[d + 32] = __builtin_bit_cast(uint16_t, f16_guard(g.ovf, y1));
         }
       }
     return;
@@ -735,7 +743,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         const int row = rbase + 32 * t + e;
         if (row < g.M) {
           const float gt = f4_at(r[t][0], e), up = f4_at(r[t][1], e);
-          const _Float16 hv = (_Float16)silu_mul(gt, up);
+          const _Float16 hv = f16_guard(g.ovf, silu_mul(gt, up));
           g.Ch[(size_t)row * g.ldc + oi] = __builtin_bit_cast(uint16_t, hv);
         }
       }
@@ -931,8 +939,8 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(RowsArgs a) {
     const int k = threadIdx.x + 256 * j;
     if (k < H4) {
       const float4 wv = w[k], v = xs[j];
-      y[k] = (half4_t){(_Float16)(v.x * inv * wv.x), (_Float16)(v.y * inv * wv.y), (_Float16)(v.z * inv * wv.z),
-                       (_Float16)(v.w * inv * wv.w)};
+      y[k] = (half4_t){f16_guard(a.ovf, v.x * inv * wv.x), f16_guard(a.ovf, v.y * inv * wv.y),
+                       f16_guard(a.ovf, v.z * inv * wv.z), f16_guard(a.ovf, v.w * inv * wv.w)};
     }
   }
 }
@@ -955,7 +963,7 @@ __device__ __forceinline__ float fold_slices(const float* row, const float* bias
 __device__ __forceinline__ void rope_store(const RopeKvArgs& a, int m, int pos, int i, float y) {
   const int nq = a.Hq * a.D, nk = a.Hkv * a.D;
   if (i < nq) {
-    a.q[(size_t)m * nq + i] = __builtin_bit_cast(uint16_t, (_Float16)y);
+    a.q[(size_t)m * nq + i] = __builtin_bit_cast(uint16_t, f16_guard(a.ovf, y));
     return;
   }
   const bool isv = i >= nq + nk;
@@ -965,7 +973,7 @@ __device__ __forceinline__ void rope_store(const RopeKvArgs& a, int m, int pos, 
   if (a.kv_f32)
     static_cast<float*>(cache)[dst] = y;
   else
-    static_cast<__half*>(cache)[dst] = __float2half(y);
+    static_cast<uint16_t*>(cache)[dst] = __builtin_bit_cast(uint16_t, f16_guard(a.ovf, y));
 }
 
 // Pair pi of a q|k|v row: head pi / (D / 2), q = pi % (D / 2).  In a rotated
