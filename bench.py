@@ -286,7 +286,11 @@ def main():
     # inside decode steps over the same positions (a pair of HIP events on the
     # model stream around each launch); then the LM head the same way
     n_k = min(steps, args.kernel_iters)
-    persistent = "persistent[off]" not in runner.model.describe() and not wl.kv_prefill
+    # the persistent kernel runs a position whose attention window is at most
+    # 1024 positions; longer windows take the per-stage layer graph
+    win = hw.recipe.sliding_window or 0
+    persistent = "persistent[off]" not in runner.model.describe() and all(
+        (min(p + 1, win) if win > 0 else p + 1) <= 1024 for p in range(pos0, pos0 + n_k))
     lay_ms = runner.model.time_layers(last, pos0, n_k)
     lay_bytes = sum(layer_bytes(hw, pos0 + i) for i in range(n_k)) / n_k
     lay_bw = lay_bytes / (lay_ms * 1e-3)
