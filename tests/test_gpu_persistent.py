@@ -112,3 +112,35 @@ def test_trace_orders_every_stage(ctx):
     with pytest.raises(tlm.TlmError):
         ps.model.trace_decode(5, 20, 3, nb + 1)
     ps.close()
+
+
+@pytest.mark.parametrize("window,rotary", [(32, 64), (48, 32)])
+def test_persistent_sliding_window_and_partial_rotary(ctx, window, rotary):
+    """The tiny decoder with a sliding window (positions past it leave the
+    attention range, TSLAttention.ts:306-428) and, in the second case, RoPE on
+    the first 32 of 64 dims: 80 positions through the persistent schedule
+    against the per-stage graph and, every 8th, the oracle."""
+    wl = W.WORKLOADS["tiny"]
+    cfg = dict(wl.config, sliding_window=window)
+    if rotary != cfg["head_dim"]:
+        cfg["partial_rotary_factor"] = rotary / cfg["head_dim"]
+    wl = W.Workload(wl.name + "-window", cfg, wl.storage, 80, 8, 128)
+    hw = W.synthetic(wl)
+    hw.keep = True
+    assert hw.recipe.sliding_window == window and hw.recipe.rotary_dim == rotary
+    ps = _runner(hw, ctx, 128, True)
+    ref = _runner(hw, ctx, 128, False)
+    assert re.search(r"persistent\[\d+ blocks", ps.model.describe())
+    om = oracle_model(hw, 128, kv_f16=True, threads=16)
+    toks = [int(t) for t in W.prompt_tokens(wl)][:80]
+    for i, t in enumerate(toks):
+        ps.computeToken(t, i, True)
+        ref.computeToken(t, i, True)
+        got = ps.readLogits()
+        close(got, ref.readLogits(), 2e-3, 1e-3)
+        want = om.forward(t, i)
+        if i % 8 == 7:
+            close(got, want, LOGIT_ATOL, LOGIT_RTOL)
+    ps.close()
+    ref.close()
+    om.close()
