@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TLM_ABI_VERSION 1
+#define TLM_ABI_VERSION 2
 
 enum {
   TLM_OK = 0,
@@ -172,6 +172,13 @@ typedef struct tlm_model_desc {
   double rms_eps;
   double attention_factor;
   const float* inv_freq; /* host, rotary_dim/2 entries */
+  /* ABI 2.  DecoderCPURunner.attention (decoder/DecoderCPURunner.ts:140-160)
+   * passes recipe.attnScale and the block's slidingWindow per layer
+   * (DecoderWeights.ts:307-311: sliding_attention layers get the recipe's
+   * window, full_attention layers 0 when the config lists layer types). */
+  double attn_scale;             /* <= 0 selects 1/sqrt(head_dim) (attnScale undefined) */
+  const int32_t* layer_windows;  /* host, num_layers entries (0 = full causal), copied at
+                                    create; NULL: every layer uses sliding_window */
 } tlm_model_desc;
 
 enum {
@@ -278,6 +285,20 @@ int tlm_time_layers(tlm_model* model, int32_t token, int32_t position, int n, do
 int tlm_trace_decode(tlm_model* model, int32_t token, int32_t position, int n, uint64_t* out, size_t n_out);
 /* Launch layout chosen for the model (for reports): per-stage grid sizes. */
 int tlm_model_describe(tlm_model* model, char* out, size_t len);
+/* Work the model has handed to its stream since it was created: the
+ * counterpart of the reference's submission count
+ * (src/test/submission.browser.test.ts:46-57: one submission per decode token,
+ * one per prefill chunk).  A captured per-token graph is one graph launch;
+ * kernels enqueued directly (the token/position write before a token, the
+ * kernels of a batched prefill chunk, the eager schedule with graphs off)
+ * count one each. */
+typedef struct tlm_model_counts {
+  uint64_t graph_launches;
+  uint64_t kernel_launches;
+  uint64_t prefill_chunks;      /* batched row chunks run (replayed ones excluded) */
+  uint64_t replayed_positions;  /* prompt positions run through the decode graph */
+} tlm_model_counts;
+int tlm_model_counts_read(tlm_model* model, tlm_model_counts* out);
 
 /* ------------------------------------------------------- host-side helpers
  * Synthetic inputs: N(0, std) from SplitMix64 -> Box-Muller, one counter

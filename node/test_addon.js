@@ -43,12 +43,12 @@ function f16ToF32(h) {
 check('every entry point is bound', () => {
   const names = ['abiVersion', 'lastError', 'open', 'close', 'sync', 'deviceInfo', 'modelCreate', 'modelUpload',
     'modelFinalize', 'modelDestroy', 'computeToken', 'prefill', 'readLogits', 'readToken', 'decodeGreedy',
-    'resetCache', 'readCandidates', 'quantizeQ4', 'f32ToF16', 'synthNormal', 'synthTokens'];
+    'resetCache', 'readCandidates', 'quantizeQ4', 'f32ToF16', 'synthNormal', 'synthTokens', 'modelCounts'];
   for (const n of names) assert.strictEqual(typeof tlm[n], 'function', n);
 });
 
 check('abiVersion is the header\'s TLM_ABI_VERSION', () => {
-  assert.strictEqual(tlm.abiVersion(), 1);
+  assert.strictEqual(tlm.abiVersion(), 2);
 });
 
 check('f32ToF16 rounds to nearest even, saturates to inf, keeps signed zero', () => {
@@ -99,6 +99,7 @@ check('a failing call throws Error(tlm_last_error()) with its code', () => {
 check('handles are checked: a model call on a non-handle throws', () => {
   throwsTlm(() => tlm.computeToken({}, 1, 0), TLM_ERR_INVALID, 'TLMAddon:');
   throwsTlm(() => tlm.readToken(42), TLM_ERR_INVALID, 'TLMAddon:');
+  throwsTlm(() => tlm.modelCounts({}), TLM_ERR_INVALID, 'TLMAddon:');
 });
 
 check('open: a context, or (no usable device) an Error from tlm_last_error', () => {

@@ -15,7 +15,7 @@
 //   readToken(model) decodeGreedy(model, token, pos, n) resetCache(model)
 //   readCandidates(model, k, softcap) quantizeQ4(Float32Array, nOut, kIn)
 //   f32ToF16(Float32Array) synthNormal(seed, stream, n, stddev)
-//   synthTokens(seed, stream, n, vocab)
+//   synthTokens(seed, stream, n, vocab) modelCounts(model)
 #include <dlfcn.h>
 #include <node_api.h>
 #include <stdint.h>
@@ -24,6 +24,7 @@
 #include <string.h>
 
 #include <string>
+#include <utility>
 
 #include "tlm.h"
 
@@ -52,6 +53,7 @@ struct Api {
   int (*f32_to_f16)(const float*, size_t, uint16_t*);
   int (*synth_normal)(uint64_t, uint64_t, size_t, float, float*);
   int (*synth_tokens)(uint64_t, uint64_t, size_t, int32_t, int32_t*);
+  int (*model_counts_read)(tlm_model*, tlm_model_counts*);
 };
 Api g_api;
 std::string g_load_error;
@@ -71,6 +73,16 @@ std::string addon_dir() {
     if (s != std::string::npos) return p.substr(0, s);
   }
   return ".";
+}
+
+// The structs this file passes (tlm_model_desc, tlm_model_counts) are the
+// header's: a library of another ABI version is refused at load.
+bool abi_matches() {
+  const int v = g_api.abi_version();
+  if (v == TLM_ABI_VERSION) return true;
+  g_load_error = "TLMAddon: libtlm.so has ABI version " + std::to_string(v) + ", this addon was built for " +
+                 std::to_string(TLM_ABI_VERSION);
+  return false;
 }
 
 bool load_library() {
@@ -96,7 +108,8 @@ bool load_library() {
          bind(lib, "tlm_read_token", a.read_token) && bind(lib, "tlm_decode_greedy", a.decode_greedy) &&
          bind(lib, "tlm_reset_cache", a.reset_cache) && bind(lib, "tlm_read_candidates", a.read_candidates) &&
          bind(lib, "tlm_quantize_q4", a.quantize_q4) && bind(lib, "tlm_f32_to_f16", a.f32_to_f16) &&
-         bind(lib, "tlm_synth_normal", a.synth_normal) && bind(lib, "tlm_synth_tokens", a.synth_tokens);
+         bind(lib, "tlm_synth_normal", a.synth_normal) && bind(lib, "tlm_synth_tokens", a.synth_tokens) &&
+         bind(lib, "tlm_model_counts_read", a.model_counts_read) && abi_matches();
 }
 
 // ---------------------------------------------------------------- helpers --
@@ -326,7 +339,8 @@ bool field_f64(napi_env env, napi_value o, const char* name, double* out, double
 // desc: {hiddenSize, intermediateSize, numLayers, numHeads, numKvHeads,
 // headDim, vocabSize, maxTokens, rotaryDim, slidingWindow, linearFmt,
 // headFmt, embedFmt, kvFmt, qkvBias, tied, rmsEps, attentionFactor,
-// invFreq: Float32Array(rotaryDim / 2)} -- the fields of tlm_model_desc.
+// invFreq: Float32Array(rotaryDim / 2), attnScale, layerWindows:
+// Int32Array(numLayers)} -- the fields of tlm_model_desc.
 napi_value ModelCreate(napi_env env, napi_callback_info info) {
   Args a(env, info);
   Handle* h = unwrap(env, a.v[0], 1);
@@ -335,6 +349,7 @@ napi_value ModelCreate(napi_env env, napi_callback_info info) {
   napi_value o = a.v[1];
   tlm_model_desc d;
   memset(&d, 0, sizeof d);
+  bool has_windows = false;
   const bool ok = field_i32(env, o, "hiddenSize", &d.hidden_size, true, 0) &&
                   field_i32(env, o, "intermediateSize", &d.intermediate_size, true, 0) &&
                   field_i32(env, o, "numLayers", &d.num_layers, true, 0) &&
@@ -351,8 +366,20 @@ napi_value ModelCreate(napi_env env, napi_callback_info info) {
                   field_i32(env, o, "kvFmt", &d.kv_fmt, false, TLM_FMT_F16) &&
                   field_i32(env, o, "qkvBias", &d.qkv_bias, false, 0) && field_i32(env, o, "tied", &d.tied, false, 0) &&
                   field_f64(env, o, "rmsEps", &d.rms_eps, 1e-6) &&
-                  field_f64(env, o, "attentionFactor", &d.attention_factor, 1.0);
+                  field_f64(env, o, "attentionFactor", &d.attention_factor, 1.0) &&
+                  field_f64(env, o, "attnScale", &d.attn_scale, 0.0);
   if (!ok) return nullptr;
+  napi_has_named_property(env, o, "layerWindows", &has_windows);
+  if (has_windows) {
+    napi_value v;
+    void* w = nullptr;
+    size_t n_w = 0;
+    napi_get_named_property(env, o, "layerWindows", &v);
+    if (!get_typed(env, v, napi_int32_array, &w, &n_w, "desc.layerWindows")) return nullptr;
+    if ((int)n_w != d.num_layers)
+      return throw_error(env, TLM_ERR_INVALID, "TLMModel: desc.layerWindows needs numLayers entries");
+    d.layer_windows = static_cast<const int32_t*>(w);
+  }
   void* inv = nullptr;
   size_t n_inv = 0;
   bool has = false;
@@ -449,6 +476,27 @@ napi_value ReadToken(napi_env env, napi_callback_info info) {
   int32_t t = 0;
   if (!m || !check(env, g_api.read_token(m, &t))) return nullptr;
   return num(env, t);
+}
+
+// {graphLaunches, kernelLaunches, prefillChunks, replayedPositions}: the
+// submission counts of the model (tlm_model_counts_read).
+napi_value ModelCounts(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  tlm_model* m = model_arg(env, a.v[0]);
+  tlm_model_counts c;
+  if (!m || !check(env, g_api.model_counts_read(m, &c))) return nullptr;
+  napi_value o;
+  napi_create_object(env, &o);
+  const std::pair<const char*, uint64_t> fields[] = {{"graphLaunches", c.graph_launches},
+                                                     {"kernelLaunches", c.kernel_launches},
+                                                     {"prefillChunks", c.prefill_chunks},
+                                                     {"replayedPositions", c.replayed_positions}};
+  for (const auto& f : fields) {
+    napi_value v;
+    napi_create_double(env, (double)f.second, &v);
+    napi_set_named_property(env, o, f.first, v);
+  }
+  return o;
 }
 
 napi_value DecodeGreedy(napi_env env, napi_callback_info info) {
@@ -579,6 +627,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"f32ToF16", nullptr, F32ToF16, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"synthNormal", nullptr, SynthNormal, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"synthTokens", nullptr, SynthTokens, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"modelCounts", nullptr, ModelCounts, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
   };
   napi_define_properties(env, exports, sizeof props / sizeof props[0], props);
   return exports;

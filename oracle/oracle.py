@@ -66,6 +66,7 @@ def lib():
         L.orc_model_new.argtypes = [ctypes.c_int] * 8 + [ctypes.c_double, ctypes.c_int, F32P, ctypes.c_int,
                                                          ctypes.c_double, ctypes.c_int, ctypes.c_int]
         L.orc_model_set.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, F32P]
+        L.orc_model_set_attention.argtypes = [ctypes.c_void_p, ctypes.c_double, ctypes.POINTER(ctypes.c_int)]
         L.orc_model_free.argtypes = [ctypes.c_void_p]
         L.orc_model_reset.argtypes = [ctypes.c_void_p]
         L.orc_model_read_cache.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, F32P, F32P]
@@ -222,7 +223,8 @@ class Model:
     numpy arrays; the object keeps references so the C side may borrow them."""
 
     def __init__(self, hidden, inter, layers, heads, kv_heads, head_dim, vocab, max_tokens, eps, inv_freq,
-                 attention_factor=1.0, rotary_dim=None, sliding_window=0, kv_f16=False):
+                 attention_factor=1.0, rotary_dim=None, sliding_window=0, kv_f16=False, attn_scale=0.0,
+                 layer_windows=None):
         self.dims = dict(hidden=hidden, inter=inter, layers=layers, heads=heads, kv_heads=kv_heads,
                          head_dim=head_dim, vocab=vocab, max_tokens=max_tokens)
         rd = head_dim if rotary_dim is None else rotary_dim
@@ -230,6 +232,15 @@ class Model:
         self._keep = [inv]
         self.ptr = lib().orc_model_new(hidden, inter, layers, heads, kv_heads, head_dim, vocab, max_tokens, eps, rd,
                                        ip, rd // 2, attention_factor, sliding_window, int(kv_f16))
+        if attn_scale or layer_windows is not None:
+            wins = None
+            if layer_windows is not None:
+                wins = np.ascontiguousarray(layer_windows, np.int32)
+                if wins.shape != (layers,) or (wins < 0).any():
+                    raise ValueError("oracle: layer_windows needs one non-negative window per layer")
+            lib().orc_model_set_attention(self.ptr, float(attn_scale),
+                                          wins.ctypes.data_as(ctypes.POINTER(ctypes.c_int)) if wins is not None
+                                          else None)
 
     def set(self, tensor, layer, data):
         if data is None:

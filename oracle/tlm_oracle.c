@@ -451,6 +451,7 @@ typedef struct {
   const float** wdown;
   float* kcache;
   float* vcache;
+  int* windows; /* per layer (block.slidingWindow); NULL: attn.sliding_window */
 } orc_model;
 
 /* Weights are borrowed (not copied): the caller keeps the arrays alive.  All
@@ -505,7 +506,22 @@ void orc_model_set(orc_model* m, int tensor, int layer, const float* data) {
   }
 }
 
+/* recipe.attnScale (<= 0: 1/sqrt(head_dim)) and the blocks' slidingWindow,
+ * as DecoderCPURunner.attention passes them (decoder/DecoderCPURunner.ts:
+ * 140-160; per-layer windows from DecoderWeights.ts:307-311).  windows may be
+ * NULL (every layer keeps the model's window); it is copied. */
+void orc_model_set_attention(orc_model* m, double attn_scale, const int* windows) {
+  m->attn.attn_scale = attn_scale > 0 ? attn_scale : 1.0 / sqrt((double)m->head_dim);
+  free(m->windows);
+  m->windows = NULL;
+  if (windows) {
+    m->windows = (int*)malloc(sizeof(int) * m->layers);
+    memcpy(m->windows, windows, sizeof(int) * m->layers);
+  }
+}
+
 void orc_model_free(orc_model* m) {
+  free(m->windows);
   free(m->attn_norm);
   free(m->ffn_norm);
   free(m->wqkv);
@@ -567,7 +583,9 @@ int orc_forward_token(orc_model* m, int token, int position, float* logits, floa
     size_t cache_off = (size_t)l * m->max_tokens * kv_size;
     orc_rmsnorm(x, m->attn_norm[l], H, m->eps, 0, norm);
     orc_linear_t(norm, m->wqkv[l], m->bqkv[l], H, qkv_n, qkv);
-    attention_impl(qkv, &m->attn, position, m->kcache + cache_off, m->vcache + cache_off, attn);
+    orc_attn_opts ao = m->attn;
+    if (m->windows) ao.sliding_window = m->windows[l];
+    attention_impl(qkv, &ao, position, m->kcache + cache_off, m->vcache + cache_off, attn);
     orc_linear_t(attn, m->wo[l], NULL, q_size, H, proj);
     for (int d = 0; d < H; d++) x[d] = (float)((double)x[d] + (double)proj[d]);
     orc_rmsnorm(x, m->ffn_norm[l], H, m->eps, 0, norm);

@@ -29,7 +29,8 @@ def oracle_model(hw, max_tokens, kv_f16=True, threads=1):
     orc.set_threads(threads)
     m = orc.Model(r.hidden_size, r.inner_size, r.layer_count, r.head_count, r.kv_head_count, r.head_dim,
                   r.vocab_size, max_tokens, r.norm_eps, inv, af, rotary_dim=r.rotary_dim,
-                  sliding_window=r.sliding_window, kv_f16=kv_f16)
+                  sliding_window=r.sliding_window, kv_f16=kv_f16, attn_scale=r.attn_scale,
+                  layer_windows=r.layer_windows if r.layer_types is not None else None)
     for kind, layer in hw.kinds():
         m.set(_ORC_ID[kind], layer, device_values(hw, kind, layer))
     if r.tied_embeddings:

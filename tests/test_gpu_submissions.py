@@ -1,0 +1,86 @@
+"""Launch counts of the decode and prefill paths: the reference's submission
+contract (src/test/submission.browser.test.ts:46-57: one submission per
+decode token; 3 for an 18-token prefill in chunks of 7).
+
+Here a decode token is one launch of its captured graph, preceded (when the
+host supplies the token) by one small kernel that writes the token and the
+position: the counterpart of the reference's uniform upload before its submit
+(DecoderTSLRunner.ts:487-501), which is not a submission.  A prompt chunk
+runs as one batched pass (a fixed sequence of row kernels per layer) when it
+has enough rows; shorter chunks replay the decode graph once per position,
+where the reference encodes the chunk's replays into one submission
+(:504-530) -- the same work and order, one graph launch per position.
+"""
+import numpy as np
+import pytest
+
+import three_llm_amd.runner as R
+import three_llm_amd.tlm as tlm
+import three_llm_amd.weights as W
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = tlm.Context(0)
+    yield c
+    c.close()
+
+
+def _delta(model, before):
+    now = model.counts()
+    return {k: now[k] - before[k] for k in now}
+
+
+def test_reference_fixture_one_graph_per_token(ctx, hf_fixture):
+    case = hf_fixture["cases"][0]
+    tensors = {k: np.asarray(v["values"], np.float32).reshape(v["shape"]) for k, v in hf_fixture["tensors"].items()}
+    hw = W.from_hf(case["config"], tensors, W.Storage(linear="f16", head="f16", embed="f32", kv="f32"))
+    runner = R.DecoderHIPRunner(hw, {"maxTokens": 64, "prefillChunkSize": 7}, ctx=ctx)
+    assert not runner.batchedPrefill  # head_dim 8: the fixture replays the decode graph
+    m = runner.model
+    assert m.counts() == {"graph_launches": 0, "kernel_launches": 0, "prefill_chunks": 0, "replayed_positions": 0}
+    runner.computeToken(1, 0, True)
+    b = m.counts()
+    runner.computeToken(5, 1, True)
+    assert _delta(m, b) == {"graph_launches": 1, "kernel_launches": 1, "prefill_chunks": 0, "replayed_positions": 0}
+    runner.resetCache()
+    b = m.counts()
+    ids = hf_fixture["input_ids"]
+    runner.prefillTokens(ids, 0, 18)  # chunks of 7, 7 and 4
+    assert _delta(m, b) == {"graph_launches": 18, "kernel_launches": 3, "prefill_chunks": 0,
+                            "replayed_positions": 18}
+    b = m.counts()
+    out = runner.decodeGreedy(ids[18], 18, 4)  # the device feeds its own tokens: one write in all
+    assert len(out) == 4
+    assert _delta(m, b) == {"graph_launches": 4, "kernel_launches": 1, "prefill_chunks": 0, "replayed_positions": 0}
+    b = m.counts()
+    runner.readLogits()
+    runner.readCandidates(3)
+    assert _delta(m, b)["graph_launches"] == 0
+    runner.close()
+
+
+def test_batched_prefill_one_pass_per_chunk(ctx):
+    wl = W.WORKLOADS["tiny"]
+    # intermediate 768: the batched GEMMs need multiples of 32 (the tiny config has 688)
+    wl = W.Workload(wl.name + "-768", dict(wl.config, intermediate_size=768), wl.storage, 18, 8, 64)
+    hw = W.synthetic(wl)
+    hw.keep = True
+    runner = R.DecoderHIPRunner(hw, {"maxTokens": 64, "prefillChunkSize": 7, "prefillBatchRows": 1}, ctx=ctx)
+    assert runner.batchedPrefill
+    m = runner.model
+    toks = [int(t) for t in W.prompt_tokens(wl)][:18]
+    b = m.counts()
+    runner.prefillTokens(toks, 0, 18)
+    d = _delta(m, b)
+    L = hw.recipe.layer_count
+    # per chunk: the embedding rows, per layer 7 or 8 row kernels and GEMMs
+    # (RoPE in the QKV GEMM's epilogue or its own kernel), the last fold
+    assert d["prefill_chunks"] == 3 and d["graph_launches"] == 0 and d["replayed_positions"] == 0
+    assert d["kernel_launches"] in (3 * (2 + 7 * L), 3 * (2 + 8 * L))
+    b = m.counts()
+    runner.computeToken(toks[-1], 18, True)
+    assert _delta(m, b) == {"graph_launches": 1, "kernel_launches": 1, "prefill_chunks": 0, "replayed_positions": 0}
+    runner.close()

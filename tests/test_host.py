@@ -27,7 +27,29 @@ def test_library_exports_every_header_symbol():
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
     assert sorted(tlm.EXPORTS) == names
-    assert tlm.lib().tlm_abi_version() == 1
+    assert tlm.lib().tlm_abi_version() == 2
+
+
+def header_struct_fields(name):
+    """Field names of `typedef struct name {...} name;` in include/tlm.h."""
+    text = (ROOT / "include" / "tlm.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (name, name), text, flags=re.S).group(1)
+    fields = []
+    for decl in body.split(";"):
+        decl = decl.strip()
+        if decl:
+            fields += [n.strip().lstrip("*") for n in re.sub(r"^[\w\s\*]*?(?=\**\w+\s*(,|$))", "", decl,
+                                                              count=1).split(",")]
+    return fields
+
+
+@pytest.mark.parametrize("cname,pytype", [("tlm_model_desc", tlm.ModelDesc), ("tlm_attn_desc", tlm.AttnDesc),
+                                          ("tlm_model_counts", tlm.ModelCounts)])
+def test_ctypes_structs_match_the_header(cname, pytype):
+    """The ctypes mirrors name the header's fields in the header's order (a
+    missing or extra field shifts every later one)."""
+    assert [f for f, _ in pytype._fields_] == header_struct_fields(cname)
 
 
 def test_open_reports_errors_through_last_error():

@@ -198,6 +198,8 @@ struct tlm_model {
   hipGraphExec_t g_ps_logits = nullptr, g_ps_prefill = nullptr;
   hipGraph_t graph_ps_logits = nullptr, graph_ps_prefill = nullptr;
   int host_pos = 0;  // position of the last token enqueued (selects the attention mode)
+  std::vector<int> windows;  // per-layer sliding window (0: full causal)
+  tlm_model_counts counts{};  // work handed to the stream (tlm_model_counts_read)
   bool finalized = false;
   bool use_graphs = true;  // TLM_GRAPHS=0 enqueues the same kernels directly (profilers, debugging)
 };
@@ -978,7 +980,6 @@ static PsArgs ps_args(const tlm_model* m) {
   a.G = d.num_heads / d.num_kv_heads;
   a.rd = d.rotary_dim;
   a.max_tokens = d.max_tokens;
-  a.window = d.sliding_window;
   a.Nqkv = m->Nqkv;
   a.QS = m->QS;
   a.Cx = L0.qkv->C;
@@ -1049,6 +1050,7 @@ static int ps_setup(tlm_model* m) {
     t.sd = Ly.down->s;
     t.kc = Ly.kc;
     t.vc = Ly.vc;
+    t.window = m->windows[l];
   }
   const size_t w8 = sizeof(unsigned long long);
   int rc = model_alloc((void**)&m->ps_layers, sizeof(PsLayer) * L);
@@ -1087,9 +1089,20 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
     return fail(TLM_ERR_INVALID, "TLMModel: head_fmt must be fp16 or q4");
   if (d->hidden_size % 4 != 0)
     return fail(TLM_ERR_INVALID, "TLMModel: hidden_size %d must be a multiple of 4", d->hidden_size);
+  if (d->sliding_window < 0) return fail(TLM_ERR_INVALID, "TLMModel: negative sliding window");
+  for (int l = 0; d->layer_windows && l < d->num_layers; l++)
+    if (d->layer_windows[l] < 0) return fail(TLM_ERR_INVALID, "TLMModel: negative sliding window of layer %d", l);
   tlm_model* m = new tlm_model();
   m->ctx = ctx;
   m->d = *d;
+  m->d.layer_windows = nullptr;  // borrowed by the call only: copied here
+  m->windows.assign(d->num_layers, d->sliding_window);
+  if (d->layer_windows) m->windows.assign(d->layer_windows, d->layer_windows + d->num_layers);
+  // the model-wide attention mode and chunk plans follow the widest window (0: full)
+  bool full = false;
+  int wmax = 0;
+  for (int w : m->windows) full |= w == 0, wmax = std::max(wmax, w);
+  const int widest = full ? 0 : wmax;
   const int H = d->hidden_size, I = d->intermediate_size, D = d->head_dim;
   m->QS = d->num_heads * D;
   m->Nqkv = m->QS + 2 * d->num_kv_heads * D;
@@ -1099,11 +1112,11 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
   ad.head_dim = D;
   ad.max_tokens = d->max_tokens;
   ad.rotary_dim = d->rotary_dim;
-  ad.sliding_window = d->sliding_window;
+  ad.sliding_window = widest;
   ad.kv_fmt = d->kv_fmt == TLM_FMT_F32 ? TLM_FMT_F32 : TLM_FMT_F16;
   ad.inv_freq = d->inv_freq;
   ad.attention_factor = d->attention_factor;
-  ad.attn_scale = 0;
+  ad.attn_scale = d->attn_scale;  // DecoderCPURunner.ts:152 (recipe.attnScale)
   int rc = attn_init(ctx, &ad, &m->attn, false);
 #define M_TRY(x)               \
   do {                         \
@@ -1289,6 +1302,11 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which, bool l
   Layer& L = m->layers[l];
   const int nl = d.num_layers;
   const size_t rstride = (size_t)kRep * H;
+  // this layer's window (DecoderCPURunner.ts:150): at a long-window position a
+  // layer whose own window spans at most kLongWindow positions stays on the
+  // short-window kernels
+  const int win = m->windows[l];
+  long_win = long_win && (win == 0 || win > kLongWindow);
   // 1. x = residual accumulator (layer 0: the staged embedding row); RMSNorm;
   //    QKV GEMV.  Block (0,0) stores x for the MLP.
   if (which < 0 || which == 4) {
@@ -1300,12 +1318,15 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which, bool l
     a.eps = (float)d.rms_eps;
     a.xout = m->xa;
     ok &= launch_linear(L.qkv, PRO_RMSF, a, st);
+    m->counts.kernel_launches++;
   }
   // 2. RoPE + KV append + split-K attention
   if (which < 0 || which == 1) {
     AttnArgs a = attn_args(&m->attn, m->pq, L.qkv->plan.splits, m->Nqkv, L.bqkv, m->ctrl, L.kc, L.vc, m->attn_out,
                            long_win);
+    a.window = win;
     ok &= launch_attention(d.kv_fmt == TLM_FMT_F32, m->attn.gmax, a, false, long_win, st);
+    m->counts.kernel_launches++;
   }
   // 3. O projection; its prologue combines the attention chunk partials
   if (which < 0 || which == 5) {
@@ -1317,7 +1338,7 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which, bool l
     a.att_D = d.head_dim;
     a.att_nsplit = long_win ? m->attn.nsplit_long : m->attn.nsplit;
     a.att_chmin = m->attn.chmin;
-    a.att_window = d.sliding_window;
+    a.att_window = win;
     a.att_max_tokens = d.max_tokens;
     // the accumulator layer l - 1 produced was last read by this layer's QKV
     // (layer 0: the previous token's final norm): clear it for its next use
@@ -1325,6 +1346,7 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which, bool l
     a.zero_n = (int)rstride;
     // more than 16 long-window chunks: the 24-slot combine keeps it to one round trip
     ok &= launch_linear(L.o, long_win && a.att_nsplit > 16 ? PRO_ATTN3 : PRO_ATTN, a, st);
+    m->counts.kernel_launches++;
   }
   // 4. x_mid = x + O partials; RMSNorm; gate|up; SwiGLU; down, accumulated
   //    with x_mid into rb[l]
@@ -1345,6 +1367,7 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which, bool l
     a.H = H;
     a.acc = m->rb + (size_t)l * rstride;
     ok &= launch_mlp(wfmt(L.gu->fmt), m->mlp_nch, m->mlp_ndb, L.gu->T, a, st);
+    m->counts.kernel_launches++;
   }
   (void)I;
   return ok;
@@ -1377,6 +1400,7 @@ static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, hipEvent_t*
   if (ev) hipEventRecord(ev[1], st);
   launch_argmax_merge(m->arg_val, m->arg_idx, m->lm_plan.gx, m->ctrl, advance ? m->tokens_out : nullptr,
                       advance ? 1 : 0, d.max_tokens, emb_stage(m), st, ps ? 1 : 0);
+  m->counts.kernel_launches += 2;
   return true;
 }
 
@@ -1384,8 +1408,10 @@ static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, hipEvent_t*
 // argmax merge, or the prefill advance.
 static bool enqueue_ps(tlm_model* m, hipStream_t st, int tail) {
   if (!launch_ps_token(m->ps, m->ps_blocks, m->ps_smem, m->ps_args_dev, st)) return false;
+  m->counts.kernel_launches++;
   if (tail == 1) return enqueue_head(m, st, true, nullptr, true);
   launch_prefill_advance(m->ctrl, m->prompt, emb_stage(m), st, 1);
+  m->counts.kernel_launches++;
   return true;
 }
 
@@ -1393,8 +1419,11 @@ static bool enqueue_ps(tlm_model* m, hipStream_t st, int tail) {
 // (LM head timing).
 enum GraphTail { TAIL_PREFILL = 0, TAIL_LOGITS = 1, TAIL_NONE = 2 };
 
+// (Kernels recorded into a graph are not handed to the stream: the capture
+// functions leave the model's counts as they found them.)
 static int capture(tlm_model* m, int tail, bool long_win, hipGraph_t* g, hipGraphExec_t* ge) {
   hipStream_t st = m->ctx->stream;
+  const tlm_model_counts kept = m->counts;
   HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
   bool ok = true;
   for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1, long_win);
@@ -1402,6 +1431,7 @@ static int capture(tlm_model* m, int tail, bool long_win, hipGraph_t* g, hipGrap
     ok &= enqueue_head(m, st, true);
   else if (tail == TAIL_PREFILL)
     launch_prefill_advance(m->ctrl, m->prompt, emb_stage(m), st);
+  m->counts = kept;
   hipError_t le = hipGetLastError();
   HIP_TRY(hipStreamEndCapture(st, g));
   if (le != hipSuccess) return fail(TLM_ERR_HIP, "TLMModel: launch during capture failed: %s", hipGetErrorString(le));
@@ -1412,8 +1442,10 @@ static int capture(tlm_model* m, int tail, bool long_win, hipGraph_t* g, hipGrap
 
 static int capture_ps(tlm_model* m, int tail, hipGraph_t* g, hipGraphExec_t* ge) {
   hipStream_t st = m->ctx->stream;
+  const tlm_model_counts kept = m->counts;
   HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
   const bool ok = enqueue_ps(m, st, tail);
+  m->counts = kept;
   hipError_t le = hipGetLastError();
   HIP_TRY(hipStreamEndCapture(st, g));
   if (le != hipSuccess) return fail(TLM_ERR_HIP, "TLMModel: launch during capture failed: %s", hipGetErrorString(le));
@@ -1455,6 +1487,7 @@ static int run_token(tlm_model* m, bool logits, int pos) {
   if (m->ps_on && !lw) {  // the persistent schedule
     if (m->use_graphs) {
       HIP_TRY(hipGraphLaunch(logits ? m->g_ps_logits : m->g_ps_prefill, st));
+      m->counts.graph_launches++;
       return TLM_OK;
     }
     if (!enqueue_ps(m, st, logits ? 1 : 0)) return fail(TLM_ERR_STATE, "TLMModel: no persistent kernel variant");
@@ -1463,14 +1496,17 @@ static int run_token(tlm_model* m, bool logits, int pos) {
   }
   if (m->use_graphs) {
     HIP_TRY(hipGraphLaunch(logits ? m->g_logits[lw] : m->g_prefill[lw], st));
+    m->counts.graph_launches++;
     return TLM_OK;
   }
   bool ok = true;
   for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1, lw);
-  if (logits)
+  if (logits) {
     ok &= enqueue_head(m, st, true);
-  else
+  } else {
     launch_prefill_advance(m->ctrl, m->prompt, emb_stage(m), st);
+    m->counts.kernel_launches++;
+  }
   if (!ok) return fail(TLM_ERR_STATE, "TLMModel: no kernel variant for a stage of this model");
   CHECK_LAUNCH("TLMModel");
   return TLM_OK;
@@ -1491,7 +1527,8 @@ int tlm_compute_token(tlm_model* m, int32_t token, int32_t position, int flags) 
   rc = tlm_model_finalize(m);
   if (rc) return rc;
   hipStream_t st = m->ctx->stream;
-  launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
+  launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);  // the token/position write
+  m->counts.kernel_launches++;
   CHECK_LAUNCH("TLMModel");
   return run_token(m, (flags & TLM_LOGITS) != 0, position);
 }
@@ -1599,6 +1636,9 @@ static int prefill_rows(tlm_model* m, const int* tokens, int p0, int M) {
   hipStream_t st = m->ctx->stream;
   const size_t rowsH = (size_t)M * H;
   launch_embed_rows(tokens, M, m->emb, d.embed_fmt == TLM_FMT_F32, H, m->pf_x, st);
+  // per layer: two row kernels, the QKV GEMM (+ rope_kv unless RoPE runs in its
+  // epilogue), attention and three GEMMs; then the last fold
+  m->counts.kernel_launches += 1 + (uint64_t)d.num_layers * (rope_epi ? 7 : 8) + 1;
   for (int l = 0; l < d.num_layers; l++) {
     const Layer& L = m->layers[l];
     bool ok = true;
@@ -1658,7 +1698,7 @@ static int prefill_rows(tlm_model* m, const int* tokens, int p0, int M) {
     pa.D = D;
     pa.G = m->attn.G;
     pa.max_tokens = d.max_tokens;
-    pa.window = d.sliding_window;
+    pa.window = m->windows[l];
     pa.scale_log2 = m->attn.scale * 1.4426950408889634f;
     ok = ok && launch_prefill_attention(pa, st);
     g = gemm_args(L.o, m->pf_att, m->QS, M);
@@ -1729,9 +1769,12 @@ int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end)
         m->pf_replayed++;
         replay = true;
       }
+      if (!replay) m->counts.prefill_chunks++;
     }
     if (replay) {  // the decode graph replayed per position
       launch_set_ctrl(m->ctrl, tokens[p], p, 0, start, end - start, emb_stage(m), st);
+      m->counts.kernel_launches++;
+      m->counts.replayed_positions += n;
       CHECK_LAUNCH("TLMModel");
       for (int i = 0; i < n && !rc; i++) rc = run_token(m, false, p + i);
     }
@@ -1802,6 +1845,7 @@ int tlm_decode_greedy(tlm_model* m, int32_t token, int32_t position, int n, int3
   if (rc) return rc;
   hipStream_t st = m->ctx->stream;
   launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
+  m->counts.kernel_launches++;
   CHECK_LAUNCH("TLMModel");
   for (int i = 0; i < n; i++) {
     rc = run_token(m, true, position + i);
@@ -2068,7 +2112,20 @@ int tlm_model_describe(tlm_model* m, char* out, size_t len) {
   }
   s += " prefill[batched from " + std::to_string(m->pf_min_rows) + " rows, chunk " + std::to_string(m->pf_chunk) +
        ", " + std::to_string(m->pf_replayed) + " replayed after fp16 overflow]";
+  bool mixed = false;
+  for (int w : m->windows) mixed |= w != m->windows[0];
+  if (mixed) {  // per-layer windows, e.g. "windows[0,512,0,512]"
+    s += " windows[";
+    for (size_t l = 0; l < m->windows.size(); l++) s += (l ? "," : "") + std::to_string(m->windows[l]);
+    s += "]";
+  }
   snprintf(out, len, "%s", s.c_str());
+  return TLM_OK;
+}
+
+int tlm_model_counts_read(tlm_model* m, tlm_model_counts* out) {
+  if (!m || !out) return fail(TLM_ERR_INVALID, "TLMModel: null argument");
+  *out = m->counts;
   return TLM_OK;
 }
 

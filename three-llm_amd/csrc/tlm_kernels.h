@@ -216,11 +216,12 @@ struct PsLayer {
   const uint16_t* sd;
   void* kc;               // [Hkv][max_tokens][D]
   void* vc;
+  int window;             // this layer's sliding window (0: full causal)
 };
 struct PsArgs {
   const PsLayer* layers;  // [L]
   const int* roles;       // [blocks][kPsRoles][2]: (stage, item) pairs in stage order; stage -1: none
-  int L, H, I, Hq, Hkv, D, G, rd, max_tokens, window;
+  int L, H, I, Hq, Hkv, D, G, rd, max_tokens;
   int Nqkv, QS;
   int Cx, Co, Cd;         // chunks per row: H-input linears (qkv, gate|up), O (K = QS), down (K = I)
   int To, Tgu, Tq;        // 64-row tiles: H outputs (O, down), gate|up (paired), qkv

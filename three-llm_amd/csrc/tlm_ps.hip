@@ -668,9 +668,10 @@ __global__ __launch_bounds__(kPsWaves * 64) void ps_token_kernel(const PsArgs* _
   const unsigned seq = (unsigned)gl(a.ctrl)[C_SEQ];
   if (pos < 0 || pos >= a.max_tokens) return;
   ps_stamp(a, a.L, 0, 0);
-  const int first = a.window > 0 ? max(pos - a.window + 1, 0) : 0;
   const TLM_GLOBAL int* rl = gl(a.roles) + blockIdx.x * kPsRoles * 2;
   for (int l = 0; l < a.L; l++) {
+    const int win = gl(a.layers)[l].window;  // DecoderCPURunner.ts:150 (block.slidingWindow)
+    const int first = win > 0 ? max(pos - win + 1, 0) : 0;
 #pragma unroll 1
     for (int r = 0; r < kPsRoles; r++) {
       const int st = rl[2 * r], it = rl[2 * r + 1];

@@ -142,6 +142,10 @@ class Recipe:
     qkv_bias: bool = False
     tied_embeddings: bool = False
     sliding_window: int = 0
+    # config layer_types (None: absent); an empty list still counts as present,
+    # as the reference's `this.layerTypes ? 0 : ...` test of an array does
+    layer_types: Optional[list] = None
+    attn_scale: float = 0.0  # attnScale: undefined (0 selects 1/sqrt(head_dim)) for this recipe
     rope_scaling: Optional[dict] = None
     end_of_text_token_id: int = 0
     stop_token_ids: list = field(default_factory=list)
@@ -157,6 +161,20 @@ class Recipe:
 
     def rope(self):
         return rope_parameters(self.rotary_dim, self.rope_theta, self.rope_scaling)
+
+    def layer_window(self, index: int) -> int:
+        """The block's slidingWindow (DecoderWeights.ts:307-311): with layer types,
+        sliding_attention layers take the recipe's window and the others 0;
+        without them every layer takes the recipe's window."""
+        types = self.layer_types
+        layer_type = (types[index] if types is not None and index < len(types) else None) or "full_attention"
+        if layer_type == "sliding_attention":
+            return self.sliding_window or 0
+        return 0 if types is not None else (self.sliding_window or 0)
+
+    @property
+    def layer_windows(self) -> list:
+        return [self.layer_window(i) for i in range(self.layer_count)]
 
 
 def recipe_for(config: dict, has_lm_head: bool = True, has_qkv_bias: bool = False) -> Recipe:
@@ -179,6 +197,14 @@ def recipe_for(config: dict, has_lm_head: bool = True, has_qkv_bias: bool = Fals
     eos = text.get("eos_token_id", 0)
     eos_ids = eos if isinstance(eos, list) else [eos]
     sliding = 0 if text.get("use_sliding_window") is False else (text.get("sliding_window") or 0)
+    layer_types = text.get("layer_types")
+    if layer_types is not None and "sliding_attention" in layer_types:
+        # sliding layers take localRopeTheta (DecoderWeights.ts:310), which
+        # differs from rope_theta only with rope_local_base_freq; one RoPE
+        # table per model here
+        local = text.get("rope_local_base_freq")
+        if local and local != (text.get("rope_theta") or 10000):
+            raise RecipeError("Per-layer RoPE bases (rope_local_base_freq) are not supported.")
     recipe = Recipe(
         hidden_size=hidden,
         inner_size=text["intermediate_size"],
@@ -196,6 +222,7 @@ def recipe_for(config: dict, has_lm_head: bool = True, has_qkv_bias: bool = Fals
         # untied only if lm_head.weight exists and tie_word_embeddings is not true.
         tied_embeddings=not (has_lm_head and text.get("tie_word_embeddings") is not True),
         sliding_window=sliding,
+        layer_types=list(layer_types) if layer_types is not None else None,
         rope_scaling=scaling_config(text),
         end_of_text_token_id=eos_ids[0] if eos_ids else 0,
         stop_token_ids=list(eos_ids),

@@ -68,7 +68,7 @@ class DecoderHIPRunner:
         self.maxTokens = min(options.get("maxTokens") or limit, limit)
         self.logitCandidateCount = min(options.get("logitCandidateCount") or 8, 16)  # device top-k holds <= 16
         desc, inv = weights.model_desc(self.maxTokens)
-        self.model = tlm.Model(self.ctx, desc, inv)
+        self.model = tlm.Model(self.ctx, desc, inv, layer_windows=weights.recipe.layer_windows)
         weights.upload(self.model)
         self.model.finalize()
         # Batched (MFMA) prefill for chunks of at least prefillBatchRows

@@ -33,7 +33,7 @@ EXPORTS = [
     "tlm_prefill", "tlm_read_logits", "tlm_read_token", "tlm_decode_greedy", "tlm_reset_cache", "tlm_kv_write",
     "tlm_kv_read", "tlm_kv_fill_normal", "tlm_read_hidden", "tlm_time_decode", "tlm_time_kernel", "tlm_time_head",
     "tlm_time_layers", "tlm_trace_decode",
-    "tlm_model_describe", "tlm_synth_normal", "tlm_synth_tokens", "tlm_quantize_q4", "tlm_f32_to_f16",
+    "tlm_model_describe", "tlm_model_counts_read", "tlm_synth_normal", "tlm_synth_tokens", "tlm_quantize_q4", "tlm_f32_to_f16",
 ]
 
 
@@ -57,7 +57,13 @@ class ModelDesc(ctypes.Structure):
                 ("rotary_dim", ctypes.c_int32), ("sliding_window", ctypes.c_int32), ("linear_fmt", ctypes.c_int32),
                 ("head_fmt", ctypes.c_int32), ("embed_fmt", ctypes.c_int32), ("kv_fmt", ctypes.c_int32),
                 ("qkv_bias", ctypes.c_int32), ("tied", ctypes.c_int32), ("rms_eps", ctypes.c_double),
-                ("attention_factor", ctypes.c_double), ("inv_freq", ctypes.POINTER(ctypes.c_float))]
+                ("attention_factor", ctypes.c_double), ("inv_freq", ctypes.POINTER(ctypes.c_float)),
+                ("attn_scale", ctypes.c_double), ("layer_windows", ctypes.POINTER(ctypes.c_int32))]
+
+
+class ModelCounts(ctypes.Structure):
+    _fields_ = [("graph_launches", ctypes.c_uint64), ("kernel_launches", ctypes.c_uint64),
+                ("prefill_chunks", ctypes.c_uint64), ("replayed_positions", ctypes.c_uint64)]
 
 
 _lib = None
@@ -125,6 +131,7 @@ def lib():
             "tlm_time_head": ([VP, i32, i32, ctypes.c_int, ctypes.POINTER(dbl)], ctypes.c_int),
             "tlm_time_layers": ([VP, i32, i32, ctypes.c_int, ctypes.POINTER(dbl)], ctypes.c_int),
             "tlm_model_describe": ([VP, ctypes.c_char_p, sz], ctypes.c_int),
+            "tlm_model_counts_read": ([VP, ctypes.POINTER(ModelCounts)], ctypes.c_int),
             "tlm_trace_decode": ([VP, i32, i32, ctypes.c_int, VP, sz], ctypes.c_int),
             "tlm_synth_normal": ([u64, u64, sz, ctypes.c_float, VP], ctypes.c_int),
             "tlm_synth_tokens": ([u64, u64, sz, i32, VP], ctypes.c_int),
@@ -374,10 +381,17 @@ def topk(ctx: Context, logits_buf: Buffer, n: int, k: int, softcap: float = 0.0)
 class Model:
     """Device model: weights, KV cache and the captured per-token graphs."""
 
-    def __init__(self, ctx: Context, desc: ModelDesc, inv_freq: np.ndarray):
+    def __init__(self, ctx: Context, desc: ModelDesc, inv_freq: np.ndarray, layer_windows=None):
+        """layer_windows: per-layer sliding windows (0 = full causal), or None
+        for desc.sliding_window in every layer."""
         self.ctx = ctx
         self._inv = np.ascontiguousarray(inv_freq, np.float32)
         desc.inv_freq = self._inv.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+        if layer_windows is not None:
+            self._windows = np.ascontiguousarray(layer_windows, np.int32)
+            if self._windows.shape != (desc.num_layers,):
+                raise ValueError(f"layer_windows needs {desc.num_layers} entries, got {self._windows.shape}")
+            desc.layer_windows = self._windows.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
         self.desc = desc
         p = VP()
         check(lib().tlm_model_create(ctx.ptr, ctypes.byref(desc), ctypes.byref(p)))
@@ -497,6 +511,13 @@ class Model:
         buf = ctypes.create_string_buffer(2048)
         check(lib().tlm_model_describe(self.ptr, buf, 2048))
         return buf.value.decode()
+
+    def counts(self) -> dict:
+        """Graph launches, direct kernel launches, batched prefill chunks and
+        replayed prompt positions handed to the model's stream so far."""
+        c = ModelCounts()
+        check(lib().tlm_model_counts_read(self.ptr, ctypes.byref(c)))
+        return {name: int(getattr(c, name)) for name, _ in ModelCounts._fields_}
 
     def close(self):
         if self.ptr:

@@ -113,6 +113,7 @@ class HostWeights:
         d.embed_fmt, d.kv_fmt = _fmt(self.storage.embed), _fmt(self.storage.kv)
         d.qkv_bias, d.tied = int(r.qkv_bias), int(r.tied_embeddings)
         d.rms_eps, d.attention_factor = r.norm_eps, af
+        d.attn_scale = r.attn_scale
         return d, inv
 
     def upload(self, model: tlm.Model) -> None:
