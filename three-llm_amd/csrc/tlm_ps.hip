@@ -282,6 +282,17 @@ __device__ __forceinline__ bool ps_qkv(const PsArgs& a, int l, int i, int pos, i
   float bias[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) bias[t] = j == 0 && wave == 0 ? gl(Ly.bqkv)[r0 + 64 * t + lane] : 0.f;
+  // RoPE factors of wave 0's elements (the position is known before the wait;
+  // rotate-half of element d with its partner, TSLAttention.ts:168-250)
+  const int half = a.rd > 0 ? a.rd / 2 : 1;
+  float rc[NT], rs[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const int d = 64 * t + lane, jj = d < half ? d : d - half;
+    const bool rot = wave == 0 && kind < 2 && d < a.rd;
+    rc[t] = rot ? gl(a.rope_cos)[(size_t)pos * half + jj] : 1.f;
+    rs[t] = rot ? gl(a.rope_sin)[(size_t)pos * half + jj] : 0.f;
+  }
   if (wave == 0) ps_stamp(a, l, PS_QKV, 0);
   float x[NX];
   bool ok = true;
@@ -304,17 +315,11 @@ __device__ __forceinline__ bool ps_qkv(const PsArgs& a, int l, int i, int pos, i
 #pragma unroll
     for (int t = 0; t < NT; t++) s.out[64 * t + lane] = bias[t] + inv * ps_sum16(s.red + t * 64 + lane, NT * 64);
     wave_lds_sync();
-    // rotate-half RoPE of element d with its partner (TSLAttention.ts:168-250)
-    const int half = a.rd > 0 ? a.rd / 2 : 1;
 #pragma unroll
     for (int t = 0; t < NT; t++) {
       const int d = 64 * t + lane;
       float val = s.out[d];
-      if (kind < 2 && d < a.rd) {
-        const int jj = d < half ? d : d - half;
-        const float rc = gl(a.rope_cos)[(size_t)pos * half + jj], rs = gl(a.rope_sin)[(size_t)pos * half + jj];
-        val = val * rc + (d < half ? -s.out[d + half] : s.out[d - half]) * rs;
-      }
+      if (kind < 2 && d < a.rd) val = val * rc[t] + (d < half ? -s.out[d + half] : s.out[d - half]) * rs[t];
       st_dev(a.pub_qkv + ((size_t)l * a.kq + j) * a.Nqkv + r0 + d, word(val, seq));
     }
     ps_stamp(a, l, PS_QKV, 3);
