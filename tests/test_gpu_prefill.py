@@ -53,6 +53,7 @@ def make_linear(ctx, fmt, w):
     (tlm.FMT_Q4, 300, 2048, 2048), (tlm.FMT_Q4, 33, 64, 32),
     (tlm.FMT_Q4, 300, 44032, 64),  # 172 x 3 blocks of 256 columns, ragged last block
     (tlm.FMT_Q4, 1100, 4096, 128),  # 9 x 16 blocks of 128 rows x 256 columns, the last 76 rows
+    (tlm.FMT_Q4, 127, 9664, 896),   # 151 x 4 K-wave blocks (more than the CUs), an odd tile count
     (tlm.FMT_F16, 70, 256, 64), (tlm.FMT_F16, 5, 37, 32), (tlm.FMT_F16, 130, 512, 256)])
 def test_linear_rows_matches_fp16_operand_product(ctx, fmt, M, N, K):
     """Each row equals bias + W x with x and W rounded to fp16 (the device's
@@ -148,11 +149,12 @@ def _kv(model, layers, count):
 @pytest.mark.parametrize("name,layers,prompt_len,chunk", [
     ("qwen2.5-0.5b", 2, 128, 2048),   # the benchmark prompt: one batched chunk of 127 rows
     ("qwen2.5-0.5b", 2, 151, 64),     # chunks 64 + 64 batched, 22 replayed
+    ("qwen2.5-0.5b", 2, 701, 2048),   # 700 rows: 22 row tiles of the K-wave kernels, RoPE epilogue
     ("llama-3.2-1b", 2, 200, 2048),
     ("llama-3.2-3b", 2, 100, 2048),   # head_dim 128
 ])
 def test_batched_prefill_matches_replay_and_oracle(ctx, name, layers, prompt_len, chunk):
-    wl = _workload(name, layers, prompt_len)
+    wl = _workload(name, layers, prompt_len, max_tokens=max(512, prompt_len + 16))
     hw = W.synthetic(wl)
     hw.keep = True
     runner = R.DecoderHIPRunner(hw, {"maxTokens": wl.max_tokens, "prefillChunkSize": chunk}, ctx=ctx)
