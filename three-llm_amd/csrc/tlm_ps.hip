@@ -13,6 +13,9 @@
 // arrive while the block waits.  Every role depends only on roles of earlier
 // stages (or of the previous layer), and every block is resident, so all waits
 // end; each is bounded anyway.
+#include <stdio.h>
+#include <stdlib.h>
+
 #include <algorithm>
 #include <type_traits>
 
@@ -778,15 +781,22 @@ PsShape ps_shape(int fmt, int kv_f32, int H, int I, int D, int Hq, int Hkv, int 
   const int nx = (Cx + 15) / 16;
   // Over the compiled variants and the K-splits of QKV (kq), O (ko) and down
   // (ks): the least multiply-adds along one item of each linear stage, plus
-  // the cost of a third role per block (about two microseconds of a CU's
-  // multiply-adds, serial behind the previous role)
+  // 16K per split (every split is one more set of producers a consumer waits
+  // for and one more partial it adds: Qwen2.5-0.5B shape, 381 us/token at
+  // kq = ko = 2 against 387.5 at 4 and 4, 383 at 1 and 2, 386.4 at 1 and 4),
+  // plus the cost of a third role per block (about two microseconds of a
+  // CU's multiply-adds, serial behind the previous role)
   PsShape best = none;
   long best_cost = 0;
+  // TLM_PS_SPLITS=kq,ko,ks fixes the K-splits (comparisons)
+  int fq = 0, fo = 0, fs = 0;
+  if (const char* e = getenv("TLM_PS_SPLITS")) sscanf(e, "%d,%d,%d", &fq, &fo, &fs);
   for (const PsVariant& v : kPsVariants) {
     if (v.fmt != fmt || v.kv_f32 != kv_f32 || v.dt != D || v.nx < nx) continue;
     for (int kq = 1; kq <= kPsMaxKs; kq++)
       for (int ko = 1; ko <= kPsMaxKs; ko++)
         for (int ks = 1; ks <= kPsMaxKs; ks++) {
+          if ((fq && kq != fq) || (fo && ko != fo) || (fs && ks != fs)) continue;
           const int cq = (Cx + kq - 1) / kq, co = (Co + ko - 1) / ko, cs = (Cd + ks - 1) / ks;
           if ((co + 15) / 16 > v.no || (cs + 15) / 16 > v.nd) continue;
           int counts[PS_STAGES];
@@ -794,7 +804,7 @@ PsShape ps_shape(int fmt, int kv_f32, int H, int I, int D, int Hq, int Hkv, int 
           const int r = ps_place(counts, cus, nullptr);
           if (!r) continue;
           const long macs = (long)D * cq * CK + 64L * co * CK + 64L * v.mw * H + 64L * cs * CK;
-          const long cost = macs + (r > 2 ? 128L * 1024 : 0);
+          const long cost = macs + 16384L * (kq + ko + ks) + (r > 2 ? 128L * 1024 : 0);
           if (!best.dt || cost < best_cost) {
             best = PsShape{v.fmt, v.kv_f32, v.dt, v.nx, v.no, v.nd, v.mw, kq, ko, ks};
             best_cost = cost;
