@@ -43,7 +43,7 @@ function f16ToF32(h) {
 check('every entry point is bound', () => {
   const names = ['abiVersion', 'lastError', 'open', 'close', 'sync', 'deviceInfo', 'modelCreate', 'modelUpload',
     'modelFinalize', 'modelDestroy', 'computeToken', 'prefill', 'readLogits', 'readToken', 'decodeGreedy',
-    'resetCache', 'readCandidates', 'quantizeQ4', 'f32ToF16', 'synthNormal', 'synthTokens', 'modelCounts'];
+    'resetCache', 'readCandidates', 'quantizeQ4', 'f32ToF16', 'synthNormal', 'synthTokens', 'modelCounts', 'modelSetPrefill'];
   for (const n of names) assert.strictEqual(typeof tlm[n], 'function', n);
 });
 
@@ -126,6 +126,40 @@ check('prefill range is checked before the call', () => {
   // a fake model handle is rejected first; a range error needs a real model,
   // so only the argument type path is exercised without a device
   throwsTlm(() => tlm.prefill(null, new Int32Array(4), 0, 8), TLM_ERR_INVALID);
+});
+
+check('runner.js: the synthetic tiny decoder\'s tensors, as the Python host builds them', () => {
+  const {syntheticTensors, recipeOf, WORKLOADS, T} = require('./runner.js');
+  const wl = WORKLOADS.tiny;
+  const r = recipeOf(wl.config);
+  const ts = syntheticTensors(tlm, r, wl.storage, wl.qkvBias);
+  assert.strictEqual(ts.length, 3 + 7 * r.layers);  // embed, untied head, final norm; 7 per layer, no bias
+  const embed = ts.find((t) => t.id === T.EMBED);
+  assert.ok(embed.data instanceof Uint16Array && embed.data.length === r.vocab * r.hidden);
+  const wqkv = ts.find((t) => t.id === T.WQKV && t.layer === 1);
+  assert.strictEqual(wqkv.data.length, (r.heads + 2 * r.kvHeads) * r.headDim * r.hidden);  // fp16 linears
+  const norm = ts.find((t) => t.id === T.ATTN_NORM && t.layer === 0);
+  assert.ok(norm.data instanceof Float32Array && norm.data.every((v) => v === 1));
+  // the same stream as the Python host: synth_normal(0x5EED, stream 6 * 4096 + 1, ...) for layer 1's q|k|v
+  const w = tlm.synthNormal(0x5EED, 6 * 4096 + 1, wqkv.data.length, 0.02);
+  assert.deepStrictEqual(Array.from(tlm.f32ToF16(w.subarray(0, 64))), Array.from(wqkv.data.subarray(0, 64)));
+  const qw = WORKLOADS['qwen2.5-0.5b'];
+  const qts = syntheticTensors(tlm, recipeOf(Object.assign({}, qw.config, {num_hidden_layers: 1, vocab_size: 64})),
+    qw.storage, qw.qkvBias);
+  const q = qts.find((t) => t.id === T.WGATE);
+  assert.ok(q.data instanceof Uint8Array && q.scales instanceof Uint16Array && q.scalesId === T.WGATE_SCALES);
+  assert.ok(qts.some((t) => t.id === T.BQKV) && !qts.some((t) => t.id === T.LM_HEAD));  // bias; tied head
+});
+
+check('runner.js: without a usable device the runner throws the library\'s error', () => {
+  const {DecoderHIPRunner, WORKLOADS} = require('./runner.js');
+  let runner = null;
+  try {
+    runner = DecoderHIPRunner.synthetic(tlm, WORKLOADS.tiny, {maxTokens: 32});
+  } catch (e) {
+    assert.ok(e instanceof Error && e.code < 0 && /^(TLMContext|HIP): /.test(e.message), e.message);
+  }
+  if (runner) runner.close();  // a device is present: construction worked
 });
 
 console.log('1..' + passed);

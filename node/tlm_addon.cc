@@ -16,6 +16,7 @@
 //   readCandidates(model, k, softcap) quantizeQ4(Float32Array, nOut, kIn)
 //   f32ToF16(Float32Array) synthNormal(seed, stream, n, stddev)
 //   synthTokens(seed, stream, n, vocab) modelCounts(model)
+//   modelSetPrefill(model, minRows, chunk)
 #include <dlfcn.h>
 #include <node_api.h>
 #include <stdint.h>
@@ -42,6 +43,7 @@ struct Api {
   void (*model_destroy)(tlm_model*);
   int (*model_upload)(tlm_model*, int, int, const void*, size_t);
   int (*model_finalize)(tlm_model*);
+  int (*model_set_prefill)(tlm_model*, int32_t, int32_t);
   int (*compute_token)(tlm_model*, int32_t, int32_t, int);
   int (*prefill)(tlm_model*, const int32_t*, int32_t, int32_t);
   int (*read_logits)(tlm_model*, float*, size_t);
@@ -109,7 +111,8 @@ bool load_library() {
          bind(lib, "tlm_reset_cache", a.reset_cache) && bind(lib, "tlm_read_candidates", a.read_candidates) &&
          bind(lib, "tlm_quantize_q4", a.quantize_q4) && bind(lib, "tlm_f32_to_f16", a.f32_to_f16) &&
          bind(lib, "tlm_synth_normal", a.synth_normal) && bind(lib, "tlm_synth_tokens", a.synth_tokens) &&
-         bind(lib, "tlm_model_counts_read", a.model_counts_read) && abi_matches();
+         bind(lib, "tlm_model_counts_read", a.model_counts_read) &&
+         bind(lib, "tlm_model_set_prefill", a.model_set_prefill) && abi_matches();
 }
 
 // ---------------------------------------------------------------- helpers --
@@ -435,6 +438,17 @@ napi_value ModelFinalize(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+// modelSetPrefill(model, minRows, chunk): the batched-prefill threshold and
+// chunk (tlm_model_set_prefill; minRows <= 0 replays the decode graph).
+napi_value ModelSetPrefill(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  tlm_model* m = model_arg(env, a.v[0]);
+  int32_t min_rows = 0, chunk = 0;
+  if (!m || !get_i32(env, a.v[1], &min_rows, "minRows") || !get_i32(env, a.v[2], &chunk, "chunk")) return nullptr;
+  if (!check(env, g_api.model_set_prefill(m, min_rows, chunk))) return nullptr;
+  return undefined(env);
+}
+
 napi_value ComputeToken(napi_env env, napi_callback_info info) {
   Args a(env, info);
   tlm_model* m = model_arg(env, a.v[0]);
@@ -628,6 +642,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"synthNormal", nullptr, SynthNormal, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"synthTokens", nullptr, SynthTokens, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"modelCounts", nullptr, ModelCounts, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"modelSetPrefill", nullptr, ModelSetPrefill, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
   };
   napi_define_properties(env, exports, sizeof props / sizeof props[0], props);
   return exports;

@@ -2,7 +2,8 @@
 the system Node headers, then node/test_addon.js checks on the CPU that every
 entry point is bound, the host-side helpers return what the C ABI computes,
 and failing calls throw an Error carrying tlm_last_error() and its TLM_ERR_*
-code.  Skipped where Node.js or its headers are absent."""
+code; node/runner.js (the DecoderHIPRunner of the Node host) builds the same
+synthetic tensors as the Python host.  Skipped where Node.js or its headers are absent."""
 import os
 import shutil
 import subprocess
@@ -36,4 +37,4 @@ def test_addon_builds_and_binds_the_c_abi():
     r = subprocess.run([node, str(NODE_DIR / "test_addon.js"), str(addon)], env=env, capture_output=True, text=True,
                        timeout=120)
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
-    assert "1..9" in r.stdout
+    assert "1..11" in r.stdout
