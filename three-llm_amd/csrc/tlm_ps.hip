@@ -709,11 +709,13 @@ struct PsVariant {
   int fmt, kv_f32, dt, nx, no, nd, mw;
 };
 // Compiled shapes (chunks per wave: nx of the H-input linears, no of O, nd of a
-// down split; mw gate|up tiles per item).
+// down split; mw gate|up tiles per item).  None for head_dim 128: at the
+// Llama-3.2-3B shape (648 items, three roles on most blocks, registers spilled)
+// the schedule took 1274 us per token at positions 127..382 against 1102 for the
+// per-stage graph; the Llama-3.2-1B shape gains (447 against 512).
 static const PsVariant kPsVariants[] = {
     {WF_Q4, 0, 64, 2, 1, 3, 1},   // hidden 896, 14 x 64 heads, inter 4864 (Qwen2.5-0.5B shape)
     {WF_Q4, 0, 64, 4, 1, 4, 1},   // hidden 2048, 32 x 64 heads, inter 8192 (Llama-3.2-1B shape)
-    {WF_Q4, 0, 128, 6, 2, 4, 2},  // hidden 3072, 24 x 128 heads, inter 8192 (Llama-3.2-3B shape)
     {WF_Q4, 0, 64, 1, 1, 1, 1},   // hidden <= 512 q4
     {WF_F16, 0, 64, 2, 1, 3, 1},  // hidden 256 fp16
 };
@@ -842,7 +844,6 @@ static const void* ps_kernel(const PsShape& sh) {
     return (const void*)ps_token_kernel<F, std::conditional_t<KV, float, uint16_t>, DTV, NXV, NOV, NDV, MWV>;
   PS_CASE(WF_Q4, 0, 64, 2, 1, 3, 1)
   PS_CASE(WF_Q4, 0, 64, 4, 1, 4, 1)
-  PS_CASE(WF_Q4, 0, 128, 6, 2, 4, 2)
   PS_CASE(WF_Q4, 0, 64, 1, 1, 1, 1)
   PS_CASE(WF_F16, 0, 64, 2, 1, 3, 1)
 #undef PS_CASE
