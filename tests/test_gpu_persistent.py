@@ -11,6 +11,7 @@ oracle's top-2 gap is under 2e-2.
 """
 import os
 import re
+import time
 
 import numpy as np
 import pytest
@@ -143,4 +144,43 @@ def test_persistent_sliding_window_and_partial_rotary(ctx, window, rotary):
             close(got, want, LOGIT_ATOL, LOGIT_RTOL)
     ps.close()
     ref.close()
+    om.close()
+
+
+def test_a_wait_that_runs_out_is_reported_and_every_block_leaves(ctx):
+    """The failure path of the bounded waits, forced from the host: layer 1's
+    QKV items report a time-out without waiting (TLM_PS_FAIL_LAYER), so every
+    item that depends on them runs out its own wait (TLM_PS_TIMEOUT_US: 2 ms
+    instead of 100) and its block leaves.  The kernel ends, the next read of the
+    model raises the library's error, the error is cleared, and a model
+    created without the knobs computes the oracle's logits on the same context."""
+    wl = _workload("tiny", 2, 64)
+    hw = W.synthetic(wl)
+    hw.keep = True
+    knobs = {"TLM_PS_FAIL_LAYER": "1", "TLM_PS_TIMEOUT_US": "2000"}
+    saved = {k: os.environ.get(k) for k in knobs}
+    os.environ.update(knobs)
+    try:
+        bad = _runner(hw, ctx, 64, True)
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
+    assert re.search(r"persistent\[\d+ blocks", bad.model.describe())
+    for step in range(2):
+        t0 = time.perf_counter()
+        bad.computeToken(5, step, True)
+        with pytest.raises(tlm.TlmError) as err:
+            bad.readLogits()
+        assert "timed out" in str(err.value)
+        assert time.perf_counter() - t0 < 5.0  # bounded: a few 2 ms waits in a row
+    bad.close()
+    good = _runner(hw, ctx, 64, True)
+    om = oracle_model(hw, 64, kv_f16=True, threads=16)
+    for i, t in enumerate([5, 9, 11]):
+        good.computeToken(t, i, True)
+        close(good.readLogits(), om.forward(t, i), LOGIT_ATOL, LOGIT_RTOL)
+    good.close()
     om.close()

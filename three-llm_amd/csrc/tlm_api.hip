@@ -1007,6 +1007,12 @@ static PsArgs ps_args(const tlm_model* m) {
   a.pub_o = m->ps_pub_o;
   a.pub_xm = m->ps_pub_xm;
   a.pub_h = m->ps_pub_h;
+  // TLM_PS_TIMEOUT_US / TLM_PS_FAIL_LAYER: a shorter bound of every wait and a
+  // layer whose QKV stage reports a time-out (tests of the failure path)
+  a.timeout = kPsTimeoutTicks;
+  a.fail_layer = -1;
+  if (const char* e = getenv("TLM_PS_TIMEOUT_US")) a.timeout = std::max(1LL, atoll(e)) * 100;  // 100 MHz clock
+  if (const char* e = getenv("TLM_PS_FAIL_LAYER")) a.fail_layer = atoi(e);
   return a;
 }
 

@@ -243,6 +243,12 @@ struct PsArgs {
   // wall-clock stamps (100 MHz) taken by the wave's first lane; stage slot
   // PS_STAGES of layer L holds the kernel's start and end
   unsigned long long* trace;
+  // bounded waits: give up after timeout ticks of the 100 MHz wall clock
+  // (kPsTimeoutTicks); fail_layer >= 0 makes the QKV stage of that layer
+  // report a time-out without waiting (the failure path, forced from the host
+  // by tests)
+  long long timeout;
+  int fail_layer;
 };
 constexpr int kPsEvents = 4;  // weights issued, input ready, computed, published
 // Template choice of the persistent kernel for a model (dt == 0: none).

@@ -42,13 +42,15 @@ __device__ __forceinline__ bool word_is(u64 w, unsigned seq) { return (unsigned)
 // has run out.  The clock is read that rarely because its read is a scalar
 // memory access that LDS waits would also wait for.
 struct PsSpin {
+  long long limit;
   int it = 0;
   long long t0 = 0;
+  __device__ __forceinline__ explicit PsSpin(long long ticks) : limit(ticks) {}
   __device__ __forceinline__ bool tick() { return (++it & 255) == 0; }
   __device__ __forceinline__ bool late() {
     const long long now = wall_clock64();
     if (!t0) t0 = now;
-    return now - t0 > kPsTimeoutTicks;
+    return now - t0 > limit;
   }
 };
 
@@ -73,11 +75,11 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 // every word carries seq; false on time-out (wave-uniform).
 template <int CK, int NU, typename F>
 __device__ __forceinline__ bool wl_gather(int cbase, int cend, int np, unsigned seq, F addr, int wave,
-                                          float (&x)[NU]) {
+                                          float (&x)[NU], long long limit) {
   constexpr int S = 64 / CK;                          // lanes per element
   constexpr int PPL = (kPsMaxKs + S - 1) / S;         // partials per lane
   const int lane = threadIdx.x & 63, e = lane % CK, slot = lane / CK;
-  PsSpin spin;
+  PsSpin spin(limit);
   for (;;) {
     u64 w[NU][PPL];
 #pragma unroll
@@ -127,8 +129,8 @@ __device__ __forceinline__ void wl_embedding(const PsArgs& a, int token, int cen
 // Residual rows of a row-tile item, lane = row: the sum of np published
 // partials at addr(p) (lane's row), polled (wave-level).
 template <typename F>
-__device__ __forceinline__ bool wl_rows(int np, unsigned seq, F addr, float& xr) {
-  PsSpin spin;
+__device__ __forceinline__ bool wl_rows(int np, unsigned seq, F addr, float& xr, long long limit) {
+  PsSpin spin(limit);
   for (;;) {
     u64 w[kPsMaxKs];
 #pragma unroll
@@ -303,8 +305,9 @@ __device__ __forceinline__ bool ps_qkv(const PsArgs& a, int l, int i, int pos, i
     wl_embedding<CK, NX>(a, token, a.Cx, wave, x);
   } else {
     const u64* px = a.pub_x + (size_t)(l - 1) * kPsMaxKs * a.H;
-    ok = wl_gather<CK, NX>(0, a.Cx, a.ks, seq, [&](int p, int k) { return px + (size_t)p * a.H + k; }, wave, x);
+    ok = wl_gather<CK, NX>(0, a.Cx, a.ks, seq, [&](int p, int k) { return px + (size_t)p * a.H + k; }, wave, x, a.timeout);
   }
+  if (l == a.fail_layer) ok = false;  // the forced failure path (tests)
   if (wave == 0) ps_stamp(a, l, PS_QKV, 1);
   float xs[NX], ss = 0.f;
   wl_stage<CK, NX>(x, nw, s.xw, xs, ss);
@@ -383,7 +386,7 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
   bool ok = true;
   if (active) {
     const u64* pq = a.pub_qkv + (size_t)l * a.kq * a.Nqkv;
-    PsSpin spin;
+    PsSpin spin(a.timeout);
     for (;;) {  // lane d: element d (+ 64 e) of q and, in the own wave, of k and v
       float sq[EPL], sk[EPL], sv[EPL];
       bool got = true;
@@ -562,7 +565,7 @@ __device__ __forceinline__ bool ps_o(const PsArgs& a, int l, int i, int token, u
 #pragma unroll
   for (int u = 0; u < NO; u++) one[u] = 1.f;
   const u64* po = a.pub_o + (size_t)l * a.QS;
-  bool ok = wl_gather<CK, NO>(c0, c1, 1, seq, [&](int, int k) { return po + k; }, wave, x);
+  bool ok = wl_gather<CK, NO>(c0, c1, 1, seq, [&](int, int k) { return po + k; }, wave, x, a.timeout);
   float xr = 0.f;
   if (wave == 0 && j == 0) {
     if (l == 0) {
@@ -571,7 +574,7 @@ __device__ __forceinline__ bool ps_o(const PsArgs& a, int l, int i, int token, u
                      : h2f(gl(reinterpret_cast<const uint16_t*>(a.emb))[k]);
     } else {
       const u64* px = a.pub_x + (size_t)(l - 1) * kPsMaxKs * H + min(row, H - 1);
-      ok &= wl_rows(a.ks, seq, [&](int p) { return px + (size_t)p * H; }, xr);
+      ok &= wl_rows(a.ks, seq, [&](int p) { return px + (size_t)p * H; }, xr, a.timeout);
     }
   }
   if (wave == 0) ps_stamp(a, l, PS_O, 1);
@@ -607,7 +610,7 @@ __device__ __forceinline__ bool ps_gu(const PsArgs& a, int l, int g, unsigned se
   if (wave == 0) ps_stamp(a, l, PS_GU, 0);
   const u64* pm = a.pub_xm + (size_t)l * a.ko * H;
   float x[NX];
-  const bool ok = wl_gather<CK, NX>(0, a.Cx, a.ko, seq, [&](int p, int k) { return pm + (size_t)p * H + k; }, wave, x);
+  const bool ok = wl_gather<CK, NX>(0, a.Cx, a.ko, seq, [&](int p, int k) { return pm + (size_t)p * H + k; }, wave, x, a.timeout);
   if (wave == 0) ps_stamp(a, l, PS_GU, 1);
   float xs[NX], ss;
   wl_stage<CK, NX>(x, nw, s.xw, xs, ss);
@@ -647,11 +650,11 @@ __device__ __forceinline__ bool ps_down(const PsArgs& a, int l, int t, int sp, u
   float x[ND], one[ND];
 #pragma unroll
   for (int u = 0; u < ND; u++) one[u] = 1.f;
-  bool ok = wl_gather<CK, ND>(c0, c1, 1, seq, [&](int, int k) { return ph + k; }, wave, x);
+  bool ok = wl_gather<CK, ND>(c0, c1, 1, seq, [&](int, int k) { return ph + k; }, wave, x, a.timeout);
   float xm = 0.f;
   if (wave == 0 && sp == 0) {
     const u64* pm = a.pub_xm + (size_t)l * a.ko * H + min(row, H - 1);
-    ok &= wl_rows(a.ko, seq, [&](int p) { return pm + (size_t)p * H; }, xm);
+    ok &= wl_rows(a.ko, seq, [&](int p) { return pm + (size_t)p * H; }, xm, a.timeout);
   }
   if (wave == 0) ps_stamp(a, l, PS_DOWN, 1);
   float xs[ND], ss;
