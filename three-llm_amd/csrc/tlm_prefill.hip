@@ -853,7 +853,7 @@ bool launch_gemm(int fmt, int epi, const GemmShape& sh, const GemmArgs& ga, hipS
     return true;                                                                                 \
   }
 #define KW_EPIS(MTV) KW_CASE(MTV, GEMM_STORE) KW_CASE(MTV, GEMM_PART) KW_CASE(MTV, GEMM_SWIGLU) KW_CASE(MTV, GEMM_ROPE)
-    KW_EPIS(1) KW_EPIS(2) KW_EPIS(4)
+    KW_EPIS(1)  // gemm_shape gives the K-wave blocks 32 rows
 #undef KW_EPIS
 #undef KW_CASE
     return false;

@@ -405,7 +405,7 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
         sq[e] = sk[e] = sv[e] = 0.f;
 #pragma unroll
         for (int j = 0; j < kPsMaxKs; j++) {
-          got &= word_is(wq[j], seq) & word_is(wk[j], seq) & word_is(wv[j], seq);
+          got &= ((int)word_is(wq[j], seq) & (int)word_is(wk[j], seq) & (int)word_is(wv[j], seq)) != 0;
           sq[e] += word_value(wq[j]);
           sk[e] += word_value(wk[j]);
           sv[e] += word_value(wv[j]);
