@@ -159,7 +159,7 @@ def test_llama1b_4095_id_prompt_and_decode(ctx):
 @pytest.mark.timeout(300)
 def test_llama3b_decode_over_16384_cached_positions(ctx):
     """28 layers, head_dim 128, the fp16 cache filled with N(0, 1) to 16384
-    positions (the long-window attention and its 24-slot combine in the O
+    positions (the matrix-core long-window attention and its 32-slot combine in the O
     projection).  The oracle gets the same cache rows; three decode steps at
     16384..16386 within tolerance, greedy tokens equal."""
     wl = W.WORKLOADS["llama-3.2-3b"]

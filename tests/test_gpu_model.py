@@ -127,27 +127,35 @@ def test_decode_reaches_the_last_cache_position(ctx):
     om.close()
 
 
-def test_long_window_decode_with_more_than_16_chunks(ctx):
-    """One kv head and a 2200-position cache give 69 short-window chunks and
-    18 long-window chunks per query head, more than the 16 the O projection's
-    prologue folds per round trip (its 24-slot form).  Prompt 1100 positions
-    (batched prefill), then logits at positions 1100..1103 (the long-window
-    mode) against the oracle."""
+@pytest.mark.parametrize("gqa,prompt_len,max_tokens,plan", [
+    ("0", 1100, 2200, "nsplit=69/18 G=4]"), ("1", 4400, 4500, "nsplit=141/32 G=4 long=mfma]")],
+    ids=["one-head-blocks", "matrix-core"])
+def test_long_window_decode_with_more_than_16_chunks(ctx, monkeypatch, gqa, prompt_len, max_tokens, plan):
+    """One kv head and four query heads, past the 1024-position window where
+    the long-window kernels take over, with more long-window chunks per query
+    head than the 16 the O projection's prologue folds per round trip (its
+    32-slot form): the one-head-per-block kernel (TLM_GQA=0) has 18 chunks of
+    at least 32 positions at 1100 positions; the matrix-core kernel, one block
+    per kv head and chunk of at least 256 positions, has 18 at 4400.  The
+    prompt runs as a batched prefill, then the logits at the next four
+    positions are checked against the oracle."""
+    monkeypatch.setenv("TLM_GQA", gqa)
     cfg = {"model_type": "llama", "hidden_size": 256, "intermediate_size": 512, "num_hidden_layers": 2,
            "num_attention_heads": 4, "num_key_value_heads": 1, "head_dim": 64, "vocab_size": 2048,
            "rope_theta": 1e4, "rms_norm_eps": 1e-6, "tie_word_embeddings": True,
-           "max_position_embeddings": 4096, "eos_token_id": -1}
-    wl = W.Workload("long-window-1kv", cfg, W.Storage(linear="q4", head="f16", embed="f16"), 1104, 1, 2200)
+           "max_position_embeddings": 8192, "eos_token_id": -1}
+    wl = W.Workload("long-window-1kv", cfg, W.Storage(linear="q4", head="f16", embed="f16"), prompt_len + 4, 1,
+                    max_tokens)
     hw = W.synthetic(wl)
     hw.keep = True
     runner = R.DecoderHIPRunner(hw, {"maxTokens": wl.max_tokens}, ctx=ctx)
-    assert "nsplit=69/18" in runner.model.describe()
+    assert plan in runner.model.describe()
     om = oracle_model(hw, wl.max_tokens, kv_f16=True, threads=16)
     prompt = W.prompt_tokens(wl)
-    runner.prefillTokens([int(x) for x in prompt[:1100]], 0, 1100)
-    for i in range(1100):
-        om.forward(int(prompt[i]), i)
-    for i in range(1100, 1104):
+    runner.prefillTokens([int(x) for x in prompt[:prompt_len]], 0, prompt_len)
+    for i in range(prompt_len):
+        om.prefill(int(prompt[i]), i)
+    for i in range(prompt_len, prompt_len + 4):
         runner.computeToken(int(prompt[i]), i, True)
         close(runner.readLogits(), om.forward(int(prompt[i]), i), LOGIT_ATOL, LOGIT_RTOL)
     runner.close()

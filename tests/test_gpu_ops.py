@@ -226,8 +226,9 @@ def test_attention_decode_after_16384_positions(ctx):
     cache) at its real window: positions 0..16383 are appended by the batched
     rows path (8 calls), the cache is read back, and three decode steps at
     16384.. are checked against the oracle over that same cache.  At this
-    window a block's chunk (~964 positions) is split over four waves that
-    merge in LDS, and the query heads of a kv head share an XCD."""
+    window the matrix-core kernel takes one block per kv head and chunk (32
+    chunks of ~513 positions, 8 waves each) for the group's 3 query heads, and
+    the combine folds 32 partials per head."""
     heads, kv, D, theta, n0 = 24, 8, 128, 5e5, 16384
     rng = np.random.default_rng(16384)
     inv, af = orc.rope_parameters(D, theta)

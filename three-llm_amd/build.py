@@ -19,7 +19,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libtlm.so"
 OBJ = HERE / "_build"
-SOURCES = ["tlm_api.hip", "tlm_kernels.hip", "tlm_prefill.hip", "tlm_ps.hip", "tlm_host.cpp"]
+SOURCES = ["tlm_api.hip", "tlm_kernels.hip", "tlm_gqa.hip", "tlm_prefill.hip", "tlm_ps.hip", "tlm_host.cpp"]
 ARCH = os.environ.get("TLM_OFFLOAD_ARCH", "gfx950")
 
 

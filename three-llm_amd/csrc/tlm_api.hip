@@ -120,8 +120,10 @@ struct tlm_attn {
   tlm_ctx* ctx = nullptr;
   tlm_attn_desc d{};
   // chunks per query head: short windows (one wave each) and long windows
-  // (up to kAttnWaves waves each); pacc / pml hold the larger
-  int G = 1, gmax = 1, nsplit = 1, nsplit_long = 1, chmin = 32, lpp = 1;
+  // (up to kAttnWaves waves each, or with `gqa` one kGqaWaves-wave block per
+  // kv head and chunk); pacc / pml hold the larger.  chmin*: smallest chunk.
+  int G = 1, gmax = 1, nsplit = 1, nsplit_long = 1, chmin = 32, chmin_long = 32, lpp = 1;
+  bool gqa = false;
   float scale = 1.f;
   void* kc = nullptr;
   void* vc = nullptr;
@@ -648,6 +650,18 @@ static int attn_init(tlm_ctx* ctx, const tlm_attn_desc* d, tlm_attn* A, bool own
   A->chmin = 32;
   A->nsplit = std::max(by_tile, std::min(by_min, by_cus));
   A->nsplit_long = (A->nsplit + kAttnWaves - 1) / kAttnWaves;
+  A->chmin_long = A->chmin;
+  // Long windows with an fp16 cache and head_dim 64 / 128: the matrix-core
+  // kernel, one block per (kv head, chunk) for all G query heads; about one
+  // block per CU, chunks of at least one 32-position tile per wave, and at
+  // most 32 chunks (the O projection's combine folds 32 in one round trip).
+  // TLM_GQA=0 keeps the one-head-per-block kernel (comparisons).
+  const char* gq = getenv("TLM_GQA");
+  A->gqa = d->kv_fmt == TLM_FMT_F16 && (d->head_dim == 64 || d->head_dim == 128) && !(gq && gq[0] == '0');
+  if (A->gqa) {
+    A->nsplit_long = std::max(1, std::min(32, ctx->cus / d->kv_heads));
+    A->chmin_long = kGqaWaves * kGqaTile;
+  }
   const int D = d->head_dim;
   const size_t esz = d->kv_fmt == TLM_FMT_F32 ? 4 : 2;
   std::vector<float> cs, sn;
@@ -719,7 +733,8 @@ static AttnArgs attn_args(const tlm_attn* A, const float* src, int n_src, int st
   a.max_tokens = A->d.max_tokens;
   a.window = A->d.sliding_window;
   a.nsplit = long_win ? A->nsplit_long : A->nsplit;
-  a.chmin = A->chmin;
+  a.chmin = long_win ? A->chmin_long : A->chmin;
+  a.gqa = long_win && A->gqa ? 1 : 0;
   a.lpp = A->lpp;
   a.scale = A->scale;
   return a;
@@ -1343,14 +1358,14 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which, bool l
     a.pml = m->attn.pml;
     a.att_D = d.head_dim;
     a.att_nsplit = long_win ? m->attn.nsplit_long : m->attn.nsplit;
-    a.att_chmin = m->attn.chmin;
+    a.att_chmin = long_win ? m->attn.chmin_long : m->attn.chmin;
     a.att_window = win;
     a.att_max_tokens = d.max_tokens;
     // the accumulator layer l - 1 produced was last read by this layer's QKV
     // (layer 0: the previous token's final norm): clear it for its next use
     a.zero_ptr = m->rb + (size_t)((l + nl - 1) % nl) * rstride;
     a.zero_n = (int)rstride;
-    // more than 16 long-window chunks: the 24-slot combine keeps it to one round trip
+    // more than 16 long-window chunks: the 32-slot combine keeps it to one round trip
     ok &= launch_linear(L.o, long_win && a.att_nsplit > 16 ? PRO_ATTN3 : PRO_ATTN, a, st);
     m->counts.kernel_launches++;
   }
@@ -2103,7 +2118,7 @@ int tlm_model_describe(tlm_model* m, char* out, size_t len) {
   std::string s = "qkv[" + p(L.qkv) + "] o[" + p(L.o) + "] mlp[" + mlp + "] head[" +
                   p(m->head) + " grid=" + std::to_string(m->lm_plan.gx) + " waves=" +
                   std::to_string(m->lm_plan.waves) + "] attn[nsplit=" + std::to_string(m->attn.nsplit) + "/" + std::to_string(m->attn.nsplit_long) +
-                  " G=" + std::to_string(m->attn.G) + "]";
+                  " G=" + std::to_string(m->attn.G) + (m->attn.gqa ? " long=mfma" : "") + "]";
   if (m->ps_on) {
     const PsArgs a = ps_args(m);
     const int To = a.To, nq = (a.Hq + 2 * a.Hkv) * a.kq, ng = (a.Tgu + a.mw - 1) / a.mw;

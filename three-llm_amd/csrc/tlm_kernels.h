@@ -9,6 +9,8 @@ constexpr int kTile = 64;      // output rows per tile: one row per lane of a wa
 constexpr int kMaxChunks = 8;  // most 16-byte chunks a wave keeps in flight per batch
 constexpr int kMaxPart = 8;    // partial vectors a consumer folds in with one round trip
 constexpr int kAttnWaves = 4;  // decode attention: waves per block, each a quarter of the block's chunk
+constexpr int kGqaWaves = 8;   // matrix-core decode attention (long windows): waves per block
+constexpr int kGqaTile = 32;   // its positions per wave tile
 constexpr int kLongWindow = 1024; // decode attention: windows above this many positions run the long-window kernels
 // Residual stream accumulators: kRep replicas of an int64 fixed-point vector
 // (value * 2^32).  Producers add into replica (block % kRep) with device-scope
@@ -29,7 +31,7 @@ enum Prologue {
   PRO_RMS2 = 4,    // PRO_RMS for K up to 8 elements per thread (chosen by launch_gemv)
   PRO_RMSF = 5,    // x = rmsnorm(sum of the kRep fixed-point replicas acc_in) * w
   PRO_RMSF2 = 6,   // PRO_RMSF for K up to 8 elements per thread (chosen by launch_gemv)
-  PRO_ATTN3 = 7,   // PRO_ATTN folding 24 chunk partials per round trip instead of 16 (long windows)
+  PRO_ATTN3 = 7,   // PRO_ATTN folding 32 chunk partials per round trip instead of 16 (long windows)
 };
 
 // Split of the attention window [first, pos] into chunks; identical on host and device.
@@ -127,6 +129,7 @@ struct AttnArgs {
   int Hq, Hkv, D, G, rd, max_tokens, window, nsplit, chmin;
   int lpp;              // lanes per position in the score pass (1, 2 or 4)
   float scale;
+  int gqa;              // long windows: the matrix-core kernel (one block per kv head and chunk)
 };
 
 // launchers (stream-ordered, graph-capturable: no memset, no host sync)
@@ -148,6 +151,8 @@ constexpr int kMlpWaves = 16;
 bool launch_lm_head(int fmt, int pro, int waves, int nch, dim3 grid, const GemvArgs& a, hipStream_t st);
 // attention chunk partials; with `combine` also the combine kernel writing a.out
 bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, bool combine, bool long_win, hipStream_t st);
+// long windows, fp16 cache, head_dim 64 or 128, G <= 16: grid Hkv x nsplit
+bool launch_gqa_attention(const AttnArgs& a, hipStream_t st);
 size_t gemv_smem_bytes(int fmt, int cps, int waves);
 void launch_rmsnorm(const float* x, const float* w, int n, float eps, int offset, float* y, hipStream_t st);
 void launch_silu_mul(const float* g, const float* u, int n, float* out, hipStream_t st);

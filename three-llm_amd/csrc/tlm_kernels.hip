@@ -103,10 +103,10 @@ struct GemvPrologue {
   float4 p[2][kMaxPart];  // RMS: partials per float4 (R rows); SWIGLU: [0] gate, [1] up partials
   static constexpr int kSlotLanes = 8;  // ATTN: lanes sharing one float4, splitting its chunk slots
   static constexpr bool kAttn = PRO == PRO_ATTN || PRO == PRO_ATTN3;
-  // chunk slots per lane: 16 per float4 and round trip, or 24 for the long-
-  // window combine (17 chunks at 16384 positions would otherwise take a second
-  // dependent round trip; the short windows keep the smaller first load)
-  static constexpr int kSlotsPerLane = PRO == PRO_ATTN3 ? 3 : 2;
+  // chunk slots per lane: 16 per float4 and round trip, or 32 for the long-
+  // window combine (up to 32 chunks per head in one round trip; the short
+  // windows keep the smaller first load)
+  static constexpr int kSlotsPerLane = PRO == PRO_ATTN3 ? 4 : 2;
   float2 ml[kSlotsPerLane];  // ATTN: (m, l) and accumulators of this lane's chunk slots
   float4 ac[kSlotsPerLane];
   int nact;
@@ -1056,6 +1056,11 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 }
 
 bool launch_attention(bool kv_f32, int gmax, const AttnArgs& a, bool combine, bool long_win, hipStream_t st) {
+  if (long_win && a.gqa) {
+    const bool ok = !kv_f32 && launch_gqa_attention(a, st);
+    if (ok && combine) hipLaunchKernelGGL(attn_combine_kernel, dim3(a.Hq), dim3(128), 0, st, a);
+    return ok;
+  }
   // long windows: XCD-aware numbering, groups of 8 (kv head, chunk) pairs x G heads
   const dim3 grid(long_win ? (unsigned)(((a.Hkv * a.nsplit + 7) / 8) * 8 * a.G) : (unsigned)(a.Hq * a.nsplit));
   const dim3 block(64 * (long_win ? kAttnWaves : 1));
