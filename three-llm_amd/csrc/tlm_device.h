@@ -79,11 +79,24 @@ __device__ __forceinline__ float wave_max(float v) {
 // Block-wide sum (blockDim.x a multiple of 64); every thread gets the result.
 // scratch holds one float per wave and must not be in use by another
 // reduction of the same kernel (each kernel calls this once per scratch).
+// Block barrier that orders LDS only.  __syncthreads() also orders global
+// memory, so every wave first waits for all of its outstanding vector loads:
+// a kernel that issues its weight (or cache) loads early and computes on LDS
+// data in between would otherwise consume nothing until the last load lands.
+// For kernels whose threads exchange data through LDS only (global outputs
+// are read by later kernels).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Sum over the block, in every thread; scratch: LDS, one float per wave.
 __device__ inline float block_sum(float v, float* scratch) {
   v = wave_sum(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   if (lane == 0) scratch[wave] = v;
-  __syncthreads();
+  lds_barrier();
   float r = 0.f;
   for (int i = 0; i < nw; i++) r += scratch[i];
   return r;

@@ -58,8 +58,10 @@ struct GqaShape {
   // banks apart (a stride of DT halves would put them all on the same banks)
   static constexpr int QS = DT + 8;
   // LDS: V regions (reused for the merge), q hi / lo [16][QS], new k / v rows,
-  // the pre-RoPE q|k|v rows [G + 2][DT] in fp32
-  static constexpr int LDS_HALVES = kGqaWaves * WAVE_HALVES + 2 * 16 * QS + 2 * DT + 2 * (16 + 2) * DT;
+  // the pre-RoPE q|k|v rows [G + 2][DT] in fp32 (RAW floats: every thread
+  // stores all kGqaPro of its slots, used or not)
+  static constexpr int RAW = kGqaPro * 64 * kGqaWaves;
+  static constexpr int LDS_HALVES = kGqaWaves * WAVE_HALVES + 2 * 16 * QS + 2 * DT + 2 * RAW;
   static_assert(16 * (2 + DT) * 2 <= WAVE_HALVES, "a wave region holds its merge record");
   static_assert((64 * kGqaWaves) % DT == 0, "a thread's prologue elements share one dim");
 };
@@ -107,7 +109,7 @@ __global__ __launch_bounds__(64 * kGqaWaves) void gqa_attn_kernel(AttnArgs a) {
   _Float16* const qlo = qhi + 16 * S::QS;                  // [16][QS]
   _Float16* const kn = qlo + 16 * S::QS;                   // [DT] new k row (rounded like the cache)
   _Float16* const vn = kn + DT;                            // [DT]
-  float* const raw = reinterpret_cast<float*>(vn + DT);    // [G + 2][DT]
+  float* const raw = reinterpret_cast<float*>(vn + DT);    // [G + 2][DT] (RAW floats)
 
   const int G = a.G, Hkv = a.Hkv;
   const int hk = blockIdx.x % Hkv, c = blockIdx.x / Hkv;
@@ -124,8 +126,9 @@ __global__ __launch_bounds__(64 * kGqaWaves) void gqa_attn_kernel(AttnArgs a) {
   const _Float16* vb = reinterpret_cast<const _Float16*>(a.vc) + (size_t)hk * a.max_tokens * DT;
 
   // Loads in the order they are needed (a wave's vector loads complete in
-  // issue order): the q|k|v inputs of this thread's first two elements and
-  // its RoPE factors, then the wave's first tile.  The q, k, v rows are formed
+  // issue order): the q|k|v inputs of this thread's elements (at most
+  // kGqaPro: (G + 2) DT <= kGqaPro * 64 kGqaWaves) and its RoPE factors, then
+  // the wave's first tile.  The q, k, v rows are formed
   // while that tile streams in; the wave's second tile is requested after
   // them.  Tile loads are unconditional (a wave past the chunk's tiles reads
   // row `last` only); a tile's registers are refilled with the wave's tile
@@ -135,9 +138,9 @@ __global__ __launch_bounds__(64 * kGqaWaves) void gqa_attn_kernel(AttnArgs a) {
     const int r = e / DT, d = e % DT;
     return r < G ? (hk * G + r) * DT + d : (r == G ? QW : QW + KW) + hk * DT + d;
   };
-  float gp[2][kMaxPart], gb[2];
+  float gp[kGqaPro][kMaxPart], gb[kGqaPro];
 #pragma unroll
-  for (int x = 0; x < 2; x++) {
+  for (int x = 0; x < kGqaPro; x++) {
     const int col = col_of(min(tid + 64 * kGqaWaves * x, E - 1));
 #pragma unroll
     for (int j = 0; j < kMaxPart; j++) gp[x][j] = a.src[(size_t)max(min(j, a.n_src - 1), 0) * a.src_stride + col];
@@ -150,27 +153,27 @@ __global__ __launch_bounds__(64 * kGqaWaves) void gqa_attn_kernel(AttnArgs a) {
   const float rs = a.rope_sin[(size_t)pos * half + min(jr, half - 1)];
   GqaK<DT> k0, k1;
   GqaV<DT> v0, v1;
+  __builtin_amdgcn_sched_barrier(0);  // the tile's loads go after the prologue's
   k0.load(kb, b0 + kGqaTile * w, last, lane);
   v0.load(vb, b0 + kGqaTile * w, last, lane);
 
-  // q (G heads), new k, new v: partial sums + bias, then RoPE through LDS
+  // q (G heads), new k, new v: partial sums + bias (stored unconditionally,
+  // so the loads above are neither moved nor waited for behind the tile's),
+  // then RoPE through LDS
 #pragma unroll
-  for (int x = 0; x < 2; x++) {
-    const int e = tid + 64 * kGqaWaves * x;
+  for (int x = 0; x < kGqaPro; x++) {
     float sum = gb[x];
 #pragma unroll
     for (int j = 0; j < kMaxPart; j++) sum = fmaf(gp[x][j], j < a.n_src ? 1.f : 0.f, sum);
-    if (e < E) raw[e] = sum;
+    raw[tid + 64 * kGqaWaves * x] = sum;
   }
-  for (int e = tid + 2 * 64 * kGqaWaves; e < E; e += 64 * kGqaWaves) {  // more than 2 elements per thread
-    const int col = col_of(e);
-    float sum = a.bias[col];
-    for (int j = 0; j < a.n_src; j++) sum += a.src[(size_t)j * a.src_stride + col];
-    raw[e] = sum;
-  }
-  __syncthreads();
+  lds_barrier();
   const float qscale = a.scale * 1.4426950408889634f;  // log2 e: the softmax runs in base 2
-  for (int e = tid; e < 16 * DT + 2 * DT; e += 64 * kGqaWaves) {
+  constexpr int NROT = (18 * DT + 64 * kGqaWaves - 1) / (64 * kGqaWaves);
+#pragma unroll
+  for (int x = 0; x < NROT; x++) {  // unrolled: no loop whose entry would wait for every load
+    const int e = tid + 64 * kGqaWaves * x;
+    if (e >= 18 * DT) break;
     const int r = e / DT, d = e % DT;  // d == dr
     if (r >= G && r < 16) {  // padding heads
       qhi[r * S::QS + d] = qlo[r * S::QS + d] = (_Float16)0.f;
@@ -199,7 +202,7 @@ __global__ __launch_bounds__(64 * kGqaWaves) void gqa_attn_kernel(AttnArgs a) {
   }
   k1.load(kb, b0 + kGqaTile * (w + kGqaWaves), last, lane);
   v1.load(vb, b0 + kGqaTile * (w + kGqaWaves), last, lane);
-  __syncthreads();
+  lds_barrier();
 
   // B operands of the scores (read from LDS once per tile): lane (i16, qd)
   // takes dims 32 jj + 8 qd .. + 7 of head i16
@@ -286,17 +289,32 @@ __global__ __launch_bounds__(64 * kGqaWaves) void gqa_attn_kernel(AttnArgs a) {
     }
   };
 
-  for (int it = w; it < ntile; it += 2 * kGqaWaves) {
+  // The wave's tiles w, w + 8, w + 16, ...: the first two in straight-line
+  // code (inside a loop the compiler's waits merge over the back edge and
+  // the first tile would wait for the second's loads), any further ones in
+  // the loop, each pair's registers refilled two tiles ahead.
+  constexpr int NW = kGqaWaves;
+  if (w < ntile) process(k0, v0, b0 + kGqaTile * w);
+  if (w + 2 * NW < ntile) {
+    k0.load(kb, b0 + kGqaTile * (w + 2 * NW), last, lane);
+    v0.load(vb, b0 + kGqaTile * (w + 2 * NW), last, lane);
+  }
+  if (w + NW < ntile) process(k1, v1, b0 + kGqaTile * (w + NW));
+  if (w + 3 * NW < ntile) {
+    k1.load(kb, b0 + kGqaTile * (w + 3 * NW), last, lane);
+    v1.load(vb, b0 + kGqaTile * (w + 3 * NW), last, lane);
+  }
+  for (int it = w + 2 * NW; it < ntile; it += 2 * NW) {
     process(k0, v0, b0 + kGqaTile * it);
-    if (it + 2 * kGqaWaves < ntile) {
-      k0.load(kb, b0 + kGqaTile * (it + 2 * kGqaWaves), last, lane);
-      v0.load(vb, b0 + kGqaTile * (it + 2 * kGqaWaves), last, lane);
+    if (it + 2 * NW < ntile) {
+      k0.load(kb, b0 + kGqaTile * (it + 2 * NW), last, lane);
+      v0.load(vb, b0 + kGqaTile * (it + 2 * NW), last, lane);
     }
-    if (it + kGqaWaves >= ntile) break;
-    process(k1, v1, b0 + kGqaTile * (it + kGqaWaves));
-    if (it + 3 * kGqaWaves < ntile) {
-      k1.load(kb, b0 + kGqaTile * (it + 3 * kGqaWaves), last, lane);
-      v1.load(vb, b0 + kGqaTile * (it + 3 * kGqaWaves), last, lane);
+    if (it + NW >= ntile) break;
+    process(k1, v1, b0 + kGqaTile * (it + NW));
+    if (it + 3 * NW < ntile) {
+      k1.load(kb, b0 + kGqaTile * (it + 3 * NW), last, lane);
+      v1.load(vb, b0 + kGqaTile * (it + 3 * NW), last, lane);
     }
   }
 
@@ -343,7 +361,7 @@ __global__ __launch_bounds__(64 * kGqaWaves) void gqa_attn_kernel(AttnArgs a) {
 }  // namespace
 
 bool launch_gqa_attention(const AttnArgs& a, hipStream_t st) {
-  if (a.G < 1 || a.G > 16) return false;
+  if (!gqa_attention_fits(a.G, a.D)) return false;
   const dim3 grid((unsigned)(a.Hkv * a.nsplit)), block(64 * kGqaWaves);
   if (a.D == 64) hipLaunchKernelGGL(gqa_attn_kernel<64>, grid, block, 0, st, a);
   else if (a.D == 128) hipLaunchKernelGGL(gqa_attn_kernel<128>, grid, block, 0, st, a);

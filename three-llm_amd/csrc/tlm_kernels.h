@@ -11,6 +11,10 @@ constexpr int kMaxPart = 8;    // partial vectors a consumer folds in with one r
 constexpr int kAttnWaves = 4;  // decode attention: waves per block, each a quarter of the block's chunk
 constexpr int kGqaWaves = 8;   // matrix-core decode attention (long windows): waves per block
 constexpr int kGqaTile = 32;   // its positions per wave tile
+constexpr int kGqaPro = 3;     // its q|k|v elements per thread: (G + 2) head_dim <= 3 * 64 kGqaWaves
+inline bool gqa_attention_fits(int G, int D) {
+  return (D == 64 || D == 128) && G >= 1 && G <= 16 && (G + 2) * D <= kGqaPro * 64 * kGqaWaves;
+}
 constexpr int kLongWindow = 1024; // decode attention: windows above this many positions run the long-window kernels
 // Residual stream accumulators: kRep replicas of an int64 fixed-point vector
 // (value * 2^32).  Producers add into replica (block % kRep) with device-scope

@@ -444,26 +444,40 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvArgs a) {
   core.load(a, t, c0, ncl, wave, W, nw, 0);  // weights in flight during the prologue (t < T: gridDim.x <= T)
   __builtin_amdgcn_sched_barrier(0);  // keep every load issued before the prologue's first wait
   pro.finish(a, L.xl, L.xsum, L.scratch, k0, k1, ncl * CK);
-  __syncthreads();
-  for (; t < a.T; t += gridDim.x) {
-    float acc = 0.f;
-    for (int b = 0; b < nw; b += NCH) {
-      if (b > 0 || t != (int)blockIdx.x) core.load(a, t, c0, ncl, wave, W, nw, b);
-      acc += core.compute(L.xl, L.xsum, wave, W, nw, b);
-    }
+  lds_barrier();
+  auto reduce_store = [&](int tt, float acc) {
     L.red[wave * kTile + lane] = acc;
-    __syncthreads();
+    lds_barrier();
     if (wave == 0) {
       float v = 0.f;
 #pragma unroll
       for (int w = 0; w < W; w++) v += L.red[w * kTile + lane];
-      const int row = t * kTile + lane;
+      const int row = tt * kTile + lane;
       if (row < a.N) {
         if (a.bias && s == 0) v += a.bias[row];
         a.out[(size_t)s * a.N + row] = v;
       }
     }
-    __syncthreads();
+    lds_barrier();
+  };
+  // The first tile's first batch (in flight since before the prologue) in
+  // straight-line code: each dot then waits for its own chunk only (inside
+  // the loops the compiler's waits merge over the back edges).
+  {
+    float acc = core.compute(L.xl, L.xsum, wave, W, nw, 0);
+    for (int b = NCH; b < nw; b += NCH) {
+      core.load(a, t, c0, ncl, wave, W, nw, b);
+      acc += core.compute(L.xl, L.xsum, wave, W, nw, b);
+    }
+    reduce_store(t, acc);
+  }
+  for (t += gridDim.x; t < a.T; t += gridDim.x) {
+    float acc = 0.f;
+    for (int b = 0; b < nw; b += NCH) {
+      core.load(a, t, c0, ncl, wave, W, nw, b);
+      acc += core.compute(L.xl, L.xsum, wave, W, nw, b);
+    }
+    reduce_store(t, acc);
   }
 }
 
@@ -707,15 +721,16 @@ __global__ __launch_bounds__(kMlpWaves * 64) void mlp_kernel(MlpArgs m) {
   dn.load(m, blk, wave, W, nd, nitems, 0);
   __builtin_amdgcn_sched_barrier(0);  // every load issued before the prologue's first wait
   pro.finish(a, xl, xsum, scratch, 0, a.K, C * CK, blk == 0 ? xm : nullptr);
-  __syncthreads();
+  lds_barrier();
 
-  float acc = 0.f;
-  for (int b = 0; b < nw; b += NCH) {
-    if (b > 0) core.load(a, blk, 0, C, wave, W, nw, b);
+  // first batch in straight-line code: each dot waits for its own chunk only
+  float acc = core.compute(xl, xsum, wave, W, nw, 0);
+  for (int b = NCH; b < nw; b += NCH) {
+    core.load(a, blk, 0, C, wave, W, nw, b);
     acc += core.compute(xl, xsum, wave, W, nw, b);
   }
   red[wave * kTile + lane] = acc;
-  __syncthreads();
+  lds_barrier();
   if (wave == 0) {
     float v = 0.f;
 #pragma unroll
@@ -728,11 +743,10 @@ __global__ __launch_bounds__(kMlpWaves * 64) void mlp_kernel(MlpArgs m) {
     const float hs = wave_sum(lane >= 32 ? hv : 0.f);
     if (lane == 0) h[32] = hs;
   }
-  __syncthreads();
+  lds_barrier();
 
   const float hsum = h[32];
-  for (int ib = 0; ib < nd; ib += DB) {
-    if (ib > 0) dn.load(m, blk, wave, W, nd, nitems, ib);
+  auto down_batch = [&](int ib) {
 #pragma unroll
     for (int u = 0; u < DB; u++) {
       if (ib + u < nd) {  // wave-uniform
@@ -743,6 +757,11 @@ __global__ __launch_bounds__(kMlpWaves * 64) void mlp_kernel(MlpArgs m) {
         if (n < m.H) atomicAdd(m.acc + (size_t)(blk % kRep) * m.H + n, to_fx(p));
       }
     }
+  };
+  down_batch(0);  // straight-line: its loads were issued before the prologue
+  for (int ib = DB; ib < nd; ib += DB) {
+    dn.load(m, blk, wave, W, nd, nitems, ib);
+    down_batch(ib);
   }
   if (blk == 0)
     for (int n = threadIdx.x; n < m.H; n += blockDim.x) atomicAdd(m.acc + n, to_fx(xm[n]));
