@@ -665,6 +665,12 @@ bool launch_lm_head(int fmt, int pro, int waves, int nch, dim3 grid, const GemvA
 
 // ------------------------------------------------------------------- MLP --
 
+// Row tile of a block's i-th down item: rotated by the block index, so the
+// blocks adding into one accumulator replica do not walk its rows in lockstep
+// (the fixed-point sums do not depend on the order).  Llama-3.2-3B shape at
+// 16384 positions: 1420 -> 1402 us per token; Llama-3.2-1B at 4096: 540 -> 534.
+__device__ __forceinline__ int mlp_down_tile(int i, int blk, int Td) { return (i + blk) % Td; }
+
 // Down-projection slice of one block: (tile, chunk) items over the block's 32
 // intermediate indices; item = tile * CPG + chunk, this wave's items are
 // wave, wave + W, ...  Loads are unconditional (items clamped).
@@ -679,7 +685,7 @@ struct MlpDown {
 #pragma unroll
     for (int u = 0; u < DB; u++) {
       const int item = min(wave + min(ib + u, max(nd, 1) - 1) * W, nitems - 1);
-      const int td = item / CPG, c = min(blk * CPG + item % CPG, m.Cd - 1);
+      const int td = mlp_down_tile(item / CPG, blk, m.Td), c = min(blk * CPG + item % CPG, m.Cd - 1);
       const size_t at = ((size_t)td * m.Cd + c) * kTile + lane;
       d[u] = m.wd[at];
       if (FMT == WF_Q4) sc[u] = m.sd[at];
@@ -751,7 +757,7 @@ __global__ __launch_bounds__(kMlpWaves * 64) void mlp_kernel(MlpArgs m) {
     for (int u = 0; u < DB; u++) {
       if (ib + u < nd) {  // wave-uniform
         const int item = wave + (ib + u) * W;
-        const int td = item / Down::CPG, cc = item % Down::CPG;
+        const int td = mlp_down_tile(item / Down::CPG, blk, m.Td), cc = item % Down::CPG;
         const float p = FMT == WF_Q4 ? dot_q4(dn.d[u], h, hsum, h2f(dn.sc[u])) : dot_f16(dn.d[u], h + cc * CK);
         const int n = td * kTile + lane;
         if (n < m.H) atomicAdd(m.acc + (size_t)(blk % kRep) * m.H + n, to_fx(p));
