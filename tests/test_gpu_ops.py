@@ -192,7 +192,12 @@ def test_attention_window_of_one_returns_the_current_value_row(ctx, kv_fmt):
     # long windows of the grouped kernel: 7 query heads per kv head (8-head
     # variant), one (multi-head attention), and head_dim 128 with a window
     (14, 2, 64, 1e6, 1100, 0, tlm.FMT_F16), (8, 8, 128, 5e5, 1100, 0, tlm.FMT_F16),
-    (6, 2, 128, 1e4, 1300, 1100, tlm.FMT_F16)])
+    (6, 2, 128, 1e4, 1300, 1100, tlm.FMT_F16),
+    # the matrix-core kernel's edges: 16 query heads on one kv head (every
+    # padded head column used), (G + 2) head_dim = 1536 exactly (three q|k|v
+    # elements per thread), and one group past that (the per-head kernel)
+    (16, 1, 64, 1e4, 1060, 0, tlm.FMT_F16), (20, 2, 128, 5e5, 1060, 0, tlm.FMT_F16),
+    (22, 2, 128, 5e5, 1040, 0, tlm.FMT_F16)])
 def test_attention_long_fp16_cache(ctx, heads, kv, D, theta, steps, window, kv_fmt):
     """fp16 (and fp32) cache, split-K over many chunks: every output against
     the oracle run with the same cache rounding.  The 1100-step cases cross the
