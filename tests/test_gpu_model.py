@@ -136,7 +136,7 @@ def test_long_window_decode_with_more_than_16_chunks(ctx, monkeypatch, gqa, prom
     head than the 16 the O projection's prologue folds per round trip (its
     32-slot form): the one-head-per-block kernel (TLM_GQA=0) has 18 chunks of
     at least 32 positions at 1100 positions; the matrix-core kernel, one block
-    per kv head and chunk of at least 256 positions, has 18 at 4400.  The
+    per kv head and chunk, has 32 chunks of 138 positions at 4400.  The
     prompt runs as a batched prefill, then the logits at the next four
     positions are checked against the oracle."""
     monkeypatch.setenv("TLM_GQA", gqa)

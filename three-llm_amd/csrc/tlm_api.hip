@@ -653,15 +653,16 @@ static int attn_init(tlm_ctx* ctx, const tlm_attn_desc* d, tlm_attn* A, bool own
   A->chmin_long = A->chmin;
   // Long windows with an fp16 cache, head_dim 64 / 128 and (G + 2) head_dim
   // <= 1536: the matrix-core kernel, one block per (kv head, chunk) for all G
-  // query heads; about one
-  // block per CU, chunks of at least one 32-position tile per wave, and at
-  // most 32 chunks (the O projection's combine folds 32 in one round trip).
+  // query heads; about one block per CU, chunks of at least four 32-position
+  // tiles (128 against 256 positions: Llama-3.2-1B at 4096, 32 blocks per kv
+  // head instead of 17, 1870 -> 1879 tok/s; 64: no better), and at most 32
+  // chunks (the O projection's combine folds 32 in one round trip).
   // TLM_GQA=0 keeps the one-head-per-block kernel (comparisons).
   const char* gq = getenv("TLM_GQA");
   A->gqa = d->kv_fmt == TLM_FMT_F16 && gqa_attention_fits(A->G, d->head_dim) && !(gq && gq[0] == '0');
   if (A->gqa) {
     A->nsplit_long = std::max(1, std::min(32, ctx->cus / d->kv_heads));
-    A->chmin_long = kGqaWaves * kGqaTile;
+    A->chmin_long = 4 * kGqaTile;
   }
   const int D = d->head_dim;
   const size_t esz = d->kv_fmt == TLM_FMT_F32 ? 4 : 2;
