@@ -162,6 +162,30 @@ def test_long_window_decode_with_more_than_16_chunks(ctx, monkeypatch, gqa, prom
     om.close()
 
 
+def test_qwen_shape_with_bias_past_1024_positions(ctx):
+    """Two layers of the Qwen2.5-0.5B shape (QKV bias, 7 query heads per kv
+    head, head_dim 64) over a 1100-id prompt (batched prefill), then three
+    decode steps in the long-window mode, where the matrix-core attention adds
+    the bias to the QKV partials: logits against the oracle at 2e-2 / 1e-2."""
+    wl = W.WORKLOADS["qwen2.5-0.5b"]
+    cfg = dict(wl.config, num_hidden_layers=2)
+    wl = W.Workload(wl.name + "-2l-long", cfg, wl.storage, 1103, 1, 1200, qkv_bias=True)
+    hw = W.synthetic(wl)
+    hw.keep = True
+    runner = R.DecoderHIPRunner(hw, {"maxTokens": wl.max_tokens}, ctx=ctx)
+    assert "long=mfma" in runner.model.describe()
+    om = oracle_model(hw, wl.max_tokens, kv_f16=True, threads=16)
+    prompt = [int(x) for x in W.prompt_tokens(wl)]
+    runner.prefillTokens(prompt[:1100], 0, 1100)
+    for i in range(1100):
+        om.prefill(prompt[i], i)
+    for i in range(1100, 1103):
+        runner.computeToken(prompt[i], i, True)
+        close(runner.readLogits(), om.forward(prompt[i], i), LOGIT_ATOL, LOGIT_RTOL)
+    runner.close()
+    om.close()
+
+
 def _reduced_qwen(layers):
     wl = W.WORKLOADS["qwen2.5-0.5b"]
     cfg = dict(wl.config, num_hidden_layers=layers)

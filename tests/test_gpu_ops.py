@@ -226,6 +226,31 @@ def test_attention_long_fp16_cache(ctx, heads, kv, D, theta, steps, window, kv_f
     A.close()
 
 
+def test_attention_long_window_partial_rotary(ctx):
+    """Partial rotary (32 of 64 dims rotated) past the 1024-position window,
+    where the matrix-core kernel rotates q and the new k in its prologue and
+    passes the other 32 dims through: every output against the oracle with the
+    same fp16 cache rounding, and the appended rows read back."""
+    heads, kv, D, rd, steps = 8, 2, 64, 32, 1060
+    rng = np.random.default_rng(3207)
+    inv, af = orc.rope_parameters(rd, 1e4)
+    M = steps + 8
+    A = tlm.Attention(ctx, heads, kv, D, M, inv, rotary_dim=rd, attention_factor=af, kv_fmt=tlm.FMT_F16)
+    kc = np.zeros((M, kv * D), np.float32)
+    vc = np.zeros_like(kc)
+    out = ctx.buffer(4 * heads * D)
+    for pos in range(steps):
+        qkv = f32(rng.standard_normal((heads + 2 * kv) * D))
+        got = A(ctx.array(qkv), pos, out).read()
+        ref = orc.attention(qkv, heads, kv, D, pos, kc, vc, inv, rotary_dim=rd, attention_factor=af, kv_f16=True)
+        if pos >= 1024 or pos % 128 == 0:
+            close(got, ref, 2e-3, 2e-3)
+    k, v = A.read_cache(steps)
+    close(v, vc[:steps], 0, 0)
+    close(k, kc[:steps], 1e-3, 1e-3)
+    A.close()
+
+
 def test_attention_decode_after_16384_positions(ctx):
     """The Llama-3.2-3B decode case (24/8 heads, head_dim 128, theta 5e5, fp16
     cache) at its real window: positions 0..16383 are appended by the batched
