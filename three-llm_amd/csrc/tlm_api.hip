@@ -1191,12 +1191,13 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
       rc = fail(TLM_ERR_INVALID, "TLMModel: hidden size %d too large for the fused MLP block", H);
     m->lm_plan = plan_gemv(m->head->T, m->head->C, ctx->cus, chunk_k(m->head->fmt), true);
     m->lm_plan.gx = lm_head_grid(m->head->T, ctx->cus);
-    {  // a wave's whole row slice in flight at once when it is at most 16
-      // chunks (Qwen2.5-0.5B: 14); longer slices in batches of 4 (Llama-3.2-1B,
-      // 32 chunks: 91.1 -> 83.1 us per launch against batches of 16, 87.3 at 8;
-      // Llama-3.2-3B, 48 chunks: 120 us at 4, 8 or 16)
+    {  // a wave's row slice in batches of 4 chunks: a wave that issues more
+      // loads than the memory pipeline takes stalls at issue.  Per launch
+      // against the whole slice in one batch: Llama-3.2-1B (32 chunks, batches
+      // of 16) 91.1 -> 83.1 us, 87.3 at 8; Qwen2.5-0.5B (14 chunks) 44.3 ->
+      // 43.4-43.7 us; Llama-3.2-3B (48 chunks) 120 us at 4, 8 or 16
       const int per = (m->head->C + m->lm_plan.waves - 1) / m->lm_plan.waves;
-      m->lm_plan.nch = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : per <= 16 ? 16 : 4;
+      m->lm_plan.nch = per <= 1 ? 1 : per <= 2 ? 2 : 4;
     }
     if (gemv_smem_bytes(wfmt(m->head->fmt), m->lm_plan.cps, m->lm_plan.waves) > 65536)
       rc = fail(TLM_ERR_INVALID, "TLMModel: hidden size %d too large for one LM head block", H);
