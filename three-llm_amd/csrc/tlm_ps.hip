@@ -357,6 +357,10 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
   constexpr int EPL = DT / 64;
   constexpr int KW = DL * ESZ / 4;
   constexpr bool PAIRD = ESZ == 2 && DT == 128;
+  // fp16 rows of 64: lane holds dims 2 (lane % 32), + 1 and sums half
+  // lane / 32 of each pass's positions
+  constexpr bool PAIR64 = ESZ == 2 && DT == 64;
+  constexpr int NOE = PAIR64 ? 2 : EPL;
   constexpr int WF = ps_wave_floats<KT, DT>();
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const TLM_GLOBAL PsLayer& Ly = gl(a.layers)[l];
@@ -380,9 +384,9 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
   const int tc0 = active ? t0 : first, tc1 = active ? t1 : first + 1;  // in-range rows for idle waves
   ld.issue(kh, vh, tc0, tc1, pl, part, DT, DT * ESZ, lane);
   if (wave == 0) ps_stamp(a, l, PS_ATT, 0);
-  float m = -INFINITY, lsum = 0.f, o[EPL];
+  float m = -INFINITY, lsum = 0.f, o[NOE];
 #pragma unroll
-  for (int e = 0; e < EPL; e++) o[e] = 0.f;
+  for (int e = 0; e < NOE; e++) o[e] = 0.f;
   bool ok = true;
   if (active) {
     const u64* pq = a.pub_qkv + (size_t)l * a.kq * a.Nqkv;
@@ -495,6 +499,28 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
           }
           o[0] = a0;
           o[1] = a1;
+        } else if constexpr (PAIR64) {
+          // batches of 8 rows, their LDS reads issued together: one wait
+          // per batch rather than one per row
+          const int hh = lane >> 5;
+          float a0 = hh == 0 ? o[0] * corr : 0.f, a1 = hh == 0 ? o[1] * corr : 0.f;
+          const float4* p4 = reinterpret_cast<const float4*>(p_l + hh * (SUB / 2));
+          const uint32_t* vw = reinterpret_cast<const uint32_t*>(vt + (size_t)hh * (SUB / 2) * DT) + (lane & 31);
+#pragma unroll
+          for (int g = 0; g < SUB / 2; g += 8) {
+            const float4 pa = p4[g / 4], pb = p4[g / 4 + 1];
+            uint32_t w[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) w[u] = vw[(size_t)(g + u) * (DT / 2)];
+            const float pu[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+              a0 = fmaf(pu[u], h2f(w[u] & 0xFFFFu), a0);
+              a1 = fmaf(pu[u], h2f(w[u] >> 16), a1);
+            }
+          }
+          o[0] = a0 + __shfl_xor(a0, 32, 64);
+          o[1] = a1 + __shfl_xor(a1, 32, 64);
         } else {
 #pragma unroll
           for (int e = 0; e < EPL; e++) {
@@ -511,8 +537,15 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
   }
   // merge the waves in order (an idle wave contributes max -inf, sum 0)
   float* mine = mg + wave * (2 + DT);
+  if constexpr (PAIR64) {
+    if (lane < 32) {
+      mine[2 + 2 * lane] = o[0];
+      mine[3 + 2 * lane] = o[1];
+    }
+  } else {
 #pragma unroll
-  for (int e = 0; e < EPL; e++) mine[2 + (PAIRD ? 2 * lane + e : lane + 64 * e)] = o[e];
+    for (int e = 0; e < EPL; e++) mine[2 + (PAIRD ? 2 * lane + e : lane + 64 * e)] = o[e];
+  }
   if (lane == 0) {
     mine[0] = m;
     mine[1] = lsum;
