@@ -342,11 +342,12 @@ constexpr int ps_wave_floats() {
 }
 
 // Item h: query head h over the window [first, pos].  Wave w takes the
-// contiguous positions [first + w per, + per) (per: a multiple of the pass
-// length); its first pass of cached K/V rows is requested before it polls
-// q (and, in the wave whose range holds pos, the new k and v): the sums of
-// the kq published partials, read by every active wave itself.  The row at
-// pos comes from those k and v (this token's cache write is not ordered
+// contiguous cached positions [first + w per, + per) below pos (per: a
+// multiple of the pass length); its first pass of K/V rows is requested
+// before it polls q: the sum of the kq published partials, read by every
+// active wave itself.  The last wave also takes the row at pos, after its
+// range: it polls the new k and v as well, appends them to the cache and
+// adds their score to its softmax (this token's cache write is not ordered
 // before the cache reads).  The 16 waves merge (max, sum, output) in LDS in
 // wave order.
 template <typename KT, int DT>
@@ -365,11 +366,11 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const TLM_GLOBAL PsLayer& Ly = gl(a.layers)[l];
   const int hk = h / a.G;
-  const int n = pos - first + 1;
+  const int n = pos - first;  // cached rows
   const int per = max(SUB, ((n + kPsWaves - 1) / kPsWaves + SUB - 1) / SUB * SUB);
-  const int t0 = min(first + wave * per, pos + 1), t1 = min(t0 + per, pos + 1);
+  const int t0 = min(first + wave * per, pos), t1 = min(t0 + per, pos);
   const bool active = t0 < t1;
-  const bool own = active && pos < t1;  // this wave's range holds pos
+  const bool own = wave == kPsWaves - 1;  // this wave takes the row at pos
   float* q_l = sm + wave * WF;
   float* kn = q_l + DT;
   float* vn = kn + DT;
@@ -388,7 +389,7 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
 #pragma unroll
   for (int e = 0; e < NOE; e++) o[e] = 0.f;
   bool ok = true;
-  if (active) {
+  if (active || own) {
     const u64* pq = a.pub_qkv + (size_t)l * a.kq * a.Nqkv;
     PsSpin spin(a.timeout);
     for (;;) {  // lane d: element d (+ 64 e) of q and, in the own wave, of k and v
@@ -441,7 +442,7 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
       }
     }
     if (wave == 0) ps_stamp(a, l, PS_ATT, 1);
-    if (ok) {
+    if (ok && active) {
       wave_lds_sync();
       const float* qp = q_l + part * DL;  // this lane's q slice (LDS broadcast reads)
       for (int tb = t0; tb < t1; tb += SUB) {
@@ -449,23 +450,10 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
         for (int j = 0; j < 4; j++) reinterpret_cast<uint4*>(vt)[j * 64 + lane] = ld.vs[j];
         const int t = tb + pl;
         const bool valid = t < t1;
-        uint32_t kw[KW];  // this lane's K slice; the row at pos is the published (cache-rounded) k
+        uint32_t kw[KW];  // this lane's K slice
 #pragma unroll
         for (int j = 0; j < KW; j++) kw[j] = ld.kw[j];
-        if (own && t == pos) {
-#pragma unroll
-          for (int j = 0; j < KW; j++) {
-            if (ESZ == 2) {
-              const KT lo = kv_store<KT>(kn[part * DL + 2 * j]), hi = kv_store<KT>(kn[part * DL + 2 * j + 1]);
-              kw[j] = (uint32_t)lo | ((uint32_t)hi << 16);
-            } else {
-              kw[j] = __float_as_uint(kn[part * DL + j]);
-            }
-          }
-        }
         wave_lds_sync();
-        if (own && pos >= tb && pos < tb + SUB)
-          for (int d = lane; d < DT; d += 64) vt[(size_t)(pos - tb) * DT + d] = kv_store<KT>(vn[d]);
         if (tb + SUB < t1) ld.issue(kh, vh, tb + SUB, t1, pl, part, DT, DT * ESZ, lane);
         float s = 0.f;
 #pragma unroll
@@ -532,6 +520,23 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
           }
         }
         wave_lds_sync();
+      }
+    }
+    if (ok && own) {  // the row at pos: q · k over the wave, then one softmax step
+      wave_lds_sync();
+      float sp = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; e++) sp = fmaf(q_l[lane + 64 * e], kn[lane + 64 * e], sp);
+      const float sc = wave_sum(sp) * a.scale;
+      const float mn = fmaxf(m, sc);
+      const float corr = m == -INFINITY ? 0.f : __expf(m - mn);
+      const float p = __expf(sc - mn);
+      lsum = lsum * corr + p;
+      m = mn;
+#pragma unroll
+      for (int e = 0; e < NOE; e++) {
+        const int d = PAIR64 ? 2 * (lane & 31) + e : PAIRD ? 2 * lane + e : lane + 64 * e;
+        o[e] = fmaf(p, vn[d], o[e] * corr);
       }
     }
   }
