@@ -115,6 +115,43 @@ def test_trace_orders_every_stage(ctx):
     ps.close()
 
 
+def test_persistent_attention_across_the_wave_ranges(ctx):
+    """Every window length the persistent attention item splits differently,
+    up to its last one (1024 positions): its 16 waves take 32-position ranges
+    of the cached rows up to 512 positions and 64-position ranges after that,
+    and the last wave also takes the row at pos (alone while its range is
+    empty, after its range from 481 cached rows on).  The tiny decoder runs
+    1024 positions token by token through the persistent schedule and the
+    per-stage graph; logits are compared at the boundaries of those splits
+    (and against the oracle, which runs every position), and the appended
+    cache rows at the end."""
+    wl = _workload("tiny", 2, 1024)
+    hw = W.synthetic(wl)
+    hw.keep = True
+    ps = _runner(hw, ctx, 1024, True)
+    ref = _runner(hw, ctx, 1024, False)
+    assert re.search(r"persistent\[\d+ blocks", ps.model.describe())
+    om = oracle_model(hw, 1024, kv_f16=True, threads=16)
+    rng = np.random.default_rng(7)
+    toks = [int(t) for t in rng.integers(0, wl.config["vocab_size"], 1024)]
+    check = {0, 1, 31, 32, 33, 479, 480, 481, 482, 496, 511, 512, 513, 514, 700, 993, 1022, 1023}
+    for i, t in enumerate(toks):
+        ps.computeToken(t, i, i in check)
+        ref.computeToken(t, i, i in check)
+        if i in check:
+            got = ps.readLogits()
+            close(got, ref.readLogits(), 2e-3, 1e-3)
+            close(got, om.forward(t, i), LOGIT_ATOL, LOGIT_RTOL)
+        else:
+            om.prefill(t, i)
+    for l in range(wl.config["num_hidden_layers"]):
+        for a, b in zip(ps.model.kv_read(l, 0, 1024), ref.model.kv_read(l, 0, 1024)):
+            close(a.view(np.float16).astype(np.float32), b.view(np.float16).astype(np.float32), 2e-3, 1e-3)
+    ps.close()
+    ref.close()
+    om.close()
+
+
 @pytest.mark.parametrize("window,rotary", [(32, 64), (48, 32)])
 def test_persistent_sliding_window_and_partial_rotary(ctx, window, rotary):
     """The tiny decoder with a sliding window (positions past it leave the
