@@ -552,10 +552,11 @@ __device__ __forceinline__ void stage_embedding(const EmbStage& es, int token) {
 
 // The persistent schedule's token number advances once its token is done
 // (never 0: zeroed words never match).
-__device__ __forceinline__ void ps_next_token(int* ctrl) {
-  const unsigned seq = (unsigned)ctrl[C_SEQ] + 1u;
-  ctrl[C_SEQ] = (int)(seq ? seq : 1u);
+__device__ __forceinline__ int ps_next_seq(int cur) {
+  const unsigned seq = (unsigned)cur + 1u;
+  return (int)(seq ? seq : 1u);
 }
+__device__ __forceinline__ void ps_next_token(int* ctrl) { ctrl[C_SEQ] = ps_next_seq(ctrl[C_SEQ]); }
 
 __global__ __launch_bounds__(1024) void argmax_merge_kernel(const float* pval, const int* pidx, int n, int* ctrl,
                                                             int* tokens_out, int advance, int max_steps,
@@ -564,6 +565,14 @@ __global__ __launch_bounds__(1024) void argmax_merge_kernel(const float* pval, c
   __shared__ int si[16];
   __shared__ int tok_s;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  // the control words this block updates, requested with the partials (no
+  // other kernel of the step writes them)
+  int step = 0, posv = 0, seqv = 0;
+  if (threadIdx.x == 0) {
+    step = ctrl[C_STEP];
+    posv = ctrl[C_POS];
+    seqv = ctrl[C_SEQ];
+  }
   float bv = kLowest;
   int bi = 0x7fffffff;
   for (int i = threadIdx.x; i < n; i += blockDim.x)
@@ -585,16 +594,13 @@ __global__ __launch_bounds__(1024) void argmax_merge_kernel(const float* pval, c
       }
     // the merge starts from (LOWEST, 0): nothing above LOWEST -> token 0
     const int token = bv > kLowest ? bi : 0;
-    if (tokens_out) {
-      const int step = ctrl[C_STEP];
-      if (step >= 0 && step < max_steps) tokens_out[step] = token;
-    }
+    if (tokens_out && step >= 0 && step < max_steps) tokens_out[step] = token;
     ctrl[C_TOKEN] = token;
     if (advance) {
-      ctrl[C_POS] += 1;
-      ctrl[C_STEP] += 1;
+      ctrl[C_POS] = posv + 1;
+      ctrl[C_STEP] = step + 1;
     }
-    if (ps) ps_next_token(ctrl);
+    if (ps) ctrl[C_SEQ] = ps_next_seq(seqv);
     tok_s = token;
   }
   __syncthreads();
