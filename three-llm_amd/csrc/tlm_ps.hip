@@ -602,8 +602,10 @@ __device__ __forceinline__ bool ps_o(const PsArgs& a, int l, int i, int token, u
   float x[NO], one[NO];
 #pragma unroll
   for (int u = 0; u < NO; u++) one[u] = 1.f;
-  const u64* po = a.pub_o + (size_t)l * a.QS;
-  bool ok = wl_gather<CK, NO>(c0, c1, 1, seq, [&](int, int k) { return po + k; }, wave, x, a.timeout);
+  // the residual rows first: they were published before this layer's QKV
+  // stage, so their wait ends while the attention outputs are still on the
+  // way (after the gather it would add a round trip to this item)
+  bool ok = true;
   float xr = 0.f;
   if (wave == 0 && j == 0) {
     if (l == 0) {
@@ -612,9 +614,11 @@ __device__ __forceinline__ bool ps_o(const PsArgs& a, int l, int i, int token, u
                      : h2f(gl(reinterpret_cast<const uint16_t*>(a.emb))[k]);
     } else {
       const u64* px = a.pub_x + (size_t)(l - 1) * kPsMaxKs * H + min(row, H - 1);
-      ok &= wl_rows(a.ks, seq, [&](int p) { return px + (size_t)p * H; }, xr, a.timeout);
+      ok = wl_rows(a.ks, seq, [&](int p) { return px + (size_t)p * H; }, xr, a.timeout);
     }
   }
+  const u64* po = a.pub_o + (size_t)l * a.QS;
+  ok &= wl_gather<CK, NO>(c0, c1, 1, seq, [&](int, int k) { return po + k; }, wave, x, a.timeout);
   if (wave == 0) ps_stamp(a, l, PS_O, 1);
   float xs[NO], ss;
   wl_stage<CK, NO>(x, one, s.xw, xs, ss);
@@ -688,12 +692,15 @@ __device__ __forceinline__ bool ps_down(const PsArgs& a, int l, int t, int sp, u
   float x[ND], one[ND];
 #pragma unroll
   for (int u = 0; u < ND; u++) one[u] = 1.f;
-  bool ok = wl_gather<CK, ND>(c0, c1, 1, seq, [&](int, int k) { return ph + k; }, wave, x, a.timeout);
+  // x_mid first: published before the gate|up stage, so its wait ends while
+  // h is still on the way
+  bool ok = true;
   float xm = 0.f;
   if (wave == 0 && sp == 0) {
     const u64* pm = a.pub_xm + (size_t)l * a.ko * H + min(row, H - 1);
-    ok &= wl_rows(a.ko, seq, [&](int p) { return pm + (size_t)p * H; }, xm, a.timeout);
+    ok = wl_rows(a.ko, seq, [&](int p) { return pm + (size_t)p * H; }, xm, a.timeout);
   }
+  ok &= wl_gather<CK, ND>(c0, c1, 1, seq, [&](int, int k) { return ph + k; }, wave, x, a.timeout);
   if (wave == 0) ps_stamp(a, l, PS_DOWN, 1);
   float xs[ND], ss;
   wl_stage<CK, ND>(x, one, s.xw, xs, ss);
