@@ -64,6 +64,13 @@ __device__ __forceinline__ void ps_stamp(const PsArgs& a, int l, int stage, int 
 
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
+// v of lane l ^ 32 (the other half of the wave), through the VALU lane swap
+// of gfx950 rather than an LDS round trip.
+__device__ __forceinline__ float lane_swap32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
 // ------------------------------------------------------- wave-level inputs --
 // A linear stage's wave owns input chunks cbase + wave + 16 u (u < NU) and
 // reads just their CK elements: no block barrier before its dot products.
@@ -318,15 +325,21 @@ __device__ __forceinline__ bool ps_qkv(const PsArgs& a, int l, int i, int pos, i
   if (wave == 0) {
     ps_stamp(a, l, PS_QKV, 2);
     const float inv = rsqrtf(ps_sum16(s.ssw, 1) / (float)a.H + a.eps);
+    if (NT == 1 && half == 32) {  // the rotation partner of lane d is lane d ^ 32
+      const float val = bias[0] + inv * ps_sum16(s.red + lane, 64), partner = lane_swap32(val);
+      const float y = kind < 2 ? val * rc[0] + (lane < 32 ? -partner : partner) * rs[0] : val;
+      st_dev(a.pub_qkv + ((size_t)l * a.kq + j) * a.Nqkv + r0 + lane, word(y, seq));
+    } else {
 #pragma unroll
-    for (int t = 0; t < NT; t++) s.out[64 * t + lane] = bias[t] + inv * ps_sum16(s.red + t * 64 + lane, NT * 64);
-    wave_lds_sync();
+      for (int t = 0; t < NT; t++) s.out[64 * t + lane] = bias[t] + inv * ps_sum16(s.red + t * 64 + lane, NT * 64);
+      wave_lds_sync();
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-      const int d = 64 * t + lane;
-      float val = s.out[d];
-      if (kind < 2 && d < a.rd) val = val * rc[t] + (d < half ? -s.out[d + half] : s.out[d - half]) * rs[t];
-      st_dev(a.pub_qkv + ((size_t)l * a.kq + j) * a.Nqkv + r0 + d, word(val, seq));
+      for (int t = 0; t < NT; t++) {
+        const int d = 64 * t + lane;
+        float val = s.out[d];
+        if (kind < 2 && d < a.rd) val = val * rc[t] + (d < half ? -s.out[d + half] : s.out[d - half]) * rs[t];
+        st_dev(a.pub_qkv + ((size_t)l * a.kq + j) * a.Nqkv + r0 + d, word(val, seq));
+      }
     }
     ps_stamp(a, l, PS_QKV, 3);
   }
@@ -665,7 +678,7 @@ __device__ __forceinline__ bool ps_gu(const PsArgs& a, int l, int g, unsigned se
   if (wave < MW && g * MW + wave < a.Tgu) {  // wave u finishes tile g mw + u
     const float inv = rsqrtf(ps_sum16(s.ssw, 1) / (float)H + a.eps);
     const float v = inv * ps_sum16(s.red + wave * 64 + lane, MW * 64);
-    const float us = __shfl_xor(v, 32, 64);      // lanes < 32: gate; their up rows sit in lanes + 32
+    const float us = lane_swap32(v);  // lanes < 32: gate; their up rows sit in lanes + 32
     const float hv = v / (1.f + __expf(-v)) * us;  // TSLSiLUMul.ts:15-29
     if (lane < 32) st_dev(a.pub_h + (size_t)l * a.Tgu * 32 + (g * MW + wave) * 32 + lane, word(hv, seq));
   }
