@@ -114,7 +114,7 @@ __device__ __forceinline__ bool wl_gather(int cbase, int cend, int np, unsigned 
   for (int u = 0; u < NU; u++) {
     if (CK <= 8) x[u] += __shfl_xor(x[u], 8, 64);
     if (CK <= 16) x[u] += __shfl_xor(x[u], 16, 64);
-    x[u] += __shfl_xor(x[u], 32, 64);
+    x[u] += lane_swap32(x[u]);
   }
   return true;
 }
@@ -520,8 +520,8 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
               a1 = fmaf(pu[u], h2f(w[u] >> 16), a1);
             }
           }
-          o[0] = a0 + __shfl_xor(a0, 32, 64);
-          o[1] = a1 + __shfl_xor(a1, 32, 64);
+          o[0] = a0 + lane_swap32(a0);
+          o[1] = a1 + lane_swap32(a1);
         } else {
 #pragma unroll
           for (int e = 0; e < EPL; e++) {
