@@ -61,6 +61,17 @@ __device__ __forceinline__ float sum8(float v) {
   return v + dpp<kDppHalfMirror>(v);
 }
 
+// v of lane l ^ 16 / l ^ 32, through gfx950's VALU lane swaps
+// (v_permlane16_swap / v_permlane32_swap) rather than an LDS round trip.
+__device__ __forceinline__ float lane_swap16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_swap32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
 // Sum / max over the 64 lanes of a wave (wave-uniform result).
 __device__ __forceinline__ float wave_sum(float v) {
   v = sum8(v);

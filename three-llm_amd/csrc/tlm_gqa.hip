@@ -256,8 +256,8 @@ __global__ __launch_bounds__(64 * kGqaWaves) void gqa_attn_kernel(AttnArgs a) {
     float mx = sv[0];
 #pragma unroll
     for (int e = 1; e < 8; e++) mx = fmaxf(mx, sv[e]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = fmaxf(mx, lane_swap16(mx));
+    mx = fmaxf(mx, lane_swap32(mx));
     const float mn = fmaxf(mrun, mx);  // finite: the tile holds a position of the chunk
     const float corr = __builtin_amdgcn_exp2f(mrun - mn);
     float ps = 0.f;
@@ -324,8 +324,8 @@ __global__ __launch_bounds__(64 * kGqaWaves) void gqa_attn_kernel(AttnArgs a) {
   }
 
   // merge the waves' (max, sum, output) per head; every wave takes part
-  lrun += __shfl_xor(lrun, 16, 64);
-  lrun += __shfl_xor(lrun, 32, 64);
+  lrun += lane_swap16(lrun);
+  lrun += lane_swap32(lrun);
   wave_lds_sync();
   float* const mine = reinterpret_cast<float*>(vt);  // [G][2 + DT]
   if (i16 < G) {

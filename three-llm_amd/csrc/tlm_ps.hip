@@ -64,12 +64,6 @@ __device__ __forceinline__ void ps_stamp(const PsArgs& a, int l, int stage, int 
 
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
-// v of lane l ^ 32 (the other half of the wave), through the VALU lane swap
-// of gfx950 rather than an LDS round trip.
-__device__ __forceinline__ float lane_swap32(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
-}
 
 // ------------------------------------------------------- wave-level inputs --
 // A linear stage's wave owns input chunks cbase + wave + 16 u (u < NU) and
