@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TLM_ABI_VERSION 2
+#define TLM_ABI_VERSION 3
 
 enum {
   TLM_OK = 0,
@@ -297,6 +297,9 @@ typedef struct tlm_model_counts {
   uint64_t kernel_launches;
   uint64_t prefill_chunks;      /* batched row chunks run (replayed ones excluded) */
   uint64_t replayed_positions;  /* prompt positions run through the decode graph */
+  uint64_t recomputed_positions; /* positions recomputed on the per-stage graph after a failed
+                                    token of the persistent schedule (a wait ran out, or an
+                                    fp16 input overflow of its q4 linears) */
 } tlm_model_counts;
 int tlm_model_counts_read(tlm_model* model, tlm_model_counts* out);
 

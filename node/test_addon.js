@@ -48,7 +48,7 @@ check('every entry point is bound', () => {
 });
 
 check('abiVersion is the header\'s TLM_ABI_VERSION', () => {
-  assert.strictEqual(tlm.abiVersion(), 2);
+  assert.strictEqual(tlm.abiVersion(), 3);
 });
 
 check('f32ToF16 rounds to nearest even, saturates to inf, keeps signed zero', () => {

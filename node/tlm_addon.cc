@@ -492,8 +492,9 @@ napi_value ReadToken(napi_env env, napi_callback_info info) {
   return num(env, t);
 }
 
-// {graphLaunches, kernelLaunches, prefillChunks, replayedPositions}: the
-// submission counts of the model (tlm_model_counts_read).
+// {graphLaunches, kernelLaunches, prefillChunks, replayedPositions,
+// recomputedPositions}: the submission counts of the model
+// (tlm_model_counts_read).
 napi_value ModelCounts(napi_env env, napi_callback_info info) {
   Args a(env, info);
   tlm_model* m = model_arg(env, a.v[0]);
@@ -504,7 +505,8 @@ napi_value ModelCounts(napi_env env, napi_callback_info info) {
   const std::pair<const char*, uint64_t> fields[] = {{"graphLaunches", c.graph_launches},
                                                      {"kernelLaunches", c.kernel_launches},
                                                      {"prefillChunks", c.prefill_chunks},
-                                                     {"replayedPositions", c.replayed_positions}};
+                                                     {"replayedPositions", c.replayed_positions},
+                                                     {"recomputedPositions", c.recomputed_positions}};
   for (const auto& f : fields) {
     napi_value v;
     napi_create_double(env, (double)f.second, &v);

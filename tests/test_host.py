@@ -27,7 +27,7 @@ def test_library_exports_every_header_symbol():
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
     assert sorted(tlm.EXPORTS) == names
-    assert tlm.lib().tlm_abi_version() == 2
+    assert tlm.lib().tlm_abi_version() == 3
 
 
 def header_struct_fields(name):

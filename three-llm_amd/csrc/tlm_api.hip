@@ -147,6 +147,29 @@ struct Layer {
   void* vc = nullptr;
 };
 
+// One logged run of tokens: n positions from pos, the first with `token`;
+// device: the later tokens came from the device's argmax (a greedy run),
+// else n is 1.  logits: the run computed the LM head.
+struct RedoEntry {
+  int32_t token, pos, n;
+  bool logits, device;
+};
+constexpr size_t kRedoMax = (size_t)1 << 20;
+
+// Persistent-schedule launches of every model on one device, in the order
+// they are enqueued: each needs all of the device's CUs at once, so two of
+// them running together (two models on two streams) would each wait for
+// blocks the other holds.  While more than one model of the device has the
+// schedule, a launch waits for the device's previous one (event `ev`,
+// recorded on stream `last`).
+struct PsDevice {
+  std::mutex mu;
+  int models = 0;
+  hipEvent_t ev = nullptr;
+  hipStream_t last = nullptr;
+};
+static PsDevice g_ps_dev[kScratchDevices];
+
 struct tlm_model {
   tlm_ctx* ctx = nullptr;
   tlm_model_desc d{};
@@ -190,6 +213,7 @@ struct tlm_model {
   // token for every layer; ps_on when the model's shape has a compiled variant
   PsShape ps{};
   bool ps_on = false;
+  bool ps_registered = false;  // counted in g_ps_dev[device].models
   int ps_blocks = 0;
   size_t ps_smem = 0;
   PsLayer* ps_layers = nullptr;  // device [L]
@@ -199,6 +223,15 @@ struct tlm_model {
                      *ps_pub_h = nullptr;
   hipGraphExec_t g_ps_logits = nullptr, g_ps_prefill = nullptr;
   hipGraph_t graph_ps_logits = nullptr, graph_ps_prefill = nullptr;
+  // Tokens enqueued since the last clean check of the persistent schedule's
+  // flags, in order: a token whose wait ran out or whose last residual was
+  // not finite (fp16 input overflow) is recomputed with everything after it
+  // on the per-stage graph (ps_recover).  redo_lost: the log outgrew
+  // kRedoMax, so such a token can only be reported.
+  std::vector<RedoEntry> redo;
+  bool redo_lost = false;
+  bool ps_suspend = false;   // recomputing: every token on the per-stage graph
+  bool ps_range_off = false;  // the persistent schedule is off after an fp16 range overflow
   int host_pos = 0;  // position of the last token enqueued (selects the attention mode)
   std::vector<int> windows;  // per-layer sliding window (0: full causal)
   tlm_model_counts counts{};  // work handed to the stream (tlm_model_counts_read)
@@ -373,6 +406,42 @@ static bool launch_linear(const tlm_linear* L, int pro, const GemvArgs& a, hipSt
 
 // The host-side helpers of tlm_host.cpp report through the same message.
 int tlm_host_fail(int code, const char* msg) { return fail(code, "%s", msg); }
+
+// Counts the model in (or out of) its device's persistent-schedule launches;
+// the device's ordering event is created with the first model (device current).
+static int ps_register(tlm_model* m, bool on) {
+  if (on == m->ps_registered) return TLM_OK;
+  PsDevice& pd = g_ps_dev[m->ctx->device];
+  std::lock_guard<std::mutex> lock(pd.mu);
+  if (on && !pd.ev) HIP_TRY(hipEventCreateWithFlags(&pd.ev, hipEventDisableTiming));
+  pd.models += on ? 1 : -1;
+  m->ps_registered = on;
+  return TLM_OK;
+}
+
+// One persistent-schedule launch (enqueue(): the graph or the kernels) in the
+// device's order: while several models of the device have the schedule, it
+// waits for the previous launch of any of them and becomes the one the next
+// waits for.
+template <typename F>
+static int ps_ordered(tlm_model* m, F enqueue) {
+  PsDevice& pd = g_ps_dev[m->ctx->device];
+  hipStream_t st = m->ctx->stream;
+  std::lock_guard<std::mutex> lock(pd.mu);
+  const bool order = pd.models > 1;
+  if (order && pd.last && pd.last != st) HIP_TRY(hipStreamWaitEvent(st, pd.ev, 0));
+  const int rc = enqueue();
+  if (rc) return rc;
+  if (order) {
+    HIP_TRY(hipEventRecord(pd.ev, st));
+    pd.last = st;
+  }
+  return TLM_OK;
+}
+
+static int model_check(tlm_model* m, const int* ctrl_host = nullptr);
+static int kv_clear(tlm_model* m, int pos0, int n);
+
 
 extern "C" {
 
@@ -1093,7 +1162,7 @@ static int ps_setup(tlm_model* m) {
   if (rc) return rc;
   const PsArgs a = ps_args(m);
   HIP_TRY(hipMemcpy(m->ps_args_dev, &a, sizeof a, hipMemcpyHostToDevice));
-  return TLM_OK;
+  return ps_register(m, true);
 }
 
 int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
@@ -1222,6 +1291,7 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
 void tlm_model_destroy(tlm_model* m) {
   if (!m) return;
   hipStreamSynchronize(m->ctx->stream);
+  ps_register(m, false);
   if (m->g_ps_logits) hipGraphExecDestroy(m->g_ps_logits);
   if (m->g_ps_prefill) hipGraphExecDestroy(m->g_ps_prefill);
   if (m->graph_ps_logits) hipGraphDestroy(m->graph_ps_logits);
@@ -1422,6 +1492,7 @@ static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, hipEvent_t*
   }
   a.norm_w = m->final_norm;
   a.eps = (float)d.rms_eps;
+  a.ctrl = m->ctrl;  // fixed-point range flag of the residual it reads
   a.xnorm = m->xf;
   a.logits = m->logits;
   a.arg_val = m->arg_val;
@@ -1516,15 +1587,17 @@ static int run_token(tlm_model* m, bool logits, int pos) {
   hipStream_t st = m->ctx->stream;
   const bool lw = long_window(&m->attn, pos);
   m->host_pos = pos;
-  if (m->ps_on && !lw) {  // the persistent schedule
-    if (m->use_graphs) {
-      HIP_TRY(hipGraphLaunch(logits ? m->g_ps_logits : m->g_ps_prefill, st));
-      m->counts.graph_launches++;
+  if (m->ps_on && !m->ps_suspend && !lw) {  // the persistent schedule
+    return ps_ordered(m, [&]() -> int {
+      if (m->use_graphs) {
+        HIP_TRY(hipGraphLaunch(logits ? m->g_ps_logits : m->g_ps_prefill, st));
+        m->counts.graph_launches++;
+        return TLM_OK;
+      }
+      if (!enqueue_ps(m, st, logits ? 1 : 0)) return fail(TLM_ERR_STATE, "TLMModel: no persistent kernel variant");
+      CHECK_LAUNCH("TLMModel");
       return TLM_OK;
-    }
-    if (!enqueue_ps(m, st, logits ? 1 : 0)) return fail(TLM_ERR_STATE, "TLMModel: no persistent kernel variant");
-    CHECK_LAUNCH("TLMModel");
-    return TLM_OK;
+    });
   }
   if (m->use_graphs) {
     HIP_TRY(hipGraphLaunch(logits ? m->g_logits[lw] : m->g_prefill[lw], st));
@@ -1552,6 +1625,18 @@ static int check_token(tlm_model* m, int32_t token, int32_t position) {
   return TLM_OK;
 }
 
+// Logs a run of n tokens from (token, pos) for ps_recover (models with the
+// persistent schedule only; not while recomputing).
+static void redo_log(tlm_model* m, int32_t token, int32_t pos, int32_t n, bool logits, bool device) {
+  if (!m->ps_on || m->ps_suspend || m->redo_lost || n <= 0) return;
+  if (m->redo.size() >= kRedoMax) {
+    m->redo.clear();
+    m->redo_lost = true;
+    return;
+  }
+  m->redo.push_back(RedoEntry{token, pos, n, logits, device});
+}
+
 int tlm_compute_token(tlm_model* m, int32_t token, int32_t position, int flags) {
   if (!m) return fail(TLM_ERR_INVALID, "TLMModel: null model");
   int rc = check_token(m, token, position);
@@ -1562,6 +1647,7 @@ int tlm_compute_token(tlm_model* m, int32_t token, int32_t position, int flags) 
   launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);  // the token/position write
   m->counts.kernel_launches++;
   CHECK_LAUNCH("TLMModel");
+  redo_log(m, token, position, 1, (flags & TLM_LOGITS) != 0, false);
   return run_token(m, (flags & TLM_LOGITS) != 0, position);
 }
 
@@ -1782,6 +1868,8 @@ int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end)
   if (rc) return rc;
   hipStream_t st = m->ctx->stream;
   HIP_TRY(hipStreamSynchronize(st));
+  rc = model_check(m);  // the earlier tokens are final before batched chunks overwrite cache rows
+  if (rc) return rc;
   HIP_TRY(hipMemcpy(m->prompt, tokens + start, sizeof(int32_t) * (end - start), hipMemcpyHostToDevice));
   const bool batched = m->pf_min_rows > 0 && !prefill_unsupported(m);
   for (int p = start; p < end;) {
@@ -1800,6 +1888,8 @@ int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end)
         HIP_TRY(hipMemcpy(m->pf_ovf, &zero, sizeof(int), hipMemcpyHostToDevice));
         m->pf_replayed++;
         replay = true;
+        rc = kv_clear(m, p, n);  // the chunk's rows may hold inf or NaN
+        if (rc) return rc;
       }
       if (!replay) m->counts.prefill_chunks++;
     }
@@ -1808,6 +1898,7 @@ int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end)
       m->counts.kernel_launches++;
       m->counts.replayed_positions += n;
       CHECK_LAUNCH("TLMModel");
+      for (int i = 0; i < n; i++) redo_log(m, tokens[p + i], p + i, 1, false, false);
       for (int i = 0; i < n && !rc; i++) rc = run_token(m, false, p + i);
     }
     if (rc) return rc;
@@ -1816,42 +1907,115 @@ int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end)
   return TLM_OK;
 }
 
-// After a sync: a time-out of one of the persistent schedule's waits (every
-// wait is bounded; a late block sets ctrl[C_ERR] and leaves) makes the read fail.
-static int ps_check(tlm_model* m, const int* ctrl_host = nullptr) {
-  if (!m->ps_on) return TLM_OK;
-  int err = 0;
-  if (ctrl_host) err = ctrl_host[C_ERR];
-  else HIP_TRY(hipMemcpy(&err, m->ctrl + C_ERR, sizeof(int), hipMemcpyDeviceToHost));
-  if (!err) return TLM_OK;
-  const int zero = 0;
-  HIP_TRY(hipMemcpy(m->ctrl + C_ERR, &zero, sizeof(int), hipMemcpyHostToDevice));
-  return fail(TLM_ERR_HIP, "TLMModel: a wait of the persistent decode schedule timed out; the tokens computed "
-                           "since the last read are invalid");
+// Zeroes the cache rows [pos0, pos0 + n) of every layer before they are
+// recomputed: the per-stage attention fills the padding slots of its last V
+// tile with the row at the position (times a zero probability), so a stale
+// NaN there (a failed token, an overflowed prefill chunk) would reach it.
+static int kv_clear(tlm_model* m, int pos0, int n) {
+  n = std::min(n, m->d.max_tokens - pos0);
+  if (pos0 < 0 || n <= 0) return TLM_OK;
+  const size_t esz = m->d.kv_fmt == TLM_FMT_F32 ? 4 : 2, row = (size_t)m->d.head_dim * esz;
+  for (auto& L : m->layers)
+    for (int h = 0; h < m->d.num_kv_heads; h++) {
+      const size_t off = ((size_t)h * m->d.max_tokens + pos0) * row;
+      HIP_TRY(hipMemsetAsync((char*)L.kc + off, 0, n * row, m->ctx->stream));
+      HIP_TRY(hipMemsetAsync((char*)L.vc + off, 0, n * row, m->ctx->stream));
+    }
+  return TLM_OK;
+}
+
+// Recomputes the logged tokens on the per-stage graph after a persistent-
+// schedule token failed (err: its ctrl[C_ERR] bits), in their order, so the
+// cache rows, logits and greedy tokens are those of the per-stage kernels.
+// A token whose last residual was not finite (an input of a q4 linear
+// overflowed its fp16 copy) turns the schedule off for the model: its
+// activations reach that range.
+static int ps_recover(tlm_model* m, int err) {
+  if (m->redo_lost) {
+    m->redo_lost = false;
+    return fail(TLM_ERR_HIP, "TLMModel: a token of the persistent decode schedule %s after more than %zu tokens "
+                             "without a read; the tokens computed since the last read are invalid",
+                err & kPsErrTimeout ? "timed out" : "overflowed fp16", kRedoMax);
+  }
+  if (err & kPsErrRange) {
+    int rc = ps_register(m, false);
+    if (rc) return rc;
+    m->ps_on = false;
+    m->ps_range_off = true;
+  }
+  std::vector<RedoEntry> log;
+  log.swap(m->redo);
+  hipStream_t st = m->ctx->stream;
+  m->ps_suspend = true;
+  int rc = TLM_OK;
+  for (const RedoEntry& e : log) {
+    rc = kv_clear(m, e.pos, e.n);
+    if (rc) break;
+    launch_set_ctrl(m->ctrl, e.token, e.pos, 0, 0, 0, emb_stage(m), st);
+    m->counts.kernel_launches++;
+    for (int i = 0; i < e.n && rc == TLM_OK; i++) rc = run_token(m, e.logits, e.pos + i);
+    if (rc) break;
+    m->counts.recomputed_positions += e.n;
+  }
+  m->ps_suspend = false;
+  if (rc) return rc;
+  HIP_TRY(hipStreamSynchronize(st));
+  return TLM_OK;
+}
+
+// After a sync: the flags of the tokens since the last check.  C_FXR (a
+// residual value of the per-stage kernels left their fixed-point range): an
+// error, the results are invalid.  C_ERR (a persistent-schedule token: a
+// bounded wait ran out, the late block left; or its last residual was not
+// finite): the logged tokens are recomputed (ps_recover) before the caller
+// reads anything.  Clean: the logged tokens are final.
+static int model_check(tlm_model* m, const int* ctrl_host) {
+  int c[8];
+  if (ctrl_host) memcpy(c, ctrl_host, sizeof c);
+  else HIP_TRY(hipMemcpy(c, m->ctrl, sizeof c, hipMemcpyDeviceToHost));
+  if (m->ps_on && c[C_ERR]) {
+    const int zero = 0;
+    HIP_TRY(hipMemcpy(m->ctrl + C_ERR, &zero, sizeof(int), hipMemcpyHostToDevice));
+    if (int rc = ps_recover(m, c[C_ERR])) return rc;
+    HIP_TRY(hipMemcpy(c, m->ctrl, sizeof c, hipMemcpyDeviceToHost));
+  }
+  m->redo.clear();
+  m->redo_lost = false;
+  if (c[C_FXR]) {
+    const int zero = 0;
+    HIP_TRY(hipMemcpy(m->ctrl + C_FXR, &zero, sizeof(int), hipMemcpyHostToDevice));
+    return fail(TLM_ERR_RANGE, "TLMModel: a residual value of the per-stage kernels reached 2^30 in magnitude "
+                               "(or NaN), past their fixed-point range; the tokens computed since the last read "
+                               "are invalid");
+  }
+  return TLM_OK;
 }
 
 int tlm_read_logits(tlm_model* m, float* out, size_t n) {
   if (!m || !out || n > (size_t)m->d.vocab_size) return fail(TLM_ERR_INVALID, "TLMModel: invalid logits read");
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
-  if (int rc = ps_check(m)) return rc;
+  if (int rc = model_check(m)) return rc;
   HIP_TRY(hipMemcpy(out, m->logits, sizeof(float) * n, hipMemcpyDeviceToHost));
   return TLM_OK;
 }
 
 int tlm_read_candidates(tlm_model* m, int k, double softcap, int32_t* tokens, float* scores) {
   if (!m || !tokens || !scores) return fail(TLM_ERR_INVALID, "TLMModel: null argument");
-  int rc = tlm_op_topk(m->ctx, m->logits, m->d.vocab_size, k, softcap, m->cand_i, m->cand_v);
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  int rc = model_check(m);  // the logits are final (recomputed if a token was flagged)
+  if (rc) return rc;
+  rc = tlm_op_topk(m->ctx, m->logits, m->d.vocab_size, k, softcap, m->cand_i, m->cand_v);
   if (rc) return rc;
   HIP_TRY(hipMemcpyAsync(tokens, m->cand_i, sizeof(int32_t) * k, hipMemcpyDeviceToHost, m->ctx->stream));
   HIP_TRY(hipMemcpyAsync(scores, m->cand_v, sizeof(float) * k, hipMemcpyDeviceToHost, m->ctx->stream));
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
-  return ps_check(m);
+  return TLM_OK;
 }
 
 int tlm_read_hidden(tlm_model* m, float* out, size_t n) {
   if (!m || !out || n > (size_t)m->d.hidden_size) return fail(TLM_ERR_INVALID, "TLMModel: invalid hidden read");
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
-  if (int rc = ps_check(m)) return rc;
+  if (int rc = model_check(m)) return rc;
   HIP_TRY(hipMemcpy(out, m->xf, sizeof(float) * n, hipMemcpyDeviceToHost));
   return TLM_OK;
 }
@@ -1861,7 +2025,10 @@ int tlm_read_token(tlm_model* m, int32_t* token) {
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
   int ctrl[8];
   HIP_TRY(hipMemcpy(ctrl, m->ctrl, sizeof ctrl, hipMemcpyDeviceToHost));
-  if (int rc = ps_check(m, ctrl)) return rc;
+  const bool recompute = m->ps_on && ctrl[C_ERR];
+  if (int rc = model_check(m, ctrl)) return rc;
+  if (recompute)  // the token is now the per-stage graph's
+    HIP_TRY(hipMemcpy(ctrl, m->ctrl, sizeof ctrl, hipMemcpyDeviceToHost));
   *token = ctrl[C_TOKEN];
   return TLM_OK;
 }
@@ -1879,18 +2046,26 @@ int tlm_decode_greedy(tlm_model* m, int32_t token, int32_t position, int n, int3
   launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
   m->counts.kernel_launches++;
   CHECK_LAUNCH("TLMModel");
+  redo_log(m, token, position, n, true, true);
   for (int i = 0; i < n; i++) {
     rc = run_token(m, true, position + i);
     if (rc) return rc;
   }
   HIP_TRY(hipStreamSynchronize(st));
-  if (int rc = ps_check(m)) return rc;
+  if (int rc = model_check(m)) return rc;
   if (n > 0) HIP_TRY(hipMemcpy(out, m->tokens_out, sizeof(int32_t) * n, hipMemcpyDeviceToHost));
   return TLM_OK;
 }
 
 int tlm_reset_cache(tlm_model* m) {
   if (!m) return fail(TLM_ERR_INVALID, "TLMModel: null model");
+  {  // the tokens since the last read are discarded with the cache: so are their flags
+    HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    const int zero[2] = {0, 0};
+    HIP_TRY(hipMemcpy(m->ctrl + C_FXR, zero, sizeof zero, hipMemcpyHostToDevice));
+    m->redo.clear();
+    m->redo_lost = false;
+  }
   const size_t esz = m->d.kv_fmt == TLM_FMT_F32 ? 4 : 2;
   const size_t cache = (size_t)m->d.num_kv_heads * m->d.max_tokens * m->d.head_dim * esz;
   for (auto& L : m->layers) {
@@ -1907,6 +2082,7 @@ static int kv_copy(tlm_model* m, int layer, int pos0, int count, void* k, void* 
   const size_t esz = m->d.kv_fmt == TLM_FMT_F32 ? 4 : 2;
   const int Hkv = m->d.num_kv_heads, D = m->d.head_dim, M = m->d.max_tokens;
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  if (int rc = model_check(m)) return rc;  // the enqueued tokens' rows are final
   for (int h = 0; h < Hkv; h++) {
     // canonical rows are [t][h][d]; device rows are [h][t][d]
     HIP_TRY(hipMemcpy2D(
@@ -1933,6 +2109,8 @@ int tlm_kv_read(tlm_model* m, int layer, int pos0, int count, void* k, void* v) 
 
 int tlm_kv_fill_normal(tlm_model* m, uint64_t seed, int count) {
   if (!m || count < 0 || count > m->d.max_tokens) return fail(TLM_ERR_RANGE, "TLMModel: invalid fill count");
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  if (int rc = model_check(m)) return rc;
   for (int l = 0; l < m->d.num_layers; l++) {
     launch_kv_fill(m->layers[l].kc, m->layers[l].vc, m->d.kv_fmt == TLM_FMT_F32, 0, m->d.num_kv_heads,
                    m->d.max_tokens, m->d.head_dim, count, seed + (uint64_t)l * 0x100000000ull, m->ctx->stream);
@@ -1954,6 +2132,8 @@ int tlm_time_decode(tlm_model* m, int32_t token, int32_t position, int warmup, i
   if (rc) return rc;
   hipStream_t st = m->ctx->stream;
   launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
+  m->counts.kernel_launches++;
+  redo_log(m, token, position, warmup + n, true, true);
   for (int i = 0; i < warmup; i++) {
     rc = run_token(m, true, position + i);
     if (rc) return rc;
@@ -1974,7 +2154,7 @@ int tlm_time_decode(tlm_model* m, int32_t token, int32_t position, int warmup, i
   hipEventDestroy(e0);
   hipEventDestroy(e1);
   *ms = f;
-  return TLM_OK;
+  return model_check(m);
 }
 
 // n decode steps from (token, position) with HIP events on the model stream
@@ -1997,21 +2177,30 @@ static int time_step_parts(tlm_model* m, int32_t token, int32_t position, int n,
   std::vector<hipEvent_t> ev(4 * (size_t)n, nullptr);
   for (auto& e : ev) HIP_TRY(hipEventCreate(&e));
   launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
+  m->counts.kernel_launches++;
+  redo_log(m, token, position, n, true, true);
   bool ok = true;
   for (int i = 0; i < n && ok; i++) {
     const bool lw = long_window(&m->attn, position + i);
     const bool ps = m->ps_on && !lw;
     m->host_pos = position + i;
-    hipEventRecord(ev[4 * (size_t)i], st);
-    if (ps) {
-      ok &= launch_ps_token(m->ps, m->ps_blocks, m->ps_smem, m->ps_args_dev, st);
-    } else if (m->use_graphs) {
-      HIP_TRY(hipGraphLaunch(m->g_layers[lw], st));
-    } else {
-      for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1, lw);
-    }
-    hipEventRecord(ev[4 * (size_t)i + 1], st);
-    ok &= enqueue_head(m, st, true, &ev[4 * (size_t)i + 2], ps);
+    auto step = [&]() -> int {
+      hipEventRecord(ev[4 * (size_t)i], st);
+      if (ps) {
+        ok &= launch_ps_token(m->ps, m->ps_blocks, m->ps_smem, m->ps_args_dev, st);
+        m->counts.kernel_launches++;
+      } else if (m->use_graphs) {
+        HIP_TRY(hipGraphLaunch(m->g_layers[lw], st));
+        m->counts.graph_launches++;
+      } else {
+        for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1, lw);
+      }
+      hipEventRecord(ev[4 * (size_t)i + 1], st);
+      ok &= enqueue_head(m, st, true, &ev[4 * (size_t)i + 2], ps);
+      return TLM_OK;
+    };
+    rc = ps ? ps_ordered(m, step) : step();
+    if (rc) return rc;
   }
   if (!ok) return fail(TLM_ERR_STATE, "TLMModel: no kernel variant for a stage of this model");
   CHECK_LAUNCH("TLMModel");
@@ -2027,7 +2216,7 @@ static int time_step_parts(tlm_model* m, int32_t token, int32_t position, int n,
   for (auto& e : ev) hipEventDestroy(e);
   if (layers_ms) *layers_ms = tl / n;
   if (head_ms) *head_ms = th / n;
-  return ps_check(m);
+  return model_check(m);
 }
 
 int tlm_time_head(tlm_model* m, int32_t token, int32_t position, int n, double* avg_ms) {
@@ -2100,18 +2289,26 @@ int tlm_trace_decode(tlm_model* m, int32_t token, int32_t position, int n, uint6
   hipStream_t st = m->ctx->stream;
   bool ok = hipMemcpy(ad, &a, sizeof a, hipMemcpyHostToDevice) == hipSuccess;
   launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
+  m->counts.kernel_launches++;
+  redo_log(m, token, position, n, true, true);
   for (int i = 0; i < n && ok; i++) {
     ok &= hipMemsetAsync(tr, 0, need * sizeof(unsigned long long), st) == hipSuccess;
-    ok &= launch_ps_token(m->ps, m->ps_blocks, m->ps_smem, ad, st);
-    ok &= enqueue_head(m, st, true, nullptr, true);
+    rc = ps_ordered(m, [&]() -> int {
+      ok &= launch_ps_token(m->ps, m->ps_blocks, m->ps_smem, ad, st);
+      ok &= enqueue_head(m, st, true, nullptr, true);
+      m->counts.kernel_launches++;
+      return TLM_OK;
+    });
+    if (rc) break;
   }
   hipError_t e = hipStreamSynchronize(st);
   if (ok && e == hipSuccess) e = hipMemcpy(out, tr, need * sizeof(unsigned long long), hipMemcpyDeviceToHost);
   hipFree(tr);
   hipFree(ad);
+  if (rc) return rc;
   if (!ok) return fail(TLM_ERR_STATE, "TLMModel: traced launch failed");
   if (e != hipSuccess) return fail(TLM_ERR_HIP, "TLMModel: %s", hipGetErrorString(e));
-  return ps_check(m);
+  return model_check(m);
 }
 
 int tlm_model_describe(tlm_model* m, char* out, size_t len) {
@@ -2140,7 +2337,7 @@ int tlm_model_describe(tlm_model* m, char* out, size_t len) {
              a.Hq, To * a.ko, a.ko, ng, a.mw, To * a.ks, a.ks, m->ps_smem, m->ps.nx, m->ps.no, m->ps.nd);
     s += b;
   } else {
-    s += " persistent[off]";
+    s += m->ps_range_off ? " persistent[off after an fp16 range overflow]" : " persistent[off]";
   }
   s += " prefill[batched from " + std::to_string(m->pf_min_rows) + " rows, chunk " + std::to_string(m->pf_chunk) +
        ", " + std::to_string(m->pf_replayed) + " replayed after fp16 overflow]";

@@ -33,6 +33,15 @@ __device__ __forceinline__ unsigned long long to_fx(float v) {
   return (unsigned long long)__float2ll_rn(v * kFxScale);
 }
 __device__ __forceinline__ float from_fx(unsigned long long s) { return __ll2float_rn((long long)s) * kFxInv; }
+// The accumulators add int64 replicas modulo 2^64, so a residual value is exact
+// while the true sum stays below 2^31 in magnitude.  A term or a sum of 2^30
+// or more (or NaN) sets ctrl[C_FXR]: the host then reports the results as
+// invalid instead of reading wrapped values.
+constexpr float kFxLimit = 1073741824.0f;  // 2^30
+__device__ __forceinline__ void fx_guard(float v, const int* ctrl) {
+  if (!(fabsf(v) < kFxLimit) && ctrl)
+    __hip_atomic_fetch_or(const_cast<int*>(ctrl) + C_FXR, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Cross-lane moves through DPP (data-parallel primitives: a VALU operand
 // modifier, no LDS round trip).  Every reduction below pairs lanes
@@ -174,6 +183,40 @@ __device__ __forceinline__ float dot_q4(const uint4 d, const float* __restrict__
     a1 = fmaf((float)(hi >> 24), xb.w, a1);
   }
   return s * ((a0 + a1) - 8.f * xsum);
+}
+
+// 32 q4 weights of one row (one 16-byte chunk) against fp16 inputs, two
+// weights per v_dot2_f32_f16.  xh: 16 dwords, dword 4 j + i = (x[8 j + i],
+// x[8 j + i + 4]); xsum = the sum of those 32 fp16 values.  Nibble m of
+// dword j (weight k = 8 j + m) is moved to bits 4..7 of one half (m < 4: the
+// low half, with m + 4 in the high half), and 0x3C00 or'ed in: the fp16
+// value 1 + n / 64 (exact).  Products of two fp16 values are exact in fp32,
+// so acc = sum_k (1 + n_k / 64) x_k, and
+// sum_k (n_k - 8) x_k = 64 acc - 72 xsum.
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+// (a & m) | c in one v_and_or_b32 (the compiler otherwise emits an and and an
+// or: VOP3 takes no literal on gfx950, so m and c sit in registers)
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float dot_q4h(const uint4 d, const uint32_t* __restrict__ xh, float xsum, float s) {
+  const uint32_t wv[4] = {d.x, d.y, d.z, d.w};
+  const uint32_t M = 0x00F000F0u, E = 0x3C003C00u;
+  float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint4 xp = *reinterpret_cast<const uint4*>(xh + 4 * j);
+    const uint32_t w = wv[j];
+    const uint32_t p0 = and_or(w << 4, M, E), p1 = and_or(w, M, E), p2 = and_or(w >> 4, M, E),
+                   p3 = and_or(w >> 8, M, E);
+    a0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p0), __builtin_bit_cast(f16x2, xp.x), a0, false);
+    a1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p1), __builtin_bit_cast(f16x2, xp.y), a1, false);
+    a0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p2), __builtin_bit_cast(f16x2, xp.z), a0, false);
+    a1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p3), __builtin_bit_cast(f16x2, xp.w), a1, false);
+  }
+  return s * fmaf(64.f, a0 + a1, -72.f * xsum);
 }
 
 // 8 fp16 weights of one row against x[0..8).

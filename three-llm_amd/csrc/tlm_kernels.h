@@ -55,8 +55,9 @@ __host__ __device__ inline ChunkPlan chunk_plan(int pos, int window, int nsplit,
 // ctrl block (device int32[8]): per-token state read by every kernel so that one
 // captured graph serves every position.  C_SEQ numbers the tokens of the
 // persistent schedule (the tag of its published words, never 0); C_ERR
-// collects its wait time-outs.
-enum Ctrl { C_TOKEN = 0, C_POS = 1, C_STEP = 2, C_BASE = 3, C_LEN = 4, C_SEQ = 5, C_ERR = 7 };
+// collects its failures (kPsErr*); C_FXR is set when a residual value of the
+// per-stage kernels leaves their fixed-point range (fx_guard).
+enum Ctrl { C_TOKEN = 0, C_POS = 1, C_STEP = 2, C_BASE = 3, C_LEN = 4, C_SEQ = 5, C_FXR = 6, C_ERR = 7 };
 
 // Embedding row staging: the kernels that choose the next token (set_ctrl,
 // prefill_advance, argmax_merge) also write its embedding row, in fixed point,
@@ -206,10 +207,18 @@ bool launch_topk(const float* logits, int n, int k, float softcap, float* wv, in
 // device-scope stores (past the per-XCD L2); a consumer polls its words until
 // they all carry the current token number.  No atomics, no clearing between
 // tokens.  Every wait is bounded (kPsTimeoutTicks); a time-out sets ctrl[C_ERR].
+// The q4 linears dot fp16 copies of their inputs (two weights per
+// v_dot2_f32_f16, fp32 sums); an input past the fp16 range makes the last
+// residual NaN, and the last layer's down items then set a bit of
+// ctrl[C_ERR] too.
 constexpr int kPsWaves = 16;
 constexpr int kPsMaxKs = 4;        // K-splits of a linear (partials its consumers add)
 constexpr int kPsRoles = 3;        // (stage, item) roles per block
 constexpr long long kPsTimeoutTicks = 10000000;  // 100 ms of the 100 MHz wall clock
+// ctrl[C_ERR] bits of a persistent-schedule token (the host recomputes it on
+// the per-stage graph): a bounded wait ran out; the last residual was not
+// finite (an input of a q4 linear overflowed its fp16 copy)
+constexpr int kPsErrTimeout = 1, kPsErrRange = 2;
 enum PsStage { PS_QKV = 0, PS_ATT = 1, PS_O = 2, PS_GU = 3, PS_DOWN = 4, PS_STAGES = 5 };
 struct PsLayer {
   const uint4* wqkv;

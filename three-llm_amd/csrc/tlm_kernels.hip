@@ -284,7 +284,9 @@ struct GemvPrologue {
         s2 += fx[kRmsF ? r : 0][q][1].x;
         s3 += fx[kRmsF ? r : 0][q][1].y;
       }
-      return make_float4(from_fx(s0), from_fx(s1), from_fx(s2), from_fx(s3));
+      const float4 y = make_float4(from_fx(s0), from_fx(s1), from_fx(s2), from_fx(s3));
+      fx_guard(fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))), a.ctrl);
+      return y;
     }
     return f4add(x[r], sum_loaded(p[r], a.n_pin));
   }
@@ -766,7 +768,10 @@ __global__ __launch_bounds__(kMlpWaves * 64) void mlp_kernel(MlpArgs m) {
         const int td = mlp_down_tile(item / Down::CPG, blk, m.Td), cc = item % Down::CPG;
         const float p = FMT == WF_Q4 ? dot_q4(dn.d[u], h, hsum, h2f(dn.sc[u])) : dot_f16(dn.d[u], h + cc * CK);
         const int n = td * kTile + lane;
-        if (n < m.H) atomicAdd(m.acc + (size_t)(blk % kRep) * m.H + n, to_fx(p));
+        if (n < m.H) {
+          fx_guard(p, a.ctrl);
+          atomicAdd(m.acc + (size_t)(blk % kRep) * m.H + n, to_fx(p));
+        }
       }
     }
   };
@@ -776,7 +781,10 @@ __global__ __launch_bounds__(kMlpWaves * 64) void mlp_kernel(MlpArgs m) {
     down_batch(ib);
   }
   if (blk == 0)
-    for (int n = threadIdx.x; n < m.H; n += blockDim.x) atomicAdd(m.acc + n, to_fx(xm[n]));
+    for (int n = threadIdx.x; n < m.H; n += blockDim.x) {
+      fx_guard(xm[n], a.ctrl);
+      atomicAdd(m.acc + n, to_fx(xm[n]));
+    }
 }
 
 size_t mlp_smem_bytes(int fmt, int C, int K) {

@@ -149,32 +149,54 @@ __device__ __forceinline__ bool wl_rows(int np, unsigned seq, F addr, float& xr,
   }
 }
 
-// Stage the wave's chunk inputs for its dot products: xw[u][e] = x[u] * nw
-// (nw: the element's norm weight, 1 without a norm) in the wave's LDS slots;
-// xs[u] = the chunk's sum of those (q4 group sums); ss = the sum of squares
-// of the raw x over the wave's chunks.  Ends with the wave's LDS writes
-// visible to its lanes.
-template <int CK, int NU>
+// Stage the wave's chunk inputs for its dot products: y = x[u] * nw (nw: the
+// element's norm weight, 1 without a norm) in the wave's LDS slots; ss = the
+// sum of squares of the raw x over the wave's chunks.
+//
+// fp16 weights (CK 8): xw[u][e] = y in fp32; xs unused.
+// q4 weights (CK 32): y rounded to fp16, stored as the pairs that dot_q4h
+// reads: dword 4 j + i of chunk u = (y[8 j + i], y[8 j + i + 4]); xs[u] =
+// the chunk's sum of those fp16 values.  An input past the fp16 range
+// becomes infinite and every dot product of its wave NaN, which reaches the
+// last residual whatever the stage: the last layer's down items raise
+// kPsErrRange from there (no check here, on the path to every dot).
+// Ends with the wave's LDS writes visible to its lanes.
+template <int FMT, int CK, int NU>
 __device__ __forceinline__ void wl_stage(const float (&x)[NU], const float (&nw)[NU], float* xw, float (&xs)[NU],
                                          float& ss) {
   const int lane = threadIdx.x & 63;
   const bool mine = lane < CK;
   float q = 0.f;
+  if constexpr (FMT == WF_Q4) {
+    _Float16* xh = reinterpret_cast<_Float16*>(xw);
+    // lane k (element k of each chunk) -> half (k / 4) & 1 of dword (k / 8) 4 + k % 4
+    const int slot = ((lane >> 3) << 3) + ((lane & 3) << 1) + ((lane >> 2) & 1);
 #pragma unroll
-  for (int u = 0; u < NU; u++) {
-    const float y = x[u] * nw[u];
-    if (mine) xw[u * CK + lane] = y;
-    q = fmaf(mine ? x[u] : 0.f, x[u], q);
-    xs[u] = CK == 32 ? wave_sum(mine ? y : 0.f) : 0.f;
+    for (int u = 0; u < NU; u++) {
+      const float y = x[u] * nw[u];
+      q = fmaf(mine ? x[u] : 0.f, x[u], q);
+      const _Float16 h = (_Float16)y;
+      if (mine) xh[u * 32 + slot] = h;
+      xs[u] = wave_sum(mine ? (float)h : 0.f);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+      const float y = x[u] * nw[u];
+      if (mine) xw[u * CK + lane] = y;
+      q = fmaf(mine ? x[u] : 0.f, x[u], q);
+      xs[u] = 0.f;
+    }
   }
   ss = wave_sum(q);
   wave_lds_sync();
 }
 
 // One 16-byte chunk of a weight row against its CK staged inputs.
+// (q4: x holds the chunk's 16 fp16-pair dwords staged by wl_stage.)
 template <int FMT>
 __device__ __forceinline__ float chunk_dot(uint4 d, uint16_t s, const float* x, float xs) {
-  if (FMT == WF_Q4) return dot_q4(d, x, xs, h2f(s));
+  if (FMT == WF_Q4) return dot_q4h(d, reinterpret_cast<const uint32_t*>(x), xs, h2f(s));
   return dot_f16(d, x);
 }
 
@@ -201,12 +223,12 @@ struct PsRows {
   }
   __device__ __forceinline__ float dot(int t, const float* xw, const float (&xs)[NU], int cbase, int clo, int chi,
                                        int wave) const {
-    constexpr int CK = FMT == WF_Q4 ? 32 : 8;
+    constexpr int XS = FMT == WF_Q4 ? 16 : 8;  // staged words per chunk
     float acc = 0.f;
 #pragma unroll
     for (int u = 0; u < NU; u++) {
       const int c = cbase + wave + 16 * u;
-      if (c >= clo && c < chi) acc += chunk_dot<FMT>(d[t][u], s[t][u], xw + u * CK, xs[u]);
+      if (c >= clo && c < chi) acc += chunk_dot<FMT>(d[t][u], s[t][u], xw + u * XS, xs[u]);
     }
     return acc;
   }
@@ -311,7 +333,7 @@ __device__ __forceinline__ bool ps_qkv(const PsArgs& a, int l, int i, int pos, i
   if (l == a.fail_layer) ok = false;  // the forced failure path (tests)
   if (wave == 0) ps_stamp(a, l, PS_QKV, 1);
   float xs[NX], ss = 0.f;
-  wl_stage<CK, NX>(x, nw, s.xw, xs, ss);
+  wl_stage<FMT, CK, NX>(x, nw, s.xw, xs, ss);
 #pragma unroll
   for (int t = 0; t < NT; t++) s.red[(wave * NT + t) * 64 + lane] = wr.dot(t, s.xw, xs, 0, c0, c1, wave);
   if (lane == 0) s.ssw[wave] = ss;
@@ -628,7 +650,7 @@ __device__ __forceinline__ bool ps_o(const PsArgs& a, int l, int i, int token, u
   ok &= wl_gather<CK, NO>(c0, c1, 1, seq, [&](int, int k) { return po + k; }, wave, x, a.timeout);
   if (wave == 0) ps_stamp(a, l, PS_O, 1);
   float xs[NO], ss;
-  wl_stage<CK, NO>(x, one, s.xw, xs, ss);
+  wl_stage<FMT, CK, NO>(x, one, s.xw, xs, ss);
   s.red[wave * 64 + lane] = wr.dot(0, s.xw, xs, c0, c0, c1, wave);
   if (!ps_all(ok, s.wf)) return false;
   if (wave == 0) {
@@ -662,7 +684,7 @@ __device__ __forceinline__ bool ps_gu(const PsArgs& a, int l, int g, unsigned se
   const bool ok = wl_gather<CK, NX>(0, a.Cx, a.ko, seq, [&](int p, int k) { return pm + (size_t)p * H + k; }, wave, x, a.timeout);
   if (wave == 0) ps_stamp(a, l, PS_GU, 1);
   float xs[NX], ss;
-  wl_stage<CK, NX>(x, nw, s.xw, xs, ss);
+  wl_stage<FMT, CK, NX>(x, nw, s.xw, xs, ss);
 #pragma unroll
   for (int u = 0; u < MW; u++)
     s.red[(wave * MW + u) * 64 + lane] = g * MW + u < a.Tgu ? wr.dot(u, s.xw, xs, 0, 0, a.Cx, wave) : 0.f;
@@ -710,13 +732,17 @@ __device__ __forceinline__ bool ps_down(const PsArgs& a, int l, int t, int sp, u
   ok &= wl_gather<CK, ND>(c0, c1, 1, seq, [&](int, int k) { return ph + k; }, wave, x, a.timeout);
   if (wave == 0) ps_stamp(a, l, PS_DOWN, 1);
   float xs[ND], ss;
-  wl_stage<CK, ND>(x, one, s.xw, xs, ss);
+  wl_stage<FMT, CK, ND>(x, one, s.xw, xs, ss);
   s.red[wave * 64 + lane] = wr.dot(0, s.xw, xs, c0, c0, c1, wave);
   if (!ps_all(ok, s.wf)) return false;
   if (wave == 0) {
     ps_stamp(a, l, PS_DOWN, 2);
     const float v = xm + ps_sum16(s.red + lane, 64);  // split 0 carries x_mid (TSLAdd.ts:10-33)
     if (row < H) st_dev(a.pub_x + ((size_t)l * kPsMaxKs + sp) * H + row, word(v, seq));
+    // a q4 input past the fp16 range made its wave's dot products NaN, and
+    // NaN reaches every later stage: the last layer's rows tell the host
+    if (l == a.L - 1 && row < H && !(fabsf(v) <= FLT_MAX))
+      __hip_atomic_fetch_or(glw(a.ctrl + C_ERR), kPsErrRange, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     ps_stamp(a, l, PS_DOWN, 3);
   }
   return true;
@@ -750,7 +776,8 @@ __global__ __launch_bounds__(kPsWaves * 64) void ps_token_kernel(const PsArgs* _
       else if (st == PS_DOWN)
         ok = ps_down<FMT, ND>(a, l, it % a.To, it / a.To, seq, sm);
       if (!ok) {  // a bounded wait ran out: report and leave (block-uniform)
-        if (threadIdx.x == 0) __hip_atomic_fetch_or(glw(a.ctrl + C_ERR), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0)
+          __hip_atomic_fetch_or(glw(a.ctrl + C_ERR), kPsErrTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
       }
       __syncthreads();  // LDS reused by the next role

@@ -63,7 +63,8 @@ class ModelDesc(ctypes.Structure):
 
 class ModelCounts(ctypes.Structure):
     _fields_ = [("graph_launches", ctypes.c_uint64), ("kernel_launches", ctypes.c_uint64),
-                ("prefill_chunks", ctypes.c_uint64), ("replayed_positions", ctypes.c_uint64)]
+                ("prefill_chunks", ctypes.c_uint64), ("replayed_positions", ctypes.c_uint64),
+                ("recomputed_positions", ctypes.c_uint64)]
 
 
 _lib = None
