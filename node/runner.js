@@ -84,6 +84,13 @@ class DecoderHIPRunner {
     this._logits = new Float32Array(desc.vocabSize);
     this._cacheTokens = [];
     this._cacheLogits = null;
+    this.softcap = withDefault(options.finalLogitSoftcap, 0);
+    // what generateAsync reads from runner.weights (generate.ts:11-16); a
+    // checkpoint loader supplies its tokenizer and stop tokens here
+    this.weights = Object.assign({
+      stopTokenIds: [], endOfTextTokenId: 0, tokenizer: {decode: (ids) => ids.join(' ')},
+      prepareGeneration: null,
+    }, options.weights || {});
   }
 
   // A runner over the synthetic weights of a benchmark workload.
@@ -128,33 +135,45 @@ class DecoderHIPRunner {
   }
 
   // ---- GenerateAsyncControls ----
+  // Enqueues one token (no wait); the reads below are the Promises.
   computeToken(tokenId, position, computeLogits) {
     this.addon.computeToken(this.model, tokenId, position, computeLogits === false ? 0 : TLM_LOGITS);
   }
 
+  // Chunks of prefillChunkSize positions, each run off the JS thread (the
+  // library waits for a batched chunk's overflow flag), then onProgress.
   async prefillTokens(inputTokens, start, end, onProgress) {
     const tokens = Int32Array.from(inputTokens);
     for (let offset = start; offset < end; offset += this.prefillChunkSize) {
       const count = Math.min(this.prefillChunkSize, end - offset);
-      this.addon.prefill(this.model, tokens, offset, offset + count);
+      await this.addon.prefillAsync(this.model, tokens, offset, offset + count);
       if (onProgress) await onProgress(offset + count);
     }
   }
 
+  // readChunkedLogits (src/tsl/TSLLogits.ts:71-83): resolves when the device
+  // has finished the token, with a copy of its logits.
   async readLogits() {
-    return Float32Array.from(this.addon.readLogits(this.model, this._logits));
+    await this.addon.readLogitsAsync(this.model, this._logits);
+    return Float32Array.from(this._logits);
   }
 
-  // Greedy reads the device argmax; k > 1 returns the device candidates to the
-  // caller's sampleTopKCandidates (TSLLogits.ts:336-355).
+  // TSLLogitSampler.sampleToken (src/tsl/TSLLogits.ts:379-383): greedy reads
+  // the device argmax; otherwise the device's top-k candidates are drawn on
+  // the host (sampleTopKCandidates).
   async sampleToken(candidateCount, opts) {
-    const temperature = opts && opts.temperature !== undefined ? opts.temperature : 0.8;
-    if (!(candidateCount > 1) || temperature <= 0) return this.addon.readToken(this.model);
-    throw new Error('DecoderHIPRunner: top-k sampling needs the host sampler (readCandidates)');
+    opts = opts || {};
+    if (candidateCount <= 1 || opts.temperature <= 0) return this.addon.readTokenAsync(this.model);
+    return sampleTopKCandidates(await this.readCandidates(candidateCount), opts);
   }
 
-  readCandidates(k) {
-    return this.addon.readCandidates(this.model, k, 0);
+  // The device's candidateCount best (token, score) pairs, best first
+  // (TSLLogitSampler.readCandidates, src/tsl/TSLLogits.ts:359-377).
+  async readCandidates(candidateCount) {
+    const c = await this.addon.readCandidatesAsync(this.model, candidateCount, this.softcap);
+    const out = [];
+    for (let i = 0; i < candidateCount; i++) out.push([c.tokens[i], c.scores[i]]);
+    return out;
   }
 
   resetCache() {
@@ -171,9 +190,28 @@ class DecoderHIPRunner {
     return 16;
   }
 
-  // The device-fed greedy loop (tokens never leave the device until the end).
+  // The controls object generateAsync takes (DecoderTSLRunner.ts:574-593).
+  controls() {
+    return {
+      rewindable: this.rewindable,
+      resetCache: () => this.resetCache(),
+      computeToken: (t, p, logits) => this.computeToken(t, p, logits),
+      prefillTokens: (toks, s, e, progress) => this.prefillTokens(toks, s, e, progress),
+      readLogits: () => this.readLogits(),
+      sampleToken: (k, o) => this.sampleToken(k, o),
+      maxGpuCandidateCount: this.maxGpuCandidateCount,
+    };
+  }
+
+  // DecoderTSLRunner.generate: generateAsync over this runner's controls.
+  generate(prompt, options) {
+    return generateAsync(this, prompt, options, this.controls());
+  }
+
+  // The device-fed greedy loop (tokens never leave the device until the
+  // end): resolves with the count tokens.
   decodeGreedy(tokenId, position, count) {
-    return this.addon.decodeGreedy(this.model, tokenId, position, count);
+    return this.addon.decodeGreedyAsync(this.model, tokenId, position, count);
   }
 
   counts() {
@@ -231,25 +269,263 @@ function syntheticTensors(addon, r, st, qkvBias) {
   return out;
 }
 
-// The greedy path of generateAsync (src/runtime/generate.ts:210-305) over the
-// runner's controls: prefill [0, n - 1), the last prompt token with logits,
-// then sample, stop on a stop token, compute the next position.
-async function generateGreedy(runner, inputTokens, maxNewTokens, stopTokenIds) {
-  const stops = new Set(stopTokenIds || []);
-  const all = inputTokens.slice();
-  const generated = [];
-  runner.resetCache();
-  const prefillEnd = maxNewTokens > 0 ? inputTokens.length - 1 : inputTokens.length;
-  if (prefillEnd > 0) await runner.prefillTokens(inputTokens, 0, prefillEnd);
-  for (let i = prefillEnd; i < inputTokens.length; i++) runner.computeToken(inputTokens[i], i, true);
-  for (let i = 0; i < maxNewTokens; i++) {
-    const next = await runner.sampleToken(1, {temperature: 0});
-    if (stops.has(next)) break;
-    all.push(next);
-    generated.push(next);
-    runner.computeToken(next, all.length - 1, true);
+// ------------------------------------------------------------ sampling --
+// softmax (src/runtime/math.ts:60-76): double exponentials stored in a
+// Float32Array.
+function softmax(values) {
+  let max = -Infinity;
+  for (let i = 0; i < values.length; i++) max = Math.max(max, values[i]);
+  const out = new Float32Array(values.length);
+  let sum = 0;
+  for (let i = 0; i < values.length; i++) {
+    const v = Math.exp(values[i] - max);
+    out[i] = v;
+    sum += v;
   }
-  return {tokens: all, generated};
+  for (let i = 0; i < out.length; i++) out[i] /= sum;
+  return out;
 }
 
-module.exports = {DecoderHIPRunner, generateGreedy, syntheticTensors, recipeOf, ropeInvFreq, WORKLOADS, FMT, T};
+// sampleTopKCandidates (src/runtime/math.ts:527-547): candidates are
+// [token, score] pairs, best first; temperature 0.8 and Math.random unless
+// given.
+function sampleTopKCandidates(candidates, opts) {
+  opts = opts || {};
+  const temperature = withDefault(opts.temperature, 0.8);
+  const random = opts.random || Math.random;
+  if (candidates.length === 0) return 0;
+  if (temperature <= 0 || candidates.length === 1) return candidates[0][0];
+  const values = new Float32Array(candidates.length);
+  for (let i = 0; i < candidates.length; i++) values[i] = candidates[i][1] / Math.max(temperature, 1e-6);
+  const p = softmax(values);
+  let r = random();
+  for (let i = 0; i < p.length; i++) {
+    r -= p[i];
+    if (r <= 0) return candidates[i][0];
+  }
+  return candidates[candidates.length - 1][0];
+}
+
+// Greedy choice over full logits (the temperature-0 branch of sampleTopK,
+// math.ts:581-593: the first maximum wins).
+function argmax(logits) {
+  let best = 0;
+  for (let i = 1; i < logits.length; i++) if (logits[i] > logits[best]) best = i;
+  return best;
+}
+
+// ------------------------------------------------------------- planning --
+// sharedPrefixLength (src/runtime/generate.ts:61-68).
+function sharedPrefixLength(a, b) {
+  a = a || [];
+  b = b || [];
+  const n = Math.min(a.length, b.length);
+  let i = 0;
+  while (i < n && a[i] === b[i]) i++;
+  return i;
+}
+
+// prepareGenerationFromTokens (generate.ts:70-81): the prompt's last
+// maxTokens - 1 tokens (the end-of-text token for an empty one) and the new
+// tokens that fit after it.
+function prepareGenerationFromTokens(tokens, maxTokens, maxNewTokens, endOfTextTokenId) {
+  const budget = Math.max(1, maxTokens - 1);
+  const inputTokens = tokens.length === 0 ? [endOfTextTokenId] : tokens.slice(-budget);
+  return {inputTokens, newTokenBudget: Math.max(0, Math.min(maxNewTokens, maxTokens - inputTokens.length))};
+}
+
+// planPromptCache (generate.ts:98-118): reuse the cached prefix (with its
+// logits when the whole cache is a prefix of the prompt), rewind to the shared
+// prefix, or reset.
+function planPromptCache(cachedTokens, cachedLogits, inputTokens, rewindable) {
+  const prefix = sharedPrefixLength(cachedTokens, inputTokens);
+  const hasLogits = cachedLogits !== null && cachedLogits !== undefined;
+  if (prefix > 0 && prefix === (cachedTokens || []).length && hasLogits)
+    return {start: prefix, logits: cachedLogits, reset: false, reused: prefix};
+  if (rewindable && prefix > 0) {
+    const start = prefix >= inputTokens.length ? inputTokens.length - 1 : prefix;
+    return {start, logits: null, reset: false, reused: start};
+  }
+  return {start: 0, logits: null, reset: true, reused: 0};
+}
+
+// needsFullLogitsForSampling (math.ts:509-523) and gpuCandidateCount
+// (generate.ts:120-130): how many device candidates sampling needs (0: full
+// logits on the host).
+function needsFullLogits(o) {
+  const rep = withDefault(o.repetitionPenalty, 1);
+  return o.forceFullLogits === true || (rep !== 1 && rep > 0) || withDefault(o.presencePenalty, 0) !== 0 ||
+    withDefault(o.frequencyPenalty, 0) !== 0 || Math.max(0, Math.floor(withDefault(o.noRepeatNgramSize, 0))) >= 2;
+}
+
+function gpuCandidateCount(options, maxCandidateCount) {
+  if (maxCandidateCount === 0 || options.gpuSampling === false || needsFullLogits(options)) return 0;
+  const temperature = withDefault(options.temperature, 0.8);
+  const topK = Math.max(1, Math.floor(withDefault(options.topK, 40)));
+  if (temperature <= 0 || topK === 1) return 1;
+  if (topK <= maxCandidateCount) return topK;
+  return 0;
+}
+
+// isStopToken (generate.ts:51-59).
+function isStopToken(runner, tokenId) {
+  const stops = runner.weights.stopTokenIds;
+  if (Array.isArray(stops) && stops.length > 0) return stops.indexOf(tokenId) >= 0;
+  return tokenId === runner.weights.endOfTextTokenId;
+}
+
+// applyRepeatPenalties (src/runtime/math.ts:438-503): repetition, presence
+// and frequency penalties over the last repeatLastN tokens, and -Infinity for
+// the token that would repeat an n-gram; a penalised copy, or the input.
+function applyRepeatPenalties(logits, tokens, o) {
+  if (!tokens || tokens.length === 0) return logits;
+  const rep = withDefault(o.repetitionPenalty, 1), pres = withDefault(o.presencePenalty, 0);
+  const freq = withDefault(o.frequencyPenalty, 0), lastN = withDefault(o.repeatLastN, 64);
+  const useRep = rep !== 1 && rep > 0, usePres = pres !== 0, useFreq = freq !== 0;
+  const ngram = Math.max(0, Math.floor(withDefault(o.noRepeatNgramSize, 0)));
+  const useNgrams = ngram >= 2 && tokens.length >= ngram - 1;
+  if (!useRep && !usePres && !useFreq && !useNgrams) return logits;
+  const out = logits.slice();
+  if (useRep || usePres || useFreq) {
+    const counts = new Map();
+    for (let i = lastN > 0 ? Math.max(0, tokens.length - lastN) : 0; i < tokens.length; i++)
+      counts.set(tokens[i], (counts.get(tokens[i]) || 0) + 1);
+    for (const [t, count] of counts) {
+      let v = out[t];
+      if (useRep) v = v < 0 ? v * rep : v / rep;
+      if (usePres) v -= pres;
+      if (useFreq) v -= freq * count;
+      out[t] = v;
+    }
+  }
+  if (useNgrams) {
+    const plen = ngram - 1, pstart = tokens.length - plen;
+    for (let i = 0; i <= tokens.length - ngram; i++) {
+      let match = true;
+      for (let j = 0; j < plen && match; j++) match = tokens[i + j] === tokens[pstart + j];
+      if (match) out[tokens[i + plen]] = -Infinity;
+    }
+  }
+  return out;
+}
+
+// sampleTopK (src/runtime/math.ts:556-620) over full logits: penalties, then
+// greedy for temperature <= 0 or topK 1 (first maximum), else a draw from the
+// softmax of the topK best logits / temperature (ties keep the lower id).
+function sampleTopK(logits, o) {
+  o = o || {};
+  logits = applyRepeatPenalties(logits, o.tokens, o);
+  const temperature = withDefault(o.temperature, 0.8);
+  const k = Math.min(Math.max(1, Math.floor(withDefault(o.topK, 40))), logits.length);
+  if (temperature <= 0 || k === 1) return argmax(logits);
+  const t = Math.max(temperature, 1e-6);
+  const best = [];  // [id, value], best first
+  for (let i = 0; i < logits.length; i++) {
+    const v = logits[i] / t;
+    if (best.length === k && !(v > best[k - 1][1])) continue;
+    let j = best.length < k ? best.length : k - 1;
+    while (j > 0 && best[j - 1][1] < v) j--;  // after the equal values already kept
+    best.splice(j, 0, [i, v]);
+    if (best.length > k) best.pop();
+  }
+  const p = softmax(best.map((c) => c[1]));
+  let r = (o.random || Math.random)();
+  for (let i = 0; i < p.length; i++) {
+    r -= p[i];
+    if (r <= 0) return best[i][0];
+  }
+  return best[best.length - 1][0];
+}
+
+// ------------------------------------------------------------- generate --
+// generateAsync (src/runtime/generate.ts:210-305), the same control flow:
+// prompt tokens (options.inputTokens, or weights.prepareGeneration(prompt)),
+// the prompt-cache plan, prefill in chunks with progress callbacks, the
+// prompt's last token with logits, then sample -> stop token? -> onToken ->
+// compute, until the budget or an aborted signal.  Resolves with the
+// GenerationResult fields (finishGeneration) and stores the cache state.
+async function generateAsync(runner, prompt, options, controls) {
+  options = options || {};
+  const maxNew = withDefault(options.maxNewTokens, 32);
+  let prepared;
+  if (options.inputTokens) {
+    prepared = prepareGenerationFromTokens(options.inputTokens, runner.maxTokens, maxNew,
+      runner.weights.endOfTextTokenId);
+  } else if (typeof runner.weights.prepareGeneration === 'function') {
+    prepared = runner.weights.prepareGeneration(prompt, runner.maxTokens, maxNew);
+  } else {
+    throw new Error('DecoderHIPRunner: no tokenizer to prepare the prompt; pass options.inputTokens');
+  }
+  const inputTokens = prepared.inputTokens, newTokenBudget = prepared.newTokenBudget;
+  const plan = planPromptCache(runner._cacheTokens || [], runner._cacheLogits, inputTokens, controls.rewindable);
+  const signal = options.signal;
+  const aborted = () => signal !== undefined && signal !== null && signal.aborted === true;
+  const candidateCount = gpuCandidateCount(options, controls.maxGpuCandidateCount || 0);
+  const useGpuSampling = candidateCount > 0 && typeof controls.sampleToken === 'function';
+  if (plan.reset) controls.resetCache();
+  if (options.onPrefill) options.onPrefill({cachedPromptTokens: plan.reused, promptTokens: inputTokens.length});
+  const allTokens = inputTokens.slice();
+  const generatedTokens = [];
+  let logits = plan.logits;
+  const needsPromptLogits = newTokenBudget > 0;
+  const prefillEnd = needsPromptLogits ? inputTokens.length - 1 : inputTokens.length;
+  let promptLoopStart = plan.start;
+  const report = async (completed) => {
+    if (options.onPrefillProgress) {
+      options.onPrefillProgress({cachedPromptTokens: plan.reused, completedPromptTokens: completed,
+        freshPromptTokens: inputTokens.length - plan.start, promptTokens: inputTokens.length});
+    }
+  };
+  if (options.prefillMode !== false && typeof controls.prefillTokens === 'function' && plan.start < prefillEnd) {
+    await controls.prefillTokens(inputTokens, plan.start, prefillEnd, report);
+    promptLoopStart = prefillEnd;
+  }
+  for (let i = promptLoopStart; i < inputTokens.length; i++) {
+    if (aborted()) break;
+    const computeLogits = needsPromptLogits && i === inputTokens.length - 1;
+    await controls.computeToken(inputTokens[i], i, computeLogits, useGpuSampling ? candidateCount : 0);
+    if (computeLogits) logits = useGpuSampling ? null : await controls.readLogits();
+    await report(i + 1);
+  }
+  if (options.onPrefillComplete) {
+    options.onPrefillComplete({cachedPromptTokens: plan.reused, promptTokens: inputTokens.length});
+  }
+  for (let i = 0; i < newTokenBudget; i++) {
+    if (aborted()) break;
+    if (!useGpuSampling && logits === null) break;
+    const sampleOpts = Object.assign({}, options, {tokens: allTokens});
+    const next = useGpuSampling ? await controls.sampleToken(candidateCount, sampleOpts)
+      : sampleTopK(logits, sampleOpts);
+    if (isStopToken(runner, next)) break;
+    allTokens.push(next);
+    generatedTokens.push(next);
+    if (options.onToken) options.onToken(runner.weights.tokenizer.decode(allTokens), next);
+    await controls.computeToken(next, allTokens.length - 1, true, useGpuSampling ? candidateCount : 0);
+    logits = useGpuSampling ? null : await controls.readLogits();
+  }
+  runner._cacheTokens = allTokens.slice();
+  runner._cacheLogits = logits;
+  const tok = runner.weights.tokenizer;
+  return {
+    tokens: allTokens, generatedTokens, text: tok.decode(allTokens), generatedText: tok.decode(generatedTokens),
+    cachedPromptTokens: plan.reused, promptTokens: inputTokens.length, aborted: aborted(),
+  };
+}
+
+// The greedy path alone: prompt ids in, greedy ids out (no cache reuse).
+async function generateGreedy(runner, inputTokens, maxNewTokens, stopTokenIds) {
+  runner.resetCache();
+  const saved = runner.weights.stopTokenIds;
+  if (stopTokenIds) runner.weights.stopTokenIds = stopTokenIds;
+  try {
+    const r = await runner.generate('', {inputTokens, maxNewTokens, temperature: 0});
+    return {tokens: r.tokens, generated: r.generatedTokens};
+  } finally {
+    runner.weights.stopTokenIds = saved;
+  }
+}
+
+module.exports = {DecoderHIPRunner, generateAsync, generateGreedy, sampleTopKCandidates, sampleTopK,
+  applyRepeatPenalties, planPromptCache,
+  gpuCandidateCount, prepareGenerationFromTokens, isStopToken, softmax, syntheticTensors, recipeOf, ropeInvFreq,
+  WORKLOADS, FMT, T};

@@ -43,7 +43,8 @@ function f16ToF32(h) {
 check('every entry point is bound', () => {
   const names = ['abiVersion', 'lastError', 'open', 'close', 'sync', 'deviceInfo', 'modelCreate', 'modelUpload',
     'modelFinalize', 'modelDestroy', 'computeToken', 'prefill', 'readLogits', 'readToken', 'decodeGreedy',
-    'resetCache', 'readCandidates', 'quantizeQ4', 'f32ToF16', 'synthNormal', 'synthTokens', 'modelCounts', 'modelSetPrefill'];
+    'resetCache', 'readCandidates', 'quantizeQ4', 'f32ToF16', 'synthNormal', 'synthTokens', 'modelCounts', 'modelSetPrefill',
+    'readLogitsAsync', 'readTokenAsync', 'readCandidatesAsync', 'decodeGreedyAsync', 'prefillAsync'];
   for (const n of names) assert.strictEqual(typeof tlm[n], 'function', n);
 });
 
@@ -100,6 +101,12 @@ check('handles are checked: a model call on a non-handle throws', () => {
   throwsTlm(() => tlm.computeToken({}, 1, 0), TLM_ERR_INVALID, 'TLMAddon:');
   throwsTlm(() => tlm.readToken(42), TLM_ERR_INVALID, 'TLMAddon:');
   throwsTlm(() => tlm.modelCounts({}), TLM_ERR_INVALID, 'TLMAddon:');
+  // the Promise reads check their arguments before queuing: they throw
+  throwsTlm(() => tlm.readLogitsAsync({}, new Float32Array(4)), TLM_ERR_INVALID, 'TLMAddon:');
+  throwsTlm(() => tlm.readTokenAsync(null), TLM_ERR_INVALID, 'TLMAddon:');
+  throwsTlm(() => tlm.readCandidatesAsync(7, 4), TLM_ERR_INVALID, 'TLMAddon:');
+  throwsTlm(() => tlm.decodeGreedyAsync({}, 1, 0, 2), TLM_ERR_INVALID, 'TLMAddon:');
+  throwsTlm(() => tlm.prefillAsync({}, new Int32Array(2), 0, 2), TLM_ERR_INVALID, 'TLMAddon:');
 });
 
 check('open: a context, or (no usable device) an Error from tlm_last_error', () => {

@@ -5,7 +5,9 @@
 // max-abs 2e-2 / rel 1e-2, and the greedy stream of generateGreedy equal to
 // the oracle's until a step whose top-2 logit gap is under 2e-2; then the
 // device-fed greedy loop equal to the host loop, and one graph launch per
-// decode token (the reference's submission contract).
+// decode token (the reference's submission contract); the device's top-8
+// candidates equal the 8 best logits, and generate() with top-k sampling
+// runs on them.
 //
 // Usage: node test_runner_gpu.js <path of tlm_addon.node>   (needs an MI355X)
 'use strict';
@@ -66,7 +68,7 @@ async function main() {
     const before = runner.counts();
     const n = c.stream.length - 1;
     const t1 = process.hrtime.bigint();
-    const dev = Array.from(runner.decodeGreedy(first, c.prompt.length, n));
+    const dev = Array.from(await runner.decodeGreedy(first, c.prompt.length, n));
     const us = Number(process.hrtime.bigint() - t1) / 1e3;
     const after = runner.counts();
     assert.deepStrictEqual([first].concat(dev), out.generated.slice(0, n + 1));
@@ -76,6 +78,23 @@ async function main() {
     }
     console.log(`ok ${++passed} - ${label}: device loop = host loop, ${after.graphLaunches - before.graphLaunches} ` +
                 `graph launches (${(us / n).toFixed(1)} us/token incl. one sync)`);
+    // device top-k: the k best logits in the greedy order (TSLLogitSampler),
+    // and generate() with top-k sampling draws its tokens from those lists
+    runner.resetCache();
+    runner.computeToken(c.prompt[0], 0, true);
+    const logits = await runner.readLogits();
+    const cands = await runner.readCandidates(8);
+    const order = Array.from(logits.keys()).sort((a, b) => logits[b] - logits[a] || a - b).slice(0, 8);
+    assert.deepStrictEqual(cands.map((x) => x[0]), order);
+    cands.forEach((x) => assert.strictEqual(x[1], logits[x[0]]));
+    let u = 0.3;
+    const drawn = [];
+    const sampled = await runner.generate('', {inputTokens: c.prompt, maxNewTokens: 4, temperature: 0.7, topK: 8,
+      random: () => (u = (u * 7.13 + 0.17) % 1), onToken: (text, t) => drawn.push(t)});
+    assert.strictEqual(sampled.generatedTokens.length, 4);
+    assert.deepStrictEqual(drawn, sampled.generatedTokens);
+    console.log(`ok ${++passed} - ${label}: device top-8 = the 8 best logits; top-k generate drew ` +
+                JSON.stringify(sampled.generatedTokens));
     runner.close();
   }
   console.log('1..' + passed);

@@ -17,6 +17,16 @@
 //   f32ToF16(Float32Array) synthNormal(seed, stream, n, stddev)
 //   synthTokens(seed, stream, n, vocab) modelCounts(model)
 //   modelSetPrefill(model, minRows, chunk)
+// and the reads as Promises, each run on the libuv thread pool so the JS
+// thread is not blocked while the device finishes (the counterpart of the
+// reference's renderer.getArrayBufferAsync, src/tsl/TSLLogits.ts:71-83,
+// 359-377): readLogitsAsync(model, Float32Array) -> the array,
+// readTokenAsync(model) -> token, readCandidatesAsync(model, k, softcap) ->
+// {tokens, scores}, decodeGreedyAsync(model, token, pos, n) -> Int32Array,
+// prefillAsync(model, Int32Array, start, end) -> undefined.
+// A failing read rejects with the same Error(tlm_last_error(), code).  While
+// a read of a model is pending, every other call on that model throws
+// (TLM_ERR_STATE): a model is used by one call at a time.
 #include <dlfcn.h>
 #include <node_api.h>
 #include <stdint.h>
@@ -224,11 +234,12 @@ napi_value new_typed(napi_env env, napi_typedarray_type t, size_t count, size_t 
 // close is a no-op, a use after close throws).
 struct Handle {
   void* p;
-  int kind;  // 1 context, 2 model
+  int kind;      // 1 context, 2 model
+  int pending;   // model: reads running on the thread pool
 };
 
 napi_value wrap(napi_env env, void* p, int kind) {
-  Handle* h = new Handle{p, kind};
+  Handle* h = new Handle{p, kind, 0};
   napi_value v;
   napi_create_external(env, h, [](napi_env, void* d, void*) { delete static_cast<Handle*>(d); }, nullptr, &v);
   return v;
@@ -407,6 +418,8 @@ napi_value ModelDestroy(napi_env env, napi_callback_info info) {
   void* d = nullptr;
   if (a.n >= 1 && napi_get_value_external(env, a.v[0], &d) == napi_ok && d) {
     Handle* h = static_cast<Handle*>(d);
+    if (h->kind == 2 && h->pending)
+      return throw_error(env, TLM_ERR_STATE, "TLMModel: a read of this model is still pending");
     if (h->kind == 2 && h->p) g_api.model_destroy(static_cast<tlm_model*>(h->p));
     if (h->kind == 2) h->p = nullptr;
   }
@@ -415,6 +428,10 @@ napi_value ModelDestroy(napi_env env, napi_callback_info info) {
 
 tlm_model* model_arg(napi_env env, napi_value v) {
   Handle* h = unwrap(env, v, 2);
+  if (h && h->pending) {
+    throw_error(env, TLM_ERR_STATE, "TLMModel: a read of this model is still pending");
+    return nullptr;
+  }
   return h ? static_cast<tlm_model*>(h->p) : nullptr;
 }
 
@@ -555,6 +572,175 @@ napi_value ReadCandidates(napi_env env, napi_callback_info info) {
   return o;
 }
 
+// ------------------------------------------------------------ async reads --
+// One read on the thread pool: execute() calls the library (which waits for
+// the model's stream) off the JS thread, complete() settles the Promise on it.
+// The arrays the read fills are kept alive by references until then, and
+// the model handle counts the read as pending.
+struct AsyncRead {
+  enum Kind { LOGITS, TOKEN, CANDIDATES, GREEDY, PREFILL } kind;
+  Handle* model;
+  napi_ref model_ref = nullptr;  // the handle's external
+  napi_ref out_ref = nullptr;    // the value the Promise resolves with (arrays: filled in place)
+  napi_deferred deferred = nullptr;
+  napi_async_work work = nullptr;
+  void* a = nullptr;  // logits / candidate ids / greedy tokens
+  void* b = nullptr;  // candidate scores
+  size_t n = 0;
+  int32_t token = 0, pos = 0, k = 0;
+  double cap = 0;
+  int rc = 0;
+  std::string err;  // tlm_last_error() of the worker thread (thread-local)
+  AsyncRead(Kind k, Handle* h) : kind(k), model(h) {}
+};
+
+void read_execute(napi_env, void* data) {
+  AsyncRead* r = static_cast<AsyncRead*>(data);
+  tlm_model* m = static_cast<tlm_model*>(r->model->p);
+  switch (r->kind) {
+    case AsyncRead::LOGITS: r->rc = g_api.read_logits(m, static_cast<float*>(r->a), r->n); break;
+    case AsyncRead::TOKEN: r->rc = g_api.read_token(m, &r->token); break;
+    case AsyncRead::CANDIDATES:
+      r->rc = g_api.read_candidates(m, r->k, r->cap, static_cast<int32_t*>(r->a), static_cast<float*>(r->b));
+      break;
+    case AsyncRead::GREEDY:
+      r->rc = r->n ? g_api.decode_greedy(m, r->token, r->pos, (int)r->n, static_cast<int32_t*>(r->a)) : TLM_OK;
+      break;
+    case AsyncRead::PREFILL:  // [pos, k) of the token array
+      r->rc = g_api.prefill(m, static_cast<const int32_t*>(r->a), r->pos, r->k);
+      break;
+  }
+  if (r->rc != TLM_OK) {
+    const char* e = g_api.last_error();
+    r->err = e && *e ? e : "TLMAddon: call failed with code " + std::to_string(r->rc);
+  }
+}
+
+void read_complete(napi_env env, napi_status status, void* data) {
+  AsyncRead* r = static_cast<AsyncRead*>(data);
+  r->model->pending--;
+  if (status != napi_ok && r->rc == TLM_OK) {
+    r->rc = TLM_ERR_STATE;
+    r->err = "TLMAddon: the read was cancelled";
+  }
+  if (r->rc != TLM_OK) {
+    napi_value msg, err, c;
+    napi_create_string_utf8(env, r->err.c_str(), NAPI_AUTO_LENGTH, &msg);
+    napi_create_error(env, nullptr, msg, &err);
+    napi_create_int32(env, r->rc, &c);
+    napi_set_named_property(env, err, "code", c);
+    napi_reject_deferred(env, r->deferred, err);
+  } else {
+    napi_value v;
+    if (r->kind == AsyncRead::TOKEN) napi_create_double(env, r->token, &v);
+    else if (r->kind == AsyncRead::PREFILL) napi_get_undefined(env, &v);
+    else napi_get_reference_value(env, r->out_ref, &v);
+    napi_resolve_deferred(env, r->deferred, v);
+  }
+  if (r->out_ref) napi_delete_reference(env, r->out_ref);
+  napi_delete_reference(env, r->model_ref);
+  napi_delete_async_work(env, r->work);
+  delete r;
+}
+
+// Queues r (its model handle is args[0]); returns the Promise, or throws.
+napi_value read_start(napi_env env, napi_value model, napi_value out, AsyncRead* r, const char* name) {
+  napi_value promise, res;
+  napi_create_promise(env, &r->deferred, &promise);
+  napi_create_reference(env, model, 1, &r->model_ref);
+  if (out) napi_create_reference(env, out, 1, &r->out_ref);
+  napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &res);
+  if (napi_create_async_work(env, nullptr, res, read_execute, read_complete, r, &r->work) != napi_ok ||
+      napi_queue_async_work(env, r->work) != napi_ok) {
+    if (r->out_ref) napi_delete_reference(env, r->out_ref);
+    napi_delete_reference(env, r->model_ref);
+    delete r;
+    return throw_error(env, TLM_ERR_STATE, "TLMAddon: cannot queue the read");
+  }
+  r->model->pending++;
+  return promise;
+}
+
+Handle* model_handle(napi_env env, napi_value v) {
+  return model_arg(env, v) ? unwrap(env, v, 2) : nullptr;
+}
+
+napi_value ReadLogitsAsync(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  Handle* h = model_handle(env, a.v[0]);
+  void* out = nullptr;
+  size_t n = 0;
+  if (!h || !get_typed(env, a.v[1], napi_float32_array, &out, &n, "logits")) return nullptr;
+  AsyncRead* r = new AsyncRead(AsyncRead::LOGITS, h);
+  r->a = out;
+  r->n = n;
+  return read_start(env, a.v[0], a.v[1], r, "tlmReadLogits");
+}
+
+napi_value ReadTokenAsync(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  Handle* h = model_handle(env, a.v[0]);
+  if (!h) return nullptr;
+  AsyncRead* r = new AsyncRead(AsyncRead::TOKEN, h);
+  return read_start(env, a.v[0], nullptr, r, "tlmReadToken");
+}
+
+napi_value ReadCandidatesAsync(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  Handle* h = model_handle(env, a.v[0]);
+  int32_t k = 0;
+  double cap = 0;
+  if (!h || !get_i32(env, a.v[1], &k, "k")) return nullptr;
+  if (a.n >= 3 && !get_f64(env, a.v[2], &cap, "softcap")) return nullptr;
+  if (k < 1 || k > 16) return throw_error(env, TLM_ERR_INVALID, "TLMLogitSampler: k must be in [1, 16]");
+  AsyncRead* r = new AsyncRead(AsyncRead::CANDIDATES, h);
+  r->k = k;
+  r->cap = cap;
+  napi_value ta = new_typed(env, napi_int32_array, (size_t)k, 4, &r->a);
+  napi_value sa = new_typed(env, napi_float32_array, (size_t)k, 4, &r->b);
+  napi_value o;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "tokens", ta);
+  napi_set_named_property(env, o, "scores", sa);
+  return read_start(env, a.v[0], o, r, "tlmReadCandidates");
+}
+
+napi_value DecodeGreedyAsync(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  Handle* h = model_handle(env, a.v[0]);
+  int32_t token = 0, pos = 0, n = 0;
+  if (!h || !get_i32(env, a.v[1], &token, "token") || !get_i32(env, a.v[2], &pos, "position") ||
+      !get_i32(env, a.v[3], &n, "n"))
+    return nullptr;
+  if (n < 0) return throw_error(env, TLM_ERR_INVALID, "TLMModel: n must be non-negative");
+  AsyncRead* r = new AsyncRead(AsyncRead::GREEDY, h);
+  r->token = token;
+  r->pos = pos;
+  r->n = (size_t)n;
+  napi_value arr = new_typed(env, napi_int32_array, (size_t)n, 4, &r->a);
+  return read_start(env, a.v[0], arr, r, "tlmDecodeGreedy");
+}
+
+// prefillAsync(model, Int32Array, start, end): tlm_prefill on the thread pool
+// (it waits for each batched chunk's overflow flag).
+napi_value PrefillAsync(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  Handle* h = model_handle(env, a.v[0]);
+  void* toks = nullptr;
+  size_t n = 0;
+  int32_t start = 0, end = 0;
+  if (!h || !get_typed(env, a.v[1], napi_int32_array, &toks, &n, "tokens") ||
+      !get_i32(env, a.v[2], &start, "start") || !get_i32(env, a.v[3], &end, "end"))
+    return nullptr;
+  if (start < 0 || end < start || (size_t)end > n)
+    return throw_error(env, TLM_ERR_RANGE, "TLMModel: prefill range outside the token array");
+  AsyncRead* r = new AsyncRead(AsyncRead::PREFILL, h);
+  r->a = toks;
+  r->pos = start;
+  r->k = end;
+  return read_start(env, a.v[0], a.v[1], r, "tlmPrefill");
+}
+
 napi_value QuantizeQ4(napi_env env, napi_callback_info info) {
   Args a(env, info);
   void* w = nullptr;
@@ -645,6 +831,11 @@ napi_value Init(napi_env env, napi_value exports) {
       {"synthTokens", nullptr, SynthTokens, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"modelCounts", nullptr, ModelCounts, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"modelSetPrefill", nullptr, ModelSetPrefill, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"readLogitsAsync", nullptr, ReadLogitsAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"readTokenAsync", nullptr, ReadTokenAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"readCandidatesAsync", nullptr, ReadCandidatesAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"decodeGreedyAsync", nullptr, DecodeGreedyAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"prefillAsync", nullptr, PrefillAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
   };
   napi_define_properties(env, exports, sizeof props / sizeof props[0], props);
   return exports;

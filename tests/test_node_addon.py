@@ -3,7 +3,13 @@ the system Node headers, then node/test_addon.js checks on the CPU that every
 entry point is bound, the host-side helpers return what the C ABI computes,
 and failing calls throw an Error carrying tlm_last_error() and its TLM_ERR_*
 code; node/runner.js (the DecoderHIPRunner of the Node host) builds the same
-synthetic tensors as the Python host.  Skipped where Node.js or its headers are absent."""
+synthetic tensors as the Python host.  Then node/test_runner_mock.js runs the
+addon and runner.js over a stand-in library with the same C ABI
+(node/test_mock_tlm.c, a formula decoder built here with gcc): the Promise
+reads run off the JS thread and reject with the worker thread's error, and
+generate() follows generateAsync (prompt cache, greedy, device top-k and host
+sampling, stop tokens, onToken).  Skipped where Node.js or its headers are
+absent."""
 import os
 import shutil
 import subprocess
@@ -38,3 +44,19 @@ def test_addon_builds_and_binds_the_c_abi():
                        timeout=120)
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
     assert "1..11" in r.stdout
+
+
+def test_runner_over_a_stand_in_library(tmp_path):
+    node, _ = _tools()
+    addon = NODE_DIR / "build" / "Release" / "tlm_addon.node"
+    if not addon.exists():
+        pytest.skip("the addon is not built (test_addon_builds_and_binds_the_c_abi builds it)")
+    mock = tmp_path / "libtlm_mock.so"
+    b = subprocess.run(["gcc", "-shared", "-fPIC", "-O2", "-Wall", "-Werror", "-I", str(ROOT / "include"), "-o",
+                        str(mock), str(NODE_DIR / "test_mock_tlm.c"), "-lpthread"], capture_output=True, text=True)
+    assert b.returncode == 0, b.stderr[-2000:]
+    env = dict(os.environ, TLM_LIB=str(mock))
+    r = subprocess.run([node, str(NODE_DIR / "test_runner_mock.js"), str(addon)], env=env, capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert "1..8" in r.stdout
