@@ -2329,10 +2329,10 @@ int tlm_model_describe(tlm_model* m, char* out, size_t len) {
                   " G=" + std::to_string(m->attn.G) + (m->attn.gqa ? " long=mfma" : "") + "]";
   if (m->ps_on) {
     const PsArgs a = ps_args(m);
-    const int To = a.To, nq = (a.Hq + 2 * a.Hkv) * a.kq, ng = (a.Tgu + a.mw - 1) / a.mw;
+    const int To = a.To, nq = 2 * a.Hkv * a.kq, ng = (a.Tgu + a.mw - 1) / a.mw;
     const int items = nq + a.Hq + To * a.ko + ng + To * a.ks;
     char b[320];
-    snprintf(b, sizeof b, " persistent[%d blocks, %d items: %d qkv (%d splits), %d att, %d o (%d splits), %d gate|up "
+    snprintf(b, sizeof b, " persistent[%d blocks, %d items: %d k|v (%d splits), %d q+att, %d o (%d splits), %d gate|up "
              "(32x%d), %d down (%d splits); %zu B LDS; variant nx=%d no=%d nd=%d]", m->ps_blocks, items, nq, a.kq,
              a.Hq, To * a.ko, a.ko, ng, a.mw, To * a.ks, a.ks, m->ps_smem, m->ps.nx, m->ps.no, m->ps.nd);
     s += b;

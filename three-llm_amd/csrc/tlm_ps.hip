@@ -285,13 +285,13 @@ __device__ __forceinline__ PsLinLds ps_lin_lds(float* sm) {
 }
 constexpr int ps_lin_floats(int ck, int nu, int r) { return kPsWaves * r * 64 + 2 * kPsWaves + 128 + kPsWaves * nu * ck; }
 
-// ---------------------------------------------------------------- QKV head --
-// Item i: head i / kq (rows of q head h, k head h - Hq or v head h - Hq - Hkv)
-// over the input chunks of split j = i % kq.  Each wave reads its chunks of
-// the whole residual (the norm needs all of it) and dots those in the split;
-// the norm's scale multiplies the summed dot products (a rotation and a
-// scale are linear).  Publishes the partial sums with RoPE applied and the
-// bias in split 0.
+// ------------------------------------------------------------ k and v heads --
+// Item i: k head i / kq or v head i / kq - Hkv (rows Hq + i / kq of q|k|v; the
+// attention items compute q themselves) over the input chunks of split
+// j = i % kq.  Each wave reads its chunks of the whole residual (the norm
+// needs all of it) and dots those in the split; the norm's scale multiplies
+// the summed dot products (a rotation and a scale are linear).  Publishes the
+// partial sums with RoPE applied (k) and the bias in split 0.
 template <int FMT, typename KT, int DT, int NX>
 __device__ __forceinline__ bool ps_qkv(const PsArgs& a, int l, int i, int pos, int token, unsigned seq, float* sm) {
   constexpr int NT = DT / 64;
@@ -299,9 +299,9 @@ __device__ __forceinline__ bool ps_qkv(const PsArgs& a, int l, int i, int pos, i
   const int lane = threadIdx.x & 63, wave = wave_id();
   const PsLinLds s = ps_lin_lds<CK, NX, NT>(sm);
   const TLM_GLOBAL PsLayer& Ly = gl(a.layers)[l];
-  const int hd = i / a.kq, j = i % a.kq;
+  const int hd = a.Hq + i / a.kq, j = i % a.kq;
   const int r0 = hd * DT;
-  const int kind = hd < a.Hq ? 0 : hd < a.Hq + a.Hkv ? 1 : 2;
+  const int kind = hd < a.Hq + a.Hkv ? 1 : 2;
   const int c0 = j * a.cq, c1 = min(c0 + a.cq, a.Cx);  // this split's input chunks
   PsRows<FMT, NX, NT> wr;
   wr.load(Ly.wqkv, Ly.sqkv, a.Cx, a.Tq, r0 / kTile, 0, c0, c1, wave);
@@ -363,29 +363,41 @@ __device__ __forceinline__ bool ps_qkv(const PsArgs& a, int l, int i, int pos, i
 }
 
 // -------------------------------------------------------------- attention --
-// Floats of one wave's LDS region: q, new k, new v, the pass's probabilities
+// Floats of one wave's LDS region: new k, new v, the pass's probabilities
 // and its V tile (4 KiB).
 template <typename KT, int DT>
 constexpr int ps_wave_floats() {
-  return (3 * DT + head_tiling(DT, sizeof(KT)).sub + 1024 + 3) & ~3;
+  return (2 * DT + head_tiling(DT, sizeof(KT)).sub + 1024 + 3) & ~3;
 }
 
-// Item h: query head h over the window [first, pos].  Wave w takes the
-// contiguous cached positions [first + w per, + per) below pos (per: a
-// multiple of the pass length); its first pass of K/V rows is requested
-// before it polls q: the sum of the kq published partials, read by every
-// active wave itself.  The last wave also takes the row at pos, after its
-// range: it polls the new k and v as well, appends them to the cache and
-// adds their score to its softmax (this token's cache write is not ordered
-// before the cache reads).  The 16 waves merge (max, sum, output) in LDS in
-// wave order.
+// Floats of the attention item's LDS before q: the wave regions, the merge
+// rows and the wave flags.
 template <typename KT, int DT>
-__device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first, int pos, unsigned seq, float* sm) {
+constexpr int ps_att_floats() {
+  return kPsWaves * ps_wave_floats<KT, DT>() + kPsWaves * (2 + DT) + kPsWaves;
+}
+
+// Item h: query head h over the window [first, pos].  The item computes q
+// itself, as a linear stage does (per-wave chunk dots of the residual, normed
+// after the dot, reduced once in LDS; bias; RoPE), so the only handoff it
+// waits for is the residual: the QKV items compute k and v alone.  Wave w
+// takes the contiguous cached positions [first + w per, + per) below pos
+// (per: a multiple of the pass length); its first pass of K/V rows is
+// requested before the residual wait.  The last wave also takes the row at
+// pos, after its range: it polls the new k and v (the sum of the kq published
+// partials, computed meanwhile by the QKV items), appends them to the cache
+// and adds their score to its softmax (this token's cache write is not
+// ordered before the cache reads).  The 16 waves merge (max, sum, output) in
+// LDS in wave order.
+template <int FMT, typename KT, int DT, int NX>
+__device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first, int pos, int token, unsigned seq,
+                                       float* sm) {
   constexpr int ESZ = sizeof(KT);
   constexpr HeadTiling TL = head_tiling(DT, ESZ);
   constexpr int LPP = TL.lpp, SUB = TL.sub, DL = TL.dl;
-  constexpr int EPL = DT / 64;
+  constexpr int EPL = DT / 64, NT = DT / 64;
   constexpr int KW = DL * ESZ / 4;
+  constexpr int CK = FMT == WF_Q4 ? 32 : 8;
   constexpr bool PAIRD = ESZ == 2 && DT == 128;
   // fp16 rows of 64: lane holds dims 2 (lane % 32), + 1 and sums half
   // lane / 32 of each pass's positions
@@ -400,13 +412,33 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
   const int t0 = min(first + wave * per, pos), t1 = min(t0 + per, pos);
   const bool active = t0 < t1;
   const bool own = wave == kPsWaves - 1;  // this wave takes the row at pos
-  float* q_l = sm + wave * WF;
-  float* kn = q_l + DT;
+  float* kn = sm + wave * WF;
   float* vn = kn + DT;
   float* p_l = vn + DT;
   KT* vt = reinterpret_cast<KT*>(p_l + SUB);
   float* mg = sm + kPsWaves * WF;  // [16][2 + DT] per-wave (max, sum, output)
   int* good = reinterpret_cast<int*>(mg + kPsWaves * (2 + DT));  // [16]
+  float* q_sh = sm + ps_att_floats<KT, DT>();  // [DT] q, read by every wave
+  // q's dot products: their LDS overlaps the wave regions, used only after
+  const PsLinLds s = ps_lin_lds<CK, NX, NT>(sm);
+  PsRows<FMT, NX, NT> wr;
+  wr.load(Ly.wqkv, Ly.sqkv, a.Cx, a.Tq, h * DT / kTile, 0, 0, a.Cx, wave);
+  float nw[NX];
+  wl_norm_weights<CK, NX>(Ly.attn_norm, a.Cx, wave, nw);
+  float bias[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) bias[t] = wave == 0 ? gl(Ly.bqkv)[h * DT + 64 * t + lane] : 0.f;
+  // RoPE factors of wave 0's elements (rotate-half of element d with its
+  // partner, TSLAttention.ts:168-250)
+  const int half = a.rd > 0 ? a.rd / 2 : 1;
+  float rc[NT], rs[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const int d = 64 * t + lane, jj = d < half ? d : d - half;
+    const bool rot = wave == 0 && d < a.rd;
+    rc[t] = rot ? gl(a.rope_cos)[(size_t)pos * half + jj] : 1.f;
+    rs[t] = rot ? gl(a.rope_sin)[(size_t)pos * half + jj] : 0.f;
+  }
   const KT* kh = reinterpret_cast<const KT*>(Ly.kc) + (size_t)hk * a.max_tokens * DT;
   const KT* vh = reinterpret_cast<const KT*>(Ly.vc) + (size_t)hk * a.max_tokens * DT;
   const int pl = lane / LPP, part = lane % LPP;
@@ -414,66 +446,48 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
   const int tc0 = active ? t0 : first, tc1 = active ? t1 : first + 1;  // in-range rows for idle waves
   ld.issue(kh, vh, tc0, tc1, pl, part, DT, DT * ESZ, lane);
   if (wave == 0) ps_stamp(a, l, PS_ATT, 0);
+  float x[NX];
+  bool ok = true;
+  if (l == 0) {
+    wl_embedding<CK, NX>(a, token, a.Cx, wave, x);
+  } else {
+    const u64* px = a.pub_x + (size_t)(l - 1) * kPsMaxKs * a.H;
+    ok = wl_gather<CK, NX>(0, a.Cx, a.ks, seq, [&](int p, int k) { return px + (size_t)p * a.H + k; }, wave, x, a.timeout);
+  }
+  if (wave == 0) ps_stamp(a, l, PS_ATT, 1);
+  {  // q = norm(x) Wq + b (TSLRMSNorm.ts:50-74, TSLLinear.ts:56-75), rotated
+    float xs[NX], ss = 0.f;
+    wl_stage<FMT, CK, NX>(x, nw, s.xw, xs, ss);
+#pragma unroll
+    for (int t = 0; t < NT; t++) s.red[(wave * NT + t) * 64 + lane] = wr.dot(t, s.xw, xs, 0, 0, a.Cx, wave);
+    if (lane == 0) s.ssw[wave] = ss;
+    if (!ps_all(ok, s.wf)) return false;
+    if (wave == 0) {
+      const float inv = rsqrtf(ps_sum16(s.ssw, 1) / (float)a.H + a.eps);
+      if (NT == 1 && half == 32) {  // the rotation partner of lane d is lane d ^ 32
+        const float val = bias[0] + inv * ps_sum16(s.red + lane, 64), partner = lane_swap32(val);
+        q_sh[lane] = val * rc[0] + (lane < 32 ? -partner : partner) * rs[0];
+      } else {
+#pragma unroll
+        for (int t = 0; t < NT; t++) s.out[64 * t + lane] = bias[t] + inv * ps_sum16(s.red + t * 64 + lane, NT * 64);
+        wave_lds_sync();
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+          const int d = 64 * t + lane;
+          float val = s.out[d];
+          if (d < a.rd) val = val * rc[t] + (d < half ? -s.out[d + half] : s.out[d - half]) * rs[t];
+          q_sh[d] = val;
+        }
+      }
+    }
+    lds_barrier();  // q visible to every wave; the dot products' LDS is free
+  }
   float m = -INFINITY, lsum = 0.f, o[NOE];
 #pragma unroll
   for (int e = 0; e < NOE; e++) o[e] = 0.f;
-  bool ok = true;
   if (active || own) {
-    const u64* pq = a.pub_qkv + (size_t)l * a.kq * a.Nqkv;
-    PsSpin spin(a.timeout);
-    for (;;) {  // lane d: element d (+ 64 e) of q and, in the own wave, of k and v
-      float sq[EPL], sk[EPL], sv[EPL];
-      bool got = true;
-#pragma unroll
-      for (int e = 0; e < EPL; e++) {
-        u64 wq[kPsMaxKs], wk[kPsMaxKs], wv[kPsMaxKs];
-        const int d = lane + 64 * e;
-#pragma unroll
-        for (int j = 0; j < kPsMaxKs; j++) {
-          const u64* pj = pq + (size_t)j * a.Nqkv;
-          const bool in = j < a.kq;
-          wq[j] = in ? ld_dev(pj + h * DT + d) : word(0.f, seq);
-          wk[j] = in && own ? ld_dev(pj + a.QS + hk * DT + d) : word(0.f, seq);
-          wv[j] = in && own ? ld_dev(pj + a.QS + a.Hkv * DT + hk * DT + d) : word(0.f, seq);
-        }
-        sq[e] = sk[e] = sv[e] = 0.f;
-#pragma unroll
-        for (int j = 0; j < kPsMaxKs; j++) {
-          got &= ((int)word_is(wq[j], seq) & (int)word_is(wk[j], seq) & (int)word_is(wv[j], seq)) != 0;
-          sq[e] += word_value(wq[j]);
-          sk[e] += word_value(wk[j]);
-          sv[e] += word_value(wv[j]);
-        }
-      }
-      if (__all(got)) {
-#pragma unroll
-        for (int e = 0; e < EPL; e++) {
-          const int d = lane + 64 * e;
-          q_l[d] = sq[e];
-          if (own) {  // k and v rounded like the cache
-            const KT kr = kv_store<KT>(sk[e]), vr = kv_store<KT>(sv[e]);
-            kn[d] = kv_load<KT>(&kr);
-            vn[d] = kv_load<KT>(&vr);
-            // the first query head of the group appends this position's k and
-            // v (TSLAttention.ts:252-286); every head of the group rounds the
-            // same sums
-            if (h % a.G == 0) {
-              glw(reinterpret_cast<KT*>(Ly.kc))[((size_t)hk * a.max_tokens + pos) * DT + d] = kr;
-              glw(reinterpret_cast<KT*>(Ly.vc))[((size_t)hk * a.max_tokens + pos) * DT + d] = vr;
-            }
-          }
-        }
-        break;
-      }
-      if (spin.tick() && spin.late()) {
-        ok = false;
-        break;
-      }
-    }
-    if (wave == 0) ps_stamp(a, l, PS_ATT, 1);
     if (ok && active) {
-      wave_lds_sync();
-      const float* qp = q_l + part * DL;  // this lane's q slice (LDS broadcast reads)
+      const float* qp = q_sh + part * DL;  // this lane's q slice (LDS broadcast reads)
       for (int tb = t0; tb < t1; tb += SUB) {
 #pragma unroll
         for (int j = 0; j < 4; j++) reinterpret_cast<uint4*>(vt)[j * 64 + lane] = ld.vs[j];
@@ -551,11 +565,59 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
         wave_lds_sync();
       }
     }
-    if (ok && own) {  // the row at pos: q · k over the wave, then one softmax step
+    if (ok && own) {  // the row at pos: its k and v, q · k over the wave, then one softmax step
+      const u64* pq = a.pub_qkv + (size_t)l * a.kq * a.Nqkv;
+      PsSpin spin(a.timeout);
+      for (;;) {  // lane d: element d (+ 64 e) of k and v
+        float sk[EPL], sv[EPL];
+        bool got = true;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) {
+          u64 wk[kPsMaxKs], wv[kPsMaxKs];
+          const int d = lane + 64 * e;
+#pragma unroll
+          for (int j = 0; j < kPsMaxKs; j++) {
+            const u64* pj = pq + (size_t)j * a.Nqkv;
+            const bool in = j < a.kq;
+            wk[j] = in ? ld_dev(pj + a.QS + hk * DT + d) : word(0.f, seq);
+            wv[j] = in ? ld_dev(pj + a.QS + a.Hkv * DT + hk * DT + d) : word(0.f, seq);
+          }
+          sk[e] = sv[e] = 0.f;
+#pragma unroll
+          for (int j = 0; j < kPsMaxKs; j++) {
+            got &= ((int)word_is(wk[j], seq) & (int)word_is(wv[j], seq)) != 0;
+            sk[e] += word_value(wk[j]);
+            sv[e] += word_value(wv[j]);
+          }
+        }
+        if (__all(got)) {
+#pragma unroll
+          for (int e = 0; e < EPL; e++) {  // k and v rounded like the cache
+            const int d = lane + 64 * e;
+            const KT kr = kv_store<KT>(sk[e]), vr = kv_store<KT>(sv[e]);
+            kn[d] = kv_load<KT>(&kr);
+            vn[d] = kv_load<KT>(&vr);
+            // the first query head of the group appends this position's k and
+            // v (TSLAttention.ts:252-286); every head of the group rounds the
+            // same sums
+            if (h % a.G == 0) {
+              glw(reinterpret_cast<KT*>(Ly.kc))[((size_t)hk * a.max_tokens + pos) * DT + d] = kr;
+              glw(reinterpret_cast<KT*>(Ly.vc))[((size_t)hk * a.max_tokens + pos) * DT + d] = vr;
+            }
+          }
+          break;
+        }
+        if (spin.tick() && spin.late()) {
+          ok = false;
+          break;
+        }
+      }
+    }
+    if (ok && own) {
       wave_lds_sync();
       float sp = 0.f;
 #pragma unroll
-      for (int e = 0; e < EPL; e++) sp = fmaf(q_l[lane + 64 * e], kn[lane + 64 * e], sp);
+      for (int e = 0; e < EPL; e++) sp = fmaf(q_sh[lane + 64 * e], kn[lane + 64 * e], sp);
       const float sc = wave_sum(sp) * a.scale;
       const float mn = fmaxf(m, sc);
       const float corr = m == -INFINITY ? 0.f : __expf(m - mn);
@@ -768,7 +830,7 @@ __global__ __launch_bounds__(kPsWaves * 64) void ps_token_kernel(const PsArgs* _
       if (st == PS_QKV)
         ok = ps_qkv<FMT, KT, DT, NX>(a, l, it, pos, token, seq, sm);
       else if (st == PS_ATT)
-        ok = ps_att<KT, DT>(a, l, it, first, pos, seq, sm);
+        ok = ps_att<FMT, KT, DT, NX>(a, l, it, first, pos, token, seq, sm);
       else if (st == PS_O)
         ok = ps_o<FMT, NO>(a, l, it, token, seq, sm);
       else if (st == PS_GU)
@@ -805,7 +867,7 @@ static const PsVariant kPsVariants[] = {
 // Items of each stage for a shape's splits.
 static void ps_counts(int H, int Hq, int Hkv, int Tgu, int kq, int ko, int mw, int ks, int* c) {
   const int To = H / 64;
-  c[PS_QKV] = (Hq + 2 * Hkv) * kq;
+  c[PS_QKV] = 2 * Hkv * kq;  // k and v heads (the attention items compute q)
   c[PS_ATT] = Hq;
   c[PS_O] = To * ko;
   c[PS_GU] = (Tgu + mw - 1) / mw;
@@ -910,7 +972,8 @@ size_t ps_smem_bytes(const PsShape& sh, int H, int QS) {
   const int CK = sh.fmt == WF_Q4 ? 32 : 8;
   const size_t esz = sh.kv_f32 ? 4 : 2;
   const int sub = head_tiling(sh.dt, (int)esz).sub;
-  const size_t att = (size_t)kPsWaves * ((3 * sh.dt + sub + 1024 + 3) & ~3) + kPsWaves * (2 + sh.dt) + kPsWaves;
+  // the attention item: wave regions, merge rows, flags, then q
+  const size_t att = (size_t)kPsWaves * ((2 * sh.dt + sub + 1024 + 3) & ~3) + kPsWaves * (2 + sh.dt) + kPsWaves + sh.dt;
   const size_t qkv = ps_lin_floats(CK, sh.nx, sh.dt / 64);
   const size_t o = ps_lin_floats(CK, sh.no, 1);
   const size_t gu = ps_lin_floats(CK, sh.nx, sh.mw);
