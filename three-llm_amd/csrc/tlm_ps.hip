@@ -649,23 +649,20 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
   if (!ps_all(ok, good)) return false;  // block-uniform
   if (wave == 0) ps_stamp(a, l, PS_ATT, 2);
   if (tid < DT) {
-    float mw[kPsWaves], lw[kPsWaves], ow[kPsWaves];
+    // lane w (and w + 16, + 32, + 48) takes wave w's (max, sum) and its
+    // scale exp(max_w - M): one exponential per lane instead of 16; the
+    // scales reach every lane as scalar operands
+    const int w16 = lane & 15;
+    const float mw = mg[w16 * (2 + DT)], lw = mg[w16 * (2 + DT) + 1];
+    float ow[kPsWaves];
 #pragma unroll
-    for (int w = 0; w < kPsWaves; w++) {
-      mw[w] = mg[w * (2 + DT)];
-      lw[w] = mg[w * (2 + DT) + 1];
-      ow[w] = mg[w * (2 + DT) + 2 + tid];
-    }
-    float M = -INFINITY;
+    for (int w = 0; w < kPsWaves; w++) ow[w] = mg[w * (2 + DT) + 2 + tid];
+    const float M = wave_max(mw);
+    const float f = mw == -INFINITY ? 0.f : __expf(mw - M);
+    const float L = wave_sum(lane < 16 ? lw * f : 0.f);
+    float od = 0.f;
 #pragma unroll
-    for (int w = 0; w < kPsWaves; w++) M = fmaxf(M, mw[w]);
-    float L = 0.f, od = 0.f;
-#pragma unroll
-    for (int w = 0; w < kPsWaves; w++) {
-      const float sc = mw[w] == -INFINITY ? 0.f : __expf(mw[w] - M);
-      L = fmaf(lw[w], sc, L);
-      od = fmaf(ow[w], sc, od);
-    }
+    for (int w = 0; w < kPsWaves; w++) od = fmaf(ow[w], readlane(f, w), od);
     st_dev(a.pub_o + (size_t)l * a.QS + h * DT + tid, word(od / L, seq));
   }
   if (wave == 0) ps_stamp(a, l, PS_ATT, 3);
