@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -223,6 +224,9 @@ struct tlm_model {
                      *ps_pub_h = nullptr;
   hipGraphExec_t g_ps_logits = nullptr, g_ps_prefill = nullptr;
   hipGraph_t graph_ps_logits = nullptr, graph_ps_prefill = nullptr;
+  // captured prompt chunks: batched chunks by row count, replayed chunks by
+  // (schedule, position count); captured on first use
+  std::map<int, std::pair<hipGraph_t, hipGraphExec_t>> pf_graphs, replay_graphs;
   // Tokens enqueued since the last clean check of the persistent schedule's
   // flags, in order: a token whose wait ran out or whose last residual was
   // not finite (fp16 input overflow) is recomputed with everything after it
@@ -1292,6 +1296,11 @@ void tlm_model_destroy(tlm_model* m) {
   if (!m) return;
   hipStreamSynchronize(m->ctx->stream);
   ps_register(m, false);
+  for (auto* gm : {&m->pf_graphs, &m->replay_graphs})
+    for (auto& kv : *gm) {
+      hipGraphExecDestroy(kv.second.second);
+      hipGraphDestroy(kv.second.first);
+    }
   if (m->g_ps_logits) hipGraphExecDestroy(m->g_ps_logits);
   if (m->g_ps_prefill) hipGraphExecDestroy(m->g_ps_prefill);
   if (m->graph_ps_logits) hipGraphDestroy(m->graph_ps_logits);
@@ -1735,60 +1744,76 @@ static RowsArgs rows_args(float* X, const float* part, int n_part, size_t pstrid
 // QKV GEMM (split-K slices) -> RoPE/cache append (folds the slices) -> flash
 // attention -> O GEMM (slices) -> fold + RMSNorm -> gate|up GEMM with SwiGLU ->
 // down GEMM (slices, folded by the next layer's first kernel).
-static int prefill_rows(tlm_model* m, const int* tokens, int p0, int M) {
+// Shapes of a batched chunk of M rows, with its row buffers allocated (on
+// first use; never while a graph is being captured).
+struct PfPlan {
+  GemmShape sq, sr, so, sg, sd;
+  bool rope_epi;
+};
+static int prefill_plan(tlm_model* m, int M, PfPlan* pp) {
   const tlm_model_desc& d = m->d;
   const int H = d.hidden_size, I = d.intermediate_size, D = d.head_dim;
   const int lf = wfmt(d.linear_fmt), cus = m->ctx->cus;
   const Layer& L0 = m->layers[0];
-  const GemmShape sq = gemm_shape(lf, GEMM_PART, M, m->Nqkv, H, cus);
+  pp->sq = gemm_shape(lf, GEMM_PART, M, m->Nqkv, H, cus);
   // small chunks (the K-wave QKV GEMM), head_dim 64, full rotary: RoPE and the
   // cache append run in the QKV GEMM's epilogue (no split-K slices, no rope_kv)
-  const GemmShape sr = gemm_shape(lf, GEMM_ROPE, M, m->Nqkv, H, cus);
-  const bool rope_epi = sr.ring && sr.kw && D == 64 && d.rotary_dim == 64;
-  const GemmShape so = gemm_shape(lf, GEMM_PART, M, H, m->QS, cus);
-  const GemmShape sg = gemm_shape(lf, GEMM_SWIGLU, M, L0.gu->T * kTile, H, cus);
-  const GemmShape sd = gemm_shape(lf, GEMM_PART, M, H, I, cus);
-  const size_t part = std::max({(size_t)sq.splits * M * m->Nqkv, (size_t)so.splits * M * H, (size_t)sd.splits * M * H});
-  int rc = prefill_alloc(m, M, part);
-  if (rc) return rc;
-  hipStream_t st = m->ctx->stream;
+  pp->sr = gemm_shape(lf, GEMM_ROPE, M, m->Nqkv, H, cus);
+  pp->rope_epi = pp->sr.ring && pp->sr.kw && D == 64 && d.rotary_dim == 64;
+  pp->so = gemm_shape(lf, GEMM_PART, M, H, m->QS, cus);
+  pp->sg = gemm_shape(lf, GEMM_SWIGLU, M, L0.gu->T * kTile, H, cus);
+  pp->sd = gemm_shape(lf, GEMM_PART, M, H, I, cus);
+  const size_t part = std::max({(size_t)pp->sq.splits * M * m->Nqkv, (size_t)pp->so.splits * M * H,
+                                (size_t)pp->sd.splits * M * H});
+  return prefill_alloc(m, M, part);
+}
+
+// Kernels of one batched chunk of M rows (the counterpart of the reference's
+// chunk of replays, DecoderTSLRunner.ts:504-530): the chunk starts at
+// position ctrl[C_POS] and its ids are m->prompt[ctrl[C_POS] - ctrl[C_BASE] ...],
+// so one captured sequence serves every chunk of M rows.  Returns the kernel
+// count (0: no kernel for a layer).
+static int prefill_enqueue(tlm_model* m, const PfPlan& pp, int M, hipStream_t st) {
+  const tlm_model_desc& d = m->d;
+  const int H = d.hidden_size, I = d.intermediate_size, D = d.head_dim;
+  const int lf = wfmt(d.linear_fmt);
   const size_t rowsH = (size_t)M * H;
-  launch_embed_rows(tokens, M, m->emb, d.embed_fmt == TLM_FMT_F32, H, m->pf_x, st);
+  launch_embed_rows(m->prompt, M, m->emb, d.embed_fmt == TLM_FMT_F32, H, m->pf_x, st, m->ctrl);
   // per layer: two row kernels, the QKV GEMM (+ rope_kv unless RoPE runs in its
   // epilogue), attention and three GEMMs; then the last fold
-  m->counts.kernel_launches += 1 + (uint64_t)d.num_layers * (rope_epi ? 7 : 8) + 1;
   for (int l = 0; l < d.num_layers; l++) {
     const Layer& L = m->layers[l];
     bool ok = true;
-    launch_rms_rows(rows_args(m->pf_x, m->pf_part, l ? sd.splits : 0, rowsH, H, L.attn_norm, d.rms_eps, m->pf_xn, m->pf_ovf),
+    launch_rms_rows(rows_args(m->pf_x, m->pf_part, l ? pp.sd.splits : 0, rowsH, H, L.attn_norm, d.rms_eps, m->pf_xn,
+                              m->pf_ovf),
                     M, st);
     GemmArgs g = gemm_args(L.qkv, m->pf_xn, H, M);
     g.ovf = m->pf_ovf;
-    if (rope_epi) {
+    if (pp.rope_epi) {
       g.bias = L.bqkv;
       g.Ch = m->pf_q;
       g.ldc = m->QS;
       g.rope_cos = m->attn.rope_cos;
       g.rope_sin = m->attn.rope_sin;
-      g.p0 = p0;
+      g.ctrl = m->ctrl;
       g.Hq = d.num_heads;
       g.Hkv = d.num_kv_heads;
       g.max_tokens = d.max_tokens;
       g.kc = static_cast<uint16_t*>(L.kc);
       g.vc = static_cast<uint16_t*>(L.vc);
-      ok = ok && launch_gemm(lf, GEMM_ROPE, sr, g, st);
+      ok = ok && launch_gemm(lf, GEMM_ROPE, pp.sr, g, st);
     } else {
       g.Cf = m->pf_part;
       g.ldc = m->Nqkv;
-      ok = ok && launch_gemm(lf, GEMM_PART, sq, g, st);
+      ok = ok && launch_gemm(lf, GEMM_PART, pp.sq, g, st);
       RopeKvArgs r;
       memset(&r, 0, sizeof r);
       r.qkv = m->pf_part;
-      r.n_part = sq.splits;
+      r.n_part = pp.sq.splits;
       r.pstride = (size_t)M * m->Nqkv;
       r.bias = L.bqkv;
       r.M = M;
-      r.p0 = p0;
+      r.ctrl = m->ctrl;
       r.Hq = d.num_heads;
       r.Hkv = d.num_kv_heads;
       r.D = D;
@@ -1810,7 +1835,7 @@ static int prefill_rows(tlm_model* m, const int* tokens, int p0, int M) {
     pa.vc = L.vc;
     pa.out = m->pf_att;
     pa.M = M;
-    pa.p0 = p0;
+    pa.ctrl = m->ctrl;
     pa.Hq = d.num_heads;
     pa.Hkv = d.num_kv_heads;
     pa.D = D;
@@ -1822,26 +1847,125 @@ static int prefill_rows(tlm_model* m, const int* tokens, int p0, int M) {
     g = gemm_args(L.o, m->pf_att, m->QS, M);
     g.Cf = m->pf_part;
     g.ldc = H;
-    ok = ok && launch_gemm(lf, GEMM_PART, so, g, st);
-    launch_rms_rows(rows_args(m->pf_x, m->pf_part, so.splits, rowsH, H, L.ffn_norm, d.rms_eps, m->pf_xn, m->pf_ovf), M, st);
+    ok = ok && launch_gemm(lf, GEMM_PART, pp.so, g, st);
+    launch_rms_rows(rows_args(m->pf_x, m->pf_part, pp.so.splits, rowsH, H, L.ffn_norm, d.rms_eps, m->pf_xn, m->pf_ovf),
+                    M, st);
     g = gemm_args(L.gu, m->pf_xn, H, M);
     g.ovf = m->pf_ovf;
     g.N = L.gu->T * kTile;
     g.Ch = m->pf_h;
     g.ldc = I;
     g.n_out = I;
-    ok = ok && launch_gemm(lf, GEMM_SWIGLU, sg, g, st);
+    ok = ok && launch_gemm(lf, GEMM_SWIGLU, pp.sg, g, st);
     g = gemm_args(L.down, m->pf_h, I, M);
     g.Cf = m->pf_part;
     g.ldc = H;
-    ok = ok && launch_gemm(lf, GEMM_PART, sd, g, st);
-    if (!ok) return fail(TLM_ERR_STATE, "TLMModel: no batched prefill kernel for layer %d", l);
-    CHECK_LAUNCH("TLMModel");
+    ok = ok && launch_gemm(lf, GEMM_PART, pp.sd, g, st);
+    if (!ok) return 0;
   }
   // the last layer's MLP output joins the residual rows
-  launch_rms_rows(rows_args(m->pf_x, m->pf_part, sd.splits, rowsH, H, nullptr, d.rms_eps, nullptr, nullptr), M, st);
-  CHECK_LAUNCH("TLMModel");
+  launch_rms_rows(rows_args(m->pf_x, m->pf_part, pp.sd.splits, rowsH, H, nullptr, d.rms_eps, nullptr, nullptr), M, st);
+  return 1 + d.num_layers * (pp.rope_epi ? 7 : 8) + 1;
+}
+
+// One batched chunk [p, p + M) of the prompt [start, end): the control block
+// names the chunk, then its captured graph (one per chunk size, captured on
+// first use) or, with graphs off, its kernels.
+static int prefill_rows(tlm_model* m, const int32_t* tokens, int start, int end, int p, int M) {
+  PfPlan pp;
+  int rc = prefill_plan(m, M, &pp);
+  if (rc) return rc;
+  hipStream_t st = m->ctx->stream;
+  launch_set_ctrl(m->ctrl, tokens[p], p, 0, start, end - start, emb_stage(m), st);
+  m->counts.kernel_launches++;
+  if (!m->use_graphs) {
+    const int k = prefill_enqueue(m, pp, M, st);
+    if (!k) return fail(TLM_ERR_STATE, "TLMModel: no batched prefill kernel for a layer");
+    m->counts.kernel_launches += k;
+    CHECK_LAUNCH("TLMModel");
+    return TLM_OK;
+  }
+  auto it = m->pf_graphs.find(M);
+  if (it == m->pf_graphs.end()) {
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    const int k = prefill_enqueue(m, pp, M, st);
+    hipError_t le = hipGetLastError();
+    HIP_TRY(hipStreamEndCapture(st, &g));
+    if (le != hipSuccess || !k) {
+      hipGraphDestroy(g);
+      if (!k) return fail(TLM_ERR_STATE, "TLMModel: no batched prefill kernel for a layer");
+      return fail(TLM_ERR_HIP, "TLMModel: launch during capture failed: %s", hipGetErrorString(le));
+    }
+    if (hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess) {
+      hipGraphDestroy(g);
+      return fail(TLM_ERR_HIP, "TLMModel: prefill graph instantiation failed");
+    }
+    it = m->pf_graphs.emplace(M, std::make_pair(g, ge)).first;
+  }
+  HIP_TRY(hipGraphLaunch(it->second.second, st));
+  m->counts.graph_launches++;
   return TLM_OK;
+}
+
+// The decode graph replayed over the n prompt positions [p, p + n) (set_ctrl
+// already named p; each step's prefill tail advances the position and stages
+// the next id): one captured graph of n token steps per schedule and size
+// (the reference encodes a chunk's replays into one submission,
+// DecoderTSLRunner.ts:472-480,504-530), or one launch per position when the
+// chunk crosses into the long-window kernels or graphs are off.
+static int replay_chunk(tlm_model* m, int p, int n) {
+  auto mode = [&](int pos) {
+    const bool lw = long_window(&m->attn, pos);
+    return m->ps_on && !m->ps_suspend && !lw ? 2 : lw ? 1 : 0;
+  };
+  const int md = mode(p);
+  bool same = true;
+  for (int i = 1; i < n && same; i++) same = mode(p + i) == md;
+  if (!m->use_graphs || !same || n < 2) {
+    int rc = TLM_OK;
+    for (int i = 0; i < n && !rc; i++) rc = run_token(m, false, p + i);
+    return rc;
+  }
+  hipStream_t st = m->ctx->stream;
+  const int key = md * 65536 + n;
+  auto it = m->replay_graphs.find(key);
+  if (it == m->replay_graphs.end()) {
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    const tlm_model_counts kept = m->counts;
+    HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    bool ok = true;
+    for (int i = 0; i < n; i++) {
+      if (md == 2) {
+        ok &= enqueue_ps(m, st, 0);
+      } else {
+        for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1, md == 1);
+        launch_prefill_advance(m->ctrl, m->prompt, emb_stage(m), st);
+      }
+    }
+    m->counts = kept;
+    hipError_t le = hipGetLastError();
+    HIP_TRY(hipStreamEndCapture(st, &g));
+    if (le != hipSuccess || !ok) {
+      hipGraphDestroy(g);
+      if (!ok) return fail(TLM_ERR_STATE, "TLMModel: no kernel variant for a stage of this model");
+      return fail(TLM_ERR_HIP, "TLMModel: launch during capture failed: %s", hipGetErrorString(le));
+    }
+    if (hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess) {
+      hipGraphDestroy(g);
+      return fail(TLM_ERR_HIP, "TLMModel: replay graph instantiation failed");
+    }
+    it = m->replay_graphs.emplace(key, std::make_pair(g, ge)).first;
+  }
+  m->host_pos = p + n - 1;
+  auto launch = [&]() -> int {
+    HIP_TRY(hipGraphLaunch(it->second.second, st));
+    m->counts.graph_launches++;
+    return TLM_OK;
+  };
+  return md == 2 ? ps_ordered(m, launch) : launch();
 }
 
 int tlm_model_set_prefill(tlm_model* m, int32_t min_rows, int32_t chunk) {
@@ -1876,7 +2000,7 @@ int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end)
     const int n = std::min(end - p, batched ? m->pf_chunk : end - p);
     bool replay = !(batched && n >= m->pf_min_rows);
     if (!replay) {
-      rc = prefill_rows(m, m->prompt + (p - start), p, n);
+      rc = prefill_rows(m, tokens, start, end, p, n);
       if (rc) return rc;
       // an fp16 activation of the chunk overflowed (or was NaN): the chunk's
       // cache rows are rewritten by the fp32 decode path
@@ -1899,7 +2023,7 @@ int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end)
       m->counts.replayed_positions += n;
       CHECK_LAUNCH("TLMModel");
       for (int i = 0; i < n; i++) redo_log(m, tokens[p + i], p + i, 1, false, false);
-      for (int i = 0; i < n && !rc; i++) rc = run_token(m, false, p + i);
+      rc = replay_chunk(m, p, n);
     }
     if (rc) return rc;
     p += n;

@@ -312,6 +312,8 @@ struct GemmArgs {
   uint16_t* kc;        // fp16 [Hkv][max_tokens][64] (this layer)
   uint16_t* vc;
   int* ovf;            // set to 1 when an fp16 output (h, q, k, v) is not finite; may be null
+  const int* ctrl;     // non-null: the first row's position is ctrl[C_POS] instead of p0 (a
+                       // captured prefill chunk serves every chunk of its size)
 };
 // Tile and split-K choice of one GEMM (gemm_shape is the only planner, so the
 // host sizes the slice buffers from the same numbers the launch uses).
@@ -342,6 +344,7 @@ struct PrefillAttnArgs {
   uint16_t* out;        // fp16 [M][Hq D]
   int M, p0, Hq, Hkv, D, G, max_tokens, window;
   float scale_log2;     // softmax scale * log2(e)
+  const int* ctrl;      // non-null: the first row's position is ctrl[C_POS] instead of p0
 };
 struct RopeKvArgs {
   const float* qkv;     // fp32 [n_part][M][Nqkv] split-K slices (summed here)
@@ -356,10 +359,15 @@ struct RopeKvArgs {
   void* vc;
   int kv_f32;
   int* ovf;             // set to 1 when an fp16 q, k or v is not finite; may be null
+  const int* ctrl;      // non-null: the first row's position is ctrl[C_POS] instead of p0
 };
 GemmShape gemm_shape(int fmt, int epi, int M, int N, int K, int cus);
 bool launch_gemm(int fmt, int epi, const GemmShape& sh, const GemmArgs& g, hipStream_t st);
-void launch_embed_rows(const int* tokens, int M, const void* emb, int f32, int H, float* X, hipStream_t st);
+// Row m of X = embedding row of tokens[m] (ctrl non-null: of
+// tokens[ctrl[C_POS] - ctrl[C_BASE] + m], the chunk of the prompt buffer at
+// the position the control block names).
+void launch_embed_rows(const int* tokens, int M, const void* emb, int f32, int H, float* X, hipStream_t st,
+                       const int* ctrl = nullptr);
 void launch_rms_rows(const RowsArgs& a, int M, hipStream_t st);
 void launch_rope_kv(const RopeKvArgs& a, hipStream_t st);
 bool launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t st);

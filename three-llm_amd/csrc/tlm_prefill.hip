@@ -705,6 +705,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     // d = l32 and d + 32 of its rows, the rotate-half pair of RoPE
     // (TSLAttention.ts:168-250 for one row; the rope_kv kernel's arithmetic)
     const int d = l32, kind = t0 < g.Hq ? 0 : t0 < g.Hq + g.Hkv ? 1 : 2;
+    const int p0 = g.ctrl ? g.ctrl[C_POS] : g.p0;
     const int hk = kind == 1 ? t0 - g.Hq : t0 - g.Hq - g.Hkv;
     const float b0 = g.bias ? g.bias[t0 * kTile + d] : 0.f, b1 = g.bias ? g.bias[t0 * kTile + d + 32] : 0.f;
 #pragma unroll
@@ -713,7 +714,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
       for (int e = 0; e < 4; e++) {
         const int row = rbase + 32 * t + e;
         if (row >= g.M) continue;
-        const int pos = g.p0 + row;
+        const int pos = p0 + row;
         const float x0 = f4_at(r[t][0], e) + b0, x1 = f4_at(r[t][1], e) + b1;
         float y0 = x0, y1 = x1;
         if (kind < 2) {
@@ -889,16 +890,17 @@ bool launch_gemm(int fmt, int epi, const GemmShape& sh, const GemmArgs& ga, hipS
 
 // X[m] = embedding row of tokens[m] in fp32 (DecoderWeights.ts:355-383 stages
 // the same rows for the replayed decode graph)
-__global__ void embed_rows_kernel(const int* tokens, const void* emb, int f32, int H, float* X) {
+__global__ void embed_rows_kernel(const int* tokens, const void* emb, int f32, int H, float* X, const int* ctrl) {
   const int m = blockIdx.x;
-  const size_t row = (size_t)tokens[m] * H;
+  const size_t row = (size_t)tokens[(ctrl ? ctrl[C_POS] - ctrl[C_BASE] : 0) + m] * H;
   for (int k = threadIdx.x; k < H; k += blockDim.x)
     X[(size_t)m * H + k] = f32 ? static_cast<const float*>(emb)[row + k]
                                : __half2float(static_cast<const __half*>(emb)[row + k]);
 }
 
-void launch_embed_rows(const int* tokens, int M, const void* emb, int f32, int H, float* X, hipStream_t st) {
-  hipLaunchKernelGGL(embed_rows_kernel, dim3(M), dim3(256), 0, st, tokens, emb, f32, H, X);
+void launch_embed_rows(const int* tokens, int M, const void* emb, int f32, int H, float* X, hipStream_t st,
+                       const int* ctrl) {
+  hipLaunchKernelGGL(embed_rows_kernel, dim3(M), dim3(256), 0, st, tokens, emb, f32, H, X, ctrl);
 }
 
 // Residual fold + RMSNorm per row (TSLRMSNorm.ts:18-81): x = X[m] + sum of
@@ -1006,10 +1008,11 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeKvArgs a) {
   bool rot;
   rope_pair(a, pi, i0, i1, rot, dr);
   const int half = a.rd / 2;
+  const int p0 = a.ctrl ? a.ctrl[C_POS] : a.p0;
   float x0[RKV_ROWS], x1[RKV_ROWS], c[RKV_ROWS], sn[RKV_ROWS];
 #pragma unroll
   for (int r = 0; r < RKV_ROWS; r++) {
-    const int m = min(blockIdx.x * RKV_ROWS + r, a.M - 1), pos = a.p0 + m;
+    const int m = min(blockIdx.x * RKV_ROWS + r, a.M - 1), pos = p0 + m;
     const float* row = a.qkv + (size_t)m * width;
     x0[r] = fold_slices(row, a.bias, a.n_part, a.pstride, i0);
     x1[r] = fold_slices(row, a.bias, a.n_part, a.pstride, i1);
@@ -1020,7 +1023,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeKvArgs a) {
   for (int r = 0; r < RKV_ROWS; r++) {
     const int m = blockIdx.x * RKV_ROWS + r;
     if (m >= a.M) break;
-    const int pos = a.p0 + m;
+    const int pos = p0 + m;
     rope_store(a, m, pos, i0, rot ? x0[r] * c[r] - x1[r] * sn[r] : x0[r]);
     rope_store(a, m, pos, i1, rot ? x1[r] * c[r] + x0[r] * sn[r] : x1[r]);
   }
@@ -1115,8 +1118,9 @@ __global__ __launch_bounds__(256 * NG) __attribute__((amdgpu_waves_per_eu(2))) v
   const int gw = (int)blockIdx.z * 4 + wave;
   const bool active = gw < a.G;
   const int h = hk * a.G + min(gw, a.G - 1);
-  const int qr = qt * 32 + l32, qpos = a.p0 + qr;
-  const int qlo = a.p0 + qt * 32, qhi = a.p0 + min(qt * 32 + 31, a.M - 1);
+  const int p0 = a.ctrl ? a.ctrl[C_POS] : a.p0;
+  const int qr = qt * 32 + l32, qpos = p0 + qr;
+  const int qlo = p0 + qt * 32, qhi = p0 + min(qt * 32 + 31, a.M - 1);
   const int kfirst = a.window > 0 ? max(0, qlo - a.window + 1) : 0;
   const int qfirst = a.window > 0 ? max(0, qpos - a.window + 1) : 0;
   const int QW = a.Hq * DT;
