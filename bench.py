@@ -286,12 +286,12 @@ def main():
     # inside decode steps over the same positions (a pair of HIP events on the
     # model stream around each launch); then the LM head the same way
     n_k = min(steps, args.kernel_iters)
-    # the persistent kernel runs a position whose attention window is at most
-    # 1024 positions; longer windows take the per-stage layer graph
-    win = hw.recipe.sliding_window or 0
-    persistent = "persistent[off]" not in runner.model.describe() and all(
-        (min(p + 1, win) if win > 0 else p + 1) <= 1024 for p in range(pos0, pos0 + n_k))
+    # which schedule ran: the library counts the token steps it ran on the
+    # persistent kernel (windows of at most 1024 positions; longer windows take
+    # the per-stage layer graph)
+    before = runner.model.counts()["persistent_tokens"]
     lay_ms = runner.model.time_layers(last, pos0, n_k)
+    persistent = runner.model.counts()["persistent_tokens"] - before == n_k
     lay_bytes = sum(layer_bytes(hw, pos0 + i) for i in range(n_k)) / n_k
     lay_bw = lay_bytes / (lay_ms * 1e-3)
     lm_ms = runner.model.time_head(last, pos0, n_k)
@@ -367,7 +367,7 @@ def main():
         "config": {"workload": wl.name, "prompt": wl.prompt_len, "decode": steps, "batch": 1,
                    "linears": wl.storage.linear + (" g32 fp16 scales" if wl.storage.linear == "q4" else ""),
                    "head": "fp16 tied" if hw.recipe.tied_embeddings else wl.storage.head, "kv": wl.storage.kv,
-                   "kv_prefill": wl.kv_prefill, "device": dev_name},
+                   "kv_prefill": wl.kv_prefill, "device": dev_name, "cus": cus},
         "roofline": {"bound": "hbm", "kernel": "ps_token_kernel" if persistent else "layer graph (per-stage kernels)",
                      "achieved": round(lay_bw / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": round(lay_bw / HBM_PEAK, 4),

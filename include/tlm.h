@@ -62,6 +62,10 @@ void tlm_close(tlm_ctx* ctx);
 int tlm_sync(tlm_ctx* ctx);
 /* Device name and compute-unit count (for reports). */
 int tlm_device_info(tlm_ctx* ctx, char* name, size_t name_len, int* cu_count);
+/* Free and total device memory of the context's GPU (hipMemGetInfo; for
+ * reports and for checking that an entry point allocates nothing).  No
+ * counterpart in the reference (the browser exposes no device memory). */
+int tlm_device_memory(tlm_ctx* ctx, size_t* free_bytes, size_t* total_bytes);
 
 /* Device buffers (thin helpers so hosts need no HIP binding of their own). */
 int tlm_alloc(tlm_ctx* ctx, size_t bytes, void** dptr);
@@ -300,6 +304,8 @@ typedef struct tlm_model_counts {
   uint64_t recomputed_positions; /* positions recomputed on the per-stage graph after a failed
                                     token of the persistent schedule (a wait ran out, or an
                                     fp16 input overflow of its q4 linears) */
+  uint64_t persistent_tokens;    /* token steps run on the persistent schedule (the rest ran
+                                    the per-stage graph: long windows, shapes without it) */
 } tlm_model_counts;
 int tlm_model_counts_read(tlm_model* model, tlm_model_counts* out);
 

@@ -510,7 +510,7 @@ napi_value ReadToken(napi_env env, napi_callback_info info) {
 }
 
 // {graphLaunches, kernelLaunches, prefillChunks, replayedPositions,
-// recomputedPositions}: the submission counts of the model
+// recomputedPositions, persistentTokens}: the submission counts of the model
 // (tlm_model_counts_read).
 napi_value ModelCounts(napi_env env, napi_callback_info info) {
   Args a(env, info);
@@ -523,7 +523,8 @@ napi_value ModelCounts(napi_env env, napi_callback_info info) {
                                                      {"kernelLaunches", c.kernel_launches},
                                                      {"prefillChunks", c.prefill_chunks},
                                                      {"replayedPositions", c.replayed_positions},
-                                                     {"recomputedPositions", c.recomputed_positions}};
+                                                     {"recomputedPositions", c.recomputed_positions},
+                                                     {"persistentTokens", c.persistent_tokens}};
   for (const auto& f : fields) {
     napi_value v;
     napi_create_double(env, (double)f.second, &v);

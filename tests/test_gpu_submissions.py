@@ -41,23 +41,23 @@ def test_reference_fixture_one_graph_per_token(ctx, hf_fixture):
     assert not runner.batchedPrefill  # head_dim 8: the fixture replays the decode graph
     m = runner.model
     assert m.counts() == {"graph_launches": 0, "kernel_launches": 0, "prefill_chunks": 0, "replayed_positions": 0,
-                            "recomputed_positions": 0}
+                            "recomputed_positions": 0, "persistent_tokens": 0}
     runner.computeToken(1, 0, True)
     b = m.counts()
     runner.computeToken(5, 1, True)
     assert _delta(m, b) == {"graph_launches": 1, "kernel_launches": 1, "prefill_chunks": 0, "replayed_positions": 0,
-                            "recomputed_positions": 0}
+                            "recomputed_positions": 0, "persistent_tokens": 0}
     runner.resetCache()
     b = m.counts()
     ids = hf_fixture["input_ids"]
     runner.prefillTokens(ids, 0, 18)  # chunks of 7, 7 and 4: one graph each
     assert _delta(m, b) == {"graph_launches": 3, "kernel_launches": 3, "prefill_chunks": 0,
-                            "replayed_positions": 18, "recomputed_positions": 0}
+                            "replayed_positions": 18, "recomputed_positions": 0, "persistent_tokens": 0}
     b = m.counts()
     out = runner.decodeGreedy(ids[18], 18, 4)  # the device feeds its own tokens: one write in all
     assert len(out) == 4
     assert _delta(m, b) == {"graph_launches": 4, "kernel_launches": 1, "prefill_chunks": 0, "replayed_positions": 0,
-                            "recomputed_positions": 0}
+                            "recomputed_positions": 0, "persistent_tokens": 0}
     b = m.counts()
     runner.readLogits()
     runner.readCandidates(3)
@@ -81,9 +81,10 @@ def test_batched_prefill_one_pass_per_chunk(ctx):
     # per chunk: the write naming it, then its captured row kernels (embedding
     # rows, per layer 7 or 8 row kernels and GEMMs, the last fold): one graph
     assert d == {"graph_launches": 3, "kernel_launches": 3, "prefill_chunks": 3, "replayed_positions": 0,
-                 "recomputed_positions": 0}
+                 "recomputed_positions": 0, "persistent_tokens": 0}
     b = m.counts()
     runner.computeToken(toks[-1], 18, True)
+    ps = int("persistent[off]" not in m.describe())  # the decode step's schedule
     assert _delta(m, b) == {"graph_launches": 1, "kernel_launches": 1, "prefill_chunks": 0, "replayed_positions": 0,
-                            "recomputed_positions": 0}
+                            "recomputed_positions": 0, "persistent_tokens": ps}
     runner.close()

@@ -3,7 +3,9 @@ attention; its query staging is the library's fixed device array) against
 tlm_op_attention_rows on the same inputs: the same kernels, so the outputs
 and the appended cache rows are bit-identical.  Two calls in a row, the
 second with fewer rows, so that the second reads only what it wrote into the
-shared array; then a call beyond the array's size is refused."""
+shared array; the free device memory is the same before and after each
+call (nothing allocated, nothing left behind); then a call beyond the
+array's size is refused."""
 import numpy as np
 import pytest
 
@@ -47,7 +49,13 @@ def test_noalloc_rows_equal_allocating_rows(ctx, heads, kv, D, theta, calls):
     for pos0, rows in calls:
         qkv = ctx.array(f32(rng.standard_normal((rows, width))))
         a = ref.rows(qkv, rows, pos0, ctx.buffer(2 * rows * heads * D)).read(np.uint16)
-        b = nal.rows_noalloc(qkv, rows, pos0, ctx.buffer(2 * rows * heads * D)).read(np.uint16)
+        out = ctx.buffer(2 * rows * heads * D)
+        ctx.sync()
+        free0 = ctx.memory()[0]
+        nal.rows_noalloc(qkv, rows, pos0, out)
+        ctx.sync()
+        assert ctx.memory()[0] == free0, "the allocation-free entry point changed the free device memory"
+        b = out.read(np.uint16)
         assert np.array_equal(a, b), f"rows {rows} at {pos0}: {int((a != b).sum())} fp16 outputs differ"
         ka, va = ref.read_cache(pos0 + rows)
         kb, vb = nal.read_cache(pos0 + rows)

@@ -468,7 +468,10 @@ int tlm_open(int device, tlm_ctx** out) {
   tlm_ctx* c = new tlm_ctx();
   c->device = device;
   c->cus = prop.multiProcessorCount;
-  snprintf(c->name, sizeof c->name, "%s (%s)", prop.name, prop.gcnArchName);
+  // the marketing name can be empty (a driver without the product table): the
+  // architecture and the CU count name the part then
+  snprintf(c->name, sizeof c->name, "%s (%s, %d CUs)", prop.name[0] ? prop.name : "AMD Instinct", prop.gcnArchName,
+           prop.multiProcessorCount);
   hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipMalloc(&c->arg_val, 4096 * sizeof(float));
   if (e == hipSuccess) e = hipMalloc(&c->arg_idx, 4096 * sizeof(int));
@@ -508,6 +511,13 @@ int tlm_device_info(tlm_ctx* ctx, char* name, size_t name_len, int* cu_count) {
   if (!ctx) return fail(TLM_ERR_INVALID, "TLMContext: null context");
   if (name && name_len) snprintf(name, name_len, "%s", ctx->name);
   if (cu_count) *cu_count = ctx->cus;
+  return TLM_OK;
+}
+
+int tlm_device_memory(tlm_ctx* ctx, size_t* free_bytes, size_t* total_bytes) {
+  if (!ctx || !free_bytes || !total_bytes) return fail(TLM_ERR_INVALID, "TLMContext: null argument");
+  HIP_TRY(hipSetDevice(ctx->device));
+  HIP_TRY(hipMemGetInfo(free_bytes, total_bytes));
   return TLM_OK;
 }
 
@@ -1597,6 +1607,7 @@ static int run_token(tlm_model* m, bool logits, int pos) {
   const bool lw = long_window(&m->attn, pos);
   m->host_pos = pos;
   if (m->ps_on && !m->ps_suspend && !lw) {  // the persistent schedule
+    m->counts.persistent_tokens++;
     return ps_ordered(m, [&]() -> int {
       if (m->use_graphs) {
         HIP_TRY(hipGraphLaunch(logits ? m->g_ps_logits : m->g_ps_prefill, st));
@@ -1963,6 +1974,7 @@ static int replay_chunk(tlm_model* m, int p, int n) {
   auto launch = [&]() -> int {
     HIP_TRY(hipGraphLaunch(it->second.second, st));
     m->counts.graph_launches++;
+    if (md == 2) m->counts.persistent_tokens += (uint64_t)n;
     return TLM_OK;
   };
   return md == 2 ? ps_ordered(m, launch) : launch();
@@ -2313,6 +2325,7 @@ static int time_step_parts(tlm_model* m, int32_t token, int32_t position, int n,
       if (ps) {
         ok &= launch_ps_token(m->ps, m->ps_blocks, m->ps_smem, m->ps_args_dev, st);
         m->counts.kernel_launches++;
+        m->counts.persistent_tokens++;
       } else if (m->use_graphs) {
         HIP_TRY(hipGraphLaunch(m->g_layers[lw], st));
         m->counts.graph_launches++;
@@ -2421,6 +2434,7 @@ int tlm_trace_decode(tlm_model* m, int32_t token, int32_t position, int n, uint6
       ok &= launch_ps_token(m->ps, m->ps_blocks, m->ps_smem, ad, st);
       ok &= enqueue_head(m, st, true, nullptr, true);
       m->counts.kernel_launches++;
+      m->counts.persistent_tokens++;
       return TLM_OK;
     });
     if (rc) break;

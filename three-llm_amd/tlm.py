@@ -23,7 +23,8 @@ TLM_ERR_INVALID, TLM_ERR_HIP, TLM_ERR_OOM, TLM_ERR_STATE, TLM_ERR_RANGE = -1, -2
 
 # exported symbols (checked by the CPU test suite against include/tlm.h)
 EXPORTS = [
-    "tlm_abi_version", "tlm_last_error", "tlm_open", "tlm_close", "tlm_sync", "tlm_device_info", "tlm_alloc",
+    "tlm_abi_version", "tlm_last_error", "tlm_open", "tlm_close", "tlm_sync", "tlm_device_info", "tlm_device_memory",
+    "tlm_alloc",
     "tlm_free", "tlm_upload", "tlm_download", "tlm_copy", "tlm_linear_create", "tlm_linear_destroy", "tlm_linear_dequant",
     "tlm_op_linear", "tlm_op_linear_rows", "tlm_op_rmsnorm", "tlm_op_silu_mul", "tlm_op_gated_mlp", "tlm_attn_create", "tlm_attn_destroy",
     "tlm_op_attention", "tlm_op_attention_rows", "tlm_op_attention_rows_noalloc", "tlm_attn_reset", "tlm_attn_read_cache", "tlm_op_logits", "tlm_op_argmax",
@@ -64,7 +65,7 @@ class ModelDesc(ctypes.Structure):
 class ModelCounts(ctypes.Structure):
     _fields_ = [("graph_launches", ctypes.c_uint64), ("kernel_launches", ctypes.c_uint64),
                 ("prefill_chunks", ctypes.c_uint64), ("replayed_positions", ctypes.c_uint64),
-                ("recomputed_positions", ctypes.c_uint64)]
+                ("recomputed_positions", ctypes.c_uint64), ("persistent_tokens", ctypes.c_uint64)]
 
 
 _lib = None
@@ -87,6 +88,7 @@ def lib():
             "tlm_close": ([VP], None),
             "tlm_sync": ([VP], ctypes.c_int),
             "tlm_device_info": ([VP, ctypes.c_char_p, sz, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
+            "tlm_device_memory": ([VP, ctypes.POINTER(sz), ctypes.POINTER(sz)], ctypes.c_int),
             "tlm_alloc": ([VP, sz, ctypes.POINTER(VP)], ctypes.c_int),
             "tlm_free": ([VP, VP], ctypes.c_int),
             "tlm_upload": ([VP, VP, VP, sz], ctypes.c_int),
@@ -239,6 +241,12 @@ class Context:
         cus = ctypes.c_int()
         check(lib().tlm_device_info(self.ptr, name, 256, ctypes.byref(cus)))
         return name.value.decode(), cus.value
+
+    def memory(self):
+        """(free, total) bytes of device memory."""
+        free, total = ctypes.c_size_t(), ctypes.c_size_t()
+        check(lib().tlm_device_memory(self.ptr, ctypes.byref(free), ctypes.byref(total)))
+        return free.value, total.value
 
     def buffer(self, nbytes: int) -> Buffer:
         return Buffer(self, nbytes)
