@@ -60,7 +60,8 @@ async function main() {
     const out = await generateGreedy(runner, c.prompt, c.stream.length);
     const same = checkStream(out.generated, c, label);
     console.log(`ok ${++passed} - ${label}: greedy stream = oracle for ${same} of ${c.stream.length} tokens`);
-    // the device-fed loop equals the host loop; one graph launch per token
+    // the device-fed loop equals the host loop; per token one graph launch, or
+    // on the persistent schedule its three kernels (layers, LM head, merge)
     runner.resetCache();
     await runner.prefillTokens(c.prompt, 0, c.prompt.length - 1);
     runner.computeToken(c.prompt[c.prompt.length - 1], c.prompt.length - 1, true);
@@ -72,12 +73,13 @@ async function main() {
     const us = Number(process.hrtime.bigint() - t1) / 1e3;
     const after = runner.counts();
     assert.deepStrictEqual([first].concat(dev), out.generated.slice(0, n + 1));
+    const ps = after.persistentTokens - before.persistentTokens;
     if (process.env.TLM_GRAPHS !== '0') {  // TLM_GRAPHS=0 (profiling) launches each kernel directly
-      assert.strictEqual(after.graphLaunches - before.graphLaunches, n);
-      assert.strictEqual(after.kernelLaunches - before.kernelLaunches, 1);
+      assert.strictEqual(after.graphLaunches - before.graphLaunches, n - ps);
+      assert.strictEqual(after.kernelLaunches - before.kernelLaunches, 1 + 3 * ps);
     }
     console.log(`ok ${++passed} - ${label}: device loop = host loop, ${after.graphLaunches - before.graphLaunches} ` +
-                `graph launches (${(us / n).toFixed(1)} us/token incl. one sync)`);
+                `graph launches, ${ps} persistent tokens (${(us / n).toFixed(1)} us/token incl. one sync)`);
     // device top-k: the k best logits in the greedy order (TSLLogitSampler),
     // and generate() with top-k sampling draws its tokens from those lists
     runner.resetCache();

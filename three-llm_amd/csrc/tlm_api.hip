@@ -193,6 +193,7 @@ struct tlm_model {
   float* logits = nullptr;
   float* arg_val = nullptr;
   int* arg_idx = nullptr;
+  unsigned long long* arg_key = nullptr;  // the LM head's folded argmax (zero between launches)
   float* cand_v = nullptr;  // top-k candidates of the last logits (kTopkMax)
   int* cand_i = nullptr;
   // attention (shared by the layers; they run one after another)
@@ -222,8 +223,10 @@ struct tlm_model {
   PsArgs* ps_args_dev = nullptr;  // the kernel's arguments (device memory)
   unsigned long long *ps_pub_x = nullptr, *ps_pub_qkv = nullptr, *ps_pub_o = nullptr, *ps_pub_xm = nullptr,
                      *ps_pub_h = nullptr;
-  hipGraphExec_t g_ps_logits = nullptr, g_ps_prefill = nullptr;
-  hipGraph_t graph_ps_logits = nullptr, graph_ps_prefill = nullptr;
+  // x0_stale: a persistent step chose the current token without staging its
+  // embedding row in x0, which the per-stage graph's first layer reads
+  // (stage_x0 does it before that graph's next step)
+  bool x0_stale = false;
   // captured prompt chunks: batched chunks by row count, replayed chunks by
   // (schedule, position count); captured on first use
   std::map<int, std::pair<hipGraph_t, hipGraphExec_t>> pf_graphs, replay_graphs;
@@ -1288,6 +1291,7 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
   M_TRY(model_alloc((void**)&m->logits, sizeof(float) * d->vocab_size));
   M_TRY(model_alloc((void**)&m->arg_val, sizeof(float) * 4096));
   M_TRY(model_alloc((void**)&m->arg_idx, sizeof(int) * 4096));
+  M_TRY(model_alloc((void**)&m->arg_key, sizeof(unsigned long long)));
   M_TRY(model_alloc((void**)&m->cand_v, sizeof(float) * kTopkMax));
   M_TRY(model_alloc((void**)&m->cand_i, sizeof(int) * kTopkMax));
   if (rc == TLM_OK) rc = ps_setup(m);
@@ -1311,10 +1315,6 @@ void tlm_model_destroy(tlm_model* m) {
       hipGraphExecDestroy(kv.second.second);
       hipGraphDestroy(kv.second.first);
     }
-  if (m->g_ps_logits) hipGraphExecDestroy(m->g_ps_logits);
-  if (m->g_ps_prefill) hipGraphExecDestroy(m->g_ps_prefill);
-  if (m->graph_ps_logits) hipGraphDestroy(m->graph_ps_logits);
-  if (m->graph_ps_prefill) hipGraphDestroy(m->graph_ps_prefill);
   for (int i = 0; i < 2; i++) {
     if (m->g_logits[i]) hipGraphExecDestroy(m->g_logits[i]);
     if (m->g_prefill[i]) hipGraphExecDestroy(m->g_prefill[i]);
@@ -1337,7 +1337,7 @@ void tlm_model_destroy(tlm_model* m) {
   tlm_linear_destroy(m->head);
   attn_free(&m->attn, false);
   void* bufs[] = {m->emb, m->final_norm, m->ctrl, m->tokens_out, m->prompt, m->xa, m->x0, m->xf, m->attn_out,
-                  m->pq, m->po, m->rb, m->logits, m->arg_val, m->arg_idx, m->cand_v, m->cand_i, m->pf_x, m->pf_part, m->pf_xn,
+                  m->pq, m->po, m->rb, m->logits, m->arg_val, m->arg_idx, m->arg_key, m->cand_v, m->cand_i, m->pf_x, m->pf_part, m->pf_xn,
                   m->pf_q, m->pf_att, m->pf_h, m->pf_ovf, m->ps_layers, m->ps_roles, m->ps_pub_x, m->ps_pub_qkv,
                   m->ps_pub_o, m->ps_pub_xm, m->ps_pub_h, m->ps_args_dev};
   for (void* p : bufs) hipFree(p);
@@ -1413,6 +1413,22 @@ int tlm_model_upload(tlm_model* m, int tensor, int layer, const void* host, size
 
 static EmbStage emb_stage(const tlm_model* m) {
   return EmbStage{m->emb, m->d.embed_fmt == TLM_FMT_F32 ? 1 : 0, m->d.hidden_size, m->x0};
+}
+
+// The host's token/position write (step 0), which also stages the token's
+// embedding row.
+static void set_ctrl(tlm_model* m, int token, int pos, int base, int len, hipStream_t st) {
+  launch_set_ctrl(m->ctrl, token, pos, 0, base, len, emb_stage(m), st);
+  m->x0_stale = false;
+}
+
+// Before a step on the per-stage graph: the embedding row of the token that a
+// persistent step chose (its LM head and prefill advance do not stage it).
+static void stage_x0(tlm_model* m, hipStream_t st) {
+  if (!m->x0_stale) return;
+  launch_stage_ctrl(m->ctrl, emb_stage(m), st);
+  m->counts.kernel_launches++;
+  m->x0_stale = false;
 }
 
 // Kernels of one layer.  which: -1 all; otherwise a single stage (timing).
@@ -1516,12 +1532,16 @@ static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, hipEvent_t*
   a.logits = m->logits;
   a.arg_val = m->arg_val;
   a.arg_idx = m->arg_idx;
+  a.arg_key = m->arg_key;  // the blocks fold their bests as they finish
   if (ev) hipEventRecord(ev[0], st);
   if (!launch_lm_head(wfmt(m->head->fmt), PRO_RMSF, m->lm_plan.waves, m->lm_plan.nch, dim3(m->lm_plan.gx), a, st))
     return false;
   if (ev) hipEventRecord(ev[1], st);
-  launch_argmax_merge(m->arg_val, m->arg_idx, m->lm_plan.gx, m->ctrl, advance ? m->tokens_out : nullptr,
-                      advance ? 1 : 0, d.max_tokens, emb_stage(m), st, ps ? 1 : 0);
+  // the persistent kernel reads its token's embedding row itself: the row is
+  // staged only before a step on the per-stage graph (stage_x0)
+  launch_greedy_pick(m->arg_key, m->ctrl, advance ? m->tokens_out : nullptr, advance ? 1 : 0, d.max_tokens,
+                     ps ? EmbStage{} : emb_stage(m), st, ps ? 1 : 0);
+  m->x0_stale = ps;
   m->counts.kernel_launches += 2;
   return true;
 }
@@ -1532,7 +1552,8 @@ static bool enqueue_ps(tlm_model* m, hipStream_t st, int tail) {
   if (!launch_ps_token(m->ps, m->ps_blocks, m->ps_smem, m->ps_args_dev, st)) return false;
   m->counts.kernel_launches++;
   if (tail == 1) return enqueue_head(m, st, true, nullptr, true);
-  launch_prefill_advance(m->ctrl, m->prompt, emb_stage(m), st, 1);
+  launch_prefill_advance(m->ctrl, m->prompt, EmbStage{}, st, 1);
+  m->x0_stale = true;
   m->counts.kernel_launches++;
   return true;
 }
@@ -1542,10 +1563,11 @@ static bool enqueue_ps(tlm_model* m, hipStream_t st, int tail) {
 enum GraphTail { TAIL_PREFILL = 0, TAIL_LOGITS = 1, TAIL_NONE = 2 };
 
 // (Kernels recorded into a graph are not handed to the stream: the capture
-// functions leave the model's counts as they found them.)
+// functions leave the model's counts and x0 state as they found them.)
 static int capture(tlm_model* m, int tail, bool long_win, hipGraph_t* g, hipGraphExec_t* ge) {
   hipStream_t st = m->ctx->stream;
   const tlm_model_counts kept = m->counts;
+  const bool stale = m->x0_stale;
   HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
   bool ok = true;
   for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1, long_win);
@@ -1554,24 +1576,11 @@ static int capture(tlm_model* m, int tail, bool long_win, hipGraph_t* g, hipGrap
   else if (tail == TAIL_PREFILL)
     launch_prefill_advance(m->ctrl, m->prompt, emb_stage(m), st);
   m->counts = kept;
+  m->x0_stale = stale;
   hipError_t le = hipGetLastError();
   HIP_TRY(hipStreamEndCapture(st, g));
   if (le != hipSuccess) return fail(TLM_ERR_HIP, "TLMModel: launch during capture failed: %s", hipGetErrorString(le));
   if (!ok) return fail(TLM_ERR_STATE, "TLMModel: no kernel variant for a stage of this model");
-  HIP_TRY(hipGraphInstantiate(ge, *g, nullptr, nullptr, 0));
-  return TLM_OK;
-}
-
-static int capture_ps(tlm_model* m, int tail, hipGraph_t* g, hipGraphExec_t* ge) {
-  hipStream_t st = m->ctx->stream;
-  const tlm_model_counts kept = m->counts;
-  HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-  const bool ok = enqueue_ps(m, st, tail);
-  m->counts = kept;
-  hipError_t le = hipGetLastError();
-  HIP_TRY(hipStreamEndCapture(st, g));
-  if (le != hipSuccess) return fail(TLM_ERR_HIP, "TLMModel: launch during capture failed: %s", hipGetErrorString(le));
-  if (!ok) return fail(TLM_ERR_STATE, "TLMModel: no persistent kernel variant for this model");
   HIP_TRY(hipGraphInstantiate(ge, *g, nullptr, nullptr, 0));
   return TLM_OK;
 }
@@ -1591,10 +1600,6 @@ int tlm_model_finalize(tlm_model* m) {
     rc = capture(m, TAIL_LOGITS, lw, &m->graph_logits[lw], &m->g_logits[lw]);
     if (rc == TLM_OK) rc = capture(m, TAIL_PREFILL, lw, &m->graph_prefill[lw], &m->g_prefill[lw]);
   }
-  if (rc == TLM_OK && m->ps_on) {
-    rc = capture_ps(m, 1, &m->graph_ps_logits, &m->g_ps_logits);
-    if (rc == TLM_OK) rc = capture_ps(m, 0, &m->graph_ps_prefill, &m->g_ps_prefill);
-  }
   if (rc) return rc;
   m->finalized = true;
   return TLM_OK;
@@ -1607,18 +1612,16 @@ static int run_token(tlm_model* m, bool logits, int pos) {
   const bool lw = long_window(&m->attn, pos);
   m->host_pos = pos;
   if (m->ps_on && !m->ps_suspend && !lw) {  // the persistent schedule
+    // its two kernels enqueued directly: a graph launch of the same pair costs
+    // ~4.6 us more per token here (Qwen2.5-0.5B decode: 328.3 -> 323.7 us)
     m->counts.persistent_tokens++;
     return ps_ordered(m, [&]() -> int {
-      if (m->use_graphs) {
-        HIP_TRY(hipGraphLaunch(logits ? m->g_ps_logits : m->g_ps_prefill, st));
-        m->counts.graph_launches++;
-        return TLM_OK;
-      }
       if (!enqueue_ps(m, st, logits ? 1 : 0)) return fail(TLM_ERR_STATE, "TLMModel: no persistent kernel variant");
       CHECK_LAUNCH("TLMModel");
       return TLM_OK;
     });
   }
+  stage_x0(m, st);
   if (m->use_graphs) {
     HIP_TRY(hipGraphLaunch(logits ? m->g_logits[lw] : m->g_prefill[lw], st));
     m->counts.graph_launches++;
@@ -1664,7 +1667,7 @@ int tlm_compute_token(tlm_model* m, int32_t token, int32_t position, int flags) 
   rc = tlm_model_finalize(m);
   if (rc) return rc;
   hipStream_t st = m->ctx->stream;
-  launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);  // the token/position write
+  set_ctrl(m, token, position, 0, 0, st);  // the token/position write
   m->counts.kernel_launches++;
   CHECK_LAUNCH("TLMModel");
   redo_log(m, token, position, 1, (flags & TLM_LOGITS) != 0, false);
@@ -1887,7 +1890,7 @@ static int prefill_rows(tlm_model* m, const int32_t* tokens, int start, int end,
   int rc = prefill_plan(m, M, &pp);
   if (rc) return rc;
   hipStream_t st = m->ctx->stream;
-  launch_set_ctrl(m->ctrl, tokens[p], p, 0, start, end - start, emb_stage(m), st);
+  set_ctrl(m, tokens[p], p, start, end - start, st);
   m->counts.kernel_launches++;
   if (!m->use_graphs) {
     const int k = prefill_enqueue(m, pp, M, st);
@@ -1946,6 +1949,7 @@ static int replay_chunk(tlm_model* m, int p, int n) {
     hipGraph_t g = nullptr;
     hipGraphExec_t ge = nullptr;
     const tlm_model_counts kept = m->counts;
+    const bool stale = m->x0_stale;
     HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
     bool ok = true;
     for (int i = 0; i < n; i++) {
@@ -1957,6 +1961,7 @@ static int replay_chunk(tlm_model* m, int p, int n) {
       }
     }
     m->counts = kept;
+    m->x0_stale = stale;
     hipError_t le = hipGetLastError();
     HIP_TRY(hipStreamEndCapture(st, &g));
     if (le != hipSuccess || !ok) {
@@ -1971,10 +1976,12 @@ static int replay_chunk(tlm_model* m, int p, int n) {
     it = m->replay_graphs.emplace(key, std::make_pair(g, ge)).first;
   }
   m->host_pos = p + n - 1;
+  if (md != 2) stage_x0(m, st);
   auto launch = [&]() -> int {
     HIP_TRY(hipGraphLaunch(it->second.second, st));
     m->counts.graph_launches++;
     if (md == 2) m->counts.persistent_tokens += (uint64_t)n;
+    m->x0_stale = md == 2;  // the persistent advance does not stage the row
     return TLM_OK;
   };
   return md == 2 ? ps_ordered(m, launch) : launch();
@@ -2030,7 +2037,7 @@ int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end)
       if (!replay) m->counts.prefill_chunks++;
     }
     if (replay) {  // the decode graph replayed per position
-      launch_set_ctrl(m->ctrl, tokens[p], p, 0, start, end - start, emb_stage(m), st);
+      set_ctrl(m, tokens[p], p, start, end - start, st);
       m->counts.kernel_launches++;
       m->counts.replayed_positions += n;
       CHECK_LAUNCH("TLMModel");
@@ -2087,7 +2094,7 @@ static int ps_recover(tlm_model* m, int err) {
   for (const RedoEntry& e : log) {
     rc = kv_clear(m, e.pos, e.n);
     if (rc) break;
-    launch_set_ctrl(m->ctrl, e.token, e.pos, 0, 0, 0, emb_stage(m), st);
+    set_ctrl(m, e.token, e.pos, 0, 0, st);
     m->counts.kernel_launches++;
     for (int i = 0; i < e.n && rc == TLM_OK; i++) rc = run_token(m, e.logits, e.pos + i);
     if (rc) break;
@@ -2179,7 +2186,7 @@ int tlm_decode_greedy(tlm_model* m, int32_t token, int32_t position, int n, int3
   rc = tlm_model_finalize(m);
   if (rc) return rc;
   hipStream_t st = m->ctx->stream;
-  launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
+  set_ctrl(m, token, position, 0, 0, st);
   m->counts.kernel_launches++;
   CHECK_LAUNCH("TLMModel");
   redo_log(m, token, position, n, true, true);
@@ -2267,7 +2274,7 @@ int tlm_time_decode(tlm_model* m, int32_t token, int32_t position, int warmup, i
   rc = tlm_model_finalize(m);
   if (rc) return rc;
   hipStream_t st = m->ctx->stream;
-  launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
+  set_ctrl(m, token, position, 0, 0, st);
   m->counts.kernel_launches++;
   redo_log(m, token, position, warmup + n, true, true);
   for (int i = 0; i < warmup; i++) {
@@ -2312,7 +2319,7 @@ static int time_step_parts(tlm_model* m, int32_t token, int32_t position, int n,
     }
   std::vector<hipEvent_t> ev(4 * (size_t)n, nullptr);
   for (auto& e : ev) HIP_TRY(hipEventCreate(&e));
-  launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
+  set_ctrl(m, token, position, 0, 0, st);
   m->counts.kernel_launches++;
   redo_log(m, token, position, n, true, true);
   bool ok = true;
@@ -2321,6 +2328,7 @@ static int time_step_parts(tlm_model* m, int32_t token, int32_t position, int n,
     const bool ps = m->ps_on && !lw;
     m->host_pos = position + i;
     auto step = [&]() -> int {
+      if (!ps) stage_x0(m, st);
       hipEventRecord(ev[4 * (size_t)i], st);
       if (ps) {
         ok &= launch_ps_token(m->ps, m->ps_blocks, m->ps_smem, m->ps_args_dev, st);
@@ -2425,7 +2433,7 @@ int tlm_trace_decode(tlm_model* m, int32_t token, int32_t position, int n, uint6
   a.trace = tr;
   hipStream_t st = m->ctx->stream;
   bool ok = hipMemcpy(ad, &a, sizeof a, hipMemcpyHostToDevice) == hipSuccess;
-  launch_set_ctrl(m->ctrl, token, position, 0, 0, 0, emb_stage(m), st);
+  set_ctrl(m, token, position, 0, 0, st);
   m->counts.kernel_launches++;
   redo_log(m, token, position, n, true, true);
   for (int i = 0; i < n && ok; i++) {

@@ -138,6 +138,19 @@ __device__ __forceinline__ void argmax_step(float& v, int& i) {
 }
 
 // Best (score, id) of the wave, in every lane.
+// A 64-bit key whose unsigned order is the greedy order of (score, id):
+// the higher score, then the lower id (better()); -0 counts as +0.
+__device__ __forceinline__ unsigned long long greedy_key(float v, int i) {
+  const unsigned u = __float_as_uint(v == 0.f ? 0.f : v);
+  const unsigned o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)o << 32) | (0xffffffffu - (unsigned)i);
+}
+__device__ __forceinline__ float greedy_key_value(unsigned long long k) {
+  const unsigned o = (unsigned)(k >> 32);
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+__device__ __forceinline__ int greedy_key_id(unsigned long long k) { return (int)(0xffffffffu - (unsigned)k); }
+
 __device__ inline void wave_argmax(float& v, int& i) {
   argmax_step<kDppXor1>(v, i);
   argmax_step<kDppXor2>(v, i);

@@ -100,8 +100,11 @@ struct GemvArgs {
   float* arg_val;      // per-block argmax partials
   int* arg_idx;
   int* tokens_out;     // greedy stream (indexed by ctrl[C_STEP]), may be null
-  int advance;         // 1: last block advances ctrl (token <- argmax, pos++, step++)
+  int advance;         // 1: the merge advances ctrl (token <- argmax, pos++, step++)
   int max_steps;
+  // LM head: each block also folds its best into *arg_key, an atomic max of
+  // greedy_key (zero between launches; may be null)
+  unsigned long long* arg_key;
   // PRO_RMSF input of the persistent schedule: acc_in holds kRep partials of
   // published words (fp32 value in bits 0..31), summed as floats
   int ps_words;
@@ -167,9 +170,16 @@ void launch_argmax(const float* logits, int n, float* pval, int* pidx, int* toke
 // ps: the token came from the persistent schedule; advance its token number (C_SEQ)
 void launch_argmax_merge(const float* pval, const int* pidx, int n, int* ctrl, int* tokens_out, int advance,
                          int max_steps, const EmbStage& es, hipStream_t st, int ps = 0);
+// The merge of an LM head launch that folded into key (greedy_key order),
+// with argmax_merge_kernel's control-word updates; clears key.
+void launch_greedy_pick(unsigned long long* key, int* ctrl, int* tokens_out, int advance, int max_steps,
+                        const EmbStage& es, hipStream_t st, int ps);
 void launch_set_ctrl(int* ctrl, int token, int pos, int step, int base, int len, const EmbStage& es,
                      hipStream_t st);
 void launch_prefill_advance(int* ctrl, const int* prompt, const EmbStage& es, hipStream_t st, int ps = 0);
+// Stages the embedding row of ctrl[C_TOKEN] (a token chosen by a persistent
+// step, which does not stage it, before a step on the per-stage graph).
+void launch_stage_ctrl(const int* ctrl, const EmbStage& es, hipStream_t st);
 void launch_copy(uint4* dst, const uint4* src, size_t n16, hipStream_t st);
 void launch_dequant(int fmt, const uint4* w, const uint16_t* s, int N, int T, int C, int K, float* out,
                     hipStream_t st);

@@ -535,6 +535,9 @@ __global__ __launch_bounds__(W * 64) void lm_head_kernel(GemvArgs a) {
     if (lane == 0) {
       a.arg_val[blockIdx.x] = best_v;
       a.arg_idx[blockIdx.x] = best_i;
+      // the merge as it goes: one device-scope atomic max per block
+      if (a.arg_key)
+        __hip_atomic_fetch_max(a.arg_key, greedy_key(best_v, best_i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -613,6 +616,37 @@ void launch_argmax_merge(const float* pval, const int* pidx, int n, int* ctrl, i
                          int max_steps, const EmbStage& es, hipStream_t st, int ps) {
   hipLaunchKernelGGL(argmax_merge_kernel, dim3(1), dim3(1024), 0, st, pval, pidx, n, ctrl, tokens_out, advance,
                      max_steps, es, ps);
+}
+
+// argmax_merge_kernel's work when the LM head blocks already folded their
+// partials into one key (greedy_key): decode it, advance the control words,
+// clear the key for the next launch.
+__global__ __launch_bounds__(256) void greedy_pick_kernel(unsigned long long* key, int* ctrl, int* tokens_out,
+                                                          int advance, int max_steps, EmbStage es, int ps) {
+  __shared__ int tok_s;
+  if (threadIdx.x == 0) {
+    const int step = ctrl[C_STEP], posv = ctrl[C_POS], seqv = ctrl[C_SEQ];
+    const unsigned long long k = __hip_atomic_load(key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // nothing above LOWEST (or nothing folded) -> token 0, as the merge
+    const int token = k != 0 && greedy_key_value(k) > kLowest ? greedy_key_id(k) : 0;
+    if (tokens_out && step >= 0 && step < max_steps) tokens_out[step] = token;
+    ctrl[C_TOKEN] = token;
+    if (advance) {
+      ctrl[C_POS] = posv + 1;
+      ctrl[C_STEP] = step + 1;
+    }
+    if (ps) ctrl[C_SEQ] = ps_next_seq(seqv);
+    __hip_atomic_store(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    tok_s = token;
+  }
+  __syncthreads();
+  stage_embedding(es, tok_s);
+}
+
+void launch_greedy_pick(unsigned long long* key, int* ctrl, int* tokens_out, int advance, int max_steps,
+                        const EmbStage& es, hipStream_t st, int ps) {
+  hipLaunchKernelGGL(greedy_pick_kernel, dim3(1), dim3(256), 0, st, key, ctrl, tokens_out, advance, max_steps, es,
+                     ps);
 }
 
 size_t gemv_smem_bytes(int fmt, int cps, int waves) {
@@ -1343,6 +1377,14 @@ __global__ void set_ctrl_kernel(int* ctrl, int token, int pos, int step, int bas
 void launch_set_ctrl(int* ctrl, int token, int pos, int step, int base, int len, const EmbStage& es,
                      hipStream_t st) {
   hipLaunchKernelGGL(set_ctrl_kernel, dim3(1), dim3(256), 0, st, ctrl, token, pos, step, base, len, es);
+}
+
+__global__ __launch_bounds__(256) void stage_ctrl_kernel(const int* ctrl, EmbStage es) {
+  stage_embedding(es, ctrl[C_TOKEN]);
+}
+
+void launch_stage_ctrl(const int* ctrl, const EmbStage& es, hipStream_t st) {
+  hipLaunchKernelGGL(stage_ctrl_kernel, dim3(1), dim3(256), 0, st, ctrl, es);
 }
 
 // prefillChunkComputeNodes' advance node (DecoderTSLRunner.ts:216-225): next
