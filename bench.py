@@ -2,9 +2,9 @@
 
     python bench.py [--steps K] [--warmup W] [--workload qwen2.5-0.5b]
 
-A step is one decode token at batch 1: one HIP graph launch (the persistent
-layer kernel, the LM head and the greedy argmax), with the token fed back on
-the device.  The default workload is the Qwen2.5-0.5B-shaped decoder (24 layers,
+A step is one decode token at batch 1: three kernel launches (the persistent
+layer kernel, the LM head, the greedy merge), with the token fed back on the
+device.  The default workload is the Qwen2.5-0.5B-shaped decoder (24 layers,
 hidden 896, q4 g32 linears, fp16 tied head): a 128-token random prompt, then
 K = 256 greedy decode steps timed (positions 127..382), after W untimed
 warm-up steps over the same positions.  Weights are synthetic N(0, 0.02).
@@ -18,7 +18,9 @@ bounded sample of the same workload.  Prefill: the prompt's 127 positions as
 one batched pass (MFMA GEMMs + flash attention; `prefill_tok_s`) and replaying
 the decode graph per position as the reference does (`prefill_replay_tok_s`);
 `prefill_chunk` is one 2048-position chunk on the Llama-3.2-1B shape with its
-FLOP/s against the dense fp16 MFMA peak.
+FLOP/s against the dense fp16 MFMA peak.  `long_window` is greedy decode on the
+Llama-3.2-3B shape over a KV cache pre-filled with N(0, 1) rows to 16384
+positions (split-K attention over the long window), with its HBM fraction.
 """
 from __future__ import annotations
 
@@ -176,6 +178,34 @@ def prefill_chunk_bench(W, R, ctx, workload: str, n: int) -> dict:
     return out
 
 
+def long_window_bench(W, R, ctx, steps: int, warmup: int = 4) -> dict:
+    """Greedy decode on the Llama-3.2-3B shape from position 16384, the fp16
+    KV cache rows [0, 16384) pre-filled with N(0, 1) values: `steps` device-fed
+    steps timed after `warmup` over the same positions; tok/s and the HBM
+    fraction of the algorithmic bytes (weights, head, the KV rows read)."""
+    wl = W.WORKLOADS["llama-3.2-3b"]
+    hw = W.synthetic(wl)
+    pos0 = wl.kv_prefill
+    runner = R.DecoderHIPRunner(hw, {"maxTokens": pos0 + max(steps, warmup) + 1}, ctx=ctx)
+    runner.model.kv_fill_normal(0xC0FFEE, pos0)
+    last = int(W.prompt_tokens(wl)[-1])
+    runner.decodeGreedy(last, pos0, warmup)
+    ctx.sync()
+    t0 = time.perf_counter()
+    runner.decodeGreedy(last, pos0, steps)
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    mean_bytes = sum(bytes_per_token(hw, pos0 + i, 0) for i in range(steps)) / steps
+    out = {"workload": wl.name, "kv_positions": pos0, "steps": steps, "tok_s": round(steps / wall, 1),
+           "ms_per_step": round(wall * 1e3 / steps, 4), "bytes_per_token": round(mean_bytes),
+           "hbm_roofline_frac": round(mean_bytes * steps / wall / HBM_PEAK, 4)}
+    log(f"[bench] long window {wl.name} from position {pos0}: {steps / wall:.1f} tok/s "
+        f"({wall * 1e6 / steps:.0f} us/token), {mean_bytes / 1e6:.1f} MB/token -> "
+        f"{100 * out['hbm_roofline_frac']:.1f}% of HBM roofline")
+    runner.close()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -188,6 +218,8 @@ def main():
                     help="model of the prefill-chunk measurement (the MFMA GEMM path)")
     ap.add_argument("--prefill-chunk", type=int, default=2048,
                     help="positions of the prefill-chunk measurement (0 skips it)")
+    ap.add_argument("--long-window-steps", type=int, default=32,
+                    help="decode steps of the long-window measurement (0 skips it)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prefill-chunk measurement (for profiling); prints its JSON object")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -273,7 +305,7 @@ def main():
         runner.decodeGreedy(last, pos0, warmup)
     ctx.sync()
     t1 = time.perf_counter()
-    tokens = runner.decodeGreedy(last, pos0, steps)  # launches K graphs, one sync at the end
+    tokens = runner.decodeGreedy(last, pos0, steps)  # K device-fed steps, one sync at the end
     ctx.sync()
     wall = time.perf_counter() - t1
     ev_ms = runner.model.time_decode(last, pos0, 0, steps)
@@ -383,6 +415,8 @@ def main():
     runner.close()
     if args.prefill_chunk:
         result["prefill_chunk"] = prefill_chunk_bench(W, R, ctx, args.prefill_workload, args.prefill_chunk)
+    if args.long_window_steps:
+        result["long_window"] = long_window_bench(W, R, ctx, args.long_window_steps)
     ctx.close()
     print(json.dumps(result), flush=True)
 
