@@ -91,3 +91,34 @@ def test_batched_prefill_one_pass_per_chunk(ctx):
     assert _delta(m, b) == {"graph_launches": 1 - ps, "kernel_launches": 1 + 3 * ps, "prefill_chunks": 0,
                             "replayed_positions": 0, "recomputed_positions": 0, "persistent_tokens": ps}
     runner.close()
+
+
+def test_long_replayed_chunk_splits_into_bounded_graphs(ctx, monkeypatch):
+    """A replayed chunk whose token steps would record more kernels than one
+    replay graph holds (2048) runs as several graphs: the tiny decoder on the
+    per-stage schedule, 600 positions in one chunk -> more than one graph
+    launch and fewer than one per position, with the cache rows and the next
+    logits bit-identical to chunks of 7 (the same kernels either way)."""
+    monkeypatch.setenv("TLM_PERSISTENT", "0")  # read at model creation
+    wl = W.WORKLOADS["tiny"]
+    wl = W.Workload(wl.name, wl.config, wl.storage, 601, 8, 640)
+    hw = W.synthetic(wl)
+    hw.keep = True
+    toks = [int(t) for t in W.prompt_tokens(wl)]
+    big = R.DecoderHIPRunner(hw, {"maxTokens": 640, "prefillChunkSize": 600, "prefillBatchRows": 0}, ctx=ctx)
+    small = R.DecoderHIPRunner(hw, {"maxTokens": 640, "prefillChunkSize": 7, "prefillBatchRows": 0}, ctx=ctx)
+    assert "persistent[off]" in big.model.describe()
+    b = big.model.counts()
+    big.prefillTokens(toks, 0, 600)
+    d = _delta(big.model, b)
+    assert d["replayed_positions"] == 600
+    assert 1 < d["graph_launches"] < 600, d
+    small.prefillTokens(toks, 0, 600)
+    for l in range(wl.config["num_hidden_layers"]):
+        for x, y in zip(big.model.kv_read(l, 0, 600), small.model.kv_read(l, 0, 600)):
+            assert np.array_equal(x, y)
+    big.computeToken(toks[600], 600, True)
+    small.computeToken(toks[600], 600, True)
+    assert np.array_equal(big.readLogits(), small.readLogits())
+    big.close()
+    small.close()

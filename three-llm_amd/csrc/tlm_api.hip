@@ -1923,11 +1923,19 @@ static int prefill_rows(tlm_model* m, const int32_t* tokens, int start, int end,
   return TLM_OK;
 }
 
+// Kernels one replay graph records at most: a chunk whose token steps would
+// record more is replayed as several graphs.  (Unbounded, a 2047-position
+// chunk of the Llama-3.2-1B shape's long-window steps, some 80 kernels each,
+// was captured as one linear graph of over 160,000 nodes, and the process took
+// a segmentation fault.)
+constexpr int kReplayGraphKernels = 2048;
+
 // The decode graph replayed over the n prompt positions [p, p + n) (set_ctrl
 // already named p; each step's prefill tail advances the position and stages
-// the next id): one captured graph of n token steps per schedule and size
+// the next id): captured graphs of up to kReplayGraphKernels kernels' worth of
+// token steps per schedule and size -- one graph per chunk for most models
 // (the reference encodes a chunk's replays into one submission,
-// DecoderTSLRunner.ts:472-480,504-530), or one launch per position when the
+// DecoderTSLRunner.ts:472-480,504-530) -- or one launch per position when the
 // chunk crosses into the long-window kernels or graphs are off.
 static int replay_chunk(tlm_model* m, int p, int n) {
   auto mode = [&](int pos) {
@@ -1942,49 +1950,60 @@ static int replay_chunk(tlm_model* m, int p, int n) {
     for (int i = 0; i < n && !rc; i++) rc = run_token(m, false, p + i);
     return rc;
   }
+  // kernels per token step: the persistent kernel and the prefill advance, or
+  // the per-stage prefill graph's nodes
+  size_t per_step = 2;
+  if (md != 2) HIP_TRY(hipGraphGetNodes(m->graph_prefill[md], nullptr, &per_step));
+  const int per = (int)std::max<size_t>(1, kReplayGraphKernels / std::max<size_t>(per_step, 1));
   hipStream_t st = m->ctx->stream;
-  const int key = md * 65536 + n;
-  auto it = m->replay_graphs.find(key);
-  if (it == m->replay_graphs.end()) {
-    hipGraph_t g = nullptr;
-    hipGraphExec_t ge = nullptr;
-    const tlm_model_counts kept = m->counts;
-    const bool stale = m->x0_stale;
-    HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-    bool ok = true;
-    for (int i = 0; i < n; i++) {
-      if (md == 2) {
-        ok &= enqueue_ps(m, st, 0);
-      } else {
-        for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1, md == 1);
-        launch_prefill_advance(m->ctrl, m->prompt, emb_stage(m), st);
-      }
-    }
-    m->counts = kept;
-    m->x0_stale = stale;
-    hipError_t le = hipGetLastError();
-    HIP_TRY(hipStreamEndCapture(st, &g));
-    if (le != hipSuccess || !ok) {
-      hipGraphDestroy(g);
-      if (!ok) return fail(TLM_ERR_STATE, "TLMModel: no kernel variant for a stage of this model");
-      return fail(TLM_ERR_HIP, "TLMModel: launch during capture failed: %s", hipGetErrorString(le));
-    }
-    if (hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess) {
-      hipGraphDestroy(g);
-      return fail(TLM_ERR_HIP, "TLMModel: replay graph instantiation failed");
-    }
-    it = m->replay_graphs.emplace(key, std::make_pair(g, ge)).first;
-  }
-  m->host_pos = p + n - 1;
   if (md != 2) stage_x0(m, st);
-  auto launch = [&]() -> int {
-    HIP_TRY(hipGraphLaunch(it->second.second, st));
-    m->counts.graph_launches++;
-    if (md == 2) m->counts.persistent_tokens += (uint64_t)n;
-    m->x0_stale = md == 2;  // the persistent advance does not stage the row
-    return TLM_OK;
-  };
-  return md == 2 ? ps_ordered(m, launch) : launch();
+  for (int done = 0; done < n;) {
+    const int cnt = std::min(per, n - done);
+    const int key = md * 65536 + cnt;
+    auto it = m->replay_graphs.find(key);
+    if (it == m->replay_graphs.end()) {
+      hipGraph_t g = nullptr;
+      hipGraphExec_t ge = nullptr;
+      const tlm_model_counts kept = m->counts;
+      const bool stale = m->x0_stale;
+      HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+      bool ok = true;
+      for (int i = 0; i < cnt; i++) {
+        if (md == 2) {
+          ok &= enqueue_ps(m, st, 0);
+        } else {
+          for (int l = 0; l < m->d.num_layers; l++) ok &= enqueue_layer(m, l, st, -1, md == 1);
+          launch_prefill_advance(m->ctrl, m->prompt, emb_stage(m), st);
+        }
+      }
+      m->counts = kept;
+      m->x0_stale = stale;
+      hipError_t le = hipGetLastError();
+      HIP_TRY(hipStreamEndCapture(st, &g));
+      if (le != hipSuccess || !ok) {
+        hipGraphDestroy(g);
+        if (!ok) return fail(TLM_ERR_STATE, "TLMModel: no kernel variant for a stage of this model");
+        return fail(TLM_ERR_HIP, "TLMModel: launch during capture failed: %s", hipGetErrorString(le));
+      }
+      if (hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess) {
+        hipGraphDestroy(g);
+        return fail(TLM_ERR_HIP, "TLMModel: replay graph instantiation failed");
+      }
+      it = m->replay_graphs.emplace(key, std::make_pair(g, ge)).first;
+    }
+    m->host_pos = p + done + cnt - 1;
+    auto launch = [&]() -> int {
+      HIP_TRY(hipGraphLaunch(it->second.second, st));
+      m->counts.graph_launches++;
+      if (md == 2) m->counts.persistent_tokens += (uint64_t)cnt;
+      m->x0_stale = md == 2;  // the persistent advance does not stage the row
+      return TLM_OK;
+    };
+    const int rc = md == 2 ? ps_ordered(m, launch) : launch();
+    if (rc) return rc;
+    done += cnt;
+  }
+  return TLM_OK;
 }
 
 int tlm_model_set_prefill(tlm_model* m, int32_t min_rows, int32_t chunk) {
