@@ -6,9 +6,9 @@ Here a decode token on the per-stage schedule is one launch of its captured
 graph, preceded (when the host supplies the token) by one small kernel that
 writes the token and the position: the counterpart of the reference's uniform
 upload before its submit (DecoderTSLRunner.ts:487-501), which is not a
-submission.  On the persistent schedule a decode token is its three kernels
-(the layers, the LM head, the greedy merge), enqueued directly: a graph launch
-of the same kernels costs more per token.  A prompt chunk is
+submission.  On the persistent schedule a decode token is its two kernels (the
+layers; the LM head, whose last block does the greedy merge), enqueued
+directly: a graph launch of the same kernels costs more per token.  A prompt chunk is
 one graph launch too, after one such write naming the chunk: a batched chunk
 (enough rows) is its captured sequence of row kernels, a shorter chunk the
 decode graph's token steps captured back to back, as the reference encodes
@@ -88,7 +88,7 @@ def test_batched_prefill_one_pass_per_chunk(ctx):
     b = m.counts()
     runner.computeToken(toks[-1], 18, True)
     ps = int("persistent[off]" not in m.describe())  # the decode step's schedule
-    assert _delta(m, b) == {"graph_launches": 1 - ps, "kernel_launches": 1 + 3 * ps, "prefill_chunks": 0,
+    assert _delta(m, b) == {"graph_launches": 1 - ps, "kernel_launches": 1 + 2 * ps, "prefill_chunks": 0,
                             "replayed_positions": 0, "recomputed_positions": 0, "persistent_tokens": ps}
     runner.close()
 

@@ -194,6 +194,7 @@ struct tlm_model {
   float* arg_val = nullptr;
   int* arg_idx = nullptr;
   unsigned long long* arg_key = nullptr;  // the LM head's folded argmax (zero between launches)
+  unsigned* arg_arrived = nullptr;        // LM head blocks done, for its in-launch merge (zero between launches)
   float* cand_v = nullptr;  // top-k candidates of the last logits (kTopkMax)
   int* cand_i = nullptr;
   // attention (shared by the layers; they run one after another)
@@ -1292,6 +1293,7 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
   M_TRY(model_alloc((void**)&m->arg_val, sizeof(float) * 4096));
   M_TRY(model_alloc((void**)&m->arg_idx, sizeof(int) * 4096));
   M_TRY(model_alloc((void**)&m->arg_key, sizeof(unsigned long long)));
+  M_TRY(model_alloc((void**)&m->arg_arrived, sizeof(unsigned)));
   M_TRY(model_alloc((void**)&m->cand_v, sizeof(float) * kTopkMax));
   M_TRY(model_alloc((void**)&m->cand_i, sizeof(int) * kTopkMax));
   if (rc == TLM_OK) rc = ps_setup(m);
@@ -1337,7 +1339,7 @@ void tlm_model_destroy(tlm_model* m) {
   tlm_linear_destroy(m->head);
   attn_free(&m->attn, false);
   void* bufs[] = {m->emb, m->final_norm, m->ctrl, m->tokens_out, m->prompt, m->xa, m->x0, m->xf, m->attn_out,
-                  m->pq, m->po, m->rb, m->logits, m->arg_val, m->arg_idx, m->arg_key, m->cand_v, m->cand_i, m->pf_x, m->pf_part, m->pf_xn,
+                  m->pq, m->po, m->rb, m->logits, m->arg_val, m->arg_idx, m->arg_key, m->arg_arrived, m->cand_v, m->cand_i, m->pf_x, m->pf_part, m->pf_xn,
                   m->pf_q, m->pf_att, m->pf_h, m->pf_ovf, m->ps_layers, m->ps_roles, m->ps_pub_x, m->ps_pub_qkv,
                   m->ps_pub_o, m->ps_pub_xm, m->ps_pub_h, m->ps_args_dev};
   for (void* p : bufs) hipFree(p);
@@ -1533,10 +1535,28 @@ static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, hipEvent_t*
   a.arg_val = m->arg_val;
   a.arg_idx = m->arg_idx;
   a.arg_key = m->arg_key;  // the blocks fold their bests as they finish
+  // after a persistent step the head's last block also does the merge
+  // (TLM_HEAD_MERGE=0: greedy_pick_kernel, comparisons)
+  static const bool merge_in_head = [] {
+    const char* e = getenv("TLM_HEAD_MERGE");
+    return !(e && e[0] == '0');
+  }();
+  const bool in_head = ps && advance && merge_in_head;
+  if (in_head) {
+    a.arrived = m->arg_arrived;
+    a.mctrl = m->ctrl;
+    a.tokens_out = m->tokens_out;
+    a.max_steps = d.max_tokens;
+  }
   if (ev) hipEventRecord(ev[0], st);
   if (!launch_lm_head(wfmt(m->head->fmt), PRO_RMSF, m->lm_plan.waves, m->lm_plan.nch, dim3(m->lm_plan.gx), a, st))
     return false;
   if (ev) hipEventRecord(ev[1], st);
+  if (in_head) {
+    m->x0_stale = true;  // the persistent kernel reads its token's row itself
+    m->counts.kernel_launches++;
+    return true;
+  }
   // the persistent kernel reads its token's embedding row itself: the row is
   // staged only before a step on the per-stage graph (stage_x0)
   launch_greedy_pick(m->arg_key, m->ctrl, advance ? m->tokens_out : nullptr, advance ? 1 : 0, d.max_tokens,

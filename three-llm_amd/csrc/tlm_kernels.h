@@ -105,6 +105,13 @@ struct GemvArgs {
   // LM head: each block also folds its best into *arg_key, an atomic max of
   // greedy_key (zero between launches; may be null)
   unsigned long long* arg_key;
+  // with arg_key: the merge in the same launch.  A block counts itself in
+  // *arrived (zero between launches) once its max has returned; the block
+  // that counts last writes the token and advances position, step and token
+  // number in mctrl (the persistent schedule's step; no embedding row is
+  // staged), then clears the key and the count.  Null: greedy_pick_kernel.
+  unsigned* arrived;
+  int* mctrl;
   // PRO_RMSF input of the persistent schedule: acc_in holds kRep partials of
   // published words (fp32 value in bits 0..31), summed as floats
   int ps_words;

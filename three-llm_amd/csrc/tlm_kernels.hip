@@ -483,6 +483,12 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(GemvArgs a) {
   }
 }
 
+// The persistent schedule's token number advances once its token is done
+// (never 0: zeroed words never match).
+__device__ __forceinline__ int ps_next_seq(int cur) {
+  const unsigned seq = (unsigned)cur + 1u;
+  return (int)(seq ? seq : 1u);
+}
 // LM head: GEMV over the vocabulary (PRO_COPY input) with the first pass of
 // the greedy sampler fused in (createChunkPartialMaxNode, TSLLogits.ts:201-248):
 // each block keeps its best (score, id) over its tiles.
@@ -536,8 +542,30 @@ __global__ __launch_bounds__(W * 64) void lm_head_kernel(GemvArgs a) {
       a.arg_val[blockIdx.x] = best_v;
       a.arg_idx[blockIdx.x] = best_i;
       // the merge as it goes: one device-scope atomic max per block
-      if (a.arg_key)
-        __hip_atomic_fetch_max(a.arg_key, greedy_key(best_v, best_i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (a.arg_key) {
+        const unsigned long long prev =
+            __hip_atomic_fetch_max(a.arg_key, greedy_key(best_v, best_i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (a.arrived) {
+          // the count goes out only once the max has returned (performed), so
+          // the block that counts last finds every block's best in the key
+          asm volatile("" ::"v"((unsigned)prev), "v"((unsigned)(prev >> 32)) : "memory");
+          const unsigned n = __hip_atomic_fetch_add(a.arrived, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (n == gridDim.x - 1) {
+            int* ctrl = a.mctrl;
+            const int step = ctrl[C_STEP], posv = ctrl[C_POS], seqv = ctrl[C_SEQ];
+            const unsigned long long k = __hip_atomic_load(a.arg_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // nothing above LOWEST (or nothing folded) -> token 0, as the merge
+            const int token = k != 0 && greedy_key_value(k) > kLowest ? greedy_key_id(k) : 0;
+            if (a.tokens_out && step >= 0 && step < a.max_steps) a.tokens_out[step] = token;
+            ctrl[C_TOKEN] = token;
+            ctrl[C_POS] = posv + 1;
+            ctrl[C_STEP] = step + 1;
+            ctrl[C_SEQ] = ps_next_seq(seqv);
+            __hip_atomic_store(a.arg_key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.arrived, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+      }
     }
   }
 }
@@ -555,12 +583,6 @@ __device__ __forceinline__ void stage_embedding(const EmbStage& es, int token) {
                             : h2f(((const uint16_t*)es.emb)[(size_t)token * es.H + i]));
 }
 
-// The persistent schedule's token number advances once its token is done
-// (never 0: zeroed words never match).
-__device__ __forceinline__ int ps_next_seq(int cur) {
-  const unsigned seq = (unsigned)cur + 1u;
-  return (int)(seq ? seq : 1u);
-}
 __device__ __forceinline__ void ps_next_token(int* ctrl) { ctrl[C_SEQ] = ps_next_seq(ctrl[C_SEQ]); }
 
 __global__ __launch_bounds__(1024) void argmax_merge_kernel(const float* pval, const int* pidx, int n, int* ctrl,
