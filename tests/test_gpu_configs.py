@@ -8,11 +8,12 @@ src/test/reference.browser.test.ts:35-39):
 * Llama-3.2-1B shape, 16 layers: a 4095-id prompt (two chunks, the second
   attending over 2048 earlier rows), batched against the replayed decode
   graph; the oracle continues from the device cache and checks the last
-  prompt rows and the first decode steps.
-* Llama-3.2-3B shape, 28 layers, decode over a 16384-position N(0, 1) cache
-  that the oracle is given too.
+  prompt rows and 32 decode steps (every greedy token, the logits every 8th).
+* Llama-3.2-3B shape, 28 layers, 8 decode steps over a 16384-position
+  N(0, 1) cache that the oracle is given too.
 * The 2048-position prefill chunk of the Llama-3.2-1B shape at 16 layers,
-  against the replayed decode graph.
+  against the replayed decode graph, and the oracle from the chunk's cache
+  rows at its last positions.
 
 Tolerances: logits max-abs 2e-2 / rel 1e-2 (fp16 storage); the greedy stream
 is identical except after a step whose oracle top-2 gap is under 2e-2.
@@ -101,7 +102,9 @@ def test_llama1b_4095_id_prompt_and_decode(ctx):
     rows against the replayed decode graph (KV rows of every layer and the
     logits at 4095).  The oracle is then given the batched cache rows
     0..4089 and computes positions 4090..4094 itself (its K/V rows must match
-    the device's) and the decode steps at 4095..4097."""
+    the device's) and 32 decode steps from 4095: every greedy token (the
+    oracle fed the device's tokens) and the logits every 8th step; the device
+    loop gives the same tokens."""
     wl = W.WORKLOADS["llama-3.2-1b"]
     L = wl.config["num_hidden_layers"]
     hw = W.synthetic(wl)
@@ -143,15 +146,22 @@ def test_llama1b_4095_id_prompt_and_decode(ctx):
     ref = om.forward(prompt[-1], n)
     close(logits, ref, LOGIT_ATOL, LOGIT_RTOL)
     tok = runner.sampleToken(1, {"temperature": 0})
-    for pos in (n + 1, n + 2):
+    host = [tok]
+    for step in range(1, 32):
+        pos = n + step
         if tok != int(np.argmax(ref)):
             assert top2_gap(ref) < LOGIT_ATOL
             break
         runner.computeToken(tok, pos, True)
         ref = om.forward(tok, pos)
-        close(runner.readLogits(), ref, LOGIT_ATOL, LOGIT_RTOL)
+        if step % 8 == 0:
+            close(runner.readLogits(), ref, LOGIT_ATOL, LOGIT_RTOL)
         tok = runner.sampleToken(1, {"temperature": 0})
-    _say("oracle checks done")
+        host.append(tok)
+    _say(f"oracle checks done ({len(host)} decode steps)")
+    # the device-fed loop from the same cache state gives the host loop's tokens
+    dev = list(runner.decodeGreedy(host[0], n + 1, len(host) - 1))
+    assert dev == host[1:]
     runner.close()
     om.close()
 
@@ -160,13 +170,15 @@ def test_llama1b_4095_id_prompt_and_decode(ctx):
 def test_llama3b_decode_over_16384_cached_positions(ctx):
     """28 layers, head_dim 128, the fp16 cache filled with N(0, 1) to 16384
     positions (the matrix-core long-window attention and its 32-slot combine in the O
-    projection).  The oracle gets the same cache rows; three decode steps at
-    16384..16386 within tolerance, greedy tokens equal."""
+    projection).  The oracle gets the same cache rows; 8 decode steps at
+    16384..16391 (the oracle takes seconds per step at this context): every
+    greedy token equal (the oracle fed the device's tokens), the logits
+    within tolerance at every 4th step."""
     wl = W.WORKLOADS["llama-3.2-3b"]
     L, fill = wl.config["num_hidden_layers"], wl.kv_prefill
     hw = W.synthetic(wl)
     hw.keep = True
-    max_tokens = fill + 8
+    max_tokens = fill + 24
     runner = R.DecoderHIPRunner(hw, {"maxTokens": max_tokens}, ctx=ctx)
     m = runner.model
     m.kv_fill_normal(0xC0FFEE, fill)
@@ -176,10 +188,12 @@ def test_llama3b_decode_over_16384_cached_positions(ctx):
         om.write_cache(l, 0, k, v)
     _say("caches filled")
     tok = int(W.prompt_tokens(wl)[0])
-    for pos in range(fill, fill + 3):
+    for pos in range(fill, fill + 8):
         runner.computeToken(tok, pos, True)
         ref = om.forward(tok, pos)
-        close(runner.readLogits(), ref, LOGIT_ATOL, LOGIT_RTOL)
+        if (pos - fill) % 4 == 0:
+            close(runner.readLogits(), ref, LOGIT_ATOL, LOGIT_RTOL)
+        _say(f"step {pos} checked")
         dev_tok = runner.sampleToken(1, {"temperature": 0})
         if dev_tok != int(np.argmax(ref)):
             assert top2_gap(ref) < LOGIT_ATOL
@@ -199,7 +213,9 @@ def test_llama3b_decode_over_16384_cached_positions(ctx):
 def test_llama1b_2048_row_chunk_at_full_depth(ctx):
     """The prefill-chunk workload (Llama-3.2-1B shape, 16 layers, 2048 random
     ids): the batched chunk against the replayed decode graph, KV rows of
-    every layer and the logits at position 2048."""
+    every layer and the logits at position 2048; then the oracle, given the
+    batched chunk's cache rows 0..2043, computes positions 2044..2047 itself
+    (its K/V rows must match the chunk's) and the logits at 2048."""
     wl = W.WORKLOADS["llama-3.2-1b"]
     L, n = wl.config["num_hidden_layers"], 2048
     hw = W.synthetic(wl)
@@ -222,4 +238,19 @@ def test_llama1b_2048_row_chunk_at_full_depth(ctx):
             close(got, ref, 2e-2, 1e-2)
     close(logits, replay_logits, LOGIT_ATOL, LOGIT_RTOL)
     _say(f"max |logits - replay| {float(np.abs(logits - replay_logits).max()):.3g}")
+    del replay_kv
+    om = oracle_model(hw, n + 8, kv_f16=True, threads=16)
+    p0 = n - 4
+    kv = [_kv_f32(m, l, 0, n) for l in range(L)]
+    for l in range(L):
+        om.write_cache(l, 0, kv[l][0][:p0], kv[l][1][:p0])
+    for i in range(p0, n):
+        om.prefill(prompt[i], i)
+    for l in range(L):
+        k_ref, v_ref = om.read_cache(l, n)
+        close(kv[l][0][p0:n].reshape(n - p0, -1), k_ref[p0:n], 2e-2, 1e-2)
+        close(kv[l][1][p0:n].reshape(n - p0, -1), v_ref[p0:n], 2e-2, 1e-2)
+    close(logits, om.forward(prompt[-1], n), LOGIT_ATOL, LOGIT_RTOL)
+    _say("oracle from the chunk's cache done")
+    om.close()
     runner.close()
