@@ -234,6 +234,64 @@ struct PsRows {
   }
 };
 
+// Whether a stage widens its q4 weights ahead (PsRowsH): up to 3 chunks per
+// wave (48 registers of pairs; with more, the kernel's registers spill).
+template <int FMT, int NU>
+constexpr bool ps_widen() {
+  return FMT == WF_Q4 && NU <= 3;
+}
+
+// PsRows' q4 weights with the nibbles already widened to the fp16 pairs that
+// dot_q4h forms (1 + n / 64): formed while the stage waits for its inputs,
+// so that only the v_dot2 multiply-adds remain once they arrive.  The same
+// operations in the same order as dot_q4h: the same results.
+template <int NU, int NT>
+struct PsRowsH {
+  uint32_t p[NT][NU][16];
+  float sc[NT][NU];
+  __device__ __forceinline__ void from(const PsRows<WF_Q4, NU, NT>& r) {
+    const uint32_t M = 0x00F000F0u, E = 0x3C003C00u;
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+      for (int u = 0; u < NU; u++) {
+        const uint32_t wv[4] = {r.d[t][u].x, r.d[t][u].y, r.d[t][u].z, r.d[t][u].w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          p[t][u][4 * j] = and_or(wv[j] << 4, M, E);
+          p[t][u][4 * j + 1] = and_or(wv[j], M, E);
+          p[t][u][4 * j + 2] = and_or(wv[j] >> 4, M, E);
+          p[t][u][4 * j + 3] = and_or(wv[j] >> 8, M, E);
+        }
+        sc[t][u] = h2f(r.s[t][u]);
+      }
+  }
+  __device__ __forceinline__ float dot(int t, const float* xw, const float (&xs)[NU], int cbase, int clo, int chi,
+                                       int wave) const {
+    float acc = 0.f;
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+      const int c = cbase + wave + 16 * u;
+      if (c < clo || c >= chi) continue;
+      const uint32_t* xh = reinterpret_cast<const uint32_t*>(xw + u * 16);
+      float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint4 xp = *reinterpret_cast<const uint4*>(xh + 4 * j);
+        a0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p[t][u][4 * j]), __builtin_bit_cast(f16x2, xp.x), a0, false);
+        a1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p[t][u][4 * j + 1]), __builtin_bit_cast(f16x2, xp.y), a1,
+                                    false);
+        a0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p[t][u][4 * j + 2]), __builtin_bit_cast(f16x2, xp.z), a0,
+                                    false);
+        a1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p[t][u][4 * j + 3]), __builtin_bit_cast(f16x2, xp.w), a1,
+                                    false);
+      }
+      acc += sc[t][u] * fmaf(64.f, a0 + a1, -72.f * xs[u]);
+    }
+    return acc;
+  }
+};
+
 // Block-uniform AND of the waves' flags (wf: 16 ints of LDS); a block barrier.
 __device__ __forceinline__ bool ps_all(bool ok, int* wf) {
   if ((threadIdx.x & 63) == 0) wf[threadIdx.x >> 6] = ok ? 1 : 0;
@@ -322,6 +380,9 @@ __device__ __forceinline__ bool ps_qkv(const PsArgs& a, int l, int i, int pos, i
     rs[t] = rot ? gl(a.rope_sin)[(size_t)pos * half + jj] : 0.f;
   }
   if (wave == 0) ps_stamp(a, l, PS_QKV, 0);
+  // q4: the weights widened to fp16 pairs while the residual is on its way
+  PsRowsH<NX, NT> wh;
+  if constexpr (ps_widen<FMT, NX>()) wh.from(wr);
   float x[NX];
   bool ok = true;
   if (l == 0) {
@@ -335,7 +396,10 @@ __device__ __forceinline__ bool ps_qkv(const PsArgs& a, int l, int i, int pos, i
   float xs[NX], ss = 0.f;
   wl_stage<FMT, CK, NX>(x, nw, s.xw, xs, ss);
 #pragma unroll
-  for (int t = 0; t < NT; t++) s.red[(wave * NT + t) * 64 + lane] = wr.dot(t, s.xw, xs, 0, c0, c1, wave);
+  for (int t = 0; t < NT; t++) {
+    if constexpr (ps_widen<FMT, NX>()) s.red[(wave * NT + t) * 64 + lane] = wh.dot(t, s.xw, xs, 0, c0, c1, wave);
+    else s.red[(wave * NT + t) * 64 + lane] = wr.dot(t, s.xw, xs, 0, c0, c1, wave);
+  }
   if (lane == 0) s.ssw[wave] = ss;
   if (!ps_all(ok, s.wf)) return false;
   if (wave == 0) {
@@ -446,6 +510,9 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
   const int tc0 = active ? t0 : first, tc1 = active ? t1 : first + 1;  // in-range rows for idle waves
   ld.issue(kh, vh, tc0, tc1, pl, part, DT, DT * ESZ, lane);
   if (wave == 0) ps_stamp(a, l, PS_ATT, 0);
+  // q4: q's weights widened to fp16 pairs while the residual is on its way
+  PsRowsH<NX, NT> wh;
+  if constexpr (ps_widen<FMT, NX>()) wh.from(wr);
   float x[NX];
   bool ok = true;
   if (l == 0) {
@@ -459,7 +526,10 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
     float xs[NX], ss = 0.f;
     wl_stage<FMT, CK, NX>(x, nw, s.xw, xs, ss);
 #pragma unroll
-    for (int t = 0; t < NT; t++) s.red[(wave * NT + t) * 64 + lane] = wr.dot(t, s.xw, xs, 0, 0, a.Cx, wave);
+    for (int t = 0; t < NT; t++) {
+      if constexpr (ps_widen<FMT, NX>()) s.red[(wave * NT + t) * 64 + lane] = wh.dot(t, s.xw, xs, 0, 0, a.Cx, wave);
+      else s.red[(wave * NT + t) * 64 + lane] = wr.dot(t, s.xw, xs, 0, 0, a.Cx, wave);
+    }
     if (lane == 0) s.ssw[wave] = ss;
     if (!ps_all(ok, s.wf)) return false;
     if (wave == 0) {
@@ -705,12 +775,16 @@ __device__ __forceinline__ bool ps_o(const PsArgs& a, int l, int i, int token, u
       ok = wl_rows(a.ks, seq, [&](int p) { return px + (size_t)p * H; }, xr, a.timeout);
     }
   }
+  // q4: the weights widened to fp16 pairs while the attention outputs are on their way
+  PsRowsH<NO, 1> wh;
+  if constexpr (ps_widen<FMT, NO>()) wh.from(wr);
   const u64* po = a.pub_o + (size_t)l * a.QS;
   ok &= wl_gather<CK, NO>(c0, c1, 1, seq, [&](int, int k) { return po + k; }, wave, x, a.timeout);
   if (wave == 0) ps_stamp(a, l, PS_O, 1);
   float xs[NO], ss;
   wl_stage<FMT, CK, NO>(x, one, s.xw, xs, ss);
-  s.red[wave * 64 + lane] = wr.dot(0, s.xw, xs, c0, c0, c1, wave);
+  if constexpr (ps_widen<FMT, NO>()) s.red[wave * 64 + lane] = wh.dot(0, s.xw, xs, c0, c0, c1, wave);
+  else s.red[wave * 64 + lane] = wr.dot(0, s.xw, xs, c0, c0, c1, wave);
   if (!ps_all(ok, s.wf)) return false;
   if (wave == 0) {
     ps_stamp(a, l, PS_O, 2);
@@ -738,6 +812,9 @@ __device__ __forceinline__ bool ps_gu(const PsArgs& a, int l, int g, unsigned se
   float nw[NX];
   wl_norm_weights<CK, NX>(Ly.ffn_norm, a.Cx, wave, nw);
   if (wave == 0) ps_stamp(a, l, PS_GU, 0);
+  // q4: the weights widened to fp16 pairs while x_mid is on its way
+  PsRowsH<NX, MW> wh;
+  if constexpr (ps_widen<FMT, NX>()) wh.from(wr);
   const u64* pm = a.pub_xm + (size_t)l * a.ko * H;
   float x[NX];
   const bool ok = wl_gather<CK, NX>(0, a.Cx, a.ko, seq, [&](int p, int k) { return pm + (size_t)p * H + k; }, wave, x, a.timeout);
@@ -745,8 +822,12 @@ __device__ __forceinline__ bool ps_gu(const PsArgs& a, int l, int g, unsigned se
   float xs[NX], ss;
   wl_stage<FMT, CK, NX>(x, nw, s.xw, xs, ss);
 #pragma unroll
-  for (int u = 0; u < MW; u++)
-    s.red[(wave * MW + u) * 64 + lane] = g * MW + u < a.Tgu ? wr.dot(u, s.xw, xs, 0, 0, a.Cx, wave) : 0.f;
+  for (int u = 0; u < MW; u++) {
+    float dv = 0.f;
+    if constexpr (ps_widen<FMT, NX>()) dv = wh.dot(u, s.xw, xs, 0, 0, a.Cx, wave);
+    else dv = wr.dot(u, s.xw, xs, 0, 0, a.Cx, wave);
+    s.red[(wave * MW + u) * 64 + lane] = g * MW + u < a.Tgu ? dv : 0.f;
+  }
   if (lane == 0) s.ssw[wave] = ss;
   if (!ps_all(ok, s.wf)) return false;
   if (wave == 0) ps_stamp(a, l, PS_GU, 2);
@@ -788,11 +869,15 @@ __device__ __forceinline__ bool ps_down(const PsArgs& a, int l, int t, int sp, u
     const u64* pm = a.pub_xm + (size_t)l * a.ko * H + min(row, H - 1);
     ok = wl_rows(a.ko, seq, [&](int p) { return pm + (size_t)p * H; }, xm, a.timeout);
   }
+  // q4: the weights widened to fp16 pairs while h is on its way
+  PsRowsH<ND, 1> wh;
+  if constexpr (ps_widen<FMT, ND>()) wh.from(wr);
   ok &= wl_gather<CK, ND>(c0, c1, 1, seq, [&](int, int k) { return ph + k; }, wave, x, a.timeout);
   if (wave == 0) ps_stamp(a, l, PS_DOWN, 1);
   float xs[ND], ss;
   wl_stage<FMT, CK, ND>(x, one, s.xw, xs, ss);
-  s.red[wave * 64 + lane] = wr.dot(0, s.xw, xs, c0, c0, c1, wave);
+  if constexpr (ps_widen<FMT, ND>()) s.red[wave * 64 + lane] = wh.dot(0, s.xw, xs, c0, c0, c1, wave);
+  else s.red[wave * 64 + lane] = wr.dot(0, s.xw, xs, c0, c0, c1, wave);
   if (!ps_all(ok, s.wf)) return false;
   if (wave == 0) {
     ps_stamp(a, l, PS_DOWN, 2);
