@@ -434,11 +434,12 @@ constexpr int ps_wave_floats() {
   return (2 * DT + head_tiling(DT, sizeof(KT)).sub + 1024 + 3) & ~3;
 }
 
-// Floats of the attention item's LDS before q: the wave regions, the merge
-// rows and the wave flags.
-template <typename KT, int DT>
-constexpr int ps_att_floats() {
-  return kPsWaves * ps_wave_floats<KT, DT>() + kPsWaves * (2 + DT) + kPsWaves;
+// Floats of the attention item's LDS before its wave regions: the merge rows,
+// the wave flags and q.  The merge rows come first so that every wave's row is
+// one base address plus an immediate offset (below 64 KiB) for the merge's reads.
+template <int DT>
+constexpr int ps_att_head_floats() {
+  return kPsWaves * (2 + DT) + kPsWaves + DT;
 }
 
 // Item h: query head h over the window [first, pos].  The item computes q
@@ -468,6 +469,8 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
   constexpr bool PAIR64 = ESZ == 2 && DT == 64;
   constexpr int NOE = PAIR64 ? 2 : EPL;
   constexpr int WF = ps_wave_floats<KT, DT>();
+  static_assert(ps_att_head_floats<DT>() % 4 == 0, "wave regions hold 16-byte rows");
+  static_assert(ps_lin_floats(CK, NX, NT) <= kPsWaves * WF, "q's dot products fit the wave regions");
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const TLM_GLOBAL PsLayer& Ly = gl(a.layers)[l];
   const int hk = h / a.G;
@@ -476,15 +479,15 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
   const int t0 = min(first + wave * per, pos), t1 = min(t0 + per, pos);
   const bool active = t0 < t1;
   const bool own = wave == kPsWaves - 1;  // this wave takes the row at pos
-  float* kn = sm + wave * WF;
+  float* mg = sm;  // [16][2 + DT] per-wave (max, sum, output)
+  int* good = reinterpret_cast<int*>(mg + kPsWaves * (2 + DT));  // [16]
+  float* q_sh = reinterpret_cast<float*>(good + kPsWaves);  // [DT] q, read by every wave
+  float* kn = sm + ps_att_head_floats<DT>() + wave * WF;
   float* vn = kn + DT;
   float* p_l = vn + DT;
   KT* vt = reinterpret_cast<KT*>(p_l + SUB);
-  float* mg = sm + kPsWaves * WF;  // [16][2 + DT] per-wave (max, sum, output)
-  int* good = reinterpret_cast<int*>(mg + kPsWaves * (2 + DT));  // [16]
-  float* q_sh = sm + ps_att_floats<KT, DT>();  // [DT] q, read by every wave
   // q's dot products: their LDS overlaps the wave regions, used only after
-  const PsLinLds s = ps_lin_lds<CK, NX, NT>(sm);
+  const PsLinLds s = ps_lin_lds<CK, NX, NT>(sm + ps_att_head_floats<DT>());
   PsRows<FMT, NX, NT> wr;
   wr.load(Ly.wqkv, Ly.sqkv, a.Cx, a.Tq, h * DT / kTile, 0, 0, a.Cx, wave);
   float nw[NX];
@@ -722,7 +725,8 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
     // lane w (and w + 16, + 32, + 48) takes wave w's (max, sum) and its
     // scale exp(max_w - M): one exponential per lane instead of 16; the
     // scales reach every lane as scalar operands
-    const int w16 = lane & 15;
+    int w16 = lane & 15;
+    asm volatile("" : "+v"(w16));  // computed here, not kept in a register from the kernel's start
     const float mw = mg[w16 * (2 + DT)], lw = mg[w16 * (2 + DT) + 1];
     float ow[kPsWaves];
 #pragma unroll
@@ -1054,8 +1058,8 @@ size_t ps_smem_bytes(const PsShape& sh, int H, int QS) {
   const int CK = sh.fmt == WF_Q4 ? 32 : 8;
   const size_t esz = sh.kv_f32 ? 4 : 2;
   const int sub = head_tiling(sh.dt, (int)esz).sub;
-  // the attention item: wave regions, merge rows, flags, then q
-  const size_t att = (size_t)kPsWaves * ((2 * sh.dt + sub + 1024 + 3) & ~3) + kPsWaves * (2 + sh.dt) + kPsWaves + sh.dt;
+  // the attention item: merge rows, flags, q, then the wave regions
+  const size_t att = (size_t)kPsWaves * (2 + sh.dt) + kPsWaves + sh.dt + (size_t)kPsWaves * ((2 * sh.dt + sub + 1024 + 3) & ~3);
   const size_t qkv = ps_lin_floats(CK, sh.nx, sh.dt / 64);
   const size_t o = ps_lin_floats(CK, sh.no, 1);
   const size_t gu = ps_lin_floats(CK, sh.nx, sh.mw);
