@@ -125,6 +125,47 @@ def test_trace_orders_every_stage(ctx):
     ps.close()
 
 
+def test_l2_handoffs_give_the_bits_of_device_scope_handoffs(ctx):
+    """At the Qwen2.5-0.5B shape the k|v, attention and O items of each O
+    split (one kv head's group: 4 k|v, 7 attention and 14 O items) share one
+    class of blocks (equal b % 8), which the hardware runs on one XCD, and the
+    k|v and attention items publish with plain stores into that XCD's L2.  The
+    arithmetic is the same as with every handoff device-scope (TLM_PS_L2=0),
+    so the logits, the appended cache rows and the greedy tokens are equal
+    bit for bit."""
+    wl = _workload("qwen2.5-0.5b", 4, 256)
+    hw = W.synthetic(wl)
+    hw.keep = True
+    l2 = _runner(hw, ctx, 256, True)
+    old = os.environ.get("TLM_PS_L2")
+    os.environ["TLM_PS_L2"] = "0"
+    try:
+        dev = _runner(hw, ctx, 256, True)
+    finally:
+        if old is None:
+            del os.environ["TLM_PS_L2"]
+        else:
+            os.environ["TLM_PS_L2"] = old
+    n = int(re.search(r"(\d+) publish through their XCD's L2", l2.model.describe()).group(1))
+    assert n == 8 + 14  # every k|v and attention item
+    assert "; 0 publish through their XCD's L2" in dev.model.describe()
+    prompt = [int(t) for t in W.prompt_tokens(wl)][:12]
+    for i, t in enumerate(prompt):
+        l2.computeToken(t, i, True)
+        dev.computeToken(t, i, True)
+        np.testing.assert_array_equal(l2.readLogits(), dev.readLogits())
+    for l in range(wl.config["num_hidden_layers"]):
+        for a, b in zip(l2.model.kv_read(l, 0, len(prompt)), dev.model.kv_read(l, 0, len(prompt))):
+            np.testing.assert_array_equal(a, b)
+    tok = l2.sampleToken(1, {"temperature": 0})
+    assert tok == dev.sampleToken(1, {"temperature": 0})
+    assert list(l2.decodeGreedy(tok, len(prompt), 16)) == list(dev.decodeGreedy(tok, len(prompt), 16))
+    assert l2.model.counts()["recomputed_positions"] == 0
+    assert dev.model.counts()["recomputed_positions"] == 0
+    l2.close()
+    dev.close()
+
+
 def test_persistent_attention_across_the_wave_ranges(ctx):
     """Every window length the persistent attention item splits differently,
     up to its last one (1024 positions): its 16 waves take 32-position ranges

@@ -220,7 +220,9 @@ struct tlm_model {
   int ps_blocks = 0;
   size_t ps_smem = 0;
   PsLayer* ps_layers = nullptr;  // device [L]
-  int* ps_roles = nullptr;       // device [blocks][2][2]
+  int* ps_roles = nullptr;       // device [blocks][kPsRoles][2]
+  int* ps_xcc = nullptr;         // device [blocks]: each block's XCD when the roles were placed
+  int ps_l2_items = 0;           // items that publish through their XCD's L2 (0: none)
   PsArgs* ps_args_dev = nullptr;  // the kernel's arguments (device memory)
   unsigned long long *ps_pub_x = nullptr, *ps_pub_qkv = nullptr, *ps_pub_o = nullptr, *ps_pub_xm = nullptr,
                      *ps_pub_h = nullptr;
@@ -1111,6 +1113,7 @@ static PsArgs ps_args(const tlm_model* m) {
   a.pub_o = m->ps_pub_o;
   a.pub_xm = m->ps_pub_xm;
   a.pub_h = m->ps_pub_h;
+  a.xcc = m->ps_l2_items > 0 ? m->ps_xcc : nullptr;
   // TLM_PS_TIMEOUT_US / TLM_PS_FAIL_LAYER: a shorter bound of every wait and a
   // layer whose QKV stage reports a time-out (tests of the failure path)
   a.timeout = kPsTimeoutTicks;
@@ -1138,6 +1141,13 @@ static int ps_setup(tlm_model* m) {
     m->ps = PsShape{};
     return TLM_OK;
   }
+  // handoffs through an XCD's L2 where a producer's consumers share its XCD
+  // (TLM_PS_L2=0: every handoff device-scope, for comparisons)
+  std::vector<int> xcc(m->ps_blocks);
+  const char* l2e = getenv("TLM_PS_L2");
+  if (!(l2e && l2e[0] == '0') && ps_xcc_probe(m->ps_blocks, xcc.data()))
+    m->ps_l2_items = ps_localize(m->ps, m->ps_blocks, d.num_heads, d.num_kv_heads, L0.o->T, xcc.data(), roles.data());
+  m->ps.l2 = m->ps_l2_items > 0 ? 1 : 0;
   m->ps_smem = ps_smem_bytes(m->ps, H, m->QS);
   if (!ps_prepare(m->ps, m->ps_smem)) {
     m->ps = PsShape{};
@@ -1170,7 +1180,9 @@ static int ps_setup(tlm_model* m) {
   if (!rc) rc = model_alloc((void**)&m->ps_pub_o, w8 * L * m->QS);
   if (!rc) rc = model_alloc((void**)&m->ps_pub_xm, w8 * L * m->ps.ko * H);
   if (!rc) rc = model_alloc((void**)&m->ps_pub_h, w8 * L * L0.gu->T * 32);
+  if (!rc) rc = model_alloc((void**)&m->ps_xcc, sizeof(int) * m->ps_blocks);
   if (rc) return rc;
+  HIP_TRY(hipMemcpy(m->ps_xcc, xcc.data(), sizeof(int) * m->ps_blocks, hipMemcpyHostToDevice));
   HIP_TRY(hipMemcpy(m->ps_layers, tab.data(), sizeof(PsLayer) * L, hipMemcpyHostToDevice));
   HIP_TRY(hipMemcpy(m->ps_roles, roles.data(), sizeof(int) * roles.size(), hipMemcpyHostToDevice));
   const int seq = 1;  // the buffers are zero: token number 0 never matches
@@ -1341,7 +1353,7 @@ void tlm_model_destroy(tlm_model* m) {
   void* bufs[] = {m->emb, m->final_norm, m->ctrl, m->tokens_out, m->prompt, m->xa, m->x0, m->xf, m->attn_out,
                   m->pq, m->po, m->rb, m->logits, m->arg_val, m->arg_idx, m->arg_key, m->arg_arrived, m->cand_v, m->cand_i, m->pf_x, m->pf_part, m->pf_xn,
                   m->pf_q, m->pf_att, m->pf_h, m->pf_ovf, m->ps_layers, m->ps_roles, m->ps_pub_x, m->ps_pub_qkv,
-                  m->ps_pub_o, m->ps_pub_xm, m->ps_pub_h, m->ps_args_dev};
+                  m->ps_pub_o, m->ps_pub_xm, m->ps_pub_h, m->ps_args_dev, m->ps_xcc};
   for (void* p : bufs) hipFree(p);
   delete m;
 }
@@ -2119,6 +2131,16 @@ static int ps_recover(tlm_model* m, int err) {
                              "without a read; the tokens computed since the last read are invalid",
                 err & kPsErrTimeout ? "timed out" : "overflowed fp16", kRedoMax);
   }
+  if ((err & kPsErrTimeout) && m->ps_l2_items > 0) {
+    // a block may have run on another XCD than its roles were placed for, where
+    // a plain store never reaches its consumers: every handoff device-scope
+    m->ps_l2_items = 0;
+    m->ps.l2 = 0;
+    PsArgs a;  // the launch's arguments as they are, without the XCD table
+    HIP_TRY(hipMemcpy(&a, m->ps_args_dev, sizeof a, hipMemcpyDeviceToHost));
+    a.xcc = nullptr;
+    HIP_TRY(hipMemcpy(m->ps_args_dev, &a, sizeof a, hipMemcpyHostToDevice));
+  }
   if (err & kPsErrRange) {
     int rc = ps_register(m, false);
     if (rc) return rc;
@@ -2518,8 +2540,9 @@ int tlm_model_describe(tlm_model* m, char* out, size_t len) {
     const int items = nq + a.Hq + To * a.ko + ng + To * a.ks;
     char b[320];
     snprintf(b, sizeof b, " persistent[%d blocks, %d items: %d k|v (%d splits), %d q+att, %d o (%d splits), %d gate|up "
-             "(32x%d), %d down (%d splits); %zu B LDS; variant nx=%d no=%d nd=%d]", m->ps_blocks, items, nq, a.kq,
-             a.Hq, To * a.ko, a.ko, ng, a.mw, To * a.ks, a.ks, m->ps_smem, m->ps.nx, m->ps.no, m->ps.nd);
+             "(32x%d), %d down (%d splits); %zu B LDS; variant nx=%d no=%d nd=%d; %d publish through their XCD's L2]",
+             m->ps_blocks, items, nq, a.kq, a.Hq, To * a.ko, a.ko, ng, a.mw, To * a.ks, a.ks, m->ps_smem, m->ps.nx,
+             m->ps.no, m->ps.nd, m->ps_l2_items);
     s += b;
   } else {
     s += m->ps_range_off ? " persistent[off after an fp16 range overflow]" : " persistent[off]";

@@ -221,8 +221,10 @@ bool launch_topk(const float* logits, int n, int k, float softcap, float* wv, in
 //         projection (split 0 adds x_mid): the residual is the sum of the ks
 //         partials
 // Producers publish 8-byte words (fp32 value, token number ctrl[C_SEQ]) with
-// device-scope stores (past the per-XCD L2); a consumer polls its words until
-// they all carry the current token number.  No atomics, no clearing between
+// device-scope stores (past the per-XCD L2), or with plain stores into their
+// XCD's L2 where every consumer runs on the same XCD (ps_localize); a consumer
+// polls its words with device-scope loads until they all carry the current
+// token number.  No atomics, no clearing between
 // tokens.  Every wait is bounded (kPsTimeoutTicks); a time-out sets ctrl[C_ERR].
 // The q4 linears dot fp16 copies of their inputs (two weights per
 // v_dot2_f32_f16, fp32 sums); an input past the fp16 range makes the last
@@ -237,6 +239,9 @@ constexpr long long kPsTimeoutTicks = 10000000;  // 100 ms of the 100 MHz wall c
 // finite (an input of a q4 linear overflowed its fp16 copy)
 constexpr int kPsErrTimeout = 1, kPsErrRange = 2;
 enum PsStage { PS_QKV = 0, PS_ATT = 1, PS_O = 2, PS_GU = 3, PS_DOWN = 4, PS_STAGES = 5 };
+// Role code bit: the item publishes through its XCD's L2 (its consumers share
+// the XCD); the stage is the code's low byte.
+constexpr int kPsLocal = 0x100, kPsStageMask = 0xFF;
 struct PsLayer {
   const uint4* wqkv;
   const uint16_t* sqkv;
@@ -255,7 +260,9 @@ struct PsLayer {
 };
 struct PsArgs {
   const PsLayer* layers;  // [L]
-  const int* roles;       // [blocks][kPsRoles][2]: (stage, item) pairs in stage order; stage -1: none
+  const int* roles;       // [blocks][kPsRoles][2]: (stage code, item) pairs in stage order; stage -1: none
+  const int* xcc;         // [blocks] the XCD each block ran on when the roles were placed (null: no
+                          // handoff through an L2; a block on another XCD publishes device-scope)
   int L, H, I, Hq, Hkv, D, G, rd, max_tokens;
   int Nqkv, QS;
   int Cx, Co, Cd;         // chunks per row: H-input linears (qkv, gate|up), O (K = QS), down (K = I)
@@ -289,12 +296,21 @@ constexpr int kPsEvents = 4;  // weights issued, input ready, computed, publishe
 // Template choice of the persistent kernel for a model (dt == 0: none).
 struct PsShape {
   int fmt, kv_f32, dt, nx, no, nd, mw, kq, ko, ks;
+  int l2;  // launch the variant whose marked roles publish through their XCD's L2
 };
 PsShape ps_shape(int fmt, int kv_f32, int H, int I, int D, int Hq, int Hkv, int cus);
 size_t ps_smem_bytes(const PsShape& sh, int H, int QS);
 // Block roles of a shape: [blocks][kPsRoles][2] (stage, item), stage -1 = none;
 // false when the items need more than kPsRoles roles per block.
 bool ps_roles(const PsShape& sh, int blocks, int H, int Hq, int Hkv, int Tgu, int* roles);
+// The XCD (XCC id) of each block of a `blocks`-block launch; false on a HIP error.
+bool ps_xcc_probe(int blocks, int* xcc);
+// Moves the roles so that each group of k|v, attention and (when an O split
+// covers whole kv heads) O items shares one class of blocks (equal b % 8,
+// one XCD by xcc) and marks the items whose consumers all share it
+// (kPsLocal); returns how many it marked, 0 (roles unchanged) when the
+// blocks' XCDs are not one per class or a group does not fit its class.
+int ps_localize(const PsShape& sh, int blocks, int Hq, int Hkv, int To, const int* xcc, int* roles);
 // once per model, outside stream capture: allows the kernel smem bytes of LDS
 bool ps_prepare(const PsShape& sh, size_t smem);
 // a_dev: the arguments in device memory (kernel reads them with scalar loads)

@@ -18,6 +18,7 @@
 
 #include <algorithm>
 #include <type_traits>
+#include <vector>
 
 #include "tlm_device.h"
 
@@ -33,6 +34,17 @@ __device__ __forceinline__ u64 ld_dev(const u64* p) {
 __device__ __forceinline__ void st_dev(u64* p, u64 v) {
   __hip_atomic_store(glw(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// A handoff word whose consumers all run on this XCD: a plain store, which
+// stays in the XCD's L2 where their device-scope loads find it (0.95 against
+// 1.5 us per producer-consumer round trip through device-scope stores).
+__device__ __forceinline__ void st_pub(bool l2, u64* p, u64 v) {
+  if (l2)
+    __hip_atomic_store(glw(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  else
+    st_dev(p, v);
+}
+// This wave's XCD (hardware register XCC_ID).
+__device__ __forceinline__ int xcc_id() { return __builtin_amdgcn_s_getreg(20 | (0 << 6) | ((16 - 1) << 11)) & 0xF; }
 __device__ __forceinline__ u64 word(float v, unsigned seq) { return ((u64)seq << 32) | __float_as_uint(v); }
 __device__ __forceinline__ float word_value(u64 w) { return __uint_as_float((unsigned)w); }
 __device__ __forceinline__ bool word_is(u64 w, unsigned seq) { return (unsigned)(w >> 32) == seq; }
@@ -351,7 +363,8 @@ constexpr int ps_lin_floats(int ck, int nu, int r) { return kPsWaves * r * 64 + 
 // the summed dot products (a rotation and a scale are linear).  Publishes the
 // partial sums with RoPE applied (k) and the bias in split 0.
 template <int FMT, typename KT, int DT, int NX>
-__device__ __forceinline__ bool ps_qkv(const PsArgs& a, int l, int i, int pos, int token, unsigned seq, float* sm) {
+__device__ __forceinline__ bool ps_qkv(const PsArgs& a, int l, int i, int pos, int token, unsigned seq, bool l2,
+                                       float* sm) {
   constexpr int NT = DT / 64;
   constexpr int CK = FMT == WF_Q4 ? 32 : 8;
   const int lane = threadIdx.x & 63, wave = wave_id();
@@ -408,7 +421,7 @@ __device__ __forceinline__ bool ps_qkv(const PsArgs& a, int l, int i, int pos, i
     if (NT == 1 && half == 32) {  // the rotation partner of lane d is lane d ^ 32
       const float val = bias[0] + inv * ps_sum16(s.red + lane, 64), partner = lane_swap32(val);
       const float y = kind < 2 ? val * rc[0] + (lane < 32 ? -partner : partner) * rs[0] : val;
-      st_dev(a.pub_qkv + ((size_t)l * a.kq + j) * a.Nqkv + r0 + lane, word(y, seq));
+      st_pub(l2, a.pub_qkv + ((size_t)l * a.kq + j) * a.Nqkv + r0 + lane, word(y, seq));
     } else {
 #pragma unroll
       for (int t = 0; t < NT; t++) s.out[64 * t + lane] = bias[t] + inv * ps_sum16(s.red + t * 64 + lane, NT * 64);
@@ -418,7 +431,7 @@ __device__ __forceinline__ bool ps_qkv(const PsArgs& a, int l, int i, int pos, i
         const int d = 64 * t + lane;
         float val = s.out[d];
         if (kind < 2 && d < a.rd) val = val * rc[t] + (d < half ? -s.out[d + half] : s.out[d - half]) * rs[t];
-        st_dev(a.pub_qkv + ((size_t)l * a.kq + j) * a.Nqkv + r0 + d, word(val, seq));
+        st_pub(l2, a.pub_qkv + ((size_t)l * a.kq + j) * a.Nqkv + r0 + d, word(val, seq));
       }
     }
     ps_stamp(a, l, PS_QKV, 3);
@@ -456,7 +469,7 @@ constexpr int ps_att_head_floats() {
 // LDS in wave order.
 template <int FMT, typename KT, int DT, int NX>
 __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first, int pos, int token, unsigned seq,
-                                       float* sm) {
+                                       bool l2, float* sm) {
   constexpr int ESZ = sizeof(KT);
   constexpr HeadTiling TL = head_tiling(DT, ESZ);
   constexpr int LPP = TL.lpp, SUB = TL.sub, DL = TL.dl;
@@ -737,7 +750,7 @@ __device__ __forceinline__ bool ps_att(const PsArgs& a, int l, int h, int first,
     float od = 0.f;
 #pragma unroll
     for (int w = 0; w < kPsWaves; w++) od = fmaf(ow[w], readlane(f, w), od);
-    st_dev(a.pub_o + (size_t)l * a.QS + h * DT + tid, word(od / L, seq));
+    st_pub(l2, a.pub_o + (size_t)l * a.QS + h * DT + tid, word(od / L, seq));
   }
   if (wave == 0) ps_stamp(a, l, PS_ATT, 3);
   return true;
@@ -897,7 +910,7 @@ __device__ __forceinline__ bool ps_down(const PsArgs& a, int l, int t, int sp, u
 }
 
 // -------------------------------------------------------------------- kernel --
-template <int FMT, typename KT, int DT, int NX, int NO, int ND, int MW>
+template <int FMT, typename KT, int DT, int NX, int NO, int ND, int MW, bool L2>
 __global__ __launch_bounds__(kPsWaves * 64) void ps_token_kernel(const PsArgs* __restrict__ ap) {
   extern __shared__ float sm[];
   const PsArgs& a = *ap;  // in device memory: field reads are scalar loads
@@ -906,17 +919,21 @@ __global__ __launch_bounds__(kPsWaves * 64) void ps_token_kernel(const PsArgs* _
   if (pos < 0 || pos >= a.max_tokens) return;
   ps_stamp(a, a.L, 0, 0);
   const TLM_GLOBAL int* rl = gl(a.roles) + blockIdx.x * kPsRoles * 2;
+  // handoffs through the L2 only on the XCD the roles were placed for
+  const bool on_xcd = L2 && a.xcc && xcc_id() == gl(a.xcc)[blockIdx.x];
   for (int l = 0; l < a.L; l++) {
     const int win = gl(a.layers)[l].window;  // DecoderCPURunner.ts:150 (block.slidingWindow)
     const int first = win > 0 ? max(pos - win + 1, 0) : 0;
 #pragma unroll 1
     for (int r = 0; r < kPsRoles; r++) {
-      const int st = rl[2 * r], it = rl[2 * r + 1];
+      const int code = rl[2 * r], it = rl[2 * r + 1];
+      const int st = code < 0 ? -1 : code & kPsStageMask;
+      const bool l2 = on_xcd && (code & kPsLocal);
       bool ok = true;
       if (st == PS_QKV)
-        ok = ps_qkv<FMT, KT, DT, NX>(a, l, it, pos, token, seq, sm);
+        ok = ps_qkv<FMT, KT, DT, NX>(a, l, it, pos, token, seq, l2, sm);
       else if (st == PS_ATT)
-        ok = ps_att<FMT, KT, DT, NX>(a, l, it, first, pos, token, seq, sm);
+        ok = ps_att<FMT, KT, DT, NX>(a, l, it, first, pos, token, seq, l2, sm);
       else if (st == PS_O)
         ok = ps_o<FMT, NO>(a, l, it, token, seq, sm);
       else if (st == PS_GU)
@@ -1052,6 +1069,95 @@ bool ps_roles(const PsShape& sh, int blocks, int H, int Hq, int Hkv, int Tgu, in
   return ps_place(counts, blocks, roles) > 0;
 }
 
+__global__ void ps_xcc_kernel(int* xcc) {
+  if (threadIdx.x == 0) xcc[blockIdx.x] = xcc_id();
+}
+
+bool ps_xcc_probe(int blocks, int* xcc) {
+  int* d = nullptr;
+  if (hipMalloc(&d, sizeof(int) * blocks) != hipSuccess) return false;
+  hipLaunchKernelGGL(ps_xcc_kernel, dim3(blocks), dim3(64), 0, 0, d);
+  const bool ok = hipGetLastError() == hipSuccess && hipDeviceSynchronize() == hipSuccess &&
+                  hipMemcpy(xcc, d, sizeof(int) * blocks, hipMemcpyDeviceToHost) == hipSuccess;
+  hipFree(d);
+  return ok;
+}
+
+// The hardware hands a launch's workgroups to the XCDs in turn, so blocks with
+// one value of b % 8 share an XCD (checked on xcc).  A group is the k|v items
+// and attention items of one kv head, and, when every O split covers whole kv
+// heads, those of all kv heads of one split together with the split's O items.
+// Each group goes to one class of blocks; the k|v items publish through the
+// L2 (their consumers are the group's attention items), and so do the
+// attention items when the O items are in the group.
+int ps_localize(const PsShape& sh, int blocks, int Hq, int Hkv, int To, const int* xcc, int* roles) {
+  constexpr int kClasses = 8;
+  if (!xcc || blocks % kClasses != 0 || Hkv <= 0 || Hq % Hkv != 0) return 0;
+  for (int b = 0; b < blocks; b++)
+    if (xcc[b] != xcc[b % kClasses]) return 0;
+  for (int c = 0; c < kClasses; c++)
+    for (int e = c + 1; e < kClasses; e++)
+      if (xcc[c] == xcc[e]) return 0;
+  const int G = Hq / Hkv, CK = sh.fmt == WF_Q4 ? 32 : 8, QS = Hq * sh.dt;
+  const int co = (QS / CK + sh.ko - 1) / sh.ko;  // O chunks per split
+  bool o_in = true;                               // every O split covers whole kv heads
+  for (int j = 0; j < sh.ko; j++) {
+    const int d0 = j * co * CK, d1 = std::min((j + 1) * co * CK, QS);
+    if (d0 % (G * sh.dt) != 0 || (d1 % (G * sh.dt) != 0 && d1 != QS)) o_in = false;
+  }
+  const int groups = o_in ? sh.ko : Hkv;
+  if (groups > kClasses) return 0;
+  auto group_of_kv = [&](int g) { return o_in ? g * G * sh.dt / (co * CK) : g; };
+  auto group_of = [&](int st, int it) {
+    if (st == PS_QKV) return group_of_kv((it / sh.kq) % Hkv);
+    if (st == PS_ATT) return group_of_kv(it / G);
+    if (st == PS_O && o_in) return it / To;
+    return -1;
+  };
+  const int per = blocks / kClasses;
+  std::vector<int> used(kClasses, 0), dest(blocks, -1);
+  std::vector<bool> taken(blocks, false);
+  // blocks holding a group's item first, each to the next free block of its class
+  for (int b = 0; b < blocks; b++) {
+    int g = -1;
+    for (int r = 0; r < kPsRoles; r++) {
+      const int st = roles[2 * (kPsRoles * b + r)];
+      if (st < 0) continue;
+      const int gi = group_of(st, roles[2 * (kPsRoles * b + r) + 1]);
+      if (gi < 0) continue;
+      if (g >= 0 && gi != g) return 0;  // two groups on one block
+      g = gi;
+    }
+    if (g < 0) continue;
+    if (used[g] == per) return 0;  // the group does not fit its class
+    const int nb = g + kClasses * used[g]++;
+    dest[b] = nb;
+    taken[nb] = true;
+  }
+  int next = 0;
+  for (int b = 0; b < blocks; b++) {
+    if (dest[b] >= 0) continue;
+    while (taken[next]) next++;
+    dest[b] = next;
+    taken[next] = true;
+  }
+  std::vector<int> out((size_t)2 * kPsRoles * blocks);
+  int marked = 0;
+  for (int b = 0; b < blocks; b++)
+    for (int r = 0; r < kPsRoles; r++) {
+      int st = roles[2 * (kPsRoles * b + r)];
+      const int it = roles[2 * (kPsRoles * b + r) + 1];
+      if (st == PS_QKV || (st == PS_ATT && o_in)) {
+        st |= kPsLocal;
+        marked++;
+      }
+      out[2 * (kPsRoles * dest[b] + r)] = st;
+      out[2 * (kPsRoles * dest[b] + r) + 1] = it;
+    }
+  std::copy(out.begin(), out.end(), roles);
+  return marked;
+}
+
 size_t ps_smem_bytes(const PsShape& sh, int H, int QS) {
   (void)H;
   (void)QS;
@@ -1068,11 +1174,14 @@ size_t ps_smem_bytes(const PsShape& sh, int H, int QS) {
 }
 
 // The compiled kernel of a shape (null: none).
-static const void* ps_kernel(const PsShape& sh) {
+// (l2: the variant that publishes through an XCD's L2 where the roles say so;
+// the other one has no such stores at all)
+static const void* ps_kernel(const PsShape& sh, bool l2) {
 #define PS_CASE(F, KV, DTV, NXV, NOV, NDV, MWV)                                                             \
   if (sh.fmt == F && sh.kv_f32 == KV && sh.dt == DTV && sh.nx == NXV && sh.no == NOV && sh.nd == NDV &&   \
       sh.mw == MWV)                                                                                       \
-    return (const void*)ps_token_kernel<F, std::conditional_t<KV, float, uint16_t>, DTV, NXV, NOV, NDV, MWV>;
+    return l2 ? (const void*)ps_token_kernel<F, std::conditional_t<KV, float, uint16_t>, DTV, NXV, NOV, NDV, MWV, true>  \
+              : (const void*)ps_token_kernel<F, std::conditional_t<KV, float, uint16_t>, DTV, NXV, NOV, NDV, MWV, false>;
   PS_CASE(WF_Q4, 0, 64, 2, 1, 3, 1)
   PS_CASE(WF_Q4, 0, 64, 4, 1, 4, 1)
   PS_CASE(WF_Q4, 0, 64, 1, 1, 1, 1)
@@ -1082,12 +1191,15 @@ static const void* ps_kernel(const PsShape& sh) {
 }
 
 bool ps_prepare(const PsShape& sh, size_t smem) {
-  const void* k = ps_kernel(sh);
-  return k && hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) == hipSuccess;
+  for (bool l2 : {false, true}) {
+    const void* k = ps_kernel(sh, l2);
+    if (!k || hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess) return false;
+  }
+  return true;
 }
 
 bool launch_ps_token(const PsShape& sh, int blocks, size_t smem, const PsArgs* a_dev, hipStream_t st) {
-  const void* k = ps_kernel(sh);
+  const void* k = ps_kernel(sh, sh.l2 != 0);
   if (!k) return false;
   const PsArgs* arg = a_dev;
   void* params[] = {&arg};
