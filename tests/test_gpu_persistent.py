@@ -242,7 +242,8 @@ def test_a_wait_that_runs_out_is_recomputed_and_every_block_leaves(ctx):
     instead of 100) and its block leaves.  The kernel ends, and the read that
     follows finds the flag and recomputes the tokens enqueued since the last
     read on the per-stage graph: it returns the oracle's logits (and a greedy
-    run the oracle's tokens), and the model keeps its persistent schedule."""
+    run the oracle's tokens), and the model keeps its persistent schedule,
+    with every handoff device-scope from then on."""
     wl = _workload("tiny", 2, 64)
     hw = W.synthetic(wl)
     hw.keep = True
@@ -258,6 +259,7 @@ def test_a_wait_that_runs_out_is_recomputed_and_every_block_leaves(ctx):
             else:
                 os.environ[k] = v
     assert re.search(r"persistent\[\d+ blocks", bad.model.describe())
+    l2_before = int(re.search(r"(\d+) publish through their XCD's L2", bad.model.describe()).group(1))
     om = oracle_model(hw, 64, kv_f16=True, threads=16)
     toks = [5, 9, 11]
     for step, t in enumerate(toks):
@@ -281,6 +283,10 @@ def test_a_wait_that_runs_out_is_recomputed_and_every_block_leaves(ctx):
         t = d
     assert bad.model.counts()["recomputed_positions"] == 3 + 2 + 4
     assert re.search(r"persistent\[\d+ blocks", bad.model.describe())
+    # a time-out also turns the handoffs through an XCD's L2 off (a block may have
+    # run on another XCD than its roles were placed for)
+    assert l2_before > 0
+    assert "; 0 publish through their XCD's L2" in bad.model.describe()
     bad.close()
     om.close()
 
