@@ -771,9 +771,9 @@ static const bool g_use_ring = [] {
   const char* e = getenv("TLM_GEMM_RING");
   return !(e && e[0] == '0');
 }();
-// TLM_GEMM_SPLIT_WAVES=n: split K until the grid holds n waves per CU (default
-// 4: with 32-row K-wave tiles, 4 beat 8 by 2-7 % from 127 to 1100 rows; every
-// split adds an M x N fp32 slice that the consuming row kernel folds)
+// TLM_GEMM_SPLIT_WAVES=n: split K while the grid holds at most n waves per CU
+// (default 4: with 32-row K-wave tiles, 4 beat 8 by 2-7 % from 127 to 1100
+// rows; every split adds an M x N fp32 slice that the consuming row kernel folds)
 static const int g_split_waves = [] {
   const char* e = getenv("TLM_GEMM_SPLIT_WAVES");
   const int v = e ? atoi(e) : 0;
@@ -827,10 +827,20 @@ GemmShape gemm_shape(int fmt, int epi, int M, int N, int K, int cus) {
       const double cost = (double)rounds * ((steps + sp - 1) / sp) + sp * slice_steps;
       if (cost < best) best = cost, splits = sp;
     }
-  } else if (epi == GEMM_PART) {  // split K until the grid holds about g_split_waves waves per CU
+  } else if (epi == GEMM_PART) {
+    // split K while the grid stays within about g_split_waves waves per CU:
+    // past one round of blocks a CU streams the same bytes either way and each
+    // split only adds a slice for the next row kernel to fold (Qwen2.5-0.5B
+    // shape, 64 to 300 rows: the down GEMM in 4 splits instead of 8, the chunk
+    // 3-6 % faster; TLM_GEMM_SPLIT_FLOOR=0 splits until the grid reaches that
+    // size instead)
     const int target = g_split_waves * cus;
     const int waves = s.gx * s.gy * (s.ring ? (s.kw ? 4 : s.wn) : 4);
-    while (splits < 32 && waves * splits < target && steps / (2 * splits * kdiv) >= min_steps) splits *= 2;
+    static const bool floor_rule = [] { const char* e = getenv("TLM_GEMM_SPLIT_FLOOR"); return !(e && e[0] == '0'); }();
+    if (floor_rule)
+      while (splits < 32 && waves * splits * 2 <= target && steps / (2 * splits * kdiv) >= min_steps) splits *= 2;
+    else
+      while (splits < 32 && waves * splits < target && steps / (2 * splits * kdiv) >= min_steps) splits *= 2;
   }
   s.spc = (steps + splits - 1) / splits;
   s.splits = (steps + s.spc - 1) / s.spc;
