@@ -171,6 +171,8 @@ struct PsDevice {
 };
 static PsDevice g_ps_dev[kScratchDevices];
 
+constexpr int kPinPrompt = 16;  // first prompt word of tlm_model::host_pin
+
 struct tlm_model {
   tlm_ctx* ctx = nullptr;
   tlm_model_desc d{};
@@ -206,6 +208,10 @@ struct tlm_model {
   int pf_min_rows = 64, pf_chunk = 2048, pf_cap = 0;
   float *pf_x = nullptr, *pf_part = nullptr;  // residual rows, split-K slices
   int* pf_ovf = nullptr;   // device flag: a batched chunk rounded a non-finite fp16 activation
+  // pinned host words: [0, 8) the control block read back, [8] the fp16 flag
+  // read back, [kPinPrompt, + max_tokens) the prompt ids on their way to the
+  // device (asynchronous copies: the host does not wait for a staging copy)
+  int* host_pin = nullptr;
   int pf_replayed = 0;     // batched chunks replayed on the decode graph after such a flag
   size_t pf_part_n = 0;
   uint16_t *pf_xn = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_h = nullptr;
@@ -450,6 +456,7 @@ static int ps_ordered(tlm_model* m, F enqueue) {
 }
 
 static int model_check(tlm_model* m, const int* ctrl_host = nullptr);
+static int read_ctrl(tlm_model* m, int* c);
 static int kv_clear(tlm_model* m, int pos0, int n);
 
 
@@ -1266,6 +1273,11 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
   M_TRY(model_alloc((void**)&m->ctrl, sizeof(int) * 8));
   M_TRY(model_alloc((void**)&m->tokens_out, sizeof(int) * d->max_tokens));
   M_TRY(model_alloc((void**)&m->prompt, sizeof(int) * d->max_tokens));
+  if (rc == TLM_OK && hipHostMalloc((void**)&m->host_pin, sizeof(int) * (kPinPrompt + d->max_tokens),
+                                    hipHostMallocDefault) != hipSuccess) {
+    m->host_pin = nullptr;
+    rc = fail(TLM_ERR_HIP, "TLMModel: pinned host buffer allocation failed");
+  }
   M_TRY(model_alloc((void**)&m->xa, sizeof(float) * H));
   M_TRY(model_alloc((void**)&m->x0, sizeof(unsigned long long) * kRep * H));
   M_TRY(model_alloc((void**)&m->rb, sizeof(unsigned long long) * kRep * H * d->num_layers));
@@ -1355,6 +1367,7 @@ void tlm_model_destroy(tlm_model* m) {
                   m->pf_q, m->pf_att, m->pf_h, m->pf_ovf, m->ps_layers, m->ps_roles, m->ps_pub_x, m->ps_pub_qkv,
                   m->ps_pub_o, m->ps_pub_xm, m->ps_pub_h, m->ps_args_dev, m->ps_xcc};
   for (void* p : bufs) hipFree(p);
+  if (m->host_pin) hipHostFree(m->host_pin);
   delete m;
 }
 
@@ -2064,7 +2077,11 @@ int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end)
   HIP_TRY(hipStreamSynchronize(st));
   rc = model_check(m);  // the earlier tokens are final before batched chunks overwrite cache rows
   if (rc) return rc;
-  HIP_TRY(hipMemcpy(m->prompt, tokens + start, sizeof(int32_t) * (end - start), hipMemcpyHostToDevice));
+  // the ids go to the device in stream order (no staging wait on the host);
+  // the pinned words are free again: the stream finished its work above
+  memcpy(m->host_pin + kPinPrompt, tokens + start, sizeof(int32_t) * (end - start));
+  HIP_TRY(hipMemcpyAsync(m->prompt, m->host_pin + kPinPrompt, sizeof(int32_t) * (end - start), hipMemcpyHostToDevice,
+                         st));
   const bool batched = m->pf_min_rows > 0 && !prefill_unsupported(m);
   for (int p = start; p < end;) {
     const int n = std::min(end - p, batched ? m->pf_chunk : end - p);
@@ -2074,10 +2091,9 @@ int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end)
       if (rc) return rc;
       // an fp16 activation of the chunk overflowed (or was NaN): the chunk's
       // cache rows are rewritten by the fp32 decode path
-      int ovf = 0;
-      HIP_TRY(hipMemcpyAsync(&ovf, m->pf_ovf, sizeof(int), hipMemcpyDeviceToHost, st));
+      HIP_TRY(hipMemcpyAsync(m->host_pin + 8, m->pf_ovf, sizeof(int), hipMemcpyDeviceToHost, st));
       HIP_TRY(hipStreamSynchronize(st));
-      if (ovf) {
+      if (m->host_pin[8]) {
         const int zero = 0;
         HIP_TRY(hipMemcpy(m->pf_ovf, &zero, sizeof(int), hipMemcpyHostToDevice));
         m->pf_replayed++;
@@ -2173,15 +2189,24 @@ static int ps_recover(tlm_model* m, int err) {
 // bounded wait ran out, the late block left; or its last residual was not
 // finite): the logged tokens are recomputed (ps_recover) before the caller
 // reads anything.  Clean: the logged tokens are final.
+// The control block, read after the model's stream has finished its work
+// (through the pinned words: a direct copy, no staging).
+static int read_ctrl(tlm_model* m, int* c) {
+  HIP_TRY(hipMemcpyAsync(m->host_pin, m->ctrl, sizeof(int) * 8, hipMemcpyDeviceToHost, m->ctx->stream));
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  memcpy(c, m->host_pin, sizeof(int) * 8);
+  return TLM_OK;
+}
+
 static int model_check(tlm_model* m, const int* ctrl_host) {
   int c[8];
   if (ctrl_host) memcpy(c, ctrl_host, sizeof c);
-  else HIP_TRY(hipMemcpy(c, m->ctrl, sizeof c, hipMemcpyDeviceToHost));
+  else if (int rc = read_ctrl(m, c)) return rc;
   if (m->ps_on && c[C_ERR]) {
     const int zero = 0;
     HIP_TRY(hipMemcpy(m->ctrl + C_ERR, &zero, sizeof(int), hipMemcpyHostToDevice));
     if (int rc = ps_recover(m, c[C_ERR])) return rc;
-    HIP_TRY(hipMemcpy(c, m->ctrl, sizeof c, hipMemcpyDeviceToHost));
+    if (int rc = read_ctrl(m, c)) return rc;
   }
   m->redo.clear();
   m->redo_lost = false;
@@ -2228,11 +2253,11 @@ int tlm_read_token(tlm_model* m, int32_t* token) {
   if (!m || !token) return fail(TLM_ERR_INVALID, "TLMModel: null argument");
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
   int ctrl[8];
-  HIP_TRY(hipMemcpy(ctrl, m->ctrl, sizeof ctrl, hipMemcpyDeviceToHost));
+  if (int rc = read_ctrl(m, ctrl)) return rc;
   const bool recompute = m->ps_on && ctrl[C_ERR];
   if (int rc = model_check(m, ctrl)) return rc;
   if (recompute)  // the token is now the per-stage graph's
-    HIP_TRY(hipMemcpy(ctrl, m->ctrl, sizeof ctrl, hipMemcpyDeviceToHost));
+    if (int rc = read_ctrl(m, ctrl)) return rc;
   *token = ctrl[C_TOKEN];
   return TLM_OK;
 }
