@@ -150,7 +150,7 @@ def prefill_flops(r, n: int, p0: int = 0) -> float:
 
 def prefill_chunk_bench(W, R, ctx, workload: str, n: int) -> dict:
     """One prefill chunk of n random ids on a full-size model (the MFMA GEMM
-    path): median of 3 timed chunks after one warm-up, FLOP/s and the
+    path): median of 9 timed chunks after one warm-up, FLOP/s and the
     fraction of the dense fp16 MFMA peak."""
     wl = W.WORKLOADS[workload]
     hw = W.synthetic(wl)
@@ -158,7 +158,7 @@ def prefill_chunk_bench(W, R, ctx, workload: str, n: int) -> dict:
     runner = R.DecoderHIPRunner(hw, {"maxTokens": n + 8, "prefillChunkSize": n}, ctx=ctx)
     ids = [int(t) for t in W.prompt_tokens(W.Workload(wl.name, wl.config, wl.storage, n, 0, n))]
     times = []
-    for rep in range(4):
+    for rep in range(10):
         runner.resetCache()
         ctx.sync()
         t0 = time.perf_counter()
@@ -166,7 +166,7 @@ def prefill_chunk_bench(W, R, ctx, workload: str, n: int) -> dict:
         ctx.sync()
         if rep:
             times.append(time.perf_counter() - t0)
-    dt = sorted(times)[1]
+    dt = sorted(times)[len(times) // 2]
     flops = prefill_flops(hw.recipe, n)
     out = {"workload": wl.name, "tokens": n, "batched": runner.batchedPrefill, "ms": round(dt * 1e3, 3),
            "tok_s": round(n / dt, 1), "tflops": round(flops / dt / 1e12, 1),
