@@ -215,6 +215,8 @@ struct tlm_model {
   int pf_replayed = 0;     // batched chunks replayed on the decode graph after such a flag
   size_t pf_part_n = 0;
   uint16_t *pf_xn = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_h = nullptr;
+  int* pf_ex = nullptr;      // per row: the exponent of the attention norm's scale (GEMM_FOLD)
+  float* pf_ss = nullptr;    // per row and 64-column tile: sums of squares of the residual (GEMM_FOLD)
   // per attention mode: [0] short windows, [1] long windows (long_window)
   hipGraphExec_t g_logits[2] = {}, g_prefill[2] = {}, g_layers[2] = {};
   hipGraph_t graph_logits[2] = {}, graph_prefill[2] = {}, graph_layers[2] = {};
@@ -1364,7 +1366,7 @@ void tlm_model_destroy(tlm_model* m) {
   attn_free(&m->attn, false);
   void* bufs[] = {m->emb, m->final_norm, m->ctrl, m->tokens_out, m->prompt, m->xa, m->x0, m->xf, m->attn_out,
                   m->pq, m->po, m->rb, m->logits, m->arg_val, m->arg_idx, m->arg_key, m->arg_arrived, m->cand_v, m->cand_i, m->pf_x, m->pf_part, m->pf_xn,
-                  m->pf_q, m->pf_att, m->pf_h, m->pf_ovf, m->ps_layers, m->ps_roles, m->ps_pub_x, m->ps_pub_qkv,
+                  m->pf_q, m->pf_att, m->pf_h, m->pf_ex, m->pf_ss, m->pf_ovf, m->ps_layers, m->ps_roles, m->ps_pub_x, m->ps_pub_qkv,
                   m->ps_pub_o, m->ps_pub_xm, m->ps_pub_h, m->ps_args_dev, m->ps_xcc};
   for (void* p : bufs) hipFree(p);
   if (m->host_pin) hipHostFree(m->host_pin);
@@ -1752,10 +1754,12 @@ static int prefill_alloc(tlm_model* m, int rows, size_t part) {
   }
   if (m->pf_cap >= rows) return TLM_OK;
   rows = std::max(rows, m->pf_chunk);  // one allocation serves every later chunk
-  void* bufs[] = {m->pf_x, m->pf_xn, m->pf_q, m->pf_att, m->pf_h};
+  void* bufs[] = {m->pf_x, m->pf_xn, m->pf_q, m->pf_att, m->pf_h, m->pf_ex, m->pf_ss};
   for (void* q : bufs) hipFree(q);
   m->pf_x = nullptr;
   m->pf_xn = m->pf_q = m->pf_att = m->pf_h = nullptr;
+  m->pf_ex = nullptr;
+  m->pf_ss = nullptr;
   m->pf_cap = 0;
   const size_t R = (size_t)rows, H = m->d.hidden_size, I = m->d.intermediate_size;
   int rc = TLM_OK;
@@ -1764,6 +1768,8 @@ static int prefill_alloc(tlm_model* m, int rows, size_t part) {
   if (!rc) rc = model_alloc((void**)&m->pf_q, 2 * R * m->QS);
   if (!rc) rc = model_alloc((void**)&m->pf_att, 2 * R * m->QS);
   if (!rc) rc = model_alloc((void**)&m->pf_h, 2 * R * I);
+  if (!rc) rc = model_alloc((void**)&m->pf_ex, sizeof(int) * R);
+  if (!rc) rc = model_alloc((void**)&m->pf_ss, sizeof(float) * R * ((H + kTile - 1) / kTile));
   if (!rc) m->pf_cap = rows;
   return rc;
 }
@@ -1794,6 +1800,7 @@ static RowsArgs rows_args(float* X, const float* part, int n_part, size_t pstrid
   r.w = w;
   r.eps = (float)eps;
   r.Y = Y;
+  r.ex = nullptr;
   return r;
 }
 
@@ -1802,13 +1809,20 @@ static RowsArgs rows_args(float* X, const float* part, int n_part, size_t pstrid
 // tokens: device array of the M token ids.  Per layer: fold + RMSNorm rows ->
 // QKV GEMM (split-K slices) -> RoPE/cache append (folds the slices) -> flash
 // attention -> O GEMM (slices) -> fold + RMSNorm -> gate|up GEMM with SwiGLU ->
-// down GEMM (slices, folded by the next layer's first kernel).
+// down GEMM (slices, folded by the next layer's first kernel).  Small chunks
+// fuse the QKV GEMM with RoPE and the O GEMM with its fold (PfPlan).
 // Shapes of a batched chunk of M rows, with its row buffers allocated (on
 // first use; never while a graph is being captured).
 struct PfPlan {
-  GemmShape sq, sr, so, sg, sd;
+  GemmShape sq, sr, so, sf, sg, sd;
   bool rope_epi;
+  bool fold;  // the O GEMM folds its rows into the residual (GEMM_FOLD): no row kernel after it
 };
+// TLM_PF_FOLD=0: the row kernel after the O GEMM for every chunk (comparisons)
+static const bool g_pf_fold = [] {
+  const char* e = getenv("TLM_PF_FOLD");
+  return !(e && e[0] == '0');
+}();
 static int prefill_plan(tlm_model* m, int M, PfPlan* pp) {
   const tlm_model_desc& d = m->d;
   const int H = d.hidden_size, I = d.intermediate_size, D = d.head_dim;
@@ -1822,6 +1836,16 @@ static int prefill_plan(tlm_model* m, int M, PfPlan* pp) {
   pp->so = gemm_shape(lf, GEMM_PART, M, H, m->QS, cus);
   pp->sg = gemm_shape(lf, GEMM_SWIGLU, M, L0.gu->T * kTile, H, cus);
   pp->sd = gemm_shape(lf, GEMM_PART, M, H, I, cus);
+  // small chunks (K-wave O and gate|up GEMMs): the O GEMM, unsplit, adds its
+  // rows to the residual and writes the FFN norm's operand as fp16(x w 2^e),
+  // e from the attention norm of the same rows (which keeps it near unit
+  // scale), with each 64-column tile's sum of squares; the gate|up GEMM then
+  // applies the row's rsqrt(mean(x^2) + eps) 2^-e after the dot.  The row
+  // kernel between them drops out (127-row Qwen2.5-0.5B chunk: its 24
+  // launches were 3.6 us each; the unsplit O GEMM costs 0.4 us more).
+  pp->sf = gemm_shape(lf, GEMM_FOLD, M, H, m->QS, cus);
+  pp->fold = g_pf_fold && lf == WF_Q4 && pp->sf.ring && pp->sf.kw && pp->sg.ring && pp->sg.kw && H % kTile == 0 &&
+             H / kTile <= 32;
   const size_t part = std::max({(size_t)pp->sq.splits * M * m->Nqkv, (size_t)pp->so.splits * M * H,
                                 (size_t)pp->sd.splits * M * H});
   return prefill_alloc(m, M, part);
@@ -1843,9 +1867,10 @@ static int prefill_enqueue(tlm_model* m, const PfPlan& pp, int M, hipStream_t st
   for (int l = 0; l < d.num_layers; l++) {
     const Layer& L = m->layers[l];
     bool ok = true;
-    launch_rms_rows(rows_args(m->pf_x, m->pf_part, l ? pp.sd.splits : 0, rowsH, H, L.attn_norm, d.rms_eps, m->pf_xn,
-                              m->pf_ovf),
-                    M, st);
+    RowsArgs ra = rows_args(m->pf_x, m->pf_part, l ? pp.sd.splits : 0, rowsH, H, L.attn_norm, d.rms_eps, m->pf_xn,
+                            m->pf_ovf);
+    if (pp.fold) ra.ex = m->pf_ex;
+    launch_rms_rows(ra, M, st);
     GemmArgs g = gemm_args(L.qkv, m->pf_xn, H, M);
     g.ovf = m->pf_ovf;
     if (pp.rope_epi) {
@@ -1904,13 +1929,32 @@ static int prefill_enqueue(tlm_model* m, const PfPlan& pp, int M, hipStream_t st
     pa.scale_log2 = m->attn.scale * 1.4426950408889634f;
     ok = ok && launch_prefill_attention(pa, st);
     g = gemm_args(L.o, m->pf_att, m->QS, M);
-    g.Cf = m->pf_part;
     g.ldc = H;
-    ok = ok && launch_gemm(lf, GEMM_PART, pp.so, g, st);
-    launch_rms_rows(rows_args(m->pf_x, m->pf_part, pp.so.splits, rowsH, H, L.ffn_norm, d.rms_eps, m->pf_xn, m->pf_ovf),
-                    M, st);
+    if (pp.fold) {
+      g.Cf = m->pf_x;
+      g.Ch = m->pf_xn;
+      g.nw = L.ffn_norm;
+      g.ex = m->pf_ex;
+      g.ss = m->pf_ss;
+      g.ss_ld = H / kTile;
+      g.ovf = m->pf_ovf;
+      ok = ok && launch_gemm(lf, GEMM_FOLD, pp.sf, g, st);
+    } else {
+      g.Cf = m->pf_part;
+      ok = ok && launch_gemm(lf, GEMM_PART, pp.so, g, st);
+      launch_rms_rows(rows_args(m->pf_x, m->pf_part, pp.so.splits, rowsH, H, L.ffn_norm, d.rms_eps, m->pf_xn,
+                                m->pf_ovf),
+                      M, st);
+    }
     g = gemm_args(L.gu, m->pf_xn, H, M);
     g.ovf = m->pf_ovf;
+    if (pp.fold) {
+      g.ss = m->pf_ss;
+      g.ex = m->pf_ex;
+      g.ss_ld = H / kTile;
+      g.n_norm = H;
+      g.eps = (float)d.rms_eps;
+    }
     g.N = L.gu->T * kTile;
     g.Ch = m->pf_h;
     g.ldc = I;
@@ -1924,7 +1968,7 @@ static int prefill_enqueue(tlm_model* m, const PfPlan& pp, int M, hipStream_t st
   }
   // the last layer's MLP output joins the residual rows
   launch_rms_rows(rows_args(m->pf_x, m->pf_part, pp.sd.splits, rowsH, H, nullptr, d.rms_eps, nullptr, nullptr), M, st);
-  return 1 + d.num_layers * (pp.rope_epi ? 7 : 8) + 1;
+  return 1 + d.num_layers * ((pp.rope_epi ? 7 : 8) - (pp.fold ? 1 : 0)) + 1;
 }
 
 // One batched chunk [p, p + M) of the prompt [start, end): the control block

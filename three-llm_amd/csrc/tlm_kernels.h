@@ -325,6 +325,9 @@ enum GemmEpi {
   GEMM_SWIGLU = 2,  // Ch[m][i] = fp16(silu(gate) * up), paired gate|up weight rows (no split-K)
   GEMM_ROPE = 3,    // q|k|v rows, head_dim 64, full rotary: + bias, RoPE at position p0 + m; q to
                     // Ch (fp16 [M][Hq 64]), k and v to the fp16 caches (K-wave kernel, no split-K)
+  GEMM_FOLD = 4,    // residual rows and the next RMSNorm's operand (K-wave kernel, no split-K):
+                    // Cf[m][n] += acc (the fp32 residual rows), Ch[m][n] = fp16(x nw[n] 2^ex[m]),
+                    // ss[m][t] = sum of x^2 over the 64 columns of tile t
 };
 struct GemmArgs {
   const uint16_t* A;   // fp16 [M][lda]
@@ -347,6 +350,15 @@ struct GemmArgs {
   int* ovf;            // set to 1 when an fp16 output (h, q, k, v) is not finite; may be null
   const int* ctrl;     // non-null: the first row's position is ctrl[C_POS] instead of p0 (a
                        // captured prefill chunk serves every chunk of its size)
+  // GEMM_FOLD: nw the norm weight, ex the rows' exponents, ss the tile sums
+  // ([M][ss_ld]).  GEMM_SWIGLU with ss non-null: its operand rows came from a
+  // GEMM_FOLD; the products of row m are scaled by
+  // rsqrt(sum_t ss[m][t] / n_norm + eps) 2^-ex[m] (the RMSNorm applied after the dot).
+  const float* nw;
+  const int* ex;
+  float* ss;
+  int ss_ld, n_norm;
+  float eps;
 };
 // Tile and split-K choice of one GEMM (gemm_shape is the only planner, so the
 // host sizes the slice buffers from the same numbers the launch uses).
@@ -369,6 +381,8 @@ struct RowsArgs {
   float eps;
   uint16_t* Y;
   int* ovf;             // set to 1 when a normed fp16 value is not finite; may be null
+  int* ex;              // with Y: row m's ilogb(rsqrt(mean(x^2) + eps)), the scale exponent of a
+                        // later GEMM_FOLD of the same rows; may be null
 };
 struct PrefillAttnArgs {
   const uint16_t* q;    // fp16 [M][Hq D], RoPE applied

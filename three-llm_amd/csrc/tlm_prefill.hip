@@ -53,9 +53,30 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * __builtin_amdgcn_rcpf(1.f + __expf(-g)) * u;
 }
 
+// Sum over each 32-lane half of the wave, the same bits in every lane of the
+// half: DPP within 8 and 16 lanes, then gfx950's v_permlane16_swap (no LDS
+// round trip: ds_bpermute steps cost a wait each).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_amdgcn_update_dpp(0.f, v, CTRL, 0xF, 0xF, false);
+}
+// v of lane l ^ 32 (v_permlane32_swap: a VALU op, no LDS round trip)
+__device__ __forceinline__ float swap32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float half_sum(float v) {
+  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
+  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+  v += dpp_f<0x141>(v);  // row_half_mirror: lane i <-> 7 - i of its 8
+  v += dpp_f<0x140>(v);  // row_mirror: lane i <-> 15 - i of its 16
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return v + __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
+
 __device__ __forceinline__ float block_sum_f(float v, float* scratch) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  v = half_sum(v);
+  v += swap32(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   if (lane == 0) scratch[wave] = v;
   __syncthreads();
@@ -654,6 +675,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   }
 #pragma unroll
   for (int i = 0; i < MT; i++) kw.acc[i][0] = kw.acc[i][1] = (float16_t){};
+  // the epilogue's per-row inputs (GEMM_FOLD: residual values, exponents and
+  // norm weights; GEMM_SWIGLU after a GEMM_FOLD: exponents and tile sums),
+  // requested before the K loop, whose waits then cover them.  Lane (l32, kh)
+  // of wave w ends with rows m0 + 32 t + 8 w + 4 kh + e, columns 32 j + l32.
+  const int rbase = m0 + 4 * kh + 8 * wave;
+  const bool post_norm = EPI == GEMM_SWIGLU && g.ss != nullptr;
+  float xv[MT][2][4], nwv[2], ssv[MT][4];
+  int exv[MT][4];
+  if (EPI == GEMM_FOLD) {
+#pragma unroll
+    for (int j = 0; j < 2; j++) nwv[j] = g.nw[t0 * kTile + 32 * j + l32];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int row = min(rbase + 32 * t + e, g.M - 1);
+        exv[t][e] = g.ex[row];
+#pragma unroll
+        for (int j = 0; j < 2; j++) xv[t][j][e] = g.Cf[(size_t)row * g.ldc + t0 * kTile + 32 * j + l32];
+      }
+  }
+  if (post_norm) {
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int row = min(rbase + 32 * t + e, g.M - 1);
+        exv[t][e] = g.ex[row];
+        ssv[t][e] = l32 < g.ss_ld ? g.ss[(size_t)row * g.ss_ld + l32] : 0.f;
+      }
+  }
   if (n > 0) {  // steps relative to c0
     kw.issue(0, 0);
     kw.issue(1, min(1, n - 1));
@@ -699,7 +751,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
       r[t][j] = v;
     }
 
-  const int rbase = m0 + 4 * kh + 8 * wave;
+  if (EPI == GEMM_FOLD) {
+    // x = residual + this tile's sum (one block per element: no split-K);
+    // the norm's operand fp16(x w 2^ex) and the tile's sum of squares per row
+    // (lanes l32 of a half-wave hold the row's 64 columns; a butterfly sum)
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int row = rbase + 32 * t + e;
+        float sq = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+          const float x = xv[t][j][e] + f4_at(r[t][j], e);
+          sq = fmaf(x, x, sq);
+          if (row < g.M) {
+            const size_t at = (size_t)row * g.ldc + t0 * kTile + 32 * j + l32;
+            g.Cf[at] = x;
+            g.Ch[at] = __builtin_bit_cast(uint16_t, f16_guard(g.ovf, ldexpf(x * nwv[j], exv[t][e])));
+          }
+        }
+        sq = half_sum(sq);
+        if (l32 == 0 && row < g.M) g.ss[(size_t)row * g.ss_ld + t0] = sq;
+      }
+    return;
+  }
   if (EPI == GEMM_ROPE) {
     // tile t0 is one head of 64: q heads, then k, then v.  Lane l32 holds dims
     // d = l32 and d + 32 of its rows, the rotate-half pair of RoPE
@@ -735,6 +811,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     return;
   }
   if (EPI == GEMM_SWIGLU) {
+    // after a GEMM_FOLD the RMSNorm scale of each row comes here: the sum of
+    // its tile sums (a butterfly over the half-wave, every lane the same bits)
+    float sc[MT][4];
+    const float inv_n = 1.f / (float)g.n_norm;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        sc[t][e] = post_norm ? ldexpf(rsqrtf(half_sum(ssv[t][e]) * inv_n + g.eps), -exv[t][e]) : 1.f;
     const int oi = t0 * 32 + l32;
     if (oi >= g.n_out) return;
 #pragma unroll
@@ -743,7 +828,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
       for (int e = 0; e < 4; e++) {
         const int row = rbase + 32 * t + e;
         if (row < g.M) {
-          const float gt = f4_at(r[t][0], e), up = f4_at(r[t][1], e);
+          const float gt = f4_at(r[t][0], e) * sc[t][e], up = f4_at(r[t][1], e) * sc[t][e];
           const _Float16 hv = f16_guard(g.ovf, silu_mul(gt, up));
           g.Ch[(size_t)row * g.ldc + oi] = __builtin_bit_cast(uint16_t, hv);
         }
@@ -852,6 +937,8 @@ bool launch_gemm(int fmt, int epi, const GemmShape& sh, const GemmArgs& ga, hipS
   if (epi == GEMM_SWIGLU && (ga.N % kTile != 0 || sh.nb != 2)) return false;
   if (epi != GEMM_PART && sh.splits != 1) return false;
   if (epi == GEMM_ROPE && !(sh.ring && sh.kw && ga.N % kTile == 0)) return false;  // the K-wave kernel only
+  if (epi == GEMM_FOLD && !(sh.ring && sh.kw && ga.N % kTile == 0 && ga.N / kTile <= ga.ss_ld)) return false;
+  if (epi == GEMM_SWIGLU && ga.ss && !(sh.ring && sh.kw && ga.ss_ld <= 32)) return false;
   GemmArgs g = ga;
   g.spc = sh.spc;
   const dim3 grid(sh.gx, sh.gy, sh.splits);
@@ -863,7 +950,8 @@ bool launch_gemm(int fmt, int epi, const GemmShape& sh, const GemmArgs& ga, hipS
     hipLaunchKernelGGL((gemm_q4_kw_kernel<MTV, E>), grid, dim3(256), 0, st, g);                  \
     return true;                                                                                 \
   }
-#define KW_EPIS(MTV) KW_CASE(MTV, GEMM_STORE) KW_CASE(MTV, GEMM_PART) KW_CASE(MTV, GEMM_SWIGLU) KW_CASE(MTV, GEMM_ROPE)
+#define KW_EPIS(MTV) KW_CASE(MTV, GEMM_STORE) KW_CASE(MTV, GEMM_PART) KW_CASE(MTV, GEMM_SWIGLU) KW_CASE(MTV, GEMM_ROPE) \
+  KW_CASE(MTV, GEMM_FOLD)
     KW_EPIS(1)  // gemm_shape gives the K-wave blocks 32 rows
 #undef KW_EPIS
 #undef KW_CASE
@@ -944,6 +1032,7 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(RowsArgs a) {
   }
   if (!a.Y) return;
   const float inv = rsqrtf(block_sum_f(ss, scratch) / (float)a.H + a.eps);
+  if (a.ex && threadIdx.x == 0) a.ex[m] = max(-64, min(64, ilogbf(inv)));
   half4_t* y = reinterpret_cast<half4_t*>(a.Y + (size_t)m * a.H);
   const float4* w = reinterpret_cast<const float4*>(a.w);
 #pragma unroll
@@ -1265,7 +1354,7 @@ __global__ __launch_bounds__(256 * NG) __attribute__((amdgpu_waves_per_eu(2))) v
       for (int w = 8; w > 0; w >>= 1)
 #pragma unroll
         for (int v = 0; v < w; v++) mv[v] = fmaxf(mv[v], mv[v + w]);
-      float mx = fmaxf(mv[0], __shfl_xor(mv[0], 32, 64)) * a.scale_log2;
+      float mx = fmaxf(mv[0], swap32(mv[0])) * a.scale_log2;
       const float mn = fmaxf(mrun, mx);
       const float mu = mn == -INFINITY ? 0.f : mn;
       const float corr = __builtin_amdgcn_exp2f(mrun - mu);
@@ -1310,7 +1399,7 @@ __global__ __launch_bounds__(256 * NG) __attribute__((amdgpu_waves_per_eu(2))) v
     sg.store(mytile + (buf ^ 1) * NG * AT::TILE_HALVES, t256);
     __syncthreads();
   }
-  lrun += __shfl_xor(lrun, 32, 64);
+  lrun += swap32(lrun);
   if (NG > 1) {  // group 1 hands (max, sum, O) to group 0 through LDS (the tiles are free now)
     float* xch = reinterpret_cast<float*>(lds) + (size_t)(wave * 64 + lane) * (2 + 16 * NDT);
     if (grp == 1) {
