@@ -275,6 +275,19 @@ def test_kv_cache_round_trip_and_reset(ctx):
     m.reset_cache()
     k3, _ = m.kv_read(1, 3, 5)
     assert not k3.any()
+    # the reset clears only the rows that can hold values (every path that
+    # writes rows extends that range): a prefill, a device-fed decode and a
+    # filled cache, then a reset, leave every row of every layer zero
+    for fill in (False, True):
+        if fill:
+            m.kv_fill_normal(3, 40)
+        runner.prefillTokens(list(range(1, 21)), 0, 20)
+        runner.decodeGreedy(5, 20, 10)
+        rows = np.concatenate([np.concatenate(m.kv_read(l, 0, 64)).ravel() for l in range(hw.recipe.layer_count)])
+        assert rows.any()
+        m.reset_cache()
+        rows = np.concatenate([np.concatenate(m.kv_read(l, 0, 64)).ravel() for l in range(hw.recipe.layer_count)])
+        assert not rows.any(), f"rows left after a reset (fill {fill})"
     with pytest.raises(tlm.TlmError):
         runner.computeToken(10 ** 6, 0, True)
     with pytest.raises(tlm.TlmError):

@@ -251,6 +251,7 @@ struct tlm_model {
   bool ps_suspend = false;   // recomputing: every token on the per-stage graph
   bool ps_range_off = false;  // the persistent schedule is off after an fp16 range overflow
   int host_pos = 0;  // position of the last token enqueued (selects the attention mode)
+  int kv_hi = 0;     // cache rows [0, kv_hi) may hold values since the cache was last cleared
   std::vector<int> windows;  // per-layer sliding window (0: full causal)
   tlm_model_counts counts{};  // work handed to the stream (tlm_model_counts_read)
   bool finalized = false;
@@ -459,6 +460,11 @@ static int ps_ordered(tlm_model* m, F enqueue) {
 
 static int model_check(tlm_model* m, const int* ctrl_host = nullptr);
 static int read_ctrl(tlm_model* m, int* c);
+// Positions up to `end` (exclusive) may now hold cache rows (what
+// tlm_reset_cache clears).
+static void kv_touch(tlm_model* m, long end) {
+  m->kv_hi = (int)std::max<long>(m->kv_hi, std::min<long>(end, m->d.max_tokens));
+}
 static int kv_clear(tlm_model* m, int pos0, int n);
 
 
@@ -1658,6 +1664,7 @@ static int run_token(tlm_model* m, bool logits, int pos) {
   hipStream_t st = m->ctx->stream;
   const bool lw = long_window(&m->attn, pos);
   m->host_pos = pos;
+  kv_touch(m, (long)pos + 1);
   if (m->ps_on && !m->ps_suspend && !lw) {  // the persistent schedule
     // its two kernels enqueued directly: a graph launch of the same pair costs
     // ~4.6 us more per token here (Qwen2.5-0.5B decode: 328.3 -> 323.7 us)
@@ -2121,6 +2128,7 @@ int tlm_prefill(tlm_model* m, const int32_t* tokens, int32_t start, int32_t end)
   HIP_TRY(hipStreamSynchronize(st));
   rc = model_check(m);  // the earlier tokens are final before batched chunks overwrite cache rows
   if (rc) return rc;
+  kv_touch(m, end);
   // the ids go to the device in stream order (no staging wait on the host);
   // the pinned words are free again: the stream finished its work above
   memcpy(m->host_pin + kPinPrompt, tokens + start, sizeof(int32_t) * (end - start));
@@ -2339,12 +2347,19 @@ int tlm_reset_cache(tlm_model* m) {
     m->redo.clear();
     m->redo_lost = false;
   }
+  // only the rows that can hold values (positions below kv_hi): clearing all
+  // max_tokens rows (402 MB at the Qwen2.5-0.5B shape's 32768) took ~80 us and
+  // evicted the weights from the 256 MB last-level cache, which the next
+  // prefill or decode then read from HBM (a 127-id prefill after it: 1.07 ms
+  // against 0.99)
   const size_t esz = m->d.kv_fmt == TLM_FMT_F32 ? 4 : 2;
-  const size_t cache = (size_t)m->d.num_kv_heads * m->d.max_tokens * m->d.head_dim * esz;
-  for (auto& L : m->layers) {
-    HIP_TRY(hipMemsetAsync(L.kc, 0, cache, m->ctx->stream));
-    HIP_TRY(hipMemsetAsync(L.vc, 0, cache, m->ctx->stream));
-  }
+  const size_t row = (size_t)m->d.head_dim * esz, pitch = row * m->d.max_tokens;
+  if (m->kv_hi > 0)
+    for (auto& L : m->layers) {
+      HIP_TRY(hipMemset2DAsync(L.kc, pitch, 0, row * m->kv_hi, m->d.num_kv_heads, m->ctx->stream));
+      HIP_TRY(hipMemset2DAsync(L.vc, pitch, 0, row * m->kv_hi, m->d.num_kv_heads, m->ctx->stream));
+    }
+  m->kv_hi = 0;
   return TLM_OK;
 }
 
@@ -2356,6 +2371,7 @@ static int kv_copy(tlm_model* m, int layer, int pos0, int count, void* k, void* 
   const int Hkv = m->d.num_kv_heads, D = m->d.head_dim, M = m->d.max_tokens;
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
   if (int rc = model_check(m)) return rc;  // the enqueued tokens' rows are final
+  if (write) kv_touch(m, (long)pos0 + count);
   for (int h = 0; h < Hkv; h++) {
     // canonical rows are [t][h][d]; device rows are [h][t][d]
     HIP_TRY(hipMemcpy2D(
@@ -2382,6 +2398,7 @@ int tlm_kv_read(tlm_model* m, int layer, int pos0, int count, void* k, void* v) 
 
 int tlm_kv_fill_normal(tlm_model* m, uint64_t seed, int count) {
   if (!m || count < 0 || count > m->d.max_tokens) return fail(TLM_ERR_RANGE, "TLMModel: invalid fill count");
+  kv_touch(m, count);
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
   if (int rc = model_check(m)) return rc;
   for (int l = 0; l < m->d.num_layers; l++) {
@@ -2401,6 +2418,7 @@ int tlm_time_decode(tlm_model* m, int32_t token, int32_t position, int warmup, i
   if (rc) return rc;
   if ((long)position + warmup + n > m->d.max_tokens)
     return fail(TLM_ERR_RANGE, "TLMModel: timed decode passes max_tokens");
+  kv_touch(m, (long)position + warmup + n);
   rc = tlm_model_finalize(m);
   if (rc) return rc;
   hipStream_t st = m->ctx->stream;
@@ -2439,6 +2457,7 @@ static int time_step_parts(tlm_model* m, int32_t token, int32_t position, int n,
   int rc = check_token(m, token, position);
   if (rc) return rc;
   if ((long)position + n > m->d.max_tokens) return fail(TLM_ERR_RANGE, "TLMModel: timed decode passes max_tokens");
+  kv_touch(m, (long)position + n);
   rc = tlm_model_finalize(m);
   if (rc) return rc;
   hipStream_t st = m->ctx->stream;
@@ -2509,6 +2528,7 @@ int tlm_time_kernel(tlm_model* m, int which, int iters, double* avg_ms) {
     return fail(TLM_ERR_INVALID, "TLMModel: invalid kernel timing argument");
   int rc = tlm_model_finalize(m);
   if (rc) return rc;
+  kv_touch(m, m->d.max_tokens);  // a stage timing writes the row at whatever position the control block names
   hipStream_t st = m->ctx->stream;
   hipEvent_t e0, e1;
   HIP_TRY(hipEventCreate(&e0));
@@ -2545,6 +2565,7 @@ int tlm_trace_decode(tlm_model* m, int32_t token, int32_t position, int n, uint6
   int rc = check_token(m, token, position);
   if (rc) return rc;
   if ((long)position + n > m->d.max_tokens) return fail(TLM_ERR_RANGE, "TLMModel: traced decode passes max_tokens");
+  kv_touch(m, (long)position + n);
   if (!m->ps_on) return fail(TLM_ERR_STATE, "TLMModel: this model has no persistent schedule");
   if (long_window(&m->attn, position + n - 1))
     return fail(TLM_ERR_STATE, "TLMModel: position %d needs the long-window kernels", position + n - 1);
