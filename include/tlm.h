@@ -240,7 +240,11 @@ int tlm_read_token(tlm_model* model, int32_t* token);
  * argmax back for n steps without host round trips; out[i] = argmax after
  * position+i.  Equals n rounds of computeToken + sampleToken. */
 int tlm_decode_greedy(tlm_model* model, int32_t token, int32_t position, int n, int32_t* out);
-/* resetCache (DecoderTSLRunner.ts:541-546). */
+/* resetCache (DecoderTSLRunner.ts:541-546): every cache row reads back zero
+ * afterwards.  Only the rows some call could have written since the last
+ * reset are cleared (positions below the highest one a compute, decode,
+ * prefill, fill, write or timing call named), so a reset after a short
+ * sequence costs little and leaves the weights in the last-level cache. */
 int tlm_reset_cache(tlm_model* model);
 /* Cache access in the canonical [count][kv_heads][head_dim] order, kv_fmt
  * element type (uint16 fp16 bits or float). */
