@@ -53,18 +53,18 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * __builtin_amdgcn_rcpf(1.f + __expf(-g)) * u;
 }
 
-// Sum over each 32-lane half of the wave, the same bits in every lane of the
-// half: DPP within 8 and 16 lanes, then gfx950's v_permlane16_swap (no LDS
-// round trip: ds_bpermute steps cost a wait each).
+// Cross-lane steps on the VALU (DPP, gfx950's v_permlane16/32_swap) instead of
+// ds_bpermute, whose LDS round trips each cost a wait.
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
   return __builtin_amdgcn_update_dpp(0.f, v, CTRL, 0xF, 0xF, false);
 }
-// v of lane l ^ 32 (v_permlane32_swap: a VALU op, no LDS round trip)
+// v of lane l ^ 32
 __device__ __forceinline__ float swap32(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
 }
+// Sum over each 32-lane half of the wave, the same bits in every lane of the half.
 __device__ __forceinline__ float half_sum(float v) {
   v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
   v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
@@ -754,7 +754,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   if (EPI == GEMM_FOLD) {
     // x = residual + this tile's sum (one block per element: no split-K);
     // the norm's operand fp16(x w 2^ex) and the tile's sum of squares per row
-    // (lanes l32 of a half-wave hold the row's 64 columns; a butterfly sum)
+    // (lanes l32 of a half-wave hold the row's 64 columns: half_sum)
 #pragma unroll
     for (int t = 0; t < MT; t++)
 #pragma unroll
