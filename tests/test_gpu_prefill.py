@@ -151,6 +151,7 @@ def _kv(model, layers, count):
     ("qwen2.5-0.5b", 2, 151, 64),     # chunks 64 + 64 batched, 22 replayed
     ("qwen2.5-0.5b", 2, 701, 2048),   # 700 rows: 22 row tiles of the K-wave kernels, RoPE epilogue
     ("llama-3.2-1b", 2, 200, 2048),
+    ("llama-3.2-1b", 2, 100, 2048),   # 99 rows: K-wave O and gate|up GEMMs, the O GEMM's fold over 32 tiles
     ("llama-3.2-3b", 2, 100, 2048),   # head_dim 128
 ])
 def test_batched_prefill_matches_replay_and_oracle(ctx, name, layers, prompt_len, chunk):
