@@ -186,10 +186,11 @@ struct tlm_model {
   int* tokens_out = nullptr;
   int* prompt = nullptr;
   float *xa = nullptr, *xf = nullptr, *attn_out = nullptr;
-  // residual accumulators (fixed point, kRep replicas of H): x0 holds the
+  // residual accumulators (fixed point, nrep of kRep replica slots of H): x0 holds the
   // current token's embedding row (staged by the control kernels), rb[l] the
   // residual after layer l's MLP
   unsigned long long *x0 = nullptr, *rb = nullptr;
+  int nrep = kRep;  // replicas the MLP adds into and the residual readers add (rep_count)
   float *pq = nullptr, *po = nullptr;
   int mlp_nch = 1, mlp_ndb = 1;
   float* logits = nullptr;
@@ -1085,6 +1086,19 @@ static int model_alloc(void** p, size_t bytes) {
 
 void tlm_model_destroy(tlm_model* m);
 
+// Replicas of the fixed-point residual for a hidden size: the MLP's down
+// atomics hit each address (blocks / nrep) times and every residual reader
+// (the next QKV GEMV, the LM head) adds nrep vectors.  Measured at long
+// windows (us per token): Llama-3.2-1B shape (hidden 2048) 502 with 2 against
+// 515 with 4; Llama-3.2-3B (3072) 1363 with 2, 1345 with 4, 1385 with 8.
+// TLM_REPLICAS=2 or 4 at model creation overrides it (comparisons).
+static int rep_count(int H) {
+  const char* e = getenv("TLM_REPLICAS");
+  const int v = e ? atoi(e) : 0;
+  if (v == 2 || v == kRep) return v;
+  return H <= 2048 ? 2 : kRep;
+}
+
 static PsArgs ps_args(const tlm_model* m) {
   const tlm_model_desc& d = m->d;
   const Layer& L0 = m->layers[0];
@@ -1287,6 +1301,7 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
     rc = fail(TLM_ERR_HIP, "TLMModel: pinned host buffer allocation failed");
   }
   M_TRY(model_alloc((void**)&m->xa, sizeof(float) * H));
+  m->nrep = rep_count(H);
   M_TRY(model_alloc((void**)&m->x0, sizeof(unsigned long long) * kRep * H));
   M_TRY(model_alloc((void**)&m->rb, sizeof(unsigned long long) * kRep * H * d->num_layers));
   M_TRY(model_alloc((void**)&m->xf, sizeof(float) * H));
@@ -1489,7 +1504,7 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which, bool l
     a.norm_w = L.attn_norm;
     a.eps = (float)d.rms_eps;
     a.xout = m->xa;
-    ok &= launch_linear(L.qkv, PRO_RMSF, a, st);
+    ok &= launch_linear(L.qkv, m->nrep == 2 ? PRO_RMSFH : PRO_RMSF, a, st);
     m->counts.kernel_launches++;
   }
   // 2. RoPE + KV append + split-K attention
@@ -1515,7 +1530,7 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which, bool l
     // the accumulator layer l - 1 produced was last read by this layer's QKV
     // (layer 0: the previous token's final norm): clear it for its next use
     a.zero_ptr = m->rb + (size_t)((l + nl - 1) % nl) * rstride;
-    a.zero_n = (int)rstride;
+    a.zero_n = m->nrep * H;
     // more than 16 long-window chunks: the 32-slot combine keeps it to one round trip
     ok &= launch_linear(L.o, long_win && a.att_nsplit > 16 ? PRO_ATTN3 : PRO_ATTN, a, st);
     m->counts.kernel_launches++;
@@ -1538,6 +1553,7 @@ static bool enqueue_layer(tlm_model* m, int l, hipStream_t st, int which, bool l
     a.Cd = L.down->C;
     a.H = H;
     a.acc = m->rb + (size_t)l * rstride;
+    a.nrep = m->nrep;
     ok &= launch_mlp(wfmt(L.gu->fmt), m->mlp_nch, m->mlp_ndb, L.gu->T, a, st);
     m->counts.kernel_launches++;
   }
@@ -1555,9 +1571,11 @@ static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, hipEvent_t*
   fill_gemv_args(a, m->head, nullptr);
   a.cps = m->lm_plan.cps;
   a.acc_in = m->rb + (size_t)(d.num_layers - 1) * kRep * d.hidden_size;
+  int pro = m->nrep == 2 ? PRO_RMSFH : PRO_RMSF;
   if (ps) {  // the persistent schedule's last residual: the published down partials
     static_assert(kPsMaxKs == kRep, "the LM head prologue folds kRep partials");
     a.acc_in = m->ps_pub_x + (size_t)(d.num_layers - 1) * kPsMaxKs * d.hidden_size;
+    pro = PRO_RMSF;
     a.ps_words = 1;
   }
   a.norm_w = m->final_norm;
@@ -1582,7 +1600,7 @@ static bool enqueue_head(tlm_model* m, hipStream_t st, bool advance, hipEvent_t*
     a.max_steps = d.max_tokens;
   }
   if (ev) hipEventRecord(ev[0], st);
-  if (!launch_lm_head(wfmt(m->head->fmt), PRO_RMSF, m->lm_plan.waves, m->lm_plan.nch, dim3(m->lm_plan.gx), a, st))
+  if (!launch_lm_head(wfmt(m->head->fmt), pro, m->lm_plan.waves, m->lm_plan.nch, dim3(m->lm_plan.gx), a, st))
     return false;
   if (ev) hipEventRecord(ev[1], st);
   if (in_head) {

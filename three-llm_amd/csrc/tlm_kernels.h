@@ -16,10 +16,12 @@ inline bool gqa_attention_fits(int G, int D) {
   return (D == 64 || D == 128) && G >= 1 && G <= 16 && (G + 2) * D <= kGqaPro * 64 * kGqaWaves;
 }
 constexpr int kLongWindow = 1024; // decode attention: windows above this many positions run the long-window kernels
-// Residual stream accumulators: kRep replicas of an int64 fixed-point vector
-// (value * 2^32).  Producers add into replica (block % kRep) with device-scope
-// atomics; integer addition is associative, so the sum is exact and the same
-// in every run.  Readers add the replicas.
+// Residual stream accumulators: up to kRep replicas of an int64 fixed-point
+// vector (value * 2^32).  Producers add into replica (block % nrep) with
+// device-scope atomics; integer addition is associative, so the sum is exact
+// and the same in every run, whatever nrep.  Readers add the nrep replicas:
+// more replicas mean fewer atomics per address in the producer and more reads
+// in every reader (a model's count: rep_count).
 constexpr int kRep = 4;
 constexpr float kFxScale = 4294967296.0f;        // 2^32
 constexpr float kFxInv = 2.3283064365386963e-10f;  // 2^-32
@@ -36,6 +38,8 @@ enum Prologue {
   PRO_RMSF = 5,    // x = rmsnorm(sum of the kRep fixed-point replicas acc_in) * w
   PRO_RMSF2 = 6,   // PRO_RMSF for K up to 8 elements per thread (chosen by launch_gemv)
   PRO_ATTN3 = 7,   // PRO_ATTN folding 32 chunk partials per round trip instead of 16 (long windows)
+  PRO_RMSFH = 8,   // PRO_RMSF over 2 replicas (models whose MLP adds into 2)
+  PRO_RMSF2H = 9,  // PRO_RMSF2 over 2 replicas
 };
 
 // Split of the attention window [first, pos] into chunks; identical on host and device.
@@ -80,7 +84,7 @@ struct GemvArgs {
   const float* in;
   // PRO_RMS
   const float* base;   // fp32 [K] residual stream
-  const unsigned long long* acc_in;  // PRO_RMSF: [kRep][K] fixed-point residual
+  const unsigned long long* acc_in;  // PRO_RMSF: [kRep][K] fixed-point residual (PRO_RMSFH: [2][K])
   unsigned long long* zero_ptr;      // optional: the grid zeroes zero_ptr[0, zero_n)
   int zero_n;
   const int* ctrl;
@@ -126,7 +130,8 @@ struct MlpArgs {
   const uint16_t* sd;       // q4 scales of the down linear
   int Td, Cd;               // down tiles (ceil(H / 64)) and chunks per row
   int H;                    // output rows
-  unsigned long long* acc;  // [kRep][H] fixed-point accumulator, zero on entry
+  unsigned long long* acc;  // [nrep][H] fixed-point accumulator, zero on entry
+  int nrep;                 // replicas of acc: 2 or kRep
 };
 
 struct AttnArgs {

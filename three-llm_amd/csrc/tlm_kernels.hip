@@ -95,11 +95,13 @@ __device__ __forceinline__ void put4(float* xl, float* xsum, int i, float4 y, bo
 // while the weight loads stay outstanding.
 template <int PRO, int FMT>
 struct GemvPrologue {
-  static constexpr bool kRmsF = PRO == PRO_RMSF || PRO == PRO_RMSF2;
+  static constexpr bool kRmsFH = PRO == PRO_RMSFH || PRO == PRO_RMSF2H;  // 2 replicas
+  static constexpr bool kRmsF = PRO == PRO_RMSF || PRO == PRO_RMSF2 || kRmsFH;
+  static constexpr int NREP = kRmsFH ? 2 : kRep;  // replicas of the fixed-point residual
   static constexpr bool kRms = PRO == PRO_RMS || PRO == PRO_RMS2 || kRmsF;
-  static constexpr int R = (PRO == PRO_RMS2 || PRO == PRO_RMSF2) ? 2 : 1;  // float4s of the residual row per thread
+  static constexpr int R = (PRO == PRO_RMS2 || PRO == PRO_RMSF2 || PRO == PRO_RMSF2H) ? 2 : 1;  // float4s of the residual row per thread
   float4 x[R], w[R];
-  ulonglong2 fx[kRmsF ? R : 1][kRep][2];  // RMSF: the 4 elements' replicas
+  ulonglong2 fx[kRmsF ? R : 1][NREP][2];  // RMSF: the 4 elements' replicas
   float4 p[2][kMaxPart];  // RMS: partials per float4 (R rows); SWIGLU: [0] gate, [1] up partials
   static constexpr int kSlotLanes = 8;  // ATTN: lanes sharing one float4, splitting its chunk slots
   static constexpr bool kAttn = PRO == PRO_ATTN || PRO == PRO_ATTN3;
@@ -166,7 +168,7 @@ struct GemvPrologue {
           w[r] = *reinterpret_cast<const float4*>(a.norm_w + 4 * f);
           if (kRmsF) {
 #pragma unroll
-            for (int q = 0; q < kRep; q++) {
+            for (int q = 0; q < NREP; q++) {
               const ulonglong2* src = reinterpret_cast<const ulonglong2*>(a.acc_in + (size_t)q * a.K + 4 * f);
               fx[kRmsF ? r : 0][q][0] = src[0];
               fx[kRmsF ? r : 0][q][1] = src[1];
@@ -179,7 +181,7 @@ struct GemvPrologue {
           w[r] = make_float4(0.f, 0.f, 0.f, 0.f);
           if (kRmsF) {
 #pragma unroll
-            for (int q = 0; q < kRep; q++) fx[kRmsF ? r : 0][q][0] = fx[kRmsF ? r : 0][q][1] = make_ulonglong2(0, 0);
+            for (int q = 0; q < NREP; q++) fx[kRmsF ? r : 0][q][0] = fx[kRmsF ? r : 0][q][1] = make_ulonglong2(0, 0);
           } else {
             x[r] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
@@ -268,7 +270,7 @@ struct GemvPrologue {
       if (a.ps_words) {  // published words: the fp32 value in the low half, partials summed in order
         float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int q = 0; q < kRep; q++) {
+        for (int q = 0; q < NREP; q++) {
           y.x += __uint_as_float((unsigned)fx[kRmsF ? r : 0][q][0].x);
           y.y += __uint_as_float((unsigned)fx[kRmsF ? r : 0][q][0].y);
           y.z += __uint_as_float((unsigned)fx[kRmsF ? r : 0][q][1].x);
@@ -278,7 +280,7 @@ struct GemvPrologue {
       }
       unsigned long long s0 = 0, s1 = 0, s2 = 0, s3 = 0;
 #pragma unroll
-      for (int q = 0; q < kRep; q++) {
+      for (int q = 0; q < NREP; q++) {
         s0 += fx[kRmsF ? r : 0][q][0].x;
         s1 += fx[kRmsF ? r : 0][q][0].y;
         s2 += fx[kRmsF ? r : 0][q][1].x;
@@ -681,7 +683,8 @@ bool launch_gemv(int fmt, int pro, int waves, int nch, dim3 grid, const GemvArgs
   // the RMS prologue keeps one (PRO_RMS) or two (PRO_RMS2) float4s of the
   // residual row per thread
   if (pro == PRO_RMSF && a.K > 4 * 64 * waves) pro = PRO_RMSF2;
-  if (pro == PRO_RMSF2 && a.K > 8 * 64 * waves) return false;
+  if (pro == PRO_RMSFH && a.K > 4 * 64 * waves) pro = PRO_RMSF2H;
+  if ((pro == PRO_RMSF2 || pro == PRO_RMSF2H) && a.K > 8 * 64 * waves) return false;
   if (pro == PRO_RMS || pro == PRO_RMS2) return false;  // residual + partials: the fused MLP kernel only
 #define GEMV_CASE(F, P, Wv, N)                                                          \
   if (fmt == F && pro == P && waves == Wv && nch == N) {                                \
@@ -693,6 +696,8 @@ bool launch_gemv(int fmt, int pro, int waves, int nch, dim3 grid, const GemvArgs
   GEMV_W(WF_Q4, PRO_COPY)
   GEMV_W(WF_Q4, PRO_RMSF)
   GEMV_W(WF_Q4, PRO_RMSF2)
+  GEMV_W(WF_Q4, PRO_RMSFH)
+  GEMV_W(WF_Q4, PRO_RMSF2H)
   GEMV_W(WF_Q4, PRO_SWIGLU)
   GEMV_W(WF_Q4, PRO_ATTN)
   GEMV_W(WF_F16, PRO_ATTN)
@@ -701,6 +706,8 @@ bool launch_gemv(int fmt, int pro, int waves, int nch, dim3 grid, const GemvArgs
   GEMV_W(WF_F16, PRO_COPY)
   GEMV_W(WF_F16, PRO_RMSF)
   GEMV_W(WF_F16, PRO_RMSF2)
+  GEMV_W(WF_F16, PRO_RMSFH)
+  GEMV_W(WF_F16, PRO_RMSF2H)
   GEMV_W(WF_F16, PRO_SWIGLU)
 #undef GEMV_W
 #undef GEMV_N
@@ -711,7 +718,8 @@ bool launch_gemv(int fmt, int pro, int waves, int nch, dim3 grid, const GemvArgs
 bool launch_lm_head(int fmt, int pro, int waves, int nch, dim3 grid, const GemvArgs& a, hipStream_t st) {
   const size_t smem = gemv_smem_bytes(fmt, a.cps, waves);
   if (pro == PRO_RMSF && a.K > 4 * 64 * waves) pro = PRO_RMSF2;
-  if (pro == PRO_RMSF2 && a.K > 8 * 64 * waves) return false;
+  if (pro == PRO_RMSFH && a.K > 4 * 64 * waves) pro = PRO_RMSF2H;
+  if ((pro == PRO_RMSF2 || pro == PRO_RMSF2H) && a.K > 8 * 64 * waves) return false;
 #define LM_CASE(F, P, Wv, N)                                                               \
   if (fmt == F && pro == P && waves == Wv && nch == N) {                                   \
     hipLaunchKernelGGL((lm_head_kernel<F, P, Wv, N>), grid, dim3(Wv * 64), smem, st, a);   \
@@ -719,7 +727,8 @@ bool launch_lm_head(int fmt, int pro, int waves, int nch, dim3 grid, const GemvA
   }
 #define LM_N(F, P, Wv) LM_CASE(F, P, Wv, 1) LM_CASE(F, P, Wv, 2) LM_CASE(F, P, Wv, 4) LM_CASE(F, P, Wv, 8) \
   LM_CASE(F, P, Wv, 16)
-#define LM_P(F, Wv) LM_N(F, PRO_COPY, Wv) LM_N(F, PRO_RMSF, Wv) LM_N(F, PRO_RMSF2, Wv)
+#define LM_P(F, Wv) LM_N(F, PRO_COPY, Wv) LM_N(F, PRO_RMSF, Wv) LM_N(F, PRO_RMSF2, Wv) LM_N(F, PRO_RMSFH, Wv) \
+  LM_N(F, PRO_RMSF2H, Wv)
   LM_P(WF_F16, 4) LM_P(WF_F16, 8) LM_P(WF_Q4, 4) LM_P(WF_Q4, 8)
 #undef LM_P
 #undef LM_N
@@ -762,7 +771,7 @@ struct MlpDown {
 //   (TSLRMSNorm.ts:50-74), [g | u] = rows of the paired gate|up tile,
 //   h = silu(g) * u (TSLSiLUMul.ts:15-29), then the down columns i0..i0+31:
 //   y[n] += sum_i Wd[n][i0 + i] h[i], added in fixed point to replica
-//   (block % kRep) of the accumulator; block 0 also adds x_mid (the residual).
+//   (block % nrep, nrep a power of two) of the accumulator; block 0 also adds x_mid (the residual).
 // TSLGatedMLP.ts:17-90 computes the same product as three dispatches.
 template <int FMT, int PRO, int NCH, int DB>
 __global__ __launch_bounds__(kMlpWaves * 64) void mlp_kernel(MlpArgs m) {
@@ -826,7 +835,7 @@ __global__ __launch_bounds__(kMlpWaves * 64) void mlp_kernel(MlpArgs m) {
         const int n = td * kTile + lane;
         if (n < m.H) {
           fx_guard(p, a.ctrl);
-          atomicAdd(m.acc + (size_t)(blk % kRep) * m.H + n, to_fx(p));
+          atomicAdd(m.acc + (size_t)(blk & (m.nrep - 1)) * m.H + n, to_fx(p));
         }
       }
     }
