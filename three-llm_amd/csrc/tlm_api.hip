@@ -1315,11 +1315,12 @@ int tlm_model_create(tlm_ctx* ctx, const tlm_model_desc* d, tlm_model** out) {
     // loads (the memory pipeline stalls a wave that issues more than it takes)
     // and into the norm sooner, and the rest of its chunks stream through the
     // loop.  Measured (tok/s), gate|up batch + down batch: Llama-3.2-3B at
-    // 16384 positions 713 with 8 + 4, 744 with 2 + 1, 749 with 1 + 1;
-    // Llama-3.2-1B at 4096 1908 with 4 + 4, 1960 with 2 + 1 or 1 + 1;
-    // Qwen2.5-0.5B per-stage graph 2263 with 2 + 1, 2249 with 1 + 1.
+    // 16384 positions 713 with 8 + 4, 744 with 2 + 1, 749 with 1 + 1 (A/B
+    // again: 1339.7 against 1344.5 us per token); Llama-3.2-1B at 4096 1908
+    // with 4 + 4, 1960 with 2 + 1 or 1 + 1; Qwen2.5-0.5B per-stage graph 2263
+    // with 2 + 1, 2249 with 1 + 1.  One chunk from six chunks per wave up.
     const int per = (L0.gu->C + kMlpWaves - 1) / kMlpWaves;
-    m->mlp_nch = per <= 1 ? 1 : 2;
+    m->mlp_nch = per <= 1 || per >= 6 ? 1 : 2;
     m->mlp_ndb = 1;
     if (mlp_smem_bytes(wfmt(lf), L0.gu->C, H) > 65536)
       rc = fail(TLM_ERR_INVALID, "TLMModel: hidden size %d too large for the fused MLP block", H);
