@@ -1827,6 +1827,10 @@ static RowsArgs rows_args(float* X, const float* part, int n_part, size_t pstrid
   r.eps = (float)eps;
   r.Y = Y;
   r.ex = nullptr;
+  r.emb = nullptr;
+  r.emb_f32 = 0;
+  r.tokens = nullptr;
+  r.ctrl = nullptr;
   return r;
 }
 
@@ -1887,15 +1891,21 @@ static int prefill_enqueue(tlm_model* m, const PfPlan& pp, int M, hipStream_t st
   const int H = d.hidden_size, I = d.intermediate_size, D = d.head_dim;
   const int lf = wfmt(d.linear_fmt);
   const size_t rowsH = (size_t)M * H;
-  launch_embed_rows(m->prompt, M, m->emb, d.embed_fmt == TLM_FMT_F32, H, m->pf_x, st, m->ctrl);
-  // per layer: two row kernels, the QKV GEMM (+ rope_kv unless RoPE runs in its
-  // epilogue), attention and three GEMMs; then the last fold
+  // per layer: two row kernels (one when the O GEMM folds its rows; layer 0's
+  // first one also gathers the embedding rows), the QKV GEMM (+ rope_kv unless
+  // RoPE runs in its epilogue), attention and three GEMMs; then the last fold
   for (int l = 0; l < d.num_layers; l++) {
     const Layer& L = m->layers[l];
     bool ok = true;
     RowsArgs ra = rows_args(m->pf_x, m->pf_part, l ? pp.sd.splits : 0, rowsH, H, L.attn_norm, d.rms_eps, m->pf_xn,
                             m->pf_ovf);
     if (pp.fold) ra.ex = m->pf_ex;
+    if (l == 0) {  // the residual rows start as the chunk's embedding rows
+      ra.emb = m->emb;
+      ra.emb_f32 = d.embed_fmt == TLM_FMT_F32;
+      ra.tokens = m->prompt;
+      ra.ctrl = m->ctrl;
+    }
     launch_rms_rows(ra, M, st);
     GemmArgs g = gemm_args(L.qkv, m->pf_xn, H, M);
     g.ovf = m->pf_ovf;
@@ -1994,7 +2004,7 @@ static int prefill_enqueue(tlm_model* m, const PfPlan& pp, int M, hipStream_t st
   }
   // the last layer's MLP output joins the residual rows
   launch_rms_rows(rows_args(m->pf_x, m->pf_part, pp.sd.splits, rowsH, H, nullptr, d.rms_eps, nullptr, nullptr), M, st);
-  return 1 + d.num_layers * ((pp.rope_epi ? 7 : 8) - (pp.fold ? 1 : 0)) + 1;
+  return d.num_layers * ((pp.rope_epi ? 7 : 8) - (pp.fold ? 1 : 0)) + 1;
 }
 
 // One batched chunk [p, p + M) of the prompt [start, end): the control block

@@ -388,6 +388,12 @@ struct RowsArgs {
   int* ovf;             // set to 1 when a normed fp16 value is not finite; may be null
   int* ex;              // with Y: row m's ilogb(rsqrt(mean(x^2) + eps)), the scale exponent of a
                         // later GEMM_FOLD of the same rows; may be null
+  // non-null emb: X[m] is first set to the embedding row of token tokens[i + m],
+  // i = ctrl[C_POS] - ctrl[C_BASE] (0 without ctrl), fp32 or fp16 table (emb_f32)
+  const void* emb;
+  int emb_f32;
+  const int* tokens;
+  const int* ctrl;
 };
 struct PrefillAttnArgs {
   const uint16_t* q;    // fp16 [M][Hq D], RoPE applied
@@ -415,11 +421,6 @@ struct RopeKvArgs {
 };
 GemmShape gemm_shape(int fmt, int epi, int M, int N, int K, int cus);
 bool launch_gemm(int fmt, int epi, const GemmShape& sh, const GemmArgs& g, hipStream_t st);
-// Row m of X = embedding row of tokens[m] (ctrl non-null: of
-// tokens[ctrl[C_POS] - ctrl[C_BASE] + m], the chunk of the prompt buffer at
-// the position the control block names).
-void launch_embed_rows(const int* tokens, int M, const void* emb, int f32, int H, float* X, hipStream_t st,
-                       const int* ctrl = nullptr);
 void launch_rms_rows(const RowsArgs& a, int M, hipStream_t st);
 void launch_rope_kv(const RopeKvArgs& a, hipStream_t st);
 bool launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t st);

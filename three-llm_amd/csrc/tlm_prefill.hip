@@ -986,25 +986,12 @@ bool launch_gemm(int fmt, int epi, const GemmShape& sh, const GemmArgs& ga, hipS
 
 // ------------------------------------------------------------ row kernels --
 
-// X[m] = embedding row of tokens[m] in fp32 (DecoderWeights.ts:355-383 stages
-// the same rows for the replayed decode graph)
-__global__ void embed_rows_kernel(const int* tokens, const void* emb, int f32, int H, float* X, const int* ctrl) {
-  const int m = blockIdx.x;
-  const size_t row = (size_t)tokens[(ctrl ? ctrl[C_POS] - ctrl[C_BASE] : 0) + m] * H;
-  for (int k = threadIdx.x; k < H; k += blockDim.x)
-    X[(size_t)m * H + k] = f32 ? static_cast<const float*>(emb)[row + k]
-                               : __half2float(static_cast<const __half*>(emb)[row + k]);
-}
-
-void launch_embed_rows(const int* tokens, int M, const void* emb, int f32, int H, float* X, hipStream_t st,
-                       const int* ctrl) {
-  hipLaunchKernelGGL(embed_rows_kernel, dim3(M), dim3(256), 0, st, tokens, emb, f32, H, X, ctrl);
-}
-
 // Residual fold + RMSNorm per row (TSLRMSNorm.ts:18-81): x = X[m] + sum of
-// the split-K slices part[s][m] (written back to X when there are any), then
-// Y[m] = fp16(x * rsqrt(mean(x^2) + eps) * w) unless Y is null.  H % 4 == 0,
-// H <= 4096: each of the 256 threads holds up to four float4 of the row.
+// the split-K slices part[s][m] (written back to X when there are any), or
+// (emb non-null, layer 0) the embedding row of the row's token in fp32, stored
+// to X (DecoderWeights.ts:355-383 stages the same rows for the replayed decode
+// graph); then Y[m] = fp16(x * rsqrt(mean(x^2) + eps) * w) unless Y is null.
+// H % 4 == 0, H <= 4096: each of the 256 threads holds up to four float4 of the row.
 constexpr int kRowVec = 4;
 __global__ __launch_bounds__(256) void rms_rows_kernel(RowsArgs a) {
   __shared__ float scratch[4];
@@ -1014,11 +1001,21 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(RowsArgs a) {
   const size_t ps4 = a.pstride >> 2;
   float4 xs[kRowVec];
   float ss = 0.f;
+  size_t erow = 0;  // the embedding row's first element
+  if (a.emb) erow = (size_t)a.tokens[(a.ctrl ? a.ctrl[C_POS] - a.ctrl[C_BASE] : 0) + m] * a.H;
 #pragma unroll
   for (int j = 0; j < kRowVec; j++) {
     const int k = threadIdx.x + 256 * j;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (k < H4) {
+    if (k < H4 && a.emb) {
+      if (a.emb_f32) {
+        v = reinterpret_cast<const float4*>(static_cast<const float*>(a.emb) + erow)[k];
+      } else {
+        const half4_t h = reinterpret_cast<const half4_t*>(static_cast<const _Float16*>(a.emb) + erow)[k];
+        v = make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+      }
+      x[k] = v;
+    } else if (k < H4) {
       v = x[k];
 #pragma unroll 4
       for (int s = 0; s < a.n_part; s++) {
